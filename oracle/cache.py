@@ -1,0 +1,250 @@
+"""numpy restatement of the three-pool SSPA cache and its append/flush (test infrastructure only).
+
+Follows, for the released ``v_fourq_k_int4_compact`` cache with INT2 generated values:
+  * ``_compact_page_layouts``      precision_pool.py:611-669  (stable FP -> INT4 -> INT2 -> evicted)
+  * ``build_three_precision_cache`` precision_pool.py:787-984 (+ arenas in compact_int4_key.py:223-281,
+                                   fused_value_pack.py:152-193, 519-575, recent ring :747-784)
+  * ``append_generated_token``     dynamic_fourq_cache.py:172-267 (flush: compact_int4_key.py:210-220,
+                                   fused_value_pack.py:474-516; ring refresh :108-117)
+
+Pinning: tests/test_oracle_golden.py compares every arena byte, scale, zero point, ring row and
+pool count against fixtures written by the reference's own CPU path (tests/golden/make_golden.py),
+before and after a flush with a partial K tail.  tests/test_oracle_cache.py checks the
+reference's own invariants (tests/test_active_cache_storage.py:72-94: 129 appends on a 128-token
+ring give 128 flushed tokens and one active token) and the FP/INT4/INT2 token-order partition.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .quant import (
+    dequantize_int4_key,
+    quantize_int2_value,
+    quantize_int4_key_per_channel,
+    quantize_int4_value,
+    round_to_dtype,
+)
+
+# PageClass values (policy/four_quadrant.py:6-12)
+EVICTED_PAGE, FP_PAGE, INT4_PAGE, RECENT_FP_PAGE, PROTECTED_FP_PAGE, INT2_PAGE = 0, 1, 2, 3, 4, 5
+
+
+def _round_up(v: int, m: int) -> int:
+    return -(-int(v) // int(m)) * int(m)
+
+
+def compact_page_layouts(page_offsets, page_lengths, page_classes):
+    """Token order of each pool: FP (incl. protected and recent pages), INT4, INT2, evicted.
+
+    Pages are stably sorted by tier (precision_pool.py:621-632); tokens keep page order.
+    Returns four int64 arrays of logical token indices.
+    """
+    classes = np.asarray(page_classes, dtype=np.int64)
+    category = np.full(classes.shape, 3, dtype=np.int64)
+    category[(classes == FP_PAGE) | (classes == PROTECTED_FP_PAGE) | (classes == RECENT_FP_PAGE)] = 0
+    category[classes == INT4_PAGE] = 1
+    category[classes == INT2_PAGE] = 2
+    order = np.argsort(category, kind="stable")
+    out = []
+    for tier in range(4):
+        pages = order[category[order] == tier]
+        parts = [np.arange(page_offsets[p], page_offsets[p] + page_lengths[p], dtype=np.int64) for p in pages]
+        out.append(np.concatenate(parts) if parts else np.zeros(0, np.int64))
+    return tuple(out)
+
+
+@dataclass
+class OracleCache:
+    dtype: str
+    hkv: int
+    page_size: int
+    superblock: int
+    group: int
+    flush_size: int
+    # compact INT4 K arena
+    k_packed: np.ndarray
+    k_scale: np.ndarray
+    k_zero: np.ndarray
+    k_active: int
+    k_capacity: int
+    k_segments: tuple
+    # value pools
+    fp_v: np.ndarray            # [H, S_FP, D] float32 (values of the input dtype)
+    v4_packed: np.ndarray       # [H, S_I4, D/2] u8
+    v4_scale: np.ndarray        # [H, S_I4, 1] f32
+    v2_packed: np.ndarray       # [H, V2cap, D/4] u8
+    v2_scale: np.ndarray        # [H, V2cap, D/G, 1] f16
+    v2_zero: np.ndarray         # [H, V2cap, D/G, 1] u8
+    v2_active: int
+    v2_capacity: int
+    # Recent-FP ring
+    recent_k: np.ndarray        # [H, cap, D] float32
+    recent_v: np.ndarray
+    recent_active: int
+    recent_global: np.ndarray   # [cap] int64
+    recent_logical: np.ndarray
+    recent_page_lengths: np.ndarray
+    # pool bookkeeping
+    pool_tokens: list = field(default_factory=list)   # [fp, int4, int2(incl. generated)]
+    int2_global: list = field(default_factory=list)
+    int2_logical: list = field(default_factory=list)
+    flushed_tokens: int = 0
+    tail_dequant_tokens: int = 0
+
+    @property
+    def recent_capacity(self) -> int:
+        return int(self.recent_k.shape[1])
+
+
+def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: str,
+                page_size: int = 32, superblock: int = 32, group: int = 32,
+                recent_capacity: int = 128, append_capacity: int = 260,
+                flush_size: int = 128) -> OracleCache:
+    """Restatement of ``build_three_precision_cache`` for ``v_fourq_k_int4_compact``.
+
+    ``key``/``value`` are float32 arrays holding values of ``dtype`` ([Hkv, S, 128]).
+    """
+    key = np.asarray(key, np.float32)
+    value = np.asarray(value, np.float32)
+    h, s, d = key.shape
+    fp_t, i4_t, i2_t, ev_t = compact_page_layouts(page_offsets, page_lengths, page_classes)
+    if len(fp_t) + len(i4_t) + len(i2_t) + len(ev_t) != s:
+        raise ValueError("compact physical pools must cover every logical token")
+    # compact INT4-K arena over the physical order FP, INT4, INT2 (compact_int4_key.py:223-281)
+    ordered = np.concatenate((fp_t, i4_t, i2_t))
+    active = len(ordered)
+    k_cap = max(128, _round_up(active + append_capacity, 128))
+    blocks = k_cap // superblock
+    k_packed = np.zeros((h, k_cap, d // 2), np.uint8)
+    k_scale = np.zeros((h, blocks, d), np.float16)
+    k_zero = np.zeros((h, blocks, d), np.uint8)
+    for start in range(0, active, superblock):
+        toks = ordered[start : start + superblock]
+        p, sc, z = quantize_int4_key_per_channel(key[:, toks], superblock)
+        k_packed[:, start : start + len(toks)] = p
+        k_scale[:, start // superblock] = sc[:, 0]
+        k_zero[:, start // superblock] = z[:, 0]
+    # value pools
+    fp_v = value[:, fp_t].copy()
+    v4_packed, v4_scale = quantize_int4_value(value[:, i4_t])
+    v2_cap = max(128, _round_up(len(i2_t) + append_capacity, 128))
+    groups = d // group
+    v2_packed = np.zeros((h, v2_cap, d // 4), np.uint8)
+    v2_scale = np.zeros((h, v2_cap, groups, 1), np.float16)
+    v2_zero = np.zeros((h, v2_cap, groups, 1), np.uint8)
+    p2, s2, z2 = quantize_int2_value(value[:, i2_t], group)
+    v2_packed[:, : len(i2_t)] = p2
+    v2_scale[:, : len(i2_t)] = s2
+    v2_zero[:, : len(i2_t)] = z2
+    # Recent-FP ring, empty at build time (precision_pool.py:747-784)
+    pages = recent_capacity // page_size
+    return OracleCache(
+        dtype=dtype, hkv=h, page_size=page_size, superblock=superblock, group=group,
+        flush_size=flush_size,
+        k_packed=k_packed, k_scale=k_scale, k_zero=k_zero, k_active=active, k_capacity=k_cap,
+        k_segments=(0, len(fp_t), len(fp_t) + len(i4_t)),
+        fp_v=fp_v, v4_packed=v4_packed, v4_scale=v4_scale,
+        v2_packed=v2_packed, v2_scale=v2_scale, v2_zero=v2_zero,
+        v2_active=len(i2_t), v2_capacity=v2_cap,
+        recent_k=np.zeros((h, recent_capacity, d), np.float32),
+        recent_v=np.zeros((h, recent_capacity, d), np.float32),
+        recent_active=0,
+        recent_global=np.full(recent_capacity, -1, np.int64),
+        recent_logical=np.full(recent_capacity, -1, np.int64),
+        recent_page_lengths=np.zeros(pages, np.int64),
+        pool_tokens=[len(fp_t), len(i4_t), len(i2_t)],
+        int2_global=list(i2_t), int2_logical=list(i2_t),
+    )
+
+
+def _flush_key_superblock(c: OracleCache, key_block: np.ndarray) -> int:
+    """``CompactInt4KeyArena.append_superblock`` (compact_int4_key.py:210-220)."""
+    n = key_block.shape[1]
+    if c.k_active + 128 > c.k_capacity:
+        raise RuntimeError("compact INT4 K capacity exhausted")
+    prefix = c.k_active // c.superblock * c.superblock
+    tail_count = c.k_active - prefix
+    tail = dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, prefix, tail_count, c.superblock)
+    tail = round_to_dtype(tail, c.dtype)
+    merged = np.concatenate((tail, key_block), axis=1)
+    p, sc, z = quantize_int4_key_per_channel(merged, c.superblock)
+    c.k_packed[:, prefix : prefix + merged.shape[1]] = p
+    b0 = prefix // c.superblock
+    c.k_scale[:, b0 : b0 + sc.shape[1]] = sc
+    c.k_zero[:, b0 : b0 + z.shape[1]] = z
+    c.k_active += n
+    return tail_count
+
+
+def _flush_value_int2(c: OracleCache, value_block: np.ndarray) -> None:
+    """``CompactInt2ValueArena.append_superblock`` (fused_value_pack.py:474-516)."""
+    n = value_block.shape[1]
+    dst = c.v2_active
+    if dst + n > c.v2_capacity:
+        raise RuntimeError(f"compact INT2 V capacity exhausted: need {dst + n}, have {c.v2_capacity}")
+    p, s, z = quantize_int2_value(value_block, c.group)
+    c.v2_packed[:, dst : dst + n] = p
+    c.v2_scale[:, dst : dst + n] = s
+    c.v2_zero[:, dst : dst + n] = z
+    c.v2_active += n
+
+
+def append_token(c: OracleCache, new_k, new_v, *, global_index: int, logical_position: int) -> bool:
+    """``append_generated_token`` with the compact INT4-K / INT2-V flush.
+
+    ``new_k``/``new_v`` are [Hkv, D] float32 holding values of the cache dtype.
+    """
+    flushed = False
+    cap = c.recent_capacity
+    f = c.flush_size
+    if c.recent_active == cap:
+        key_block = c.recent_k[:, :f].copy()
+        value_block = c.recent_v[:, :f].copy()
+        g_block = c.recent_global[:f].copy()
+        l_block = c.recent_logical[:f].copy()
+        c.tail_dequant_tokens += _flush_key_superblock(c, key_block)
+        _flush_value_int2(c, value_block)
+        c.int2_global.extend(g_block.tolist())
+        c.int2_logical.extend(l_block.tolist())
+        c.pool_tokens[2] += f
+        rem = c.recent_active - f
+        c.recent_k[:, :rem] = c.recent_k[:, f : c.recent_active].copy()
+        c.recent_v[:, :rem] = c.recent_v[:, f : c.recent_active].copy()
+        c.recent_global[:rem] = c.recent_global[f : c.recent_active].copy()
+        c.recent_logical[:rem] = c.recent_logical[f : c.recent_active].copy()
+        c.recent_active = rem
+        c.flushed_tokens += f
+        flushed = True
+    pos = c.recent_active
+    c.recent_k[:, pos] = np.asarray(new_k, np.float32).reshape(c.hkv, -1)
+    c.recent_v[:, pos] = np.asarray(new_v, np.float32).reshape(c.hkv, -1)
+    c.recent_global[pos] = int(global_index)
+    c.recent_logical[pos] = int(logical_position)
+    c.recent_active += 1
+    offsets = np.arange(len(c.recent_page_lengths)) * c.page_size
+    c.recent_page_lengths[:] = np.clip(c.recent_active - offsets, 0, c.page_size)
+    return flushed
+
+
+def pool_kv(c: OracleCache):
+    """Dequantised (K, V) float32 per non-empty pool, in the oracle's pool order FP, INT4, INT2, Recent."""
+    from .quant import dequantize_int2_value, dequantize_int4_value, round_to_dtype
+
+    out = []
+    s_fp, s_i4, s_i2 = c.pool_tokens
+    segs = c.k_segments
+    if s_fp:
+        out.append((dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, segs[0], s_fp, c.superblock), c.fp_v))
+    if s_i4:
+        # PackedTensor.dequantize rounds the fp32 product back to the input dtype
+        # (packed_kv_layout.py:30-32); the compact INT4-K / INT2-V arenas stay fp32.
+        out.append((dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, segs[1], s_i4, c.superblock),
+                    round_to_dtype(dequantize_int4_value(c.v4_packed, c.v4_scale), c.dtype)))
+    if s_i2:
+        out.append((dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, segs[2], s_i2, c.superblock),
+                    dequantize_int2_value(c.v2_packed[:, :s_i2], c.v2_scale[:, :s_i2], c.v2_zero[:, :s_i2], c.group)))
+    if c.recent_active:
+        out.append((c.recent_k[:, : c.recent_active], c.recent_v[:, : c.recent_active]))
+    return out

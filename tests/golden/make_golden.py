@@ -1,0 +1,183 @@
+"""Write the golden fixtures for the SSPA packed-KV cache from the reference's own CPU path.
+
+This script is run by hand, in the build container only, where the reference checkout is
+mounted read-only at ``/root/reference``.  It imports the reference's torch-only runtime
+(r2omni/sspa/runtime/*, r2omni/sspa/policy/page_assignment.py, cache_plan.py and
+kernels/triton_fourq_attention.py) and records inputs and outputs as ``.npz`` fixtures next
+to this file.  Nothing else in this repository imports the reference; the fixtures are data.
+
+What the fixtures pin (functions with no closed form; every other function is also checked
+against closed forms and invariants in tests/test_oracle_*.py):
+
+* ``_compact_page_layouts`` stable FP -> INT4 -> INT2 token order and therefore the INT4-K
+  superblock membership (precision_pool.py:611-669, compact_int4_key.py:223-281);
+* ``append_superblock`` dequantise-then-requantise of a partial K tail on a flush
+  (compact_int4_key.py:210-220) and the INT2-V flush append (fused_value_pack.py:474-516);
+* the Recent-FP ring state after ``append_generated_token`` (dynamic_fourq_cache.py:172-267);
+* ``triton_mixed_reference`` attention outputs on those caches (triton_fourq_attention.py:72-125).
+
+Usage:  python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REFERENCE = "/root/reference"
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().clone().contiguous()  # never a view of a tensor mutated later
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def _modality(total: int, gen: torch.Generator) -> torch.Tensor:
+    """Runs of random length so that pages are ragged at modality boundaries."""
+    out = []
+    kind = 1
+    while len(out) < total:
+        run = int(torch.randint(5, 70, (1,), generator=gen))
+        out.extend([kind] * run)
+        kind = 1 + (kind % 2)
+    return torch.tensor(out[:total], dtype=torch.long)
+
+
+def _case(name, *, seq, hkv, dtype, page_size, sb, group, tier_probs, appends, seed):
+    sys.path.insert(0, REFERENCE)
+    from r2omni.sspa.policy.page_assignment import build_page_table, project_token_bits_to_pages
+    from r2omni.sspa.runtime.cache_plan import build_layer_compression_plan
+    from r2omni.sspa.runtime.precision_pool import build_three_precision_cache
+    from r2omni.sspa.runtime.dynamic_fourq_cache import DynamicCacheStats, append_generated_token
+    from r2omni.sspa.kernels.triton_fourq_attention import triton_mixed_reference
+
+    gen = torch.Generator().manual_seed(seed)
+    d = 128
+    key = torch.randn(hkv, seq, d, generator=gen).to(dtype)
+    outlier = torch.randperm(d, generator=gen)[:4]
+    key[:, :, outlier] = (key[:, :, outlier].float() * 8.0).to(dtype)
+    value = torch.randn(hkv, seq, d, generator=gen).to(dtype)
+    modality = _modality(seq, gen)
+    table = build_page_table(
+        modality,
+        page_size=page_size,
+        protected_mask=torch.zeros(seq, dtype=torch.bool),
+        recent_mask=torch.zeros(seq, dtype=torch.bool),
+    )
+    # one precision per page, drawn from a seeded categorical over (16, 4, 2) bits
+    probs = torch.tensor(tier_probs, dtype=torch.float)
+    page_tier = torch.multinomial(probs, table.num_pages, replacement=True, generator=gen)
+    bits_per_tier = torch.tensor([16, 4, 2], dtype=torch.int8)
+    bits = torch.empty(seq, dtype=torch.int8)
+    for page, (off, ln) in enumerate(zip(table.offsets.tolist(), table.lengths.tolist())):
+        bits[off : off + ln] = bits_per_tier[page_tier[page]]
+    assignment = project_token_bits_to_pages(table, bits)
+    plan = build_layer_compression_plan(0, assignment, recent_fp_capacity=128)
+    cache = build_three_precision_cache(
+        key,
+        value,
+        plan,
+        page_size=page_size,
+        key_quantization_superblock=sb,
+        int2_group_size=group,
+        compact_key_append_capacity=260,
+        recent_flush_size=128,
+    )
+    hq = hkv * 8
+    query = torch.randn(1, hq, d, generator=gen)
+    record = {
+        "key": _np(key),
+        "value": _np(value),
+        "dtype": np.array(str(dtype)),
+        "page_offsets": _np(plan.page_offsets),
+        "page_lengths": _np(plan.page_lengths),
+        "page_classes": _np(plan.page_classes.to(torch.int64)),
+        "page_size": np.array(page_size),
+        "superblock": np.array(sb),
+        "group": np.array(group),
+        "query": _np(query),
+    }
+
+    def snapshot(prefix: str) -> None:
+        ck = cache.compact_key
+        record[prefix + "k_packed"] = _np(ck.packed[:, : ck.active_length])
+        blocks = (ck.active_length + ck.superblock_size - 1) // ck.superblock_size
+        record[prefix + "k_scale"] = _np(ck.scale[:, :blocks])
+        record[prefix + "k_zero"] = _np(ck.zero_point[:, :blocks])
+        record[prefix + "k_active"] = np.array(ck.active_length)
+        record[prefix + "k_capacity"] = np.array(ck.capacity)
+        record[prefix + "k_segments"] = np.array(ck.segment_offsets)
+        cv = cache.compact_value
+        record[prefix + "v2_packed"] = _np(cv.packed[:, : cv.active_length])
+        record[prefix + "v2_scale"] = _np(cv.scale[:, : cv.active_length])
+        record[prefix + "v2_zero"] = _np(cv.zero_point[:, : cv.active_length])
+        record[prefix + "v2_active"] = np.array(cv.active_length)
+        record[prefix + "v2_capacity"] = np.array(cv.capacity)
+        i4 = cache.int4_pool
+        if i4.token_count:
+            record[prefix + "v4_packed"] = _np(i4.packed_v.packed)
+            record[prefix + "v4_scale"] = _np(i4.packed_v.scale)
+        else:
+            record[prefix + "v4_packed"] = np.zeros(0, np.uint8)
+            record[prefix + "v4_scale"] = np.zeros((hkv, 0, 1), np.float32)
+        fp = cache.fp_pool
+        record[prefix + "fp_v"] = (
+            _np(fp.fp_v) if fp.token_count else np.zeros((hkv, 0, d), np.uint16 if dtype == torch.bfloat16 else np.float16)
+        )
+        rec = cache.recent_fp_pool
+        record[prefix + "recent_k"] = _np(rec.fp_k[:, : rec.active_length])
+        record[prefix + "recent_v"] = _np(rec.fp_v[:, : rec.active_length])
+        record[prefix + "recent_active"] = np.array(rec.active_length)
+        record[prefix + "recent_global"] = _np(rec.global_index_buffer[: rec.active_length])
+        record[prefix + "recent_page_lengths"] = _np(rec.page_index.lengths)
+        record[prefix + "pool_tokens"] = np.array(
+            [fp.token_count, i4.token_count, cache.int2_pool.token_count, rec.token_count]
+        )
+        record[prefix + "int2_global"] = _np(cache.int2_pool.page_index.global_token_indices[: cache.int2_pool.token_count])
+        record[prefix + "attn"] = _np(triton_mixed_reference(query, cache).float())
+
+    snapshot("build_")
+    stats = DynamicCacheStats()
+    app_k = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
+    app_v = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
+    record["append_k"] = _np(app_k)
+    record["append_v"] = _np(app_v)
+    flushed_at = []
+    for step in range(appends):
+        flushed = append_generated_token(
+            cache,
+            app_k[step],
+            app_v[step],
+            global_token_index=seq + step,
+            logical_position=seq + step,
+            stats=stats,
+        )
+        if flushed:
+            flushed_at.append(step)
+    record["flushed_at"] = np.array(flushed_at, dtype=np.int64)
+    record["tail_dequant_tokens"] = np.array(stats.local_tail_dequant_tokens)
+    snapshot("after_")
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **record)
+    print(f"wrote {path}: flushes at {flushed_at}, tail tokens {stats.local_tail_dequant_tokens}")
+
+
+def main() -> None:
+    # Qwen profile: 32-token pages (ragged at modality boundaries), K superblock 32, INT2 group 32.
+    _case("qwen_ragged_bf16", seq=333, hkv=2, dtype=torch.bfloat16, page_size=32, sb=32,
+          group=32, tier_probs=(0.2, 0.5, 0.3), appends=140, seed=11)
+    # fp16 inputs, as in the reference's own cache test, with 64-token pages.
+    _case("qwen_pages64_fp16", seq=420, hkv=2, dtype=torch.float16, page_size=64, sb=32,
+          group=32, tier_probs=(0.15, 0.45, 0.4), appends=130, seed=12)
+    # MiniCPM all-lowbit profile: K superblock 128, INT2 group 128, all INT2 values.
+    _case("minicpm_lowbit_bf16", seq=300, hkv=2, dtype=torch.bfloat16, page_size=32, sb=128,
+          group=128, tier_probs=(0.0, 0.0, 1.0), appends=129, seed=13)
+
+
+if __name__ == "__main__":
+    main()

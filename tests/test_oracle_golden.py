@@ -1,0 +1,77 @@
+"""Pin the CPU oracle against fixtures written by the reference's own CPU path."""
+import numpy as np
+import pytest
+
+from golden_io import as_f32, fixture_names, load
+from oracle.attention import mixed_reference
+from oracle.cache import append_token, build_cache
+
+NAMES = fixture_names()
+
+
+def _dtype(g):
+    return "bfloat16" if "bfloat16" in str(g["dtype"]) else "float16"
+
+
+def _build(g):
+    dt = _dtype(g)
+    return build_cache(
+        as_f32(g["key"], dt), as_f32(g["value"], dt),
+        g["page_offsets"], g["page_lengths"], g["page_classes"],
+        dtype=dt, page_size=int(g["page_size"]), superblock=int(g["superblock"]),
+        group=int(g["group"]), recent_capacity=128, append_capacity=260,
+    )
+
+
+def _check_snapshot(c, g, prefix, dt):
+    k = c.k_active
+    blocks = -(-k // c.superblock)
+    assert k == int(g[prefix + "k_active"]) and c.k_capacity == int(g[prefix + "k_capacity"])
+    assert tuple(c.k_segments) == tuple(int(v) for v in g[prefix + "k_segments"])
+    np.testing.assert_array_equal(c.k_packed[:, :k], g[prefix + "k_packed"])
+    np.testing.assert_array_equal(c.k_scale[:, :blocks].view(np.uint16), g[prefix + "k_scale"].view(np.uint16))
+    np.testing.assert_array_equal(c.k_zero[:, :blocks], g[prefix + "k_zero"])
+    a = c.v2_active
+    assert a == int(g[prefix + "v2_active"]) and c.v2_capacity == int(g[prefix + "v2_capacity"])
+    np.testing.assert_array_equal(c.v2_packed[:, :a], g[prefix + "v2_packed"])
+    np.testing.assert_array_equal(c.v2_scale[:, :a].view(np.uint16), g[prefix + "v2_scale"].view(np.uint16))
+    np.testing.assert_array_equal(c.v2_zero[:, :a], g[prefix + "v2_zero"])
+    np.testing.assert_array_equal(c.v4_packed.reshape(-1), g[prefix + "v4_packed"].reshape(-1))
+    np.testing.assert_array_equal(c.v4_scale.view(np.uint32), g[prefix + "v4_scale"].view(np.uint32))
+    np.testing.assert_array_equal(c.fp_v, as_f32(g[prefix + "fp_v"], dt))
+    r = c.recent_active
+    assert r == int(g[prefix + "recent_active"])
+    np.testing.assert_array_equal(c.recent_k[:, :r], as_f32(g[prefix + "recent_k"], dt))
+    np.testing.assert_array_equal(c.recent_v[:, :r], as_f32(g[prefix + "recent_v"], dt))
+    np.testing.assert_array_equal(c.recent_global[:r], g[prefix + "recent_global"])
+    np.testing.assert_array_equal(c.recent_page_lengths, g[prefix + "recent_page_lengths"])
+    assert list(c.pool_tokens) + [r] == [int(v) for v in g[prefix + "pool_tokens"]]
+    np.testing.assert_array_equal(np.array(c.int2_global), g[prefix + "int2_global"])
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_build_matches_reference(name):
+    g = load(name)
+    c = _build(g)
+    _check_snapshot(c, g, "build_", _dtype(g))
+    out = mixed_reference(g["query"], c)
+    np.testing.assert_allclose(out, g["build_attn"], rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_append_and_flush_match_reference(name):
+    g = load(name)
+    dt = _dtype(g)
+    c = _build(g)
+    ak = as_f32(g["append_k"], dt)
+    av = as_f32(g["append_v"], dt)
+    seq = g["key"].shape[1]
+    flushed = []
+    for step in range(ak.shape[0]):
+        if append_token(c, ak[step, :, 0], av[step, :, 0], global_index=seq + step, logical_position=seq + step):
+            flushed.append(step)
+    assert flushed == list(g["flushed_at"])
+    assert c.tail_dequant_tokens == int(g["tail_dequant_tokens"])
+    _check_snapshot(c, g, "after_", dt)
+    out = mixed_reference(g["query"], c)
+    np.testing.assert_allclose(out, g["after_attn"], rtol=0, atol=2e-6)
