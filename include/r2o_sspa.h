@@ -1,0 +1,171 @@
+/*
+ * r2o_sspa.h — C ABI of the MI355X (gfx950) SSPA packed-KV decode library (libr2o_sspa.so).
+ *
+ * The reference (Fabulous1496/R2-Omni) is pure Python: its hot path is Triton kernels launched
+ * from r2omni/sspa/kernels/triton_fourq_splitk.py and the runtime packers in
+ * r2omni/sspa/runtime/ (*.py).  There is no FFI in the reference; each entry point below replaces
+ * one Triton launch (or one torch-op sequence) of that Python API and is bound with ctypes by
+ * r2omni_amd/_lib.py.  Every entry point:
+ *   - takes plain device pointers, int64 sizes and an opaque hipStream_t (as void*);
+ *   - launches asynchronously on that stream and allocates nothing;
+ *   - returns 0 on success, R2O_EINVAL for an argument the kernel's grid cannot honour
+ *     (checked on the host before any launch), R2O_ELAUNCH if the launch itself failed.
+ * Tensor layouts are the reference's "wire format"  so caches built by the
+ * reference and by this library are byte-identical.
+ *
+ * dtype codes: 0 = bfloat16, 1 = float16 (element type of K/V/Q rows).
+ */
+#ifndef R2O_SSPA_H
+#define R2O_SSPA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define R2O_OK 0
+#define R2O_EINVAL 1
+#define R2O_ELAUNCH 2
+
+#define R2O_HEAD_DIM 128
+#define R2O_MAX_GQA 16
+#define R2O_MAX_BATCH 32
+
+/* ---------------------------------------------------------------- decode (hot path) ---- */
+
+/* One request's static cache geometry; an array of these lives in device memory and is
+ * rebuilt only when the cache layout changes (prefill, flush), like the reference's
+ * prepare_splitk_executor (triton_fourq_splitk.py:1695-1907).  All fields are 8 bytes. */
+typedef struct r2o_request_desc {
+    const uint8_t* k_packed;      /* compact INT4-K arena  u8  [Hkv, k_capacity, 64]            */
+    const uint16_t* k_scale;      /* fp16 [Hkv, k_superblocks, 128]                              */
+    const uint8_t* k_zero;        /* u8   [Hkv, k_superblocks, 128]                              */
+    int64_t k_capacity;
+    int64_t k_superblocks;
+    const uint16_t* fp_v;         /* bf16 [Hkv, fp_stride, 128]  (FP-V pool)                     */
+    int64_t fp_stride;
+    const uint8_t* i4_v;          /* u8   [Hkv, i4_stride, 64]   (per-token symmetric INT4-V)   */
+    const float* i4_scale;        /* f32  [Hkv, i4_stride]                                       */
+    int64_t i4_stride;
+    const uint8_t* i2_v;          /* u8   [Hkv, i2_stride, 32]   (per-token-group INT2-V)       */
+    const uint16_t* i2_scale;     /* fp16 [Hkv, i2_stride, 128/G]                                */
+    const uint8_t* i2_zero;       /* u8   [Hkv, i2_stride, 128/G]                                */
+    int64_t i2_stride;
+    uint16_t* recent_k;           /* bf16 [Hkv, recent_capacity, 128]  Recent-FP ring            */
+    uint16_t* recent_v;
+    int64_t recent_capacity;
+    int32_t* recent_length;       /* device int32 active length (written by the fused append)   */
+    int64_t* recent_global;       /* int64 [recent_capacity]                                     */
+    int64_t* recent_logical;      /* int64 [recent_capacity]                                     */
+    int64_t* recent_page_lengths; /* int64 [recent_capacity / page_size]                         */
+} r2o_request_desc;
+
+/* One unit of split-K work: a run of 32-token tiles of one pool segment of one (request,
+ * kv head).  Tiles are aligned to 32 positions of the compact K arena so that every tile lies
+ * in one K superblock; positions outside [lo, hi) are masked.  For the Recent-FP ring, arena
+ * positions are ring slots.  V row = arena position - v_delta.  All fields are 8 bytes. */
+typedef struct r2o_work_item {
+    int64_t req;
+    int64_t kvh;
+    int64_t kind;      /* 0 = FP-V (bf16), 1 = INT4-V, 2 = INT2-V, 3 = Recent-FP (bf16 K and V) */
+    int64_t tile0;     /* arena position of the first tile (multiple of 32)                      */
+    int64_t ntiles;
+    int64_t lo;        /* valid arena positions [lo, hi)                                          */
+    int64_t hi;
+    int64_t v_delta;
+} r2o_work_item;
+
+typedef struct r2o_decode_params {
+    const r2o_request_desc* reqs;   /* device [batch]                                  */
+    const r2o_work_item* items;     /* device [n_items], grouped by (req, kvh)         */
+    const int32_t* group_begin;     /* device [batch*hkv + 1] item range of each group */
+    int64_t n_items;
+    float* partial_max;             /* device f32 [n_items, 16]      (log2 domain)     */
+    float* partial_sum;             /* device f32 [n_items, 16]                        */
+    float* partial_out;             /* device f32 [n_items, 16, 128]                   */
+    const uint16_t* query;          /* device [batch, hq, 128] (dtype q_dtype)         */
+    uint16_t* out;                  /* device bf16 [batch, hq, 128]                    */
+    const uint16_t* append_k;       /* device bf16 [batch, hkv, 128] or NULL           */
+    const uint16_t* append_v;
+    int64_t batch;
+    int64_t hq;
+    int64_t hkv;
+    int64_t superblock;             /* K superblock: 32, 64 or 128                     */
+    int64_t int2_group;             /* INT2-V group: 32, 64 or 128                     */
+    int64_t page_size;              /* Recent-FP page size (16, 32, 64)                */
+    int64_t q_dtype;                /* 0 = bf16, 1 = fp16                              */
+    int64_t output_hadamard;        /* 1: out = bf16(FWHT128(bf16(out)))               */
+    int64_t do_append;              /* 1: fused Recent-FP append of append_k/append_v  */
+    float sm_scale;                 /* softmax scale (head_dim^-1/2 by default)        */
+    int32_t recent_len[R2O_MAX_BATCH];     /* host-tracked Recent-FP active length     */
+    int64_t append_global[R2O_MAX_BATCH];  /* global token index of the appended token */
+    int64_t append_logical[R2O_MAX_BATCH]; /* logical position of the appended token   */
+} r2o_decode_params;
+
+/* Split-K partial pass.  Replaces _fourq_page_partial_kernel / _full_head_page_partial_kernel
+ * (triton_fourq_splitk.py:456-931, :144-375, launched at :1393-1462). */
+int r2o_decode_partial(const r2o_decode_params* params, void* stream);
+
+/* Split-K combine + output (bf16, optional FWHT) + fused Recent-FP append.  Replaces
+ * _fourq_hierarchical_group_reduce_kernel and _fourq_partial_reduce_kernel
+ * (triton_fourq_splitk.py:1023-1155, :936-1020, launched at :1467-1541). */
+int r2o_decode_combine(const r2o_decode_params* params, void* stream);
+
+/* ----------------------------------------------------------------- pack / append --------- */
+
+/* Per-channel affine INT4-K over `superblock`-token blocks into the compact arena.
+ * Arena positions [dst_start, dst_start + tail + n) are (re)written; dst_start must be a
+ * multiple of `superblock`.  The first `tail` positions are read back from the arena itself
+ * (dequantised, rounded to `dtype`) — the flush rule of CompactInt4KeyArena.append_superblock
+ * (compact_int4_key.py:210-220); the next n come from src[h, index[i]] (index NULL: i).
+ * Replaces _gather_pack_int4_key_kernel (compact_int4_key.py:22-76) and the torch flush path. */
+int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
+                    const int64_t* index, int64_t n, int64_t tail, int64_t dst_start,
+                    uint8_t* packed, uint16_t* scale, uint8_t* zero, int64_t capacity,
+                    int64_t superblocks, int64_t superblock, void* stream);
+
+/* Per-token symmetric INT4-V: packed[h, dst+i] / scale[h, dst+i] from src[h, index[i]].
+ * Replaces _gather_pack_int4_value_kernel (fused_value_pack.py:28-70). */
+int r2o_pack_int4_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
+                    const int64_t* index, int64_t n, int64_t dst_start,
+                    uint8_t* packed, float* scale, int64_t capacity, void* stream);
+
+/* Per-token-group affine INT2-V (group 32/64/128).  Replaces _gather_pack_int2_value_kernel
+ * (fused_value_pack.py:75-149), both the gathered prefill and the contiguous flush forms. */
+int r2o_pack_int2_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
+                    const int64_t* index, int64_t n, int64_t dst_start, int64_t group,
+                    uint8_t* packed, uint16_t* scale, uint8_t* zero, int64_t capacity,
+                    void* stream);
+
+/* Row gather dst[h, i, :] = src[h, index[i], :] of 16-bit elements (FP-V pool build,
+ * replaces value.index_select(1, tokens) at precision_pool.py:697-698). */
+int r2o_gather_rows(const uint16_t* src, int64_t hkv, int64_t src_tokens, const int64_t* index,
+                    int64_t n, uint16_t* dst, int64_t dst_stride, void* stream);
+
+/* Non-fused Recent-FP append of one token at `position` + metadata.  Replaces
+ * _append_recent_fp_kernel (triton_fourq_splitk.py:413-447, host :1557-1604). */
+int r2o_recent_append(uint16_t* recent_k, uint16_t* recent_v, int64_t hkv, int64_t capacity,
+                      const uint16_t* new_k, const uint16_t* new_v, int64_t position,
+                      int64_t global_index, int64_t logical_position, int32_t* length,
+                      int64_t* global_buf, int64_t* logical_buf, int64_t* page_lengths,
+                      int64_t page_size, void* stream);
+
+/* Flush bookkeeping of the ring: move slots [flush, active) to [0, active - flush) for K, V
+ * and both index buffers, then refresh page lengths for the new active length.  Replaces the
+ * clone/copy sequence of dynamic_fourq_cache.py:246-253 and _refresh_recent_pages :108-117. */
+int r2o_recent_shift(uint16_t* recent_k, uint16_t* recent_v, int64_t hkv, int64_t capacity,
+                     int64_t flush, int64_t active, int64_t* global_buf, int64_t* logical_buf,
+                     int32_t* length, int64_t* page_lengths, int64_t page_size, void* stream);
+
+/* Orthonormal 128-point FWHT of `rows` rows (in place allowed), dtype in/out.  Replaces
+ * triton_fwht_128 (triton_qwen_mrope.py:325-346). */
+int r2o_fwht128(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t dtype, void* stream);
+
+/* Library identification: returns the gfx target the code objects were built for. */
+const char* r2o_build_target(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* R2O_SSPA_H */

@@ -1,0 +1,307 @@
+// Quantise/pack, gather, Recent-FP append/shift and FWHT kernels for gfx950.
+//
+// Bit-exactness with the reference's torch CPU quantisers (compact_int4_key.py:83-110,
+// quantization.py:19-50, int2_reference.py:96-151): IEEE fp32 division (__fdiv_rn), round half
+// to even (__builtin_rintf -> v_rndne_f32), no contraction (the file is built with
+// -ffp-contract=off), fp32 step quantisation with fp16-RNE storage of the step.
+#include "r2o_common.hpp"
+
+namespace {
+
+constexpr float kEps = 1.0e-6f;
+
+// ----------------------------------------------------------------------------- INT4 keys
+// grid (superblocks to write, hkv), block 64: thread t owns channels 2t, 2t+1 (byte t).
+__global__ __launch_bounds__(64) void pack_int4_k_kernel(
+    const uint16_t* __restrict__ src, int dtype, int64_t src_tokens, const int64_t* __restrict__ index,
+    int64_t n, int64_t tail, int64_t dst_start, uint8_t* packed, uint16_t* scale, uint8_t* zero,
+    int64_t capacity, int64_t superblocks, int sb) {
+    const int t = threadIdx.x;
+    const int64_t h = blockIdx.y;
+    const int64_t total = tail + n;
+    const int64_t first = (int64_t)blockIdx.x * sb;  // relative to dst_start
+    const int64_t count = min((int64_t)sb, total - first);
+    if (count <= 0) return;
+    const int64_t block_row = dst_start / sb + blockIdx.x;
+    uint8_t* prow = packed + (h * capacity + dst_start + first) * 64 + t;
+    uint16_t* srow = scale + (h * superblocks + block_row) * 128 + 2 * t;
+    uint8_t* zrow = zero + (h * superblocks + block_row) * 128 + 2 * t;
+    // old metadata of the tail superblock (only block 0 can hold tail positions)
+    const float os0 = r2o_f16_to_f32(srow[0]), os1 = r2o_f16_to_f32(srow[1]);
+    const float oz0 = (float)zrow[0], oz1 = (float)zrow[1];
+    auto value = [&](int64_t j, float& x0, float& x1) {
+        const int64_t pos = first + j;
+        if (pos < tail) {  // dequantise-then-round the partial tail (compact_int4_key.py:215-216)
+            const uint32_t b = prow[j * 64];
+            x0 = r2o_round_dtype(((float)(b & 15u) - oz0) * os0, dtype);
+            x1 = r2o_round_dtype(((float)(b >> 4) - oz1) * os1, dtype);
+        } else {
+            const int64_t i = pos - tail;
+            const int64_t row = index ? index[i] : i;
+            const uint32_t pair = *reinterpret_cast<const uint32_t*>(src + (h * src_tokens + row) * 128 + 2 * t);
+            x0 = dtype == 0 ? r2o_bf16_to_f32(pair & 0xffffu) : r2o_f16_to_f32(pair & 0xffffu);
+            x1 = dtype == 0 ? r2o_bf16_to_f32(pair >> 16) : r2o_f16_to_f32(pair >> 16);
+        }
+    };
+    float mn0 = 0.f, mn1 = 0.f, mx0 = 0.f, mx1 = 0.f;  // min(min x, 0), max(max x, 0)
+    for (int64_t j = 0; j < count; ++j) {
+        float x0, x1;
+        value(j, x0, x1);
+        mn0 = fminf(mn0, x0); mx0 = fmaxf(mx0, x0);
+        mn1 = fminf(mn1, x1); mx1 = fmaxf(mx1, x1);
+    }
+    const float st0 = fmaxf(__fdiv_rn(mx0 - mn0, 15.0f), kEps);
+    const float st1 = fmaxf(__fdiv_rn(mx1 - mn1, 15.0f), kEps);
+    const float zp0 = fminf(fmaxf(__builtin_rintf(__fdiv_rn(-mn0, st0)), 0.f), 15.f);
+    const float zp1 = fminf(fmaxf(__builtin_rintf(__fdiv_rn(-mn1, st1)), 0.f), 15.f);
+    for (int64_t j = 0; j < count; ++j) {
+        float x0, x1;
+        value(j, x0, x1);  // reads the old tail code before this thread overwrites it
+        const float c0 = fminf(fmaxf(__builtin_rintf(__fdiv_rn(x0, st0) + zp0), 0.f), 15.f);
+        const float c1 = fminf(fmaxf(__builtin_rintf(__fdiv_rn(x1, st1) + zp1), 0.f), 15.f);
+        prow[j * 64] = (uint8_t)((uint32_t)c0 | ((uint32_t)c1 << 4));
+    }
+    srow[0] = (uint16_t)r2o_f32_to_f16(st0);
+    srow[1] = (uint16_t)r2o_f32_to_f16(st1);
+    zrow[0] = (uint8_t)zp0;
+    zrow[1] = (uint8_t)zp1;
+}
+
+// ---------------------------------------------------------------------------- INT4 values
+// grid (n, hkv), block 64: thread t owns channels 2t, 2t+1.
+__global__ __launch_bounds__(64) void pack_int4_v_kernel(
+    const uint16_t* __restrict__ src, int dtype, int64_t src_tokens, const int64_t* __restrict__ index,
+    int64_t dst_start, uint8_t* packed, float* scale, int64_t capacity) {
+    const int t = threadIdx.x;
+    const int64_t i = blockIdx.x, h = blockIdx.y;
+    const int64_t row = index ? index[i] : i;
+    const uint32_t pair = *reinterpret_cast<const uint32_t*>(src + (h * src_tokens + row) * 128 + 2 * t);
+    const float x0 = dtype == 0 ? r2o_bf16_to_f32(pair & 0xffffu) : r2o_f16_to_f32(pair & 0xffffu);
+    const float x1 = dtype == 0 ? r2o_bf16_to_f32(pair >> 16) : r2o_f16_to_f32(pair >> 16);
+    const float amax = r2o_wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+    const float s = fmaxf(__fdiv_rn(amax, 7.0f), kEps);
+    const int q0 = (int)fminf(fmaxf(__builtin_rintf(__fdiv_rn(x0, s)), -7.f), 7.f);
+    const int q1 = (int)fminf(fmaxf(__builtin_rintf(__fdiv_rn(x1, s)), -7.f), 7.f);
+    const int64_t dst = h * capacity + dst_start + i;
+    packed[dst * 64 + t] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+    if (t == 0) scale[dst] = s;
+}
+
+// ---------------------------------------------------------------------------- INT2 values
+// grid (n, hkv), block 64: thread t owns channels 2t, 2t+1; a group of G channels is G/2
+// consecutive threads.
+__global__ __launch_bounds__(64) void pack_int2_v_kernel(
+    const uint16_t* __restrict__ src, int dtype, int64_t src_tokens, const int64_t* __restrict__ index,
+    int64_t dst_start, int group, uint8_t* packed, uint16_t* scale, uint8_t* zero, int64_t capacity) {
+    const int t = threadIdx.x;
+    const int64_t i = blockIdx.x, h = blockIdx.y;
+    const int64_t row = index ? index[i] : i;
+    const uint32_t pair = *reinterpret_cast<const uint32_t*>(src + (h * src_tokens + row) * 128 + 2 * t);
+    const float x0 = dtype == 0 ? r2o_bf16_to_f32(pair & 0xffffu) : r2o_f16_to_f32(pair & 0xffffu);
+    const float x1 = dtype == 0 ? r2o_bf16_to_f32(pair >> 16) : r2o_f16_to_f32(pair >> 16);
+    float mn = fminf(x0, x1), mx = fmaxf(x0, x1);
+    for (int o = 1; o < group / 2; o <<= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o, R2O_WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, o, R2O_WAVE));
+    }
+    mn = fminf(mn, 0.f);
+    mx = fmaxf(mx, 0.f);
+    const float s = fmaxf(__fdiv_rn(mx - mn, 3.0f), kEps);
+    const float z = fminf(fmaxf(__builtin_rintf(__fdiv_rn(-mn, s)), 0.f), 3.f);
+    const uint32_t c0 = (uint32_t)fminf(fmaxf(__builtin_rintf(__fdiv_rn(x0, s) + z), 0.f), 3.f);
+    const uint32_t c1 = (uint32_t)fminf(fmaxf(__builtin_rintf(__fdiv_rn(x1, s) + z), 0.f), 3.f);
+    const uint32_t mine = c0 | (c1 << 2);
+    const uint32_t next = (uint32_t)__shfl_down((int)mine, 1, R2O_WAVE);
+    const int64_t dst = h * capacity + dst_start + i;
+    if ((t & 1) == 0) packed[dst * 32 + t / 2] = (uint8_t)(mine | (next << 4));
+    const int groups = 128 / group;
+    if (t % (group / 2) == 0) {
+        const int gi = t / (group / 2);
+        scale[dst * groups + gi] = (uint16_t)r2o_f32_to_f16(s);
+        zero[dst * groups + gi] = (uint8_t)z;
+    }
+}
+
+// ---------------------------------------------------------------------------- gather rows
+__global__ __launch_bounds__(64) void gather_rows_kernel(const uint16_t* __restrict__ src, int64_t src_tokens,
+                                                         const int64_t* __restrict__ index, uint16_t* dst,
+                                                         int64_t dst_stride) {
+    const int64_t i = blockIdx.x, h = blockIdx.y;
+    const int64_t row = index ? index[i] : i;
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(src + (h * src_tokens + row) * 128);
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst + (h * dst_stride + i) * 128);
+    d[threadIdx.x] = s[threadIdx.x];
+}
+
+// ------------------------------------------------------------------------ Recent-FP ring
+__global__ __launch_bounds__(256) void recent_append_kernel(
+    uint16_t* rk, uint16_t* rv, int64_t hkv, int64_t capacity, const uint16_t* __restrict__ nk,
+    const uint16_t* __restrict__ nv, int64_t pos, int64_t gidx, int64_t lpos, int32_t* length,
+    int64_t* gbuf, int64_t* lbuf, int64_t* page_lengths, int64_t page_size) {
+    for (int64_t e = threadIdx.x; e < hkv * 128; e += blockDim.x) {
+        const int64_t h = e / 128, d = e % 128;
+        rk[(h * capacity + pos) * 128 + d] = nk[e];
+        rv[(h * capacity + pos) * 128 + d] = nv[e];
+    }
+    if (threadIdx.x == 0) {
+        gbuf[pos] = gidx;
+        lbuf[pos] = lpos;
+        *length = (int32_t)(pos + 1);
+        page_lengths[pos / page_size] = pos % page_size + 1;
+    }
+}
+
+// Single block: moves slots [flush, active) down by `flush` in rounds of at most `flush` rows
+// so that no round reads a slot another round writes.
+__global__ __launch_bounds__(256) void recent_shift_kernel(
+    uint16_t* rk, uint16_t* rv, int64_t hkv, int64_t capacity, int64_t flush, int64_t active,
+    int64_t* gbuf, int64_t* lbuf, int32_t* length, int64_t* page_lengths, int64_t page_size) {
+    const int64_t remaining = active - flush;
+    for (int64_t base = 0; base < remaining; base += flush) {
+        const int64_t rows = min(flush, remaining - base);
+        for (int64_t e = threadIdx.x; e < hkv * rows * 128; e += blockDim.x) {
+            const int64_t h = e / (rows * 128), r = (e / 128) % rows, d = e % 128;
+            const int64_t dst = (h * capacity + base + r) * 128 + d;
+            const int64_t srcp = (h * capacity + base + r + flush) * 128 + d;
+            rk[dst] = rk[srcp];
+            rv[dst] = rv[srcp];
+        }
+        for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
+            gbuf[base + r] = gbuf[base + r + flush];
+            lbuf[base + r] = lbuf[base + r + flush];
+        }
+        __syncthreads();
+    }
+    const int64_t new_active = remaining > 0 ? remaining : 0;
+    for (int64_t p = threadIdx.x; p < capacity / page_size; p += blockDim.x) {
+        const int64_t v = new_active - p * page_size;
+        page_lengths[p] = v < 0 ? 0 : (v > page_size ? page_size : v);
+    }
+    if (threadIdx.x == 0) *length = (int32_t)new_active;
+}
+
+// ---------------------------------------------------------------------------------- FWHT
+// One 128-thread block per row; butterflies in the reference's stage order (stride 1 .. 64),
+// then the fp32 normalisation 0.08838834764831845.
+__global__ __launch_bounds__(128) void fwht128_kernel(const uint16_t* __restrict__ src, uint16_t* dst, int dtype) {
+    __shared__ float buf[128];
+    const int64_t row = blockIdx.x;
+    const int d = threadIdx.x;
+    buf[d] = r2o_load_elem(src, row * 128 + d, dtype);
+    __syncthreads();
+    for (int stride = 1; stride < 128; stride <<= 1) {
+        const int pos = d & (stride - 1);
+        const int base = (d / stride) * stride * 2;  // only the first 64 threads are used
+        float a = 0.f, b = 0.f;
+        if (d < 64) {
+            const int blk = d / stride;
+            const int i0 = blk * 2 * stride + pos;
+            a = buf[i0];
+            b = buf[i0 + stride];
+        }
+        __syncthreads();
+        if (d < 64) {
+            const int blk = d / stride;
+            const int i0 = blk * 2 * stride + pos;
+            buf[i0] = a + b;
+            buf[i0 + stride] = a - b;
+        }
+        (void)base;
+        __syncthreads();
+    }
+    const float y = buf[d] * 0.08838834764831845f;
+    dst[row * 128 + d] = (uint16_t)(dtype == 0 ? r2o_f32_to_bf16(y) : r2o_f32_to_f16(y));
+}
+
+}  // namespace
+
+extern "C" {
+
+int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens, const int64_t* index,
+                    int64_t n, int64_t tail, int64_t dst_start, uint8_t* packed, uint16_t* scale, uint8_t* zero,
+                    int64_t capacity, int64_t superblocks, int64_t superblock, void* stream) {
+    if (!(superblock == 32 || superblock == 64 || superblock == 128) || (dtype != 0 && dtype != 1)) return R2O_EINVAL;
+    if (hkv <= 0 || n < 0 || tail < 0 || tail >= superblock || dst_start < 0 || dst_start % superblock) return R2O_EINVAL;
+    if (dst_start + tail + n > capacity || capacity % superblock || superblocks * superblock != capacity) return R2O_EINVAL;
+    if (n > 0 && (!src || src_tokens <= 0)) return R2O_EINVAL;
+    const int64_t total = tail + n;
+    if (total == 0) return R2O_OK;
+    const int64_t blocks = (total + superblock - 1) / superblock;
+    hipLaunchKernelGGL(pack_int4_k_kernel, dim3((unsigned)blocks, (unsigned)hkv), dim3(64), 0, (hipStream_t)stream,
+                       src, (int)dtype, src_tokens, index, n, tail, dst_start, packed, scale, zero, capacity,
+                       superblocks, (int)superblock);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int r2o_pack_int4_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens, const int64_t* index,
+                    int64_t n, int64_t dst_start, uint8_t* packed, float* scale, int64_t capacity, void* stream) {
+    if ((dtype != 0 && dtype != 1) || hkv <= 0 || n < 0 || dst_start < 0 || dst_start + n > capacity) return R2O_EINVAL;
+    if (n == 0) return R2O_OK;
+    if (!src || src_tokens <= 0 || n > 0x7fffffff) return R2O_EINVAL;
+    hipLaunchKernelGGL(pack_int4_v_kernel, dim3((unsigned)n, (unsigned)hkv), dim3(64), 0, (hipStream_t)stream, src,
+                       (int)dtype, src_tokens, index, dst_start, packed, scale, capacity);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int r2o_pack_int2_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens, const int64_t* index,
+                    int64_t n, int64_t dst_start, int64_t group, uint8_t* packed, uint16_t* scale, uint8_t* zero,
+                    int64_t capacity, void* stream) {
+    if ((dtype != 0 && dtype != 1) || !(group == 32 || group == 64 || group == 128)) return R2O_EINVAL;
+    if (hkv <= 0 || n < 0 || dst_start < 0 || dst_start + n > capacity) return R2O_EINVAL;
+    if (n == 0) return R2O_OK;
+    if (!src || src_tokens <= 0 || n > 0x7fffffff) return R2O_EINVAL;
+    hipLaunchKernelGGL(pack_int2_v_kernel, dim3((unsigned)n, (unsigned)hkv), dim3(64), 0, (hipStream_t)stream, src,
+                       (int)dtype, src_tokens, index, dst_start, (int)group, packed, scale, zero, capacity);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int r2o_gather_rows(const uint16_t* src, int64_t hkv, int64_t src_tokens, const int64_t* index, int64_t n,
+                    uint16_t* dst, int64_t dst_stride, void* stream) {
+    if (hkv <= 0 || n < 0 || n > dst_stride || n > 0x7fffffff) return R2O_EINVAL;
+    if (n == 0) return R2O_OK;
+    if (!src || !dst) return R2O_EINVAL;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)n, (unsigned)hkv), dim3(64), 0, (hipStream_t)stream, src,
+                       src_tokens, index, dst, dst_stride);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int r2o_recent_append(uint16_t* recent_k, uint16_t* recent_v, int64_t hkv, int64_t capacity, const uint16_t* new_k,
+                      const uint16_t* new_v, int64_t position, int64_t global_index, int64_t logical_position,
+                      int32_t* length, int64_t* global_buf, int64_t* logical_buf, int64_t* page_lengths,
+                      int64_t page_size, void* stream) {
+    if (hkv <= 0 || position < 0 || position >= capacity || page_size <= 0 || capacity % page_size) return R2O_EINVAL;
+    if (!recent_k || !recent_v || !new_k || !new_v || !length || !global_buf || !logical_buf || !page_lengths)
+        return R2O_EINVAL;
+    hipLaunchKernelGGL(recent_append_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, recent_k, recent_v, hkv,
+                       capacity, new_k, new_v, position, global_index, logical_position, length, global_buf,
+                       logical_buf, page_lengths, page_size);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int r2o_recent_shift(uint16_t* recent_k, uint16_t* recent_v, int64_t hkv, int64_t capacity, int64_t flush,
+                     int64_t active, int64_t* global_buf, int64_t* logical_buf, int32_t* length,
+                     int64_t* page_lengths, int64_t page_size, void* stream) {
+    if (hkv <= 0 || flush <= 0 || active < flush || active > capacity || page_size <= 0 || capacity % page_size)
+        return R2O_EINVAL;
+    hipLaunchKernelGGL(recent_shift_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, recent_k, recent_v, hkv,
+                       capacity, flush, active, global_buf, logical_buf, length, page_lengths, page_size);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int r2o_fwht128(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t dtype, void* stream) {
+    if (rows < 0 || rows > 0x7fffffff || (dtype != 0 && dtype != 1)) return R2O_EINVAL;
+    if (rows == 0) return R2O_OK;
+    hipLaunchKernelGGL(fwht128_kernel, dim3((unsigned)rows), dim3(128), 0, (hipStream_t)stream, src, dst, (int)dtype);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+const char* r2o_build_target(void) { return "gfx950"; }
+
+}  // extern "C"

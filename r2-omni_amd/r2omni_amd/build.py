@@ -1,0 +1,78 @@
+"""Compile the gfx950 HIP sources into the in-tree C-ABI library ``libr2o_sspa.so``.
+
+Usage: ``python -m r2omni_amd.build`` (from ``r2-omni_amd/``) or ``build_library()``.
+Every HIP translation unit is compiled for gfx950 only, with packed-FP32 instruction
+selection disabled and FP contraction off (the quantisers must round exactly like the
+reference's torch CPU path).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT_DIR = os.path.dirname(PKG_DIR)                 # r2-omni_amd/
+REPO_DIR = os.path.dirname(ROOT_DIR)
+CSRC = os.path.join(ROOT_DIR, "csrc")
+INCLUDE = os.path.join(REPO_DIR, "include")
+LIB_NAME = "libr2o_sspa.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+SOURCES = ("r2o_decode.hip", "r2o_pack.hip")
+ARCH = "gfx950"
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libr2o_sspa.so")
+
+
+def common_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-fPIC",
+        "-std=c++17",
+        "-ffp-contract=off",
+        "-munsafe-fp-atomics",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", INCLUDE,
+        "-I", CSRC,
+    ]
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile every source and link ``libr2o_sspa.so`` next to this file; returns its path."""
+    hipcc = _hipcc()
+    build_dir = os.path.join(ROOT_DIR, "_build")
+    os.makedirs(build_dir, exist_ok=True)
+    objects = []
+    for src in SOURCES:
+        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+        cmd = [hipcc, *common_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+        _run(cmd, verbose)
+        objects.append(obj)
+    tmp = LIB_PATH + ".tmp"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", tmp], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"HIP build failed: {' '.join(cmd[:3])} ... ({res.returncode})")
+    noise = "is not a recognized feature for this target"
+    rest = [ln for ln in (res.stderr or "").splitlines() if noise not in ln and ln.strip()]
+    if verbose and rest:
+        sys.stderr.write("\n".join(rest) + "\n")
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

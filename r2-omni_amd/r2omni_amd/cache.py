@@ -1,0 +1,719 @@
+"""Three-pool SSPA packed-KV cache on the GPU: arenas, builder, append and flush.
+
+Drop-in for the reference runtime (same names, fields, layouts and error messages):
+  CompactInt4KeyArena        r2omni/sspa/runtime/compact_int4_key.py:113-220
+  build (INT4-K gather-pack) compact_int4_key.py:223-281
+  PackedTensor (INT4-V pool) packed_kv_layout.py:11-32, fused_value_pack.py:152-193
+  CompactInt2ValueArena      fused_value_pack.py:401-516, build :519-575
+  PrecisionPool, ThreePrecisionCache, build_three_precision_cache  precision_pool.py:152-274, 787-984
+  append_generated_token, DynamicCacheStats  dynamic_fourq_cache.py:16-24, 172-267
+All payload bytes are produced by the gfx950 kernels of libr2o_sspa.so (r2o_pack_int4_k,
+r2o_pack_int4_v, r2o_pack_int2_v, r2o_gather_rows, r2o_recent_append, r2o_recent_shift);
+torch only allocates the tensors and keeps small index vectors.  Supported variant: the
+released ``v_fourq_k_int4_compact`` cache with INT2 generated values.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Literal
+
+import torch
+
+from . import _lib
+from .policy import LayerCompressionPlan, PageClass
+
+CacheVariant = Literal["v_fourq_k_int2_compact", "v_fourq_k_int4_compact", "v_fourq_k_bf16"]
+
+
+def _round_up(value: int, multiple: int) -> int:
+    return -(-int(value) // int(multiple)) * int(multiple)
+
+
+def _nbytes(t: torch.Tensor | None) -> int:
+    return 0 if t is None else int(t.numel() * t.element_size())
+
+
+# ----------------------------------------------------------------------------- page index
+@dataclass(frozen=True)
+class PhysicalPageIndex:
+    original_page_ids: torch.Tensor
+    physical_offsets: torch.Tensor
+    lengths: torch.Tensor
+    global_token_indices: torch.Tensor
+    logical_positions: torch.Tensor
+
+
+# ------------------------------------------------------------------------ compact INT4 K
+@dataclass
+class CompactInt4KeyArena:
+    """Per-channel affine INT4 K for all FP/INT4/INT2 tokens in physical order."""
+
+    packed: torch.Tensor          # u8  [H, capacity, D/2]
+    scale: torch.Tensor           # f16 [H, capacity/SB, D]
+    zero_point: torch.Tensor      # u8  [H, capacity/SB, D]
+    active_length: int
+    capacity: int
+    segment_offsets: tuple[int, int, int]
+    original_dtype: torch.dtype
+    superblock_size: int = 128
+    bit_width: int = 4
+
+    def __post_init__(self) -> None:
+        if self.packed.ndim != 3 or self.packed.dtype != torch.uint8:
+            raise ValueError("compact INT4 K storage must be uint8 [H,capacity,D/2]")
+        h, capacity, d2 = map(int, self.packed.shape)
+        if self.superblock_size not in (32, 64, 128):
+            raise ValueError("compact INT4 K superblock must be 32, 64, or 128 tokens")
+        blocks = -(-capacity // self.superblock_size)
+        if capacity != self.capacity or not 0 <= self.active_length <= capacity:
+            raise ValueError("compact INT4 K active length/capacity is invalid")
+        if tuple(self.scale.shape) != (h, blocks, d2 * 2):
+            raise ValueError("compact INT4 K scale shape is invalid")
+        if self.zero_point.shape != self.scale.shape:
+            raise ValueError("compact INT4 K zero-point shape is invalid")
+        if self.scale.dtype != torch.float16 or self.zero_point.dtype != torch.uint8:
+            raise ValueError("compact INT4 K metadata dtypes are invalid")
+        if tuple(sorted(self.segment_offsets)) != tuple(self.segment_offsets):
+            raise ValueError("compact INT4 K segment offsets must be monotonic")
+
+    @property
+    def head_count(self) -> int:
+        return int(self.packed.shape[0])
+
+    @property
+    def head_dim(self) -> int:
+        return int(self.packed.shape[2]) * 2
+
+    @property
+    def superblock_count(self) -> int:
+        return int(self.scale.shape[1])
+
+    @property
+    def nbytes(self) -> int:
+        return sum(_nbytes(t) for t in self.allocation_tensors())
+
+    @property
+    def active_nbytes(self) -> int:
+        if self.active_length <= 0:
+            return 0
+        blocks = -(-self.active_length // self.superblock_size)
+        per_block = self.head_count * blocks * self.head_dim
+        return int(self.head_count * self.active_length * self.head_dim // 2
+                   + per_block * self.scale.element_size() + per_block * self.zero_point.element_size())
+
+    def allocation_tensors(self):
+        return self.packed, self.scale, self.zero_point
+
+    def dequantize_range(self, start: int, length: int) -> torch.Tensor:
+        """fp32 (code - z) * s of arena positions [start, start+length) (inspection only)."""
+        start, length = int(start), int(length)
+        if start < 0 or length < 0 or start + length > self.active_length:
+            raise ValueError("compact INT4 K range is outside the active payload")
+        payload = self.packed[:, start : start + length]
+        codes = torch.stack((payload & 15, payload >> 4), dim=-1).reshape(self.head_count, length, self.head_dim)
+        blocks = torch.arange(start, start + length, device=payload.device) // self.superblock_size
+        s = self.scale.index_select(1, blocks).float()
+        z = self.zero_point.index_select(1, blocks).float()
+        return (codes.float() - z) * s
+
+    def dequantize(self) -> torch.Tensor:
+        return self.dequantize_range(0, self.active_length)
+
+    def append_superblock(self, key_block: torch.Tensor, *, source_tokens: int | None = None) -> int:
+        """Flush 128 tokens: re-quantise the partial tail superblock together with them.
+
+        ``key_block`` may be a [H, 128, D] view whose rows are strided by ``source_tokens``
+        (the Recent-FP ring passes its first 128 slots without a copy).
+        """
+        if tuple(key_block.shape) != (self.head_count, 128, self.head_dim):
+            raise ValueError("compact INT4 K flush requires 128 matching tokens")
+        if self.active_length + 128 > self.capacity:
+            raise RuntimeError("compact INT4 K capacity exhausted")
+        _lib.require_device(key_block, "compact INT4 K flush block")
+        rows = int(source_tokens) if source_tokens is not None else 128
+        if key_block.stride() != (rows * self.head_dim, self.head_dim, 1):
+            raise ValueError("compact INT4 K flush block must have contiguous rows")
+        prefix = self.active_length // self.superblock_size * self.superblock_size
+        tail = self.active_length - prefix
+        _lib.call("r2o_pack_int4_k", _lib.ptr(key_block), _lib.dtype_code(key_block.dtype), self.head_count, rows,
+                  None, 128, tail, prefix, _lib.ptr(self.packed), _lib.ptr(self.scale), _lib.ptr(self.zero_point),
+                  self.capacity, self.superblock_count, self.superblock_size, _lib.stream_of(key_block.device))
+        self.active_length += 128
+        return tail
+
+
+def build_compact_int4_key_arena(key: torch.Tensor, segment_token_indices, *, append_capacity: int = 0,
+                                 superblock_size: int = 128) -> CompactInt4KeyArena:
+    if key.ndim != 3 or not torch.is_floating_point(key) or int(key.shape[2]) % 2:
+        raise ValueError("key must be floating [H,S,D] with even D")
+    if superblock_size not in (32, 64, 128):
+        raise ValueError("compact per-channel INT4 K superblock must be 32, 64, or 128 tokens")
+    _lib.require_device(key, "key")
+    lengths = tuple(int(ix.numel()) for ix in segment_token_indices)
+    offsets = (0, lengths[0], lengths[0] + lengths[1])
+    active = sum(lengths)
+    capacity = max(128, _round_up(active + int(append_capacity), 128))
+    h, s, d = map(int, key.shape)
+    blocks = capacity // superblock_size
+    dev = key.device
+    arena = CompactInt4KeyArena(
+        packed=torch.zeros((h, capacity, d // 2), device=dev, dtype=torch.uint8),
+        scale=torch.zeros((h, blocks, d), device=dev, dtype=torch.float16),
+        zero_point=torch.zeros((h, blocks, d), device=dev, dtype=torch.uint8),
+        active_length=active, capacity=capacity, segment_offsets=offsets,
+        original_dtype=key.dtype, superblock_size=superblock_size,
+    )
+    if active:
+        key = key.contiguous()
+        ordered = torch.cat([ix.to(device=dev, dtype=torch.long) for ix in segment_token_indices]).contiguous()
+        _lib.call("r2o_pack_int4_k", _lib.ptr(key), _lib.dtype_code(key.dtype), h, s, _lib.ptr(ordered), active,
+                  0, 0, _lib.ptr(arena.packed), _lib.ptr(arena.scale), _lib.ptr(arena.zero_point), capacity,
+                  blocks, superblock_size, _lib.stream_of(dev))
+    return arena
+
+
+# ---------------------------------------------------------------------- INT4-V pool payload
+@dataclass
+class PackedTensor:
+    packed: torch.Tensor
+    scale: torch.Tensor
+    zero_point: torch.Tensor | None
+    num_bits: int
+    original_shape: tuple[int, ...]
+    dtype: torch.dtype
+    quant_scheme: str
+    pack_metadata: dict[str, Any]
+    quant_metadata: dict[str, Any] = field(default_factory=dict)
+
+    @property
+    def nbytes(self) -> int:
+        return _nbytes(self.packed) + _nbytes(self.scale) + _nbytes(self.zero_point)
+
+    def dequantize(self) -> torch.Tensor:
+        """Per-token INT4 dequantised and rounded to the input dtype (packed_kv_layout.py:30-32)."""
+        h, s, d = self.original_shape
+        p = self.packed.reshape(h, s, d // 2)
+        lo = (p & 15).to(torch.int16)
+        hi = (p >> 4).to(torch.int16)
+        codes = torch.stack((torch.where(lo >= 8, lo - 16, lo), torch.where(hi >= 8, hi - 16, hi)), -1)
+        return (codes.reshape(h, s, d).float() * self.scale.float()).to(self.dtype)
+
+
+def fused_gather_pack_int4_value(value: torch.Tensor, token_indices: torch.Tensor) -> PackedTensor:
+    if value.ndim != 3 or int(value.shape[2]) != 128:
+        raise ValueError("INT4 V source must be [Hkv,S,128]")
+    if token_indices.ndim != 1 or token_indices.device != value.device:
+        raise ValueError("INT4 V token indices must be rank-1 on the V device")
+    _lib.require_device(value, "value")
+    h, s, d = map(int, value.shape)
+    n = int(token_indices.numel())
+    packed = torch.empty((h, n, d // 2), device=value.device, dtype=torch.uint8)
+    scale = torch.empty((h, n, 1), device=value.device, dtype=torch.float32)
+    if n:
+        value = value.contiguous()
+        idx = token_indices.to(torch.long).contiguous()
+        _lib.call("r2o_pack_int4_v", _lib.ptr(value), _lib.dtype_code(value.dtype), h, s, _lib.ptr(idx), n, 0,
+                  _lib.ptr(packed), _lib.ptr(scale), n, _lib.stream_of(value.device))
+    return PackedTensor(packed=packed.flatten(), scale=scale, zero_point=None, num_bits=4, original_shape=(h, n, d),
+                        dtype=value.dtype, quant_scheme="per_token",
+                        pack_metadata={"pack_axis": "flatten_c_order", "fused_gather": True},
+                        quant_metadata={"dim": 2, "fused_gather": True})
+
+
+# ------------------------------------------------------------------------ compact INT2 V
+@dataclass
+class CompactInt2ValueArena:
+    """Per-token-group affine INT2 V with in-place generated flushes."""
+
+    packed: torch.Tensor          # u8  [H, capacity, D/4]
+    scale: torch.Tensor           # f16 [H, capacity, D/G, 1]
+    zero_point: torch.Tensor      # u8  [H, capacity, D/G, 1]
+    active_length: int
+    capacity: int
+    original_dtype: torch.dtype
+    group_size: int = 32
+    axis: str = "per_token_group"
+    superblock_size: int = 128
+
+    def __post_init__(self) -> None:
+        if self.packed.ndim != 3 or self.packed.dtype != torch.uint8:
+            raise ValueError("compact INT2 V packed storage must be uint8 [H,capacity,D/4]")
+        h, capacity, d4 = map(int, self.packed.shape)
+        groups = d4 * 4 // self.group_size
+        if capacity != self.capacity or not 0 <= self.active_length <= capacity:
+            raise ValueError("compact INT2 V active length/capacity is invalid")
+        if tuple(self.scale.shape) != (h, capacity, groups, 1):
+            raise ValueError("compact INT2 V scale shape is invalid")
+        if self.zero_point.shape != self.scale.shape:
+            raise ValueError("compact INT2 V zero-point shape is invalid")
+        if self.scale.dtype != torch.float16 or self.zero_point.dtype != torch.uint8:
+            raise ValueError("compact INT2 V metadata dtypes are invalid")
+
+    @property
+    def original_shape(self) -> tuple[int, int, int]:
+        return int(self.packed.shape[0]), int(self.active_length), int(self.packed.shape[2]) * 4
+
+    @property
+    def nbytes(self) -> int:
+        return sum(_nbytes(t) for t in self.allocation_tensors())
+
+    @property
+    def active_nbytes(self) -> int:
+        h, _, d4 = map(int, self.packed.shape)
+        groups = d4 * 4 // self.group_size
+        return int(h * self.active_length * (d4 + groups * (self.scale.element_size() + self.zero_point.element_size())))
+
+    def allocation_tensors(self):
+        return self.packed, self.scale, self.zero_point
+
+    def dequantize_range(self, start: int, length: int) -> torch.Tensor:
+        start, length = int(start), int(length)
+        if start < 0 or length < 0 or start + length > self.active_length:
+            raise ValueError("compact INT2 V dequantization range is outside active storage")
+        h, _, d4 = map(int, self.packed.shape)
+        d = d4 * 4
+        p = self.packed[:, start : start + length]
+        codes = torch.stack([(p >> (2 * k)) & 3 for k in range(4)], dim=-1).reshape(h, length, d)
+        grouped = codes.reshape(h, length, d // self.group_size, self.group_size).float()
+        s = self.scale[:, start : start + length].float()
+        z = self.zero_point[:, start : start + length].float()
+        return ((grouped - z) * s).reshape(h, length, d)
+
+    def dequantize(self) -> torch.Tensor:
+        return self.dequantize_range(0, self.active_length)
+
+    def append_superblock(self, value_block: torch.Tensor, *, source_tokens: int | None = None) -> None:
+        h, _, d = self.original_shape
+        if value_block.ndim != 3 or int(value_block.shape[0]) != h or int(value_block.shape[2]) != d \
+                or int(value_block.shape[1]) <= 0:
+            raise ValueError("compact INT2 V flush must contain matching tokens")
+        n = int(value_block.shape[1])
+        dst = self.active_length
+        if dst + n > self.capacity:
+            raise RuntimeError(f"compact INT2 V capacity exhausted: need {dst + n}, have {self.capacity}")
+        _lib.require_device(value_block, "compact INT2 V flush block")
+        rows = int(source_tokens) if source_tokens is not None else n
+        if value_block.stride() != (rows * d, d, 1):
+            raise ValueError("compact INT2 V flush block must have contiguous rows")
+        _lib.call("r2o_pack_int2_v", _lib.ptr(value_block), _lib.dtype_code(value_block.dtype), h, rows, None, n,
+                  dst, self.group_size, _lib.ptr(self.packed), _lib.ptr(self.scale), _lib.ptr(self.zero_point),
+                  self.capacity, _lib.stream_of(value_block.device))
+        self.active_length += n
+
+
+def build_compact_int2_value_arena(value: torch.Tensor, token_indices: torch.Tensor, *, append_capacity: int = 0,
+                                   group_size: int = 32) -> CompactInt2ValueArena:
+    if value.ndim != 3 or int(value.shape[2]) != 128:
+        raise ValueError("compact INT2 V source must be [Hkv,S,128]")
+    if group_size not in (32, 64, 128):
+        raise ValueError("compact INT2 V requires group_size 32, 64, or 128")
+    if append_capacity < 0:
+        raise ValueError("append_capacity must be non-negative")
+    _lib.require_device(value, "value")
+    n = int(token_indices.numel())
+    capacity = max(128, _round_up(n + int(append_capacity), 128))
+    h, s, d = map(int, value.shape)
+    groups = d // group_size
+    dev = value.device
+    arena = CompactInt2ValueArena(
+        packed=torch.zeros((h, capacity, d // 4), device=dev, dtype=torch.uint8),
+        scale=torch.zeros((h, capacity, groups, 1), device=dev, dtype=torch.float16),
+        zero_point=torch.zeros((h, capacity, groups, 1), device=dev, dtype=torch.uint8),
+        active_length=n, capacity=capacity, original_dtype=value.dtype, group_size=group_size,
+    )
+    if n:
+        value = value.contiguous()
+        idx = token_indices.to(device=dev, dtype=torch.long).contiguous()
+        _lib.call("r2o_pack_int2_v", _lib.ptr(value), _lib.dtype_code(value.dtype), h, s, _lib.ptr(idx), n, 0,
+                  group_size, _lib.ptr(arena.packed), _lib.ptr(arena.scale), _lib.ptr(arena.zero_point), capacity,
+                  _lib.stream_of(dev))
+    return arena
+
+
+# ----------------------------------------------------------------------------- pools/cache
+@dataclass
+class PrecisionPool:
+    name: str
+    page_index: PhysicalPageIndex
+    fp_k: torch.Tensor | None = None
+    fp_v: torch.Tensor | None = None
+    packed_k: Any = None
+    packed_v: Any = None
+    active_length: int | None = None
+    capacity: int = 0
+    length_device: torch.Tensor | None = None
+    global_index_buffer: torch.Tensor | None = None
+    logical_position_buffer: torch.Tensor | None = None
+
+    @property
+    def token_count(self) -> int:
+        if self.active_length is not None:
+            return int(self.active_length)
+        return int(self.page_index.global_token_indices.numel())
+
+    @property
+    def payload_bytes(self) -> int:
+        return int(_nbytes(self.fp_k) + _nbytes(self.fp_v)
+                   + (0 if self.packed_k is None else self.packed_k.nbytes)
+                   + (0 if self.packed_v is None else self.packed_v.nbytes))
+
+    @property
+    def active_payload_bytes(self) -> int:
+        n = self.token_count
+
+        def fp(t):
+            if t is None:
+                return 0
+            if self.active_length is None:
+                return _nbytes(t)
+            return int(t.shape[0]) * int(t.shape[2]) * n * t.element_size()
+
+        def packed(x):
+            return 0 if x is None else int(getattr(x, "active_nbytes", x.nbytes))
+
+        return int(fp(self.fp_k) + fp(self.fp_v) + packed(self.packed_k) + packed(self.packed_v))
+
+
+@dataclass
+class ThreePrecisionCache:
+    fp_pool: PrecisionPool
+    int4_pool: PrecisionPool
+    int2_pool: PrecisionPool
+    recent_fp_pool: PrecisionPool
+    evicted_global_indices: torch.Tensor
+    page_size: int
+    quantization_superblock: int
+    matched_fp: bool
+    cache_variant: str
+    compact_key: CompactInt4KeyArena | None = None
+    compact_value: CompactInt2ValueArena | None = None
+    compact_int4_value: Any = None
+    metadata_arena: Any = None
+    recent_flush_size: int = 128
+    generated_value_precision: str = "int2"
+    static_int4_tokens: int = 0
+    generated_k_offset: int = 0
+
+    @property
+    def pools(self):
+        return (self.fp_pool, self.int4_pool, self.int2_pool, self.recent_fp_pool)
+
+    @property
+    def payload_bytes(self) -> int:
+        return sum(p.payload_bytes for p in self.pools) + (0 if self.compact_key is None else self.compact_key.nbytes)
+
+    @property
+    def survivor_count(self) -> int:
+        return sum(p.token_count for p in self.pools)
+
+    @property
+    def uniform_int4_key(self) -> bool:
+        return self.cache_variant == "v_fourq_k_int4_compact" and not self.matched_fp
+
+    @property
+    def uniform_int2_key(self) -> bool:
+        return self.cache_variant == "v_fourq_k_int2_compact" and not self.matched_fp
+
+    @property
+    def full_precision_key(self) -> bool:
+        return self.cache_variant == "v_fourq_k_bf16" or self.matched_fp
+
+    @property
+    def compact_int4_key(self) -> bool:
+        return self.compact_key is not None and self.compact_key.bit_width == 4
+
+    @property
+    def compact_int2_key(self) -> bool:
+        return self.compact_key is not None and self.compact_key.bit_width == 2
+
+    @property
+    def compact_int2_value(self) -> bool:
+        return self.compact_value is not None
+
+    @property
+    def storage_bytes(self) -> int:
+        return precision_cache_storage_breakdown(self)["persistent_cache_bytes"]
+
+
+def _pool_metadata(pool: PrecisionPool):
+    pi = pool.page_index
+    return (pi.original_page_ids, pi.physical_offsets, pi.lengths, pi.global_token_indices, pi.logical_positions,
+            pool.length_device, pool.global_index_buffer, pool.logical_position_buffer)
+
+
+def precision_cache_storage_breakdown(cache: ThreePrecisionCache) -> dict[str, int]:
+    """Allocated bytes, counting each storage once (precision_pool.py:296-344)."""
+    payload: list[torch.Tensor] = []
+    if cache.compact_key is not None:
+        payload.extend(cache.compact_key.allocation_tensors())
+    for pool in cache.pools:
+        payload.extend(t for t in (pool.fp_k, pool.fp_v) if t is not None)
+        for pk in (pool.packed_k, pool.packed_v):
+            if pk is not None:
+                payload.extend(t for t in (pk.packed, pk.scale, pk.zero_point) if t is not None)
+    seen: set[int] = set()
+    pay = 0
+    for t in payload:
+        key = t.untyped_storage().data_ptr()
+        if key not in seen:
+            seen.add(key)
+            pay += int(t.untyped_storage().nbytes())
+    meta_seen: set[int] = set()
+    meta = 0
+    for t in [cache.evicted_global_indices] + [m for p in cache.pools for m in _pool_metadata(p)]:
+        if t is None:
+            continue
+        key = t.untyped_storage().data_ptr()
+        if key in seen or key in meta_seen:
+            continue
+        meta_seen.add(key)
+        meta += int(t.untyped_storage().nbytes())
+    return {"kv_payload_bytes": pay, "kv_payload_allocation_count": len(seen), "metadata_bytes": meta,
+            "metadata_allocation_count": len(meta_seen), "persistent_cache_bytes": pay + meta,
+            "persistent_allocation_count": len(seen) + len(meta_seen)}
+
+
+def precision_cache_active_storage_breakdown(cache: ThreePrecisionCache) -> dict[str, int]:
+    """Populated payload and the metadata that addresses it (precision_pool.py:347-397)."""
+    payload = sum(p.active_payload_bytes for p in cache.pools)
+    if cache.compact_key is not None:
+        payload += cache.compact_key.active_nbytes
+    meta = _nbytes(cache.evicted_global_indices)
+    fields = 0
+    for pool in cache.pools:
+        n = pool.token_count
+        pages = int(pool.page_index.lengths.numel()) if pool.active_length is None else -(-n // cache.page_size)
+        pi = pool.page_index
+        meta += sum(pages * t.element_size() for t in (pi.original_page_ids, pi.physical_offsets, pi.lengths))
+        meta += sum(n * t.element_size() for t in (pi.global_token_indices, pi.logical_positions))
+        fields += 3 * (pages > 0) + 2 * (n > 0)
+        if pool.length_device is not None:
+            meta += pool.length_device.element_size()
+            fields += 1
+    return {"kv_payload_bytes": int(payload), "kv_payload_allocation_count": 0, "metadata_bytes": int(meta),
+            "metadata_allocation_count": int(fields), "persistent_cache_bytes": int(payload + meta),
+            "persistent_allocation_count": int(fields)}
+
+
+def _compact_page_layouts(plan: LayerCompressionPlan):
+    """(tokens, offsets, lengths, page ids) of FP, INT4, INT2, Recent(empty), evicted pools.
+
+    Pages are stably sorted by tier FP(+protected, recent) < INT4 < INT2 < evicted and keep
+    their token order (precision_pool.py:611-669).  Computed on the host from the page table.
+    """
+    classes = plan.page_classes.detach().to("cpu", torch.long)
+    starts = plan.page_offsets.detach().to("cpu", torch.long)
+    lens = plan.page_lengths.detach().to("cpu", torch.long)
+    cat = torch.full_like(classes, 3)
+    cat[(classes == PageClass.FP_PAGE) | (classes == PageClass.PROTECTED_FP_PAGE)
+        | (classes == PageClass.RECENT_FP_PAGE)] = 0
+    cat[classes == PageClass.INT4_PAGE] = 1
+    cat[classes == PageClass.INT2_PAGE] = 2
+    order = torch.argsort(cat, stable=True)
+    layouts = []
+    for tier in range(4):
+        pages = order[cat[order] == tier]
+        pl = lens[pages]
+        toks = [torch.arange(int(starts[p]), int(starts[p]) + int(lens[p])) for p in pages.tolist()]
+        tokens = torch.cat(toks) if toks else torch.zeros(0, dtype=torch.long)
+        layouts.append((tokens, pl.cumsum(0) - pl, pl, pages))
+    empty = torch.zeros(0, dtype=torch.long)
+    return layouts[0], layouts[1], layouts[2], (empty, empty, empty, empty), layouts[3]
+
+
+def _make_page_index(plan: LayerCompressionPlan, layout, device) -> PhysicalPageIndex:
+    tokens, offsets, lengths, pages = layout
+    gi = plan.global_token_indices.detach().to("cpu", torch.long)
+    lp = plan.logical_positions.detach().to("cpu", torch.long)
+    return PhysicalPageIndex(original_page_ids=pages.to(device), physical_offsets=offsets.to(device),
+                             lengths=lengths.to(device), global_token_indices=gi[tokens].to(device),
+                             logical_positions=lp[tokens].to(device))
+
+
+def _preallocate_recent_pool(name: str, key: torch.Tensor, *, page_size: int, capacity: int) -> PrecisionPool:
+    if capacity < page_size or capacity % page_size:
+        raise ValueError("Recent-FP capacity must be positive and page aligned")
+    h, _, d = map(int, key.shape)
+    dev = key.device
+    gbuf = torch.full((capacity,), -1, device=dev, dtype=torch.long)
+    lbuf = torch.full((capacity,), -1, device=dev, dtype=torch.long)
+    pages = capacity // page_size
+    return PrecisionPool(
+        name=name,
+        page_index=PhysicalPageIndex(
+            original_page_ids=torch.full((pages,), -1, device=dev, dtype=torch.long),
+            physical_offsets=torch.arange(pages, device=dev, dtype=torch.long) * page_size,
+            lengths=torch.zeros(pages, device=dev, dtype=torch.long),
+            global_token_indices=gbuf, logical_positions=lbuf),
+        fp_k=torch.zeros((h, capacity, d), device=dev, dtype=key.dtype),
+        fp_v=torch.zeros((h, capacity, d), device=dev, dtype=key.dtype),
+        active_length=0, capacity=capacity,
+        length_device=torch.zeros((), device=dev, dtype=torch.int32),
+        global_index_buffer=gbuf, logical_position_buffer=lbuf,
+    )
+
+
+def build_three_precision_cache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    plan: LayerCompressionPlan,
+    *,
+    page_size: int = 32,
+    quantization_superblock: int = 128,
+    key_quantization_superblock: int = 32,
+    int2_group_size: int = 32,
+    generated_value_precision: str = "int2",
+    matched_fp: bool = False,
+    preallocate_recent: bool = True,
+    cache_variant: str = "v_fourq_k_int4_compact",
+    compact_key_append_capacity: int | None = None,
+    recent_flush_size: int = 128,
+) -> ThreePrecisionCache:
+    """Stable page reorder into contiguous FP/INT4/INT2/Recent-FP pools, packed on the GPU."""
+    if key.shape != value.shape or key.ndim != 3:
+        raise ValueError("key/value must be logical [Hkv,S,D]")
+    if int(key.shape[1]) != int(plan.logical_positions.numel()):
+        raise ValueError("K/V sequence length must match the static plan")
+    if page_size not in (16, 32, 64):
+        raise ValueError("page_size must be 16, 32, or 64")
+    if quantization_superblock != 128:
+        raise ValueError("formal precision pools use 128-token quantization superblocks")
+    if key_quantization_superblock not in (32, 64, 128):
+        raise ValueError("K quantization superblock must be 32, 64, or 128")
+    if recent_flush_size not in (32, 64, 128) or recent_flush_size % page_size \
+            or recent_flush_size % key_quantization_superblock:
+        raise ValueError("recent_flush_size must be 32/64/128 and align to page/K blocks")
+    if preallocate_recent and plan.recent_fp_capacity < recent_flush_size:
+        raise ValueError("Recent-FP capacity must cover one configured flush")
+    if cache_variant not in ("v_fourq_k_int2_compact", "v_fourq_k_int4_compact", "v_fourq_k_bf16"):
+        raise ValueError(f"unsupported cache_variant: {cache_variant}")
+    if generated_value_precision not in ("int2", "int4"):
+        raise ValueError("generated_value_precision must be int2 or int4")
+    if cache_variant != "v_fourq_k_int4_compact" or matched_fp or generated_value_precision != "int2" \
+            or not preallocate_recent:
+        raise NotImplementedError(
+            "the gfx950 path implements the released v_fourq_k_int4_compact cache with INT2 generated "
+            "values and a preallocated Recent-FP ring")
+    if int(key.shape[2]) != 128:
+        raise ValueError("the SSPA decode path requires head_dim 128")
+    _lib.require_device(key, "key")
+    _lib.dtype_code(key.dtype)
+    key = key.contiguous()
+    value = value.contiguous()
+    dev = key.device
+    fp_l, i4_l, i2_l, rec_l, ev_l = _compact_page_layouts(plan)
+    if sum(int(l[0].numel()) for l in (fp_l, i4_l, i2_l, ev_l)) != int(key.shape[1]):
+        raise ValueError("compact physical pools must cover every logical token")
+    h = int(key.shape[0])
+    fp_tokens, i4_tokens, i2_tokens = (l[0].to(dev) for l in (fp_l, i4_l, i2_l))
+    s_fp, s_i4 = int(fp_tokens.numel()), int(i4_tokens.numel())
+    stream = _lib.stream_of(dev)
+
+    fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(plan, fp_l, dev))
+    if s_fp:
+        fp_pool.fp_v = torch.empty((h, s_fp, 128), device=dev, dtype=value.dtype)
+        _lib.call("r2o_gather_rows", _lib.ptr(value), h, int(value.shape[1]), _lib.ptr(fp_tokens), s_fp,
+                  _lib.ptr(fp_pool.fp_v), s_fp, stream)
+    int4_pool = PrecisionPool(name="int4", page_index=_make_page_index(plan, i4_l, dev))
+    if s_i4:
+        int4_pool.packed_v = fused_gather_pack_int4_value(value, i4_tokens)
+    int2_pool = PrecisionPool(name="int2", page_index=_make_page_index(plan, i2_l, dev))
+    append_capacity = plan.recent_fp_capacity if compact_key_append_capacity is None \
+        else int(compact_key_append_capacity)
+    compact_value = build_compact_int2_value_arena(value, i2_tokens, append_capacity=append_capacity,
+                                                   group_size=int2_group_size)
+    int2_pool.packed_v = compact_value
+    compact_key = build_compact_int4_key_arena(key, (fp_tokens, i4_tokens, i2_tokens),
+                                               append_capacity=append_capacity,
+                                               superblock_size=key_quantization_superblock)
+    recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity)
+    gi = plan.global_token_indices.detach().to("cpu", torch.long)
+    return ThreePrecisionCache(
+        fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent,
+        evicted_global_indices=gi[ev_l[0]].to(dev), page_size=int(page_size),
+        quantization_superblock=int(quantization_superblock), matched_fp=False, cache_variant=cache_variant,
+        compact_key=compact_key, compact_value=compact_value, recent_flush_size=int(recent_flush_size),
+        generated_value_precision="int2", static_int4_tokens=s_i4, generated_k_offset=compact_key.active_length,
+    )
+
+
+# ------------------------------------------------------------------------- append / flush
+@dataclass
+class DynamicCacheStats:
+    appended_tokens: int = 0
+    flushed_superblocks: int = 0
+    flushed_tokens: int = 0
+    flushed_int4_value_tokens: int = 0
+    recent_reallocation_count: int = 0
+    local_tail_dequant_tokens: int = 0
+    full_dequant_tensor_count: int = 0
+
+
+def _append_int2_page_metadata(pool: PrecisionPool, global_block: torch.Tensor, logical_block: torch.Tensor,
+                               page_size: int) -> None:
+    n = int(global_block.numel())
+    if n <= 0 or n % page_size:
+        raise ValueError("low-bit metadata append must contain complete pages")
+    pages = n // page_size
+    old = pool.page_index
+    dev = global_block.device
+    start = pool.token_count
+    pool.page_index = PhysicalPageIndex(
+        original_page_ids=torch.cat((old.original_page_ids, torch.full((pages,), -1, device=dev, dtype=torch.long))),
+        physical_offsets=torch.cat((old.physical_offsets,
+                                    start + torch.arange(pages, device=dev, dtype=torch.long) * page_size)),
+        lengths=torch.cat((old.lengths, torch.full((pages,), page_size, device=dev, dtype=torch.long))),
+        global_token_indices=torch.cat((old.global_token_indices, global_block)),
+        logical_positions=torch.cat((old.logical_positions, logical_block)),
+    )
+
+
+def append_generated_token(cache: ThreePrecisionCache, new_key: torch.Tensor, new_value: torch.Tensor, *,
+                           global_token_index: int, logical_position: int, stats: DynamicCacheStats) -> bool:
+    """Append one token to the Recent-FP ring; when it is full, flush its oldest chunk first."""
+    pool = cache.recent_fp_pool
+    flush = int(cache.recent_flush_size)
+    if pool.active_length is None or pool.capacity < flush or pool.length_device is None:
+        raise RuntimeError("Recent-FP pool was not preallocated for dynamic generation")
+    if new_key.ndim == 4:
+        new_key, new_value = new_key[0], new_value[0]
+    if new_key.shape != new_value.shape or new_key.ndim != 3 or int(new_key.shape[1]) != 1:
+        raise ValueError("new K/V must be [Hkv,1,D] or [1,Hkv,1,D]")
+    _lib.require_device(new_key, "new_key")
+    if new_key.dtype != pool.fp_k.dtype or new_value.dtype != pool.fp_v.dtype:
+        raise ValueError("new K/V dtype must match the Recent-FP ring")
+    h, cap = int(pool.fp_k.shape[0]), int(pool.capacity)
+    stream = _lib.stream_of(new_key.device)
+    flushed = False
+    if pool.active_length == pool.capacity:
+        if cache.compact_key is None or cache.compact_value is None:
+            raise RuntimeError("compact INT4 K cache is missing its compact INT2 V arena")
+        key_block = pool.fp_k[:, :flush]
+        value_block = pool.fp_v[:, :flush]
+        # copy the index slices before the ring shift overwrites them
+        global_block = pool.global_index_buffer[:flush].clone()
+        logical_block = pool.logical_position_buffer[:flush].clone()
+        stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
+            if flush == 128 else _flush_size_error(flush)
+        cache.compact_value.append_superblock(value_block, source_tokens=cap)
+        _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
+        _lib.call("r2o_recent_shift", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, flush, pool.active_length,
+                  _lib.ptr(pool.global_index_buffer), _lib.ptr(pool.logical_position_buffer),
+                  _lib.ptr(pool.length_device), _lib.ptr(pool.page_index.lengths), cache.page_size, stream)
+        pool.active_length -= flush
+        stats.flushed_superblocks += 1
+        stats.flushed_tokens += flush
+        flushed = True
+    nk = new_key.reshape(h, -1).contiguous()
+    nv = new_value.reshape(h, -1).contiguous()
+    _lib.call("r2o_recent_append", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, _lib.ptr(nk), _lib.ptr(nv),
+              pool.active_length, int(global_token_index), int(logical_position), _lib.ptr(pool.length_device),
+              _lib.ptr(pool.global_index_buffer), _lib.ptr(pool.logical_position_buffer),
+              _lib.ptr(pool.page_index.lengths), cache.page_size, stream)
+    pool.active_length += 1
+    stats.appended_tokens += 1
+    return flushed
+
+
+def _flush_size_error(flush: int) -> int:
+    raise ValueError(f"compact INT4 K flush requires 128 tokens, the cache flushes {flush}")

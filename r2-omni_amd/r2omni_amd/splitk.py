@@ -1,0 +1,381 @@
+"""Split-K executor over the SSPA packed cache: the drop-in decode call surface.
+
+Same names, arguments, return values and error behaviour as the reference
+(r2omni/sspa/kernels/triton_fourq_splitk.py):
+  allocate_splitk_workspace   :1607-1676   required_splitk_blocks :1679-1692
+  prepare_splitk_executor     :1695-1907   SplitKExecutor.__call__ :1243-1547
+  append_recent_fp_triton     :1557-1604   (name kept; it launches r2o_recent_append)
+  stack_homogeneous_splitk_executors :1995-2241 (here also for ragged batches: no payload copy)
+  allocated_workspace_bytes   :2244-2256
+Launch knobs of the Triton kernels (block_n, num_warps, num_stages, tensor-core flags, ...)
+are accepted and ignored: the gfx950 kernels fix their own tiling.  A "block" of the
+workspace is one split-K work item (a run of 32-token tiles handled by one workgroup).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import torch
+
+from . import _lib
+from .cache import ThreePrecisionCache
+
+TILE = 32
+_MIN_TILES_PER_ITEM = 4      # one tile per wave of the 4-wave workgroup
+_MAX_TILES_PER_ITEM = 256
+
+
+@dataclass
+class SplitKWorkspace:
+    partial_max: torch.Tensor      # f32 [total_blocks, 16]
+    partial_sum: torch.Tensor      # f32 [total_blocks, 16]
+    partial_output: torch.Tensor   # f32 [total_blocks, 16, 128]
+    output: torch.Tensor           # bf16 [B, Hq, 128]
+    total_blocks: int
+    block_n: int = 128
+    hierarchical_group_blocks: int = 64
+    empty_bf16: torch.Tensor | None = None
+
+
+def _num_cus(device: torch.device) -> int:
+    return int(torch.cuda.get_device_properties(device).multi_processor_count)
+
+
+def _segments(cache: ThreePrecisionCache, extra_int2: int = 0):
+    """(kind, lo, hi, v_delta) arena ranges of the FP, INT4 and INT2(+generated) pools."""
+    ck = cache.compact_key
+    if ck is None or not cache.compact_int4_key:
+        raise NotImplementedError("the gfx950 decode path requires the compact INT4-K arena")
+    k_fp, k_i4, k_i2 = ck.segment_offsets
+    s_fp = cache.fp_pool.token_count
+    s_i4 = cache.int4_pool.token_count
+    s_i2 = cache.compact_value.active_length + int(extra_int2)
+    out = []
+    for kind, lo, n in ((_lib.KIND_FP, k_fp, s_fp), (_lib.KIND_INT4, k_i4, s_i4), (_lib.KIND_INT2, k_i2, s_i2)):
+        if n > 0:
+            out.append((kind, lo, lo + n, lo))
+    return out
+
+
+def _tiles(lo: int, hi: int) -> tuple[int, int]:
+    t0 = lo // TILE * TILE
+    return t0, -(-(hi - t0) // TILE)
+
+
+def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_int2: int = 0):
+    """Split every (request, kv head, pool segment) into runs of tiles for ~3 workgroups per CU.
+
+    Returns (items [n, 8] int64, group_begin [B*hkv + 1] int32) on the host, items grouped by
+    (request, kv head).
+    """
+    segs = [_segments(c, extra_int2) for c in caches]
+    total_tiles = 0
+    for c, ss in zip(caches, segs):
+        total_tiles += hkv * (sum(_tiles(lo, hi)[1] for _, lo, hi, _ in ss) + c.recent_fp_pool.capacity // TILE)
+    target = 3 * max(1, num_cus)
+    tpi = -(-total_tiles // target)
+    tpi = max(_MIN_TILES_PER_ITEM, min(_MAX_TILES_PER_ITEM, -(-tpi // 4) * 4))
+    items = []
+    begins = [0]
+    for r, (c, ss) in enumerate(zip(caches, segs)):
+        rcap = c.recent_fp_pool.capacity
+        if rcap % TILE:
+            raise ValueError("Recent-FP capacity must be a multiple of 32 for the gfx950 decode path")
+        for h in range(hkv):
+            for kind, lo, hi, vd in ss:
+                t0, nt = _tiles(lo, hi)
+                for first in range(0, nt, tpi):
+                    items.append((r, h, kind, t0 + TILE * first, min(tpi, nt - first), lo, hi, vd))
+            for first in range(0, rcap // TILE, tpi):
+                items.append((r, h, _lib.KIND_RECENT, TILE * first, min(tpi, rcap // TILE - first), 0, rcap, 0))
+            begins.append(len(items))
+    return torch.tensor(items, dtype=torch.int64), torch.tensor(begins, dtype=torch.int32)
+
+
+def required_splitk_blocks(cache: ThreePrecisionCache, *, block_n: int = 128, reserve_tokens: int = 0) -> int:
+    """Partial-state slots a workspace needs for ``cache`` grown by ``reserve_tokens`` low-bit tokens."""
+    if block_n < 1:
+        raise ValueError("block_n must be positive")
+    dev = cache.recent_fp_pool.fp_k.device
+    hkv = int(cache.recent_fp_pool.fp_k.shape[0])
+    cus = _num_cus(dev) if dev.type == "cuda" else 256
+    now, _ = plan_work_items([cache], hkv, cus)
+    grown, _ = plan_work_items([cache], hkv, cus, extra_int2=max(0, int(reserve_tokens)))
+    return int(max(now.shape[0], grown.shape[0])) + 4 * hkv
+
+
+def allocate_splitk_workspace(cache: ThreePrecisionCache, *, num_query_heads: int = 16, block_n: int = 128,
+                              reserve_tokens: int = 0, device: torch.device | None = None,
+                              partial_output_dtype: torch.dtype = torch.float32,
+                              hierarchical_group_blocks: int = 64, batch_size: int = 1,
+                              total_blocks: int | None = None) -> SplitKWorkspace:
+    if partial_output_dtype not in (torch.float16, torch.float32):
+        raise ValueError("partial_output_dtype must be float16 or float32")
+    if hierarchical_group_blocks not in (16, 32, 64):
+        raise ValueError("hierarchical_group_blocks must be 16, 32, or 64")
+    if int(num_query_heads) < 1:
+        raise ValueError("num_query_heads must be positive")
+    if cache.survivor_count <= 0 and cache.recent_fp_pool.capacity <= 0:
+        raise ValueError("cannot allocate workspace for an empty cache")
+    dev = device if device is not None else cache.recent_fp_pool.fp_k.device
+    total = int(total_blocks) if total_blocks is not None else \
+        required_splitk_blocks(cache, block_n=block_n, reserve_tokens=reserve_tokens)
+    # Partials stay fp32 whatever the requested dtype: the split-K merge is exact in fp32.
+    return SplitKWorkspace(
+        partial_max=torch.empty((total, 16), device=dev, dtype=torch.float32),
+        partial_sum=torch.empty((total, 16), device=dev, dtype=torch.float32),
+        partial_output=torch.empty((total, 16, 128), device=dev, dtype=torch.float32),
+        output=torch.empty((int(batch_size), int(num_query_heads), 128), device=dev, dtype=torch.bfloat16),
+        total_blocks=total, block_n=int(block_n), hierarchical_group_blocks=int(hierarchical_group_blocks),
+        empty_bf16=torch.empty(1, device=dev, dtype=torch.bfloat16),
+    )
+
+
+def allocated_workspace_bytes(workspace: SplitKWorkspace) -> int:
+    return int(sum(t.numel() * t.element_size() for t in (workspace.partial_max, workspace.partial_sum,
+                                                          workspace.partial_output, workspace.output)))
+
+
+def _request_desc(cache: ThreePrecisionCache) -> list[int]:
+    ck, cv = cache.compact_key, cache.compact_value
+    fp, i4, rec = cache.fp_pool, cache.int4_pool, cache.recent_fp_pool
+    if rec.fp_k.dtype != torch.bfloat16:
+        raise ValueError("the gfx950 decode path requires bfloat16 FP-V / Recent-FP rows")
+    i4_packed = i4.packed_v.packed if i4.token_count else None
+    i4_scale = i4.packed_v.scale if i4.token_count else None
+    words = {
+        "k_packed": ck.packed.data_ptr(), "k_scale": ck.scale.data_ptr(), "k_zero": ck.zero_point.data_ptr(),
+        "k_capacity": ck.capacity, "k_superblocks": ck.superblock_count,
+        "fp_v": fp.fp_v.data_ptr() if fp.token_count else 0, "fp_stride": fp.token_count,
+        "i4_v": i4_packed.data_ptr() if i4_packed is not None else 0,
+        "i4_scale": i4_scale.data_ptr() if i4_scale is not None else 0, "i4_stride": i4.token_count,
+        "i2_v": cv.packed.data_ptr(), "i2_scale": cv.scale.data_ptr(), "i2_zero": cv.zero_point.data_ptr(),
+        "i2_stride": cv.capacity,
+        "recent_k": rec.fp_k.data_ptr(), "recent_v": rec.fp_v.data_ptr(), "recent_capacity": rec.capacity,
+        "recent_length": rec.length_device.data_ptr(), "recent_global": rec.global_index_buffer.data_ptr(),
+        "recent_logical": rec.logical_position_buffer.data_ptr(),
+        "recent_page_lengths": rec.page_index.lengths.data_ptr(),
+    }
+    return [int(words[f]) for f in _lib.REQUEST_FIELDS]
+
+
+@dataclass
+class SplitKExecutor:
+    caches: list
+    workspace: SplitKWorkspace
+    reqs: torch.Tensor          # device int64 [B, 21]
+    items: torch.Tensor         # device int64 [n, 8]
+    group_begin: torch.Tensor   # device int32 [B*Hkv + 1]
+    n_items: int
+    num_query_heads: int
+    num_key_value_heads: int
+    head_dim: int = 128
+    superblock: int = 32
+    int2_group: int = 32
+    page_size: int = 32
+    output_hadamard: bool = False
+    block_n: int = 128
+    batched: bool = False
+    host_items: torch.Tensor | None = None
+    _keep: list = field(default_factory=list)
+
+    @property
+    def cache(self) -> ThreePrecisionCache:
+        return self.caches[0]
+
+    @property
+    def total(self) -> int:
+        return self.n_items
+
+    def _params(self, query: torch.Tensor, out: torch.Tensor, append) -> _lib.DecodeParams:
+        p = _lib.DecodeParams()
+        ws = self.workspace
+        p.reqs, p.items, p.group_begin = self.reqs.data_ptr(), self.items.data_ptr(), self.group_begin.data_ptr()
+        p.n_items = self.n_items
+        p.partial_max, p.partial_sum = ws.partial_max.data_ptr(), ws.partial_sum.data_ptr()
+        p.partial_out = ws.partial_output.data_ptr()
+        p.query, p.out = query.data_ptr(), out.data_ptr()
+        p.batch, p.hq, p.hkv = len(self.caches), self.num_query_heads, self.num_key_value_heads
+        p.superblock, p.int2_group, p.page_size = self.superblock, self.int2_group, self.page_size
+        p.q_dtype = _lib.dtype_code(query.dtype)
+        p.output_hadamard = int(self.output_hadamard)
+        p.sm_scale = float(self.head_dim ** -0.5)
+        for r, c in enumerate(self.caches):
+            p.recent_len[r] = int(c.recent_fp_pool.active_length)
+        if append is not None:
+            ak, av, gidx, lpos = append
+            p.append_k, p.append_v, p.do_append = ak.data_ptr(), av.data_ptr(), 1
+            for r in range(len(self.caches)):
+                p.append_global[r] = int(gidx[r])
+                p.append_logical[r] = int(lpos[r])
+        return p
+
+    def __call__(self, query: torch.Tensor, append=None) -> torch.Tensor:
+        if query.ndim == 4:
+            query = query[:, :, 0]
+        b = len(self.caches)
+        out = self.workspace.output
+        if tuple(query.shape) != (b, self.num_query_heads, self.head_dim) or query.device != out.device \
+                or not query.is_contiguous():
+            raise ValueError("query does not match prepared split-K executor")
+        if tuple(out.shape) != (b, self.num_query_heads, self.head_dim):
+            raise ValueError("split-K workspace geometry is inconsistent")
+        fused = None
+        if append is not None:
+            ak, av, gidx, lpos = append
+            if ak.ndim == 4:
+                ak, av = ak[:, :, 0], av[:, :, 0]
+            n = b * self.num_key_value_heads * self.head_dim
+            if ak.numel() != n or av.numel() != n or ak.device != query.device or av.device != query.device \
+                    or not ak.is_contiguous() or not av.is_contiguous():
+                raise ValueError("append K/V must be contiguous [B,Hkv,1,D] or [B,Hkv,D]")
+            if ak.dtype != torch.bfloat16 or av.dtype != torch.bfloat16:
+                raise ValueError("append K/V must be bfloat16 like the Recent-FP ring")
+            for c in self.caches:
+                rec = c.recent_fp_pool
+                if rec.active_length is None or rec.active_length >= rec.capacity:
+                    raise RuntimeError(
+                        "prepared batched executor cannot fuse an append into a full Recent-FP pool" if self.batched
+                        else "prepared executor cannot fuse an append into a full Recent-FP pool")
+            gl = _per_request(gidx, b)
+            lp = _per_request(lpos, b)
+            fused = (ak, av, gl, lp)
+        p = self._params(query, out, fused)
+        stream = ctypes.c_void_p(_lib.stream_of(query.device))
+        lib = _lib.load()
+        _lib.check(lib.r2o_decode_partial(ctypes.byref(p), stream), "r2o_decode_partial")
+        _lib.check(lib.r2o_decode_combine(ctypes.byref(p), stream), "r2o_decode_combine")
+        if fused is not None and self.batched:
+            for c in self.caches:
+                c.recent_fp_pool.active_length += 1
+        return out
+
+
+def _per_request(value, b: int) -> list[int]:
+    if isinstance(value, int):
+        return [int(value)] * b
+    vals = torch.as_tensor(value).reshape(-1).tolist()
+    if len(vals) == 1:
+        return [int(vals[0])] * b
+    if len(vals) != b:
+        raise ValueError("batched append indices must contain one value per request")
+    return [int(v) for v in vals]
+
+
+def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWorkspace, *, output_hadamard: bool,
+                    block_n: int, batched: bool) -> SplitKExecutor:
+    first = caches[0]
+    rec = first.recent_fp_pool
+    if rec.fp_k is None or rec.fp_k.ndim != 3:
+        raise ValueError("Recent-FP pool must expose [Hkv,capacity,D] K storage")
+    if rec.length_device is None:
+        raise ValueError("Recent-FP pool must expose a device-side active length")
+    hkv, head_dim = int(rec.fp_k.shape[0]), int(rec.fp_k.shape[2])
+    hq = int(workspace.output.shape[1])
+    if head_dim != 128:
+        raise ValueError("split-K executor currently requires head_dim=128")
+    if hq % hkv:
+        raise ValueError("query heads must be divisible by key/value heads")
+    if hq // hkv > 16:
+        raise ValueError("split-K executor supports at most 16 GQA heads per KV head")
+    if len(caches) > _lib.MAX_BATCH:
+        raise ValueError(f"split-K executor supports at most {_lib.MAX_BATCH} requests per launch")
+    sb = first.compact_key.superblock_size
+    group = first.compact_value.group_size
+    for r, c in enumerate(caches):
+        ck = c.compact_key
+        if ck is None or ck.superblock_size != sb or c.compact_value.group_size != group \
+                or int(c.recent_fp_pool.fp_k.shape[0]) != hkv or c.page_size != first.page_size:
+            raise ValueError(f"batched split-K geometry differs for request {r}")
+    dev = workspace.output.device
+    host_items, begins = plan_work_items(caches, hkv, _num_cus(dev))
+    n = int(host_items.shape[0])
+    if n > workspace.total_blocks:
+        raise ValueError("workspace block capacity is smaller than the active cache")
+    reqs = torch.tensor([_request_desc(c) for c in caches], dtype=torch.int64).to(dev)
+    return SplitKExecutor(
+        caches=list(caches), workspace=workspace, reqs=reqs, items=host_items.to(dev), group_begin=begins.to(dev),
+        n_items=n, num_query_heads=hq, num_key_value_heads=hkv, head_dim=head_dim, superblock=sb, int2_group=group,
+        page_size=first.page_size, output_hadamard=bool(output_hadamard), block_n=block_n, batched=batched,
+        host_items=host_items,
+    )
+
+
+def prepare_splitk_executor(cache: ThreePrecisionCache, workspace: SplitKWorkspace, *, block_n: int = 128,
+                            num_warps: int = 8, num_stages: int = 2, reduce_num_warps: int = 8,
+                            use_tensor_cores_qk: bool = True, use_tensor_cores_pv: bool = False,
+                            broadcast_k_metadata: bool = False, single_request_fastpath: bool | None = None,
+                            tight_metadata_rows: bool | None = None, output_hadamard: bool = False,
+                            hierarchical_reduce: bool = True) -> SplitKExecutor:
+    if workspace.block_n != block_n:
+        raise ValueError("cache/workspace is incompatible with a mixed split-K executor")
+    if int(workspace.output.shape[0]) != 1:
+        raise ValueError("split-K workspace geometry is inconsistent")
+    return _build_executor([cache], workspace, output_hadamard=output_hadamard, block_n=block_n, batched=False)
+
+
+def stack_homogeneous_splitk_executors(executors: Sequence[SplitKExecutor], *,
+                                       workspace: SplitKWorkspace | None = None,
+                                       throughput_use_tensor_cores_pv: bool = False,
+                                       throughput_direct_reduce_max_splits: int = 0) -> SplitKExecutor:
+    """One launch pair over several requests; unlike the reference, lengths may differ (ragged)."""
+    if len(executors) < 2:
+        raise ValueError("batched split-K requires at least two executors")
+    caches = [e.cache for e in executors]
+    first = executors[0]
+    for r, e in enumerate(executors[1:], start=1):
+        if e.num_query_heads != first.num_query_heads or e.output_hadamard != first.output_hadamard:
+            raise ValueError(f"batched split-K executor {r} differs in heads or output transform")
+    hkv = first.num_key_value_heads
+    dev = first.workspace.output.device
+    if workspace is None:
+        items, _ = plan_work_items(caches, hkv, _num_cus(dev))
+        workspace = allocate_splitk_workspace(caches[0], num_query_heads=first.num_query_heads,
+                                              block_n=first.block_n, batch_size=len(caches),
+                                              total_blocks=int(items.shape[0]) + 4 * hkv * len(caches))
+    if int(workspace.output.shape[0]) != len(caches):
+        raise ValueError("batched workspace output must hold one row per request")
+    return _build_executor(caches, workspace, output_hadamard=first.output_hadamard, block_n=first.block_n,
+                           batched=True)
+
+
+def append_recent_fp_triton(cache: ThreePrecisionCache, new_key: torch.Tensor, new_value: torch.Tensor, *,
+                            global_token_index: int, logical_position: int) -> None:
+    """Append one decode token to the Recent-FP ring with one launch (non-fused path)."""
+    pool = cache.recent_fp_pool
+    if new_key.ndim == 4:
+        new_key, new_value = new_key[0], new_value[0]
+    if new_key.shape != new_value.shape or new_key.ndim != 3 or int(new_key.shape[1]) != 1:
+        raise ValueError("new K/V must be [Hkv,1,D] or [1,Hkv,1,D]")
+    if pool.active_length is None or pool.active_length >= pool.capacity:
+        raise RuntimeError("Recent-FP staging buffer has no append capacity")
+    if any(v is None for v in (pool.fp_k, pool.fp_v, pool.global_index_buffer, pool.logical_position_buffer,
+                               pool.length_device)):
+        raise RuntimeError("Recent-FP staging buffers are incomplete")
+    _lib.require_device(new_key, "new_key")
+    h = int(new_key.shape[0])
+    nk = new_key.reshape(h, -1).contiguous()
+    nv = new_value.reshape(h, -1).contiguous()
+    _lib.call("r2o_recent_append", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, pool.capacity, _lib.ptr(nk),
+              _lib.ptr(nv), pool.active_length, int(global_token_index), int(logical_position),
+              _lib.ptr(pool.length_device), _lib.ptr(pool.global_index_buffer),
+              _lib.ptr(pool.logical_position_buffer), _lib.ptr(pool.page_index.lengths), cache.page_size,
+              _lib.stream_of(new_key.device))
+    pool.active_length += 1
+
+
+def triton_fwht_128(tensor: torch.Tensor, *, output: torch.Tensor | None = None) -> torch.Tensor:
+    """Normalised 128-wide FWHT in one launch (name kept from triton_qwen_mrope.py:325)."""
+    if tensor.shape[-1] != 128 or not torch.is_floating_point(tensor):
+        raise ValueError("fused FWHT requires a floating tensor with last dimension 128")
+    _lib.require_device(tensor, "FWHT input")
+    tensor = tensor.contiguous()
+    if output is None:
+        output = torch.empty_like(tensor)
+    elif output.shape != tensor.shape or output.device != tensor.device or output.dtype != tensor.dtype:
+        raise ValueError("fused FWHT output must match input shape, device, and dtype")
+    _lib.call("r2o_fwht128", _lib.ptr(tensor), _lib.ptr(output), tensor.numel() // 128, _lib.dtype_code(tensor.dtype),
+              _lib.stream_of(tensor.device))
+    return output

@@ -1,0 +1,227 @@
+"""GPU parity of the HIP path against the CPU oracle and the reference-written golden fixtures.
+
+Bars: packing and quantisation bit-exact; attention output within
+max-abs 2e-2 and mean-abs 2e-3 of the fp32 dequantise-then-softmax oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from golden_io import as_f32, fixture_names, load
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+
+
+def _cuda():
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    return torch.device("cuda:0")
+
+
+def _to_torch(arr, dtype, dev):
+    if "bfloat16" in str(dtype):
+        return torch.from_numpy(np.ascontiguousarray(arr).view(np.int16)).view(torch.bfloat16).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(dev)
+
+
+def _bf16_np(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+# --------------------------------------------------------------------------- golden builds
+@pytest.mark.parametrize("name", fixture_names())
+def test_build_and_flush_bit_exact_against_reference_fixtures(name):
+    import r2omni_amd as ro
+
+    dev = _cuda()
+    g = load(name)
+    dt = str(g["dtype"])
+    key = _to_torch(g["key"], dt, dev)
+    value = _to_torch(g["value"], dt, dev)
+    plan = ro.plan_from_pages(g["page_offsets"], g["page_lengths"], g["page_classes"], recent_fp_capacity=128,
+                              device=dev)
+    cache = ro.build_three_precision_cache(
+        key, value, plan, page_size=int(g["page_size"]), key_quantization_superblock=int(g["superblock"]),
+        int2_group_size=int(g["group"]), compact_key_append_capacity=260, recent_flush_size=128)
+
+    def check(prefix):
+        torch.cuda.synchronize()
+        ck, cv = cache.compact_key, cache.compact_value
+        k = ck.active_length
+        blocks = -(-k // ck.superblock_size)
+        assert k == int(g[prefix + "k_active"]) and ck.capacity == int(g[prefix + "k_capacity"])
+        np.testing.assert_array_equal(ck.packed[:, :k].cpu().numpy(), g[prefix + "k_packed"])
+        np.testing.assert_array_equal(ck.scale[:, :blocks].cpu().view(torch.int16).numpy(),
+                                      g[prefix + "k_scale"].view(np.int16))
+        np.testing.assert_array_equal(ck.zero_point[:, :blocks].cpu().numpy(), g[prefix + "k_zero"])
+        a = cv.active_length
+        assert a == int(g[prefix + "v2_active"]) and cv.capacity == int(g[prefix + "v2_capacity"])
+        np.testing.assert_array_equal(cv.packed[:, :a].cpu().numpy(), g[prefix + "v2_packed"])
+        np.testing.assert_array_equal(cv.scale[:, :a].cpu().view(torch.int16).numpy(),
+                                      g[prefix + "v2_scale"].view(np.int16))
+        np.testing.assert_array_equal(cv.zero_point[:, :a].cpu().numpy(), g[prefix + "v2_zero"])
+        i4 = cache.int4_pool
+        if i4.token_count:
+            np.testing.assert_array_equal(i4.packed_v.packed.cpu().numpy(), g[prefix + "v4_packed"])
+            np.testing.assert_array_equal(i4.packed_v.scale.cpu().numpy().view(np.uint32),
+                                          g[prefix + "v4_scale"].view(np.uint32))
+        if cache.fp_pool.token_count:
+            got = cache.fp_pool.fp_v.cpu()
+            want = _to_torch(g[prefix + "fp_v"], dt, "cpu")
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        rec = cache.recent_fp_pool
+        r = rec.active_length
+        assert r == int(g[prefix + "recent_active"])
+        assert int(rec.length_device.item()) == r
+        want_k = _to_torch(g[prefix + "recent_k"], dt, "cpu")
+        assert torch.equal(rec.fp_k[:, :r].cpu().view(torch.int16), want_k.view(torch.int16))
+        np.testing.assert_array_equal(rec.global_index_buffer[:r].cpu().numpy(), g[prefix + "recent_global"])
+        np.testing.assert_array_equal(rec.page_index.lengths.cpu().numpy(), g[prefix + "recent_page_lengths"])
+        pools = [cache.fp_pool.token_count, cache.int4_pool.token_count, cache.int2_pool.token_count, r]
+        assert pools == [int(v) for v in g[prefix + "pool_tokens"]]
+        np.testing.assert_array_equal(
+            cache.int2_pool.page_index.global_token_indices.cpu().numpy(), g[prefix + "int2_global"])
+
+    check("build_")
+    stats = ro.DynamicCacheStats()
+    ak = _to_torch(g["append_k"], dt, dev)
+    av = _to_torch(g["append_v"], dt, dev)
+    seq = int(g["key"].shape[1])
+    flushed = []
+    for step in range(int(ak.shape[0])):
+        if ro.append_generated_token(cache, ak[step], av[step], global_token_index=seq + step,
+                                     logical_position=seq + step, stats=stats):
+            flushed.append(step)
+    assert flushed == list(g["flushed_at"])
+    assert stats.local_tail_dequant_tokens == int(g["tail_dequant_tokens"])
+    check("after_")
+
+
+# ------------------------------------------------------------------------ decode parity
+def _oracle_for(data, cfg, append_steps=0):
+    from oracle.cache import append_token, build_cache
+    from oracle.quant import bf16_bits_to_f32
+
+    f32 = lambda t: bf16_bits_to_f32(_bf16_np(t))  # noqa: E731
+    c = build_cache(f32(data.key), f32(data.value), data.page_offsets.numpy(), data.page_lengths.numpy(),
+                    data.page_classes.numpy(), dtype="bfloat16", page_size=cfg.page, superblock=cfg.superblock,
+                    group=cfg.group, recent_capacity=128, append_capacity=260)
+    hist = int(data.key.shape[1])
+    rk, rv = f32(data.recent_k), f32(data.recent_v)
+    for i in range(rk.shape[0]):
+        append_token(c, rk[i], rv[i], global_index=hist + i, logical_position=hist + i)
+    return c
+
+
+def _compare(got_bf16, want_f32, what):
+    got = got_bf16.float().cpu().numpy()
+    err = np.abs(got - want_f32)
+    assert np.isfinite(got).all(), what
+    assert err.max() <= MAX_ABS, f"{what}: max-abs {err.max():.3e}"
+    assert err.mean() <= MEAN_ABS, f"{what}: mean-abs {err.mean():.3e}"
+    return float(err.max()), float(err.mean())
+
+
+SMALL = [
+    # hq, hkv, total tokens, tier probs, recent, superblock, group
+    (16, 2, 1024 + 64, (0.2, 0.5, 0.3), 64, 32, 32),
+    (16, 2, 2048 + 128, (0.0, 1.0, 0.0), 0, 32, 32),
+    (28, 4, 1536 + 100, (0.15, 0.45, 0.4), 100, 32, 32),
+    (32, 8, 1024 + 128, (0.0, 0.0, 1.0), 128, 128, 128),
+    (16, 2, 640 + 17, (1.0, 0.0, 0.0), 17, 64, 64),
+]
+
+
+@pytest.mark.parametrize("case", range(len(SMALL)))
+@pytest.mark.parametrize("hadamard", [False, True])
+def test_decode_matches_oracle(case, hadamard):
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    hq, hkv, total, probs, recent, sb, grp = SMALL[case]
+    cfg = DecodeConfig("t", hq, hkv, (total,), probs, recent=recent, superblock=sb, group=grp)
+    hist = ((total - recent) // 64) * 64
+    data = make_request(cfg, hist + recent, seed=100 + case, device=dev)
+    cache = build_request_cache(cfg, data)
+    ws = ro.allocate_splitk_workspace(cache, num_query_heads=hq)
+    ex = ro.prepare_splitk_executor(cache, ws, output_hadamard=hadamard)
+    out = ex(data.query.contiguous())
+    torch.cuda.synchronize()
+    oc = _oracle_for(data, cfg)
+    q = bf16_bits_to_f32(_bf16_np(data.query))
+    want = output_transform(mixed_reference(q, oc), hadamard)
+    _compare(out, want, f"case {case} hadamard {hadamard}")
+
+
+def test_fused_append_then_flush_matches_oracle():
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.cache import append_token
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    cfg = DecodeConfig("t", 16, 2, (1), (0.2, 0.5, 0.3), recent=120)
+    data = make_request(cfg, 1280 + 120, seed=7, device=dev)
+    cache = build_request_cache(cfg, data)
+    oc = _oracle_for(data, cfg)
+    ws = ro.allocate_splitk_workspace(cache, num_query_heads=16, reserve_tokens=260)
+    ex = ro.prepare_splitk_executor(cache, ws)
+    gen = torch.Generator(device=dev).manual_seed(8)
+    stats = ro.DynamicCacheStats()
+    hist = int(data.key.shape[1]) + 120
+    for step in range(20):
+        q = torch.randn(1, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn(1, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+        pos = hist + step
+        rec = cache.recent_fp_pool
+        if rec.active_length < rec.capacity:
+            out = ex(q, append=(k, v, pos, pos))
+            rec.active_length += 1  # the caller advances the host length after a fused append
+            kf, vf = bf16_bits_to_f32(_bf16_np(k[0])), bf16_bits_to_f32(_bf16_np(v[0]))
+            want = mixed_reference(bf16_bits_to_f32(_bf16_np(q)), oc, append=(kf, vf))
+            append_token(oc, kf, vf, global_index=pos, logical_position=pos)
+        else:
+            assert ro.append_generated_token(cache, k, v, global_token_index=pos, logical_position=pos, stats=stats)
+            ex = ro.prepare_splitk_executor(cache, ws)
+            kf, vf = bf16_bits_to_f32(_bf16_np(k[0])), bf16_bits_to_f32(_bf16_np(v[0]))
+            append_token(oc, kf, vf, global_index=pos, logical_position=pos)
+            out = ex(q)
+            want = mixed_reference(bf16_bits_to_f32(_bf16_np(q)), oc)
+        torch.cuda.synchronize()
+        _compare(out, output_transform(want, False), f"step {step}")
+    assert stats.flushed_tokens == 128
+    # the ring, lengths and arenas agree with the oracle after the flush
+    assert cache.recent_fp_pool.active_length == oc.recent_active
+    assert int(cache.recent_fp_pool.length_device.item()) == oc.recent_active
+    ck = cache.compact_key
+    np.testing.assert_array_equal(ck.packed[:, : ck.active_length].cpu().numpy(), oc.k_packed[:, : oc.k_active])
+
+
+def test_ragged_batch_matches_per_request_oracle():
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    cfg = DecodeConfig("t", 28, 4, (0,), (0.15, 0.45, 0.4), recent=128)
+    totals = (512 + 128, 1024 + 128, 2048 + 128, 3072 + 128)
+    datas = [make_request(cfg, t, seed=200 + i, device=dev) for i, t in enumerate(totals)]
+    caches = [build_request_cache(cfg, d) for d in datas]
+    wss = [ro.allocate_splitk_workspace(c, num_query_heads=28) for c in caches]
+    exs = [ro.prepare_splitk_executor(c, w, output_hadamard=True) for c, w in zip(caches, wss)]
+    batched = ro.stack_homogeneous_splitk_executors(exs)
+    q = torch.cat([d.query for d in datas]).contiguous()
+    out = batched(q)
+    torch.cuda.synchronize()
+    for r, d in enumerate(datas):
+        want = output_transform(mixed_reference(bf16_bits_to_f32(_bf16_np(d.query)), _oracle_for(d, cfg)), True)
+        _compare(out[r : r + 1], want, f"request {r}")
