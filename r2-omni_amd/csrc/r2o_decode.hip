@@ -13,8 +13,8 @@
 //   PV  O[h, d] += sum_tok P[h, tok] V[tok, d]: V rows are staged in LDS in their packed form
 //       and read back transposed per lane (8 tokens of 8 adjacent dims) so that the MFMA B
 //       operand holds consecutive tokens.  BF16 V: bf16 MFMA.  INT4 V: the per-token scale is
-//       folded into P (P' = p * s) and the codes enter as (1032 + c); the bias is removed at the
-//       end with the running sum of P'.  INT2 V: (c - z) * s is formed in f16 per element.
+//       folded into P (P' = p * s) and the signed codes enter exactly as f16 ((1032 + c) built
+//       with one and-or, minus 1032).  INT2 V: (c - z) * s is formed in f16 per element.
 // The 4 waves' states are merged in LDS and one (max, sum, acc[GQA][128]) partial is written.
 //
 // Combine pass: one 128-thread block per (request, query head) merges the partials of its
@@ -51,7 +51,6 @@ __device__ __forceinline__ int tile_token(int g, int k) { return (k < 4) ? 4 * g
 struct WaveState {
     float m;        // running max (log2 domain) of head l16
     float l;        // partial sum of p over this lane's tokens
-    float u;        // INT4-V: partial sum of P' over this lane's tokens
     r2o_f4 acc[8];  // O[4g+i][8*l16 + q] for q = 0..7
 };
 
@@ -225,7 +224,6 @@ __device__ void run_item(const r2o_decode_params& p, const r2o_work_item& it, co
         if (__any(m_new > st.m)) {
             const float alpha = (m_new > st.m) ? (st.m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m - m_new)) : 1.f;
             st.l *= alpha;
-            st.u *= alpha;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float ai = __shfl(alpha, 4 * g + i, R2O_WAVE);
@@ -256,11 +254,7 @@ __device__ void run_item(const r2o_decode_params& p, const r2o_work_item& it, co
                 pv[k] = pk[k] * sc;
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                ap[u] = r2o_pack_h2(pv[2 * u], pv[2 * u + 1]);
-                const r2o_h2 hv = __builtin_bit_cast(r2o_h2, ap[u]);
-                st.u += (float)hv.x + (float)hv.y;
-            }
+            for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_h2(pv[2 * u], pv[2 * u + 1]);
         } else {
 #pragma unroll
             for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_h2(pk[2 * u], pk[2 * u + 1]);
@@ -294,8 +288,14 @@ __device__ void run_item(const r2o_decode_params& p, const r2o_work_item& it, co
                                    (y[2] & 0x000F000Fu) | 0x64006400u, (y[3] & 0x000F000Fu) | 0x64006400u};
                 const r2o_u4 hi = {((y[0] >> 4) & 0x000F000Fu) | 0x64006400u, ((y[1] >> 4) & 0x000F000Fu) | 0x64006400u,
                                    ((y[2] >> 4) & 0x000F000Fu) | 0x64006400u, ((y[3] >> 4) & 0x000F000Fu) | 0x64006400u};
-                st.acc[2 * bb] = r2o_mfma_f16(ap, lo, st.acc[2 * bb]);
-                st.acc[2 * bb + 1] = r2o_mfma_f16(ap, hi, st.acc[2 * bb + 1]);
+                r2o_u4 lo2, hi2;
+#pragma unroll
+                for (int pr = 0; pr < 4; ++pr) {  // (1032 + c) - 1032 = c exactly in fp16
+                    lo2[pr] = r2o_h2_sub(lo[pr], 0x64086408u);
+                    hi2[pr] = r2o_h2_sub(hi[pr], 0x64086408u);
+                }
+                st.acc[2 * bb] = r2o_mfma_f16(ap, lo2, st.acc[2 * bb]);
+                st.acc[2 * bb + 1] = r2o_mfma_f16(ap, hi2, st.acc[2 * bb + 1]);
             }
         } else {
             const int groups = (int)(128 / p.int2_group);
@@ -347,7 +347,6 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     WaveState st;
     st.m = -INFINITY;
     st.l = 0.f;
-    st.u = 0.f;
 #pragma unroll
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
@@ -362,17 +361,6 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     float l_h = st.l;
     l_h += __shfl_xor(l_h, 16, R2O_WAVE);
     l_h += __shfl_xor(l_h, 32, R2O_WAVE);
-    if (it.kind == kI4) {
-        float u_h = st.u;
-        u_h += __shfl_xor(u_h, 16, R2O_WAVE);
-        u_h += __shfl_xor(u_h, 32, R2O_WAVE);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float corr = 1032.0f * __shfl(u_h, 4 * g + i, R2O_WAVE);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) st.acc[q][i] -= corr;
-        }
-    }
     __syncthreads();  // every wave is done with its staging area
     float* mrg = reinterpret_cast<float*>(smem) + wave * kMergeFloats;
     if (g == 0) {

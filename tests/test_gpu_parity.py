@@ -167,7 +167,7 @@ def test_fused_append_then_flush_matches_oracle():
     from oracle.quant import bf16_bits_to_f32
 
     dev = _cuda()
-    cfg = DecodeConfig("t", 16, 2, (1), (0.2, 0.5, 0.3), recent=120)
+    cfg = DecodeConfig("t", 16, 2, (0,), (0.2, 0.5, 0.3), recent=120)
     data = make_request(cfg, 1280 + 120, seed=7, device=dev)
     cache = build_request_cache(cfg, data)
     oc = _oracle_for(data, cfg)
@@ -189,7 +189,8 @@ def test_fused_append_then_flush_matches_oracle():
             want = mixed_reference(bf16_bits_to_f32(_bf16_np(q)), oc, append=(kf, vf))
             append_token(oc, kf, vf, global_index=pos, logical_position=pos)
         else:
-            assert ro.append_generated_token(cache, k, v, global_token_index=pos, logical_position=pos, stats=stats)
+            assert ro.append_generated_token(cache, k[0][:, None], v[0][:, None], global_token_index=pos,
+                                             logical_position=pos, stats=stats)
             ex = ro.prepare_splitk_executor(cache, ws)
             kf, vf = bf16_bits_to_f32(_bf16_np(k[0])), bf16_bits_to_f32(_bf16_np(v[0]))
             append_token(oc, kf, vf, global_index=pos, logical_position=pos)
