@@ -108,6 +108,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the decode path "
@@ -122,6 +124,15 @@ def main() -> int:
     from r2omni_amd.workloads import CONFIGS, algorithmic_bytes, build_request_cache, make_request
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
+        return 0
     cfg = CONFIGS[args.config]
     _log(f"building {args.layers} layer caches of {cfg.name} ...")
     layers = []

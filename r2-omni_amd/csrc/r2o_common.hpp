@@ -15,6 +15,16 @@ typedef float r2o_f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t r2o_u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t r2o_u2 __attribute__((ext_vector_type(2)));
 
+// ------------------------------------------------------------------- global-memory loads
+// Pointers read from device-side descriptor tables are generic; loading through them would
+// emit flat loads, which also count against lgkmcnt and so make every LDS wait drain the
+// outstanding HBM prefetches.  Cast to the global address space before dereferencing.
+#define R2O_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ T r2o_ldg(const T* p) {
+    return *(const R2O_GLOBAL T*)p;
+}
+
 // ------------------------------------------------------------------ element conversions
 __device__ __forceinline__ float r2o_bf16_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);

@@ -54,10 +54,369 @@ struct WaveState {
     r2o_f4 acc[8];  // O[4g+i][8*l16 + q] for q = 0..7
 };
 
+// Query operand of head l16 of the KV group (padded heads are zero), channels 32g .. 32g+31:
+// f16 pairs (channel 8j+u, 8j+u+4) scaled by D^-1/2 log2(e) for the INT4-K MFMA, or bf16
+// pairs in channel order for the Recent-FP bf16 MFMA.
+template <bool BF16_ORDER>
+__device__ __forceinline__ void load_query(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa, int l16,
+                                           int g, float qscale, uint32_t (&qp)[4][4]) {
+    const bool head_ok = l16 < gqa;
+    const uint16_t* qrow = p.query + ((b * p.hq) + kvh * gqa + (head_ok ? l16 : 0)) * 128 + 32 * g;
+    const r2o_u4* q4 = reinterpret_cast<const r2o_u4*>(qrow);
+    r2o_u4 raw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) raw[j] = head_ok ? r2o_ldg(q4 + j) : r2o_u4{0, 0, 0, 0};
+    float qf[32];
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const uint32_t v = raw[w / 4][w % 4];
+        qf[2 * w] = p.q_dtype == 0 ? r2o_bf16_to_f32(v & 0xffffu) : r2o_f16_to_f32(v & 0xffffu);
+        qf[2 * w + 1] = p.q_dtype == 0 ? r2o_bf16_to_f32(v >> 16) : r2o_f16_to_f32(v >> 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            qp[j][u] = BF16_ORDER ? r2o_pack_bf2(qf[8 * j + 2 * u], qf[8 * j + 2 * u + 1])
+                                  : r2o_pack_h2(qf[8 * j + u] * qscale, qf[8 * j + u + 4] * qscale);
+}
+
+// Max / sum over the 4 lanes l16 + 16g (g = 0..3) that hold one head, with VALU lane swaps.
+__device__ __forceinline__ float head_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+
+// Online-softmax update for one tile: sv are the lane's 8 logits (log2 domain, -inf = masked).
+// Returns the probabilities in pk and rescales the running state (and `extra`, a 4-row
+// accumulator in the PV output layout) when the max grows.
+__device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8], float (&pk)[8], int g,
+                                             r2o_f4* extra = nullptr) {
+    float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+    tmax = head_max(tmax);
+    const float m_new = fmaxf(st.m, tmax);
+    if (__any(m_new > st.m)) {
+        // exp2(-inf) = 0 when the state was empty; a head with no valid token keeps alpha = 1
+        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
+        st.l *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * g + i, R2O_WAVE);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) st.acc[q][i] *= ai;
+            if (extra) (*extra)[i] *= ai;
+        }
+        st.m = m_new;
+    }
+    const float m_use = st.m == -INFINITY ? 0.f : st.m;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        pk[k] = __builtin_amdgcn_exp2f(sv[k] - m_use);  // exp2(-inf) = 0 for masked tokens
+        st.l += pk[k];
+    }
+}
+
+// PV for bf16 V rows held as R[k] = 8 dims (8*l16 ..) of token tile_token(g, k).
+__device__ __forceinline__ void pv_bf16(WaveState& st, const r2o_u4& ap, const r2o_u4 (&R)[8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const uint32_t sel = (q & 1) ? 0x07060302u : 0x05040100u;
+        const r2o_u4 bop = {r2o_perm(R[1][q >> 1], R[0][q >> 1], sel), r2o_perm(R[3][q >> 1], R[2][q >> 1], sel),
+                            r2o_perm(R[5][q >> 1], R[4][q >> 1], sel), r2o_perm(R[7][q >> 1], R[6][q >> 1], sel)};
+        st.acc[q] = r2o_mfma_bf16(ap, bop, st.acc[q]);
+    }
+}
+
+// Constants kept in VGPRs so that (x & mask) | magic selects one v_and_or_b32 (gfx9 VOP3 can
+// take at most one literal/SGPR operand).
+struct VConst {
+    uint32_t nib;    // 0x000F000F
+    uint32_t crumb;  // 0x00030003
+    uint32_t magic;  // 0x64006400 = fp16 (1024, 1024)
+};
+
+__device__ __forceinline__ VConst make_vconst() {
+    VConst c;
+    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(c.nib));
+    asm volatile("v_mov_b32 %0, 0x00030003" : "=v"(c.crumb));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.magic));
+    return c;
+}
+
+// ------------------------------------------------------------------ pool segment tiles
+// LDS stage of one wave (one tile): V rows in natural row order (bf16 256 B, INT4 64 B, INT2
+// 32 B per row), filled by global->LDS copies of 16 B per lane.  K codes, K superblock metadata
+// and the per-token V metadata of the lane's 8 tokens are prefetched into registers.
+struct TileRegs {
+    r2o_u4 kx[2];     // INT4-K codes of tokens a0 + 16 mg + l16, channels 32g .. 32g+31
+    r2o_u4 ks[4];     // fp16 K scales of the tile's superblock, channels 32g .. 32g+31
+    r2o_u4 kz[2];     // u8 K zero points, same channels
+    uint32_t vm[8];   // INT4-V: f32 scale bits of tokens tile_token(g, k); INT2-V: fp16 scale bits
+    uint32_t vz[8];   // INT2-V: u8 zero point of tokens tile_token(g, k)
+};
+
+__device__ __forceinline__ void lds_copy16(const void* gsrc, unsigned char* lds_base, int offset) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
+                                     (__attribute__((address_space(3))) void*)(lds_base + offset), 16, 0, 0);
+}
+
+// Per-item, per-lane addressing of one pool segment (32-bit positions; one head's arena).
+struct SegCtx {
+    const uint8_t* kcode;    // k_packed of this head + l16*64 + 16g   (+ a0*64 + mg*1024)
+    const uint16_t* kscale;  // k_scale of this head + 32g              (+ sb*128)
+    const uint8_t* kzero;
+    const uint8_t* vrows;    // V rows of this head (byte pointer)
+    const void* vmeta;       // INT4: f32 scales of this head; INT2: fp16 scales
+    const uint8_t* vzero;    // INT2: u8 zero points
+    int lo, hi, vdelta;      // valid arena positions, V row = arena - vdelta
+    int sb_shift, groups, gamma;
+};
+
 template <int KIND>
-__device__ void run_item(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
-                         unsigned char* smem, WaveState& st) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+__device__ __forceinline__ void issue_seg_tile(const SegCtx& c, int a0, int lane, int g, unsigned char* stage,
+                                               TileRegs& tr) {
+    constexpr int kRow = KIND == kFP ? 256 : (KIND == kI4 ? 64 : 32);
+    tr.kx[0] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64));
+    tr.kx[1] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64 + 1024));
+    const int meta = (a0 >> c.sb_shift) * 128;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) tr.ks[w] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kscale + meta) + w);
+#pragma unroll
+    for (int w = 0; w < 2; ++w) tr.kz[w] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kzero + meta) + w);
+    const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
+    const int row0 = a0 - c.vdelta;
+    // V rows; rows outside [lo, hi) read a clamped valid row (finite data, probability 0)
+    auto vrow = [&](int r) -> int {
+        if (full) return row0 + r;
+        const int pos = min(max(a0 + r, c.lo), c.hi - 1);
+        return pos - c.vdelta;
+    };
+    constexpr int kChunks = 32 * kRow / 1024;  // 16-byte chunks per lane per tile
+#pragma unroll
+    for (int itn = 0; itn < kChunks; ++itn) {
+        const int ch = itn * 64 + lane;               // chunk ch covers row ch*16/kRow
+        const int r = ch * 16 / kRow, col = ch * 16 % kRow;
+        lds_copy16(c.vrows + vrow(r) * kRow + col, stage, itn * 1024);
+    }
+    if (KIND == kI4) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            tr.vm[k] = r2o_ldg(reinterpret_cast<const uint32_t*>(c.vmeta) + vrow(tile_token(g, k)));
+    } else if (KIND == kI2) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int m = vrow(tile_token(g, k)) * c.groups + c.gamma;
+            tr.vm[k] = r2o_ldg(reinterpret_cast<const uint16_t*>(c.vmeta) + m);
+            tr.vz[k] = r2o_ldg(c.vzero + m);
+        }
+    }
+}
+
+template <int KIND>
+struct SegState {
+    uint32_t qp[4][4];   // q (scaled), f16 pairs in the K-unpack channel order
+    uint32_t qs[4][4];   // Q' = q * s of the current superblock
+    r2o_f4 negcorr;      // -sum_c Q'(1024 + z_c), identical in all rows
+    int cur_sb;
+    r2o_f4 bias;         // INT4-V: sum_k P'_k * 1032 per head row (removed at the end)
+};
+
+template <int KIND>
+__device__ __forceinline__ void seg_step(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
+                                         int a0, bool has_next, int lane, int l16, int g, bool head_ok,
+                                         unsigned char* stage, const TileRegs& cur, TileRegs& nxt) {
+    __builtin_amdgcn_s_waitcnt(0);  // tile a0: registers and LDS copies complete
+    __builtin_amdgcn_wave_barrier();
+    // ---- transposed V reads: 8 tokens x 8 dims (8*l16 ..) per lane
+    r2o_u4 R[8];
+    uint32_t X[8], Y[8];
+    if (KIND == kFP) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) R[k] = *reinterpret_cast<const r2o_u4*>(stage + tile_token(g, k) * 256 + 16 * l16);
+    } else if (KIND == kI4) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) X[k] = *reinterpret_cast<const uint32_t*>(stage + tile_token(g, k) * 64 + 4 * l16);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) Y[k] = *reinterpret_cast<const uint16_t*>(stage + tile_token(g, k) * 32 + 2 * l16);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage reads done before it is refilled
+    __builtin_amdgcn_wave_barrier();
+    if (has_next) issue_seg_tile<KIND>(c, a0 + 32, lane, g, stage, nxt);
+
+    // ---- QK^T: Q' and -sum Q'(1024 + z) for the tile's superblock
+    const int sb = a0 >> c.sb_shift;
+    if (sb != ss.cur_sb) {
+        ss.cur_sb = sb;
+        uint32_t sd[16], zd[8];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            sd[4 * w] = cur.ks[w].x; sd[4 * w + 1] = cur.ks[w].y; sd[4 * w + 2] = cur.ks[w].z; sd[4 * w + 3] = cur.ks[w].w;
+        }
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            zd[4 * w] = cur.kz[w].x; zd[4 * w + 1] = cur.kz[w].y; zd[4 * w + 2] = cur.kz[w].z; zd[4 * w + 3] = cur.kz[w].w;
+        }
+        ss.negcorr = r2o_f4{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r2o_u4 zop;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t sp = r2o_perm(sd[4 * j + 2 + u / 2], sd[4 * j + u / 2], (u & 1) ? 0x07060302u : 0x05040100u);
+                ss.qs[j][u] = r2o_h2_mul(ss.qp[j][u], sp);
+                const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + u) << 16) | (uint32_t)u;
+                zop[u] = r2o_perm(zd[2 * j + 1], zd[2 * j], sel) | 0xE400E400u;  // -(1024 + z)
+            }
+            ss.negcorr = r2o_mfma_f16(zop, r2o_u4{ss.qs[j][0], ss.qs[j][1], ss.qs[j][2], ss.qs[j][3]}, ss.negcorr);
+        }
+    }
+    r2o_f4 s[2];
+#pragma unroll
+    for (int mg = 0; mg < 2; ++mg) {
+        r2o_f4 acc = ss.negcorr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w = cur.kx[mg][j];
+            const r2o_u4 a = {(w & vc.nib) | vc.magic, ((w >> 4) & vc.nib) | vc.magic, ((w >> 8) & vc.nib) | vc.magic,
+                              ((w >> 12) & vc.nib) | vc.magic};
+            acc = r2o_mfma_f16(a, r2o_u4{ss.qs[j][0], ss.qs[j][1], ss.qs[j][2], ss.qs[j][3]}, acc);
+        }
+        s[mg] = acc;
+    }
+
+    // ---- softmax (masks only on partial tiles and padded heads)
+    const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);
+    float sv[8], pk[8];
+    if (full) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sv[k] = head_ok ? s[k >> 2][k & 3] : -INFINITY;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int pos = a0 + tile_token(g, k);
+            const bool ok = head_ok & (pos >= c.lo) & (pos < c.hi);
+            sv[k] = ok ? s[k >> 2][k & 3] : -INFINITY;
+        }
+    }
+    softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
+
+    // ---- PV
+    r2o_u4 ap;
+    if (KIND == kFP) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
+        pv_bf16(st, ap, R);
+    } else if (KIND == kI4) {
+        // P' = p * s_t; codes enter as (1032 + c) and sum_k P'_k * 1032 is accumulated by one
+        // more MFMA on the same A operand (so both see identical f16 inputs).
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            ap[u] = r2o_pack_h2(pk[2 * u] * __uint_as_float(cur.vm[2 * u]), pk[2 * u + 1] * __uint_as_float(cur.vm[2 * u + 1]));
+        ss.bias = r2o_mfma_f16(ap, r2o_u4{0x64086408u, 0x64086408u, 0x64086408u, 0x64086408u}, ss.bias);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) X[k] ^= 0x88888888u;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + bb) << 16) | (uint32_t)bb;
+            r2o_u4 lo, hi;
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) {
+                const uint32_t y = r2o_perm(X[2 * pr + 1], X[2 * pr], sel);
+                lo[pr] = (y & vc.nib) | vc.magic;
+                hi[pr] = ((y >> 4) & vc.nib) | vc.magic;
+            }
+            st.acc[2 * bb] = r2o_mfma_f16(ap, lo, st.acc[2 * bb]);
+            st.acc[2 * bb + 1] = r2o_mfma_f16(ap, hi, st.acc[2 * bb + 1]);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_h2(pk[2 * u], pk[2 * u + 1]);
+        uint32_t yp[4], zp[4], sp[4];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+            yp[pr] = Y[2 * pr] | (Y[2 * pr + 1] << 16);
+            zp[pr] = (cur.vz[2 * pr] | (cur.vz[2 * pr + 1] << 16)) | vc.magic;
+            sp[pr] = cur.vm[2 * pr] | (cur.vm[2 * pr + 1] << 16);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int shift = (q < 4) ? 2 * q : 8 + 2 * (q - 4);
+            r2o_u4 bop;
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) {
+                const uint32_t cc = ((yp[pr] >> shift) & vc.crumb) | vc.magic;
+                bop[pr] = r2o_h2_mul(r2o_h2_sub(cc, zp[pr]), sp[pr]);
+            }
+            st.acc[q] = r2o_mfma_f16(ap, bop, st.acc[q]);
+        }
+    }
+}
+
+template <int KIND>
+__device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
+                            unsigned char* smem, WaveState& st) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+    const int gqa = (int)(p.hq / p.hkv);
+    const int64_t kvh = it.kvh, b = it.req;
+    const int per = (int)((it.ntiles + kWaves - 1) / kWaves);
+    const int t_begin = wave * per;
+    const int t_end = min((int)it.ntiles, t_begin + per);
+    if (t_begin >= t_end) return;
+    unsigned char* stage = smem + wave * kStageBytes;
+    const bool head_ok = l16 < gqa;
+
+    SegCtx c;
+    c.kcode = rq.k_packed + (kvh * rq.k_capacity + l16) * 64 + 16 * g;
+    c.kscale = rq.k_scale + kvh * rq.k_superblocks * 128 + 32 * g;
+    c.kzero = rq.k_zero + kvh * rq.k_superblocks * 128 + 32 * g;
+    c.lo = (int)it.lo;
+    c.hi = (int)it.hi;
+    c.vdelta = (int)it.v_delta;
+    c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
+    c.groups = (int)(128 / p.int2_group);
+    c.gamma = (8 * l16) / (int)p.int2_group;
+    if (KIND == kFP) {
+        c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128);
+    } else if (KIND == kI4) {
+        c.vrows = rq.i4_v + kvh * rq.i4_stride * 64;
+        c.vmeta = rq.i4_scale + kvh * rq.i4_stride;
+    } else {
+        c.vrows = rq.i2_v + kvh * rq.i2_stride * 32;
+        c.vmeta = rq.i2_scale + kvh * rq.i2_stride * c.groups;
+        c.vzero = rq.i2_zero + kvh * rq.i2_stride * c.groups;
+    }
+    const VConst vc = make_vconst();
+    SegState<KIND> ss;
+    load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
+    ss.cur_sb = -1;
+    ss.negcorr = r2o_f4{0, 0, 0, 0};
+    ss.bias = r2o_f4{0, 0, 0, 0};
+
+    TileRegs ra, rb;
+    const int base = (int)it.tile0;
+    issue_seg_tile<KIND>(c, base + 32 * t_begin, lane, g, stage, ra);
+    for (int t = t_begin; t < t_end; t += 2) {
+        seg_step<KIND>(c, st, ss, vc, base + 32 * t, t + 1 < t_end, lane, l16, g, head_ok, stage, ra, rb);
+        if (t + 1 >= t_end) break;
+        seg_step<KIND>(c, st, ss, vc, base + 32 * (t + 1), t + 2 < t_end, lane, l16, g, head_ok, stage, rb, ra);
+    }
+    if (KIND == kI4) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st.acc[q] -= ss.bias;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
+// Recent-FP ring tiles (bf16 K and V, plus the fused-append token): at most a few tiles per
+// item, loaded synchronously.
+__device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
+                           unsigned char* smem, WaveState& st) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
     const int64_t kvh = it.kvh, b = it.req;
     const int per = (int)((it.ntiles + kWaves - 1) / kWaves);
@@ -65,274 +424,49 @@ __device__ void run_item(const r2o_decode_params& p, const r2o_work_item& it, co
     const int t_end = min((int)it.ntiles, t_begin + per);
     unsigned char* stage = smem + wave * kStageBytes;
     const float qscale = p.sm_scale * kLog2e;
-
-    // ---- query operand (head l16 of the KV group; padded heads are zero)
     const bool head_ok = l16 < gqa;
-    const uint16_t* qrow = p.query + ((b * p.hq) + kvh * gqa + (head_ok ? l16 : 0)) * 128 + 32 * g;
-    uint32_t qp[4][4];  // f16 pairs (channel 8j+u, 8j+u+4) of 32g.. (INT4-K path) or bf16 pairs (recent)
-    {
-        const r2o_u4* q4 = reinterpret_cast<const r2o_u4*>(qrow);
-        r2o_u4 raw[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) raw[j] = head_ok ? q4[j] : r2o_u4{0, 0, 0, 0};
-        float qf[32];
-#pragma unroll
-        for (int w = 0; w < 16; ++w) {
-            const uint32_t v = raw[w / 4][w % 4];
-            qf[2 * w] = p.q_dtype == 0 ? r2o_bf16_to_f32(v & 0xffffu) : r2o_f16_to_f32(v & 0xffffu);
-            qf[2 * w + 1] = p.q_dtype == 0 ? r2o_bf16_to_f32(v >> 16) : r2o_f16_to_f32(v >> 16);
-        }
-        if (KIND == kRecent) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int u = 0; u < 4; ++u) qp[j][u] = r2o_pack_bf2(qf[8 * j + 2 * u], qf[8 * j + 2 * u + 1]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    qp[j][u] = r2o_pack_h2(qf[8 * j + u] * qscale, qf[8 * j + u + 4] * qscale);
-        }
-    }
-
-    uint32_t qs[4][4];            // Q' = q * s for the current K superblock (f16 pairs)
-    r2o_f4 negcorr = {0, 0, 0, 0};
-    int64_t cur_sb = -1;
-    const int recent_len = (KIND == kRecent) ? p.recent_len[b] : 0;
-    const bool app = (KIND == kRecent) && p.do_append;
-
+    uint32_t qp[4][4];
+    load_query<true>(p, b, kvh, gqa, l16, g, qscale, qp);
+    const int recent_len = p.recent_len[b];
+    const bool app = p.do_append != 0;
+    const int valid_end = recent_len + (app ? 1 : 0);
     for (int t = t_begin; t < t_end; ++t) {
-        const int64_t a0 = it.tile0 + 32 * (int64_t)t;
-        // ------------------------------------------------------------ QK^T for 32 tokens
+        const int a0 = (int)it.tile0 + 32 * t;
         r2o_f4 s[2];
-        if (KIND != kRecent) {
-            const int64_t sb = a0 / p.superblock;
-            if (sb != cur_sb) {
-                cur_sb = sb;
-                const int64_t meta = (kvh * rq.k_superblocks + sb) * 128 + 32 * g;
-                const r2o_u4* s4 = reinterpret_cast<const r2o_u4*>(rq.k_scale + meta);
-                const r2o_u4* z4 = reinterpret_cast<const r2o_u4*>(rq.k_zero + meta);
-                uint32_t sd[16], zd[8];
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const r2o_u4 v = s4[w];
-                    sd[4 * w] = v.x; sd[4 * w + 1] = v.y; sd[4 * w + 2] = v.z; sd[4 * w + 3] = v.w;
-                }
+        for (int mg = 0; mg < 2; ++mg) {
+            const int slot = a0 + 16 * mg + l16;
+            const uint16_t* krow = nullptr;
+            if (slot < recent_len) krow = rq.recent_k + (kvh * rq.recent_capacity + slot) * 128;
+            else if (app && slot == recent_len) krow = p.append_k + (b * p.hkv + kvh) * 128;
+            r2o_f4 acc = {0, 0, 0, 0};
 #pragma unroll
-                for (int w = 0; w < 2; ++w) {
-                    const r2o_u4 v = z4[w];
-                    zd[4 * w] = v.x; zd[4 * w + 1] = v.y; zd[4 * w + 2] = v.z; zd[4 * w + 3] = v.w;
-                }
-                negcorr = r2o_f4{0, 0, 0, 0};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    r2o_u4 zop;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const uint32_t sp = r2o_perm(sd[4 * j + 2 + u / 2], sd[4 * j + u / 2],
-                                                     (u & 1) ? 0x07060302u : 0x05040100u);
-                        qs[j][u] = r2o_h2_mul(qp[j][u], sp);
-                        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + u) << 16) | (uint32_t)u;
-                        zop[u] = r2o_perm(zd[2 * j + 1], zd[2 * j], sel) | 0xE400E400u;  // -(1024 + z)
-                    }
-                    negcorr = r2o_mfma_f16(zop, r2o_u4{qs[j][0], qs[j][1], qs[j][2], qs[j][3]}, negcorr);
-                }
+            for (int j = 0; j < 4; ++j) {
+                const r2o_u4 a = krow ? r2o_ldg(reinterpret_cast<const r2o_u4*>(krow + 32 * g) + j) : r2o_u4{0, 0, 0, 0};
+                acc = r2o_mfma_bf16(a, r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
             }
-#pragma unroll
-            for (int mg = 0; mg < 2; ++mg) {
-                const int64_t tok = a0 + 16 * mg + l16;
-                const r2o_u4 kx = *reinterpret_cast<const r2o_u4*>(rq.k_packed + (kvh * rq.k_capacity + tok) * 64 + 16 * g);
-                r2o_f4 acc = negcorr;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t w = kx[j];
-                    const r2o_u4 a = {(w & 0x000F000Fu) | 0x64006400u, ((w >> 4) & 0x000F000Fu) | 0x64006400u,
-                                      ((w >> 8) & 0x000F000Fu) | 0x64006400u, ((w >> 12) & 0x000F000Fu) | 0x64006400u};
-                    acc = r2o_mfma_f16(a, r2o_u4{qs[j][0], qs[j][1], qs[j][2], qs[j][3]}, acc);
-                }
-                s[mg] = acc;
-            }
-        } else {
-#pragma unroll
-            for (int mg = 0; mg < 2; ++mg) {
-                const int slot = (int)a0 + 16 * mg + l16;
-                const uint16_t* krow = nullptr;
-                if (slot < recent_len) krow = rq.recent_k + (kvh * rq.recent_capacity + slot) * 128;
-                else if (app && slot == recent_len) krow = p.append_k + (b * p.hkv + kvh) * 128;
-                r2o_f4 acc = {0, 0, 0, 0};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const r2o_u4 a = krow ? reinterpret_cast<const r2o_u4*>(krow + 32 * g)[j] : r2o_u4{0, 0, 0, 0};
-                    acc = r2o_mfma_bf16(a, r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
-                }
-                s[mg] = acc * qscale;
-            }
+            s[mg] = acc * qscale;
         }
-
-        // ------------------------------------------------------------ V tile -> LDS
-        const int64_t vbase = a0 - it.v_delta;  // V row of tile row 0 (segment kinds)
-        auto row_valid = [&](int r) -> bool {
-            if (KIND == kRecent) return (int)a0 + r < recent_len + (app ? 1 : 0);
-            const int64_t pos = a0 + r;
-            return pos >= it.lo && pos < it.hi;
-        };
-        if (KIND == kFP || KIND == kRecent) {
 #pragma unroll
-            for (int itn = 0; itn < 8; ++itn) {
-                const int c = itn * 64 + lane, r = c >> 4, col = c & 15;
-                r2o_u4 v = {0, 0, 0, 0};
-                if (row_valid(r)) {
-                    const uint16_t* vrow;
-                    if (KIND == kFP) vrow = rq.fp_v + (kvh * rq.fp_stride + vbase + r) * 128;
-                    else if ((int)a0 + r < recent_len) vrow = rq.recent_v + (kvh * rq.recent_capacity + a0 + r) * 128;
-                    else vrow = p.append_v + (b * p.hkv + kvh) * 128;
-                    v = reinterpret_cast<const r2o_u4*>(vrow)[col];
-                }
-                *reinterpret_cast<r2o_u4*>(stage + r * 256 + col * 16) = v;
-            }
-        } else if (KIND == kI4) {
-#pragma unroll
-            for (int itn = 0; itn < 2; ++itn) {
-                const int c = itn * 64 + lane, r = c >> 2, col = c & 3;
-                r2o_u4 v = {0, 0, 0, 0};
-                if (row_valid(r)) v = reinterpret_cast<const r2o_u4*>(rq.i4_v + (kvh * rq.i4_stride + vbase + r) * 64)[col];
-                *reinterpret_cast<r2o_u4*>(stage + r * kRowI4 + col * 16) = v;
-            }
-        } else {
-            const int r = lane >> 1, col = lane & 1;
+        for (int itn = 0; itn < 8; ++itn) {
+            const int c = itn * 64 + lane, r = c >> 4, col = c & 15;
             r2o_u4 v = {0, 0, 0, 0};
-            if (row_valid(r)) v = reinterpret_cast<const r2o_u4*>(rq.i2_v + (kvh * rq.i2_stride + vbase + r) * 32)[col];
-            *reinterpret_cast<r2o_u4*>(stage + r * kRowI2 + col * 16) = v;
+            if (a0 + r < recent_len) v = r2o_ldg(reinterpret_cast<const r2o_u4*>(rq.recent_v + (kvh * rq.recent_capacity + a0 + r) * 128) + col);
+            else if (a0 + r < valid_end) v = r2o_ldg(reinterpret_cast<const r2o_u4*>(p.append_v + (b * p.hkv + kvh) * 128) + col);
+            *reinterpret_cast<r2o_u4*>(stage + r * 256 + col * 16) = v;
         }
-
-        // ------------------------------------------------------------ online softmax
-        float sv[8];
-        bool vk[8];
+        float sv[8], pk[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int r = tile_token(g, k);
-            vk[k] = row_valid(r) && head_ok;
-            sv[k] = vk[k] ? s[k >> 2][k & 3] : -INFINITY;
-        }
-        float tmax = sv[0];
-#pragma unroll
-        for (int k = 1; k < 8; ++k) tmax = fmaxf(tmax, sv[k]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, R2O_WAVE));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, R2O_WAVE));
-        const float m_new = fmaxf(st.m, tmax);
-        if (__any(m_new > st.m)) {
-            const float alpha = (m_new > st.m) ? (st.m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m - m_new)) : 1.f;
-            st.l *= alpha;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float ai = __shfl(alpha, 4 * g + i, R2O_WAVE);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) st.acc[q][i] *= ai;
-            }
-            st.m = m_new;
-        }
-        const float m_use = st.m == -INFINITY ? 0.f : st.m;
-        float pk[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            pk[k] = vk[k] ? __builtin_amdgcn_exp2f(sv[k] - m_use) : 0.f;
-            st.l += pk[k];
-        }
-
-        // ------------------------------------------------------------ P operand
+        for (int k = 0; k < 8; ++k) sv[k] = ((a0 + tile_token(g, k) < valid_end) & head_ok) ? s[k >> 2][k & 3] : -INFINITY;
+        softmax_tile(st, sv, pk, g);
         r2o_u4 ap;
-        if (KIND == kFP || KIND == kRecent) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
-        } else if (KIND == kI4) {
-            float pv[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int r = tile_token(g, k);
-                const float sc = row_valid(r) ? rq.i4_scale[kvh * rq.i4_stride + vbase + r] : 0.f;
-                pv[k] = pk[k] * sc;
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_h2(pv[2 * u], pv[2 * u + 1]);
-        } else {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_h2(pk[2 * u], pk[2 * u + 1]);
-        }
-
-        // ------------------------------------------------------------ PV from LDS
+        for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
         wave_lds_fence();
-        if (KIND == kFP || KIND == kRecent) {
-            r2o_u4 R[8];
+        r2o_u4 R[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) R[k] = *reinterpret_cast<const r2o_u4*>(stage + tile_token(g, k) * 256 + 16 * l16);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const uint32_t sel = (q & 1) ? 0x07060302u : 0x05040100u;
-                const r2o_u4 bop = {r2o_perm(R[1][q >> 1], R[0][q >> 1], sel), r2o_perm(R[3][q >> 1], R[2][q >> 1], sel),
-                                    r2o_perm(R[5][q >> 1], R[4][q >> 1], sel), r2o_perm(R[7][q >> 1], R[6][q >> 1], sel)};
-                st.acc[q] = r2o_mfma_bf16(ap, bop, st.acc[q]);
-            }
-        } else if (KIND == kI4) {
-            uint32_t X[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                X[k] = *reinterpret_cast<const uint32_t*>(stage + tile_token(g, k) * kRowI4 + 4 * l16) ^ 0x88888888u;
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-                const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + bb) << 16) | (uint32_t)bb;
-                uint32_t y[4];
-#pragma unroll
-                for (int pr = 0; pr < 4; ++pr) y[pr] = r2o_perm(X[2 * pr + 1], X[2 * pr], sel);
-                const r2o_u4 lo = {(y[0] & 0x000F000Fu) | 0x64006400u, (y[1] & 0x000F000Fu) | 0x64006400u,
-                                   (y[2] & 0x000F000Fu) | 0x64006400u, (y[3] & 0x000F000Fu) | 0x64006400u};
-                const r2o_u4 hi = {((y[0] >> 4) & 0x000F000Fu) | 0x64006400u, ((y[1] >> 4) & 0x000F000Fu) | 0x64006400u,
-                                   ((y[2] >> 4) & 0x000F000Fu) | 0x64006400u, ((y[3] >> 4) & 0x000F000Fu) | 0x64006400u};
-                r2o_u4 lo2, hi2;
-#pragma unroll
-                for (int pr = 0; pr < 4; ++pr) {  // (1032 + c) - 1032 = c exactly in fp16
-                    lo2[pr] = r2o_h2_sub(lo[pr], 0x64086408u);
-                    hi2[pr] = r2o_h2_sub(hi[pr], 0x64086408u);
-                }
-                st.acc[2 * bb] = r2o_mfma_f16(ap, lo2, st.acc[2 * bb]);
-                st.acc[2 * bb + 1] = r2o_mfma_f16(ap, hi2, st.acc[2 * bb + 1]);
-            }
-        } else {
-            const int groups = (int)(128 / p.int2_group);
-            const int gamma = (8 * l16) / (int)p.int2_group;
-            uint32_t Y[8], zh[8], sh[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int r = tile_token(g, k);
-                Y[k] = *reinterpret_cast<const uint16_t*>(stage + r * kRowI2 + 2 * l16);
-                if (row_valid(r)) {
-                    const int64_t mrow = (kvh * rq.i2_stride + vbase + r) * groups + gamma;
-                    zh[k] = 0x6400u | rq.i2_zero[mrow];
-                    sh[k] = rq.i2_scale[mrow];
-                } else {
-                    zh[k] = 0x6400u;
-                    sh[k] = 0u;
-                }
-            }
-            uint32_t yp[4], zp[4], sp[4];
-#pragma unroll
-            for (int pr = 0; pr < 4; ++pr) {
-                yp[pr] = Y[2 * pr] | (Y[2 * pr + 1] << 16);
-                zp[pr] = zh[2 * pr] | (zh[2 * pr + 1] << 16);
-                sp[pr] = sh[2 * pr] | (sh[2 * pr + 1] << 16);
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int shift = (q < 4) ? 2 * q : 8 + 2 * (q - 4);
-                r2o_u4 bop;
-#pragma unroll
-                for (int pr = 0; pr < 4; ++pr) {
-                    const uint32_t c = ((yp[pr] >> shift) & 0x00030003u) | 0x64006400u;
-                    bop[pr] = r2o_h2_mul(r2o_h2_sub(c, zp[pr]), sp[pr]);
-                }
-                st.acc[q] = r2o_mfma_f16(ap, bop, st.acc[q]);
-            }
-        }
+        for (int k = 0; k < 8; ++k) R[k] = *reinterpret_cast<const r2o_u4*>(stage + tile_token(g, k) * 256 + 16 * l16);
+        pv_bf16(st, ap, R);
         wave_lds_fence();
     }
 }
@@ -341,7 +475,8 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     __shared__ __align__(16) unsigned char smem[kSmemBytes];
     const r2o_work_item it = p.items[blockIdx.x];
     const r2o_request_desc rq = p.reqs[it.req];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
 
     WaveState st;
@@ -351,10 +486,10 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_item<kFP>(p, it, rq, smem, st); break;
-        case kI4: run_item<kI4>(p, it, rq, smem, st); break;
-        case kI2: run_item<kI2>(p, it, rq, smem, st); break;
-        default: run_item<kRecent>(p, it, rq, smem, st); break;
+        case kFP: run_segment<kFP>(p, it, rq, smem, st); break;
+        case kI4: run_segment<kI4>(p, it, rq, smem, st); break;
+        case kI2: run_segment<kI2>(p, it, rq, smem, st); break;
+        default: run_recent(p, it, rq, smem, st); break;
     }
 
     // ---- per-wave epilogue: reduce l (and u) over the 4 lane groups of each head
@@ -399,47 +534,88 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     }
 }
 
-__global__ __launch_bounds__(128) void decode_combine_kernel(r2o_decode_params p) {
+// One 1024-thread block per (request, query head): 8 slices x 128 dims.  Slice s merges the
+// partials beg+s, beg+s+8, ... (loads of independent partials in flight together), then the
+// slices are merged through LDS.  All merges are the exact fp32 softmax-state merge.
+constexpr int kCombineSlices = 8;
+
+__global__ __launch_bounds__(1024) void decode_combine_kernel(r2o_decode_params p) {
+    __shared__ float red_m[32];
+    __shared__ float sl_l[kCombineSlices];
+    __shared__ float sl_a[kCombineSlices][128];
     __shared__ float buf[128];
     const int64_t b = blockIdx.y;
     const int hqi = blockIdx.x;
-    const int d = threadIdx.x;
+    const int tid = threadIdx.x, d = tid & 127, slice = tid >> 7;
     const int gqa = (int)(p.hq / p.hkv);
     const int kvh = hqi / gqa, h = hqi % gqa;
-    const int beg = p.group_begin[b * p.hkv + kvh], end = p.group_begin[b * p.hkv + kvh + 1];
-    float M = -INFINITY;
-    for (int i = beg; i < end; ++i) M = fmaxf(M, p.partial_max[(int64_t)i * 16 + h]);
+    const int beg = r2o_ldg(p.group_begin + b * p.hkv + kvh), end = r2o_ldg(p.group_begin + b * p.hkv + kvh + 1);
+    // ---- global max over the group's partials
+    float m = -INFINITY;
+    for (int i = beg + tid; i < end; i += 1024) m = fmaxf(m, r2o_ldg(p.partial_max + (int64_t)i * 16 + h));
+    m = r2o_wave_max(m);
+    if ((tid & 63) == 0) red_m[tid >> 6] = m;
+    __syncthreads();
+    float M = red_m[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) M = fmaxf(M, red_m[w]);
+    // ---- per-slice weighted sums
     float L = 0.f, A = 0.f;
     if (M != -INFINITY) {
-        for (int i = beg; i < end; ++i) {
-            const int64_t slot = (int64_t)i * 16 + h;
-            const float m = p.partial_max[slot];
-            const float sc = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-            L += p.partial_sum[slot] * sc;
-            A += p.partial_out[slot * 128 + d] * sc;
+        int i = beg + slice;
+        for (; i + kCombineSlices < end; i += 2 * kCombineSlices) {
+            const int64_t s0 = (int64_t)i * 16 + h, s1 = (int64_t)(i + kCombineSlices) * 16 + h;
+            const float m0 = r2o_ldg(p.partial_max + s0), m1 = r2o_ldg(p.partial_max + s1);
+            const float l0 = r2o_ldg(p.partial_sum + s0), l1 = r2o_ldg(p.partial_sum + s1);
+            const float a0 = r2o_ldg(p.partial_out + s0 * 128 + d), a1 = r2o_ldg(p.partial_out + s1 * 128 + d);
+            const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - M);
+            const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
+            L += l0 * w0 + l1 * w1;
+            A += a0 * w0 + a1 * w1;
+        }
+        if (i < end) {
+            const int64_t s0 = (int64_t)i * 16 + h;
+            const float m0 = r2o_ldg(p.partial_max + s0);
+            const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - M);
+            L += r2o_ldg(p.partial_sum + s0) * w0;
+            A += r2o_ldg(p.partial_out + s0 * 128 + d) * w0;
         }
     }
-    float y = r2o_bf16_to_f32(r2o_f32_to_bf16(A / L));
+    sl_a[slice][d] = A;
+    if (d == 0) sl_l[slice] = L;
+    __syncthreads();
+    const bool lead = tid < 128;  // the first 128 threads finish the head (all threads meet the barriers)
+    float y = 0.f;
+    if (lead) {
+        float At = 0.f, Lt = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < kCombineSlices; ++s2) {
+            At += sl_a[s2][d];
+            Lt += sl_l[s2];
+        }
+        y = r2o_bf16_to_f32(r2o_f32_to_bf16(At / Lt));
+    }
     if (p.output_hadamard) {
-        buf[d] = y;
+        if (lead) buf[d] = y;
         __syncthreads();
         for (int stride = 1; stride < 128; stride <<= 1) {
             float a = 0.f, c = 0.f;
             int i0 = 0;
-            if (d < 64) {
+            if (tid < 64) {
                 i0 = (d / stride) * 2 * stride + (d & (stride - 1));
                 a = buf[i0];
                 c = buf[i0 + stride];
             }
             __syncthreads();
-            if (d < 64) {
+            if (tid < 64) {
                 buf[i0] = a + c;
                 buf[i0 + stride] = a - c;
             }
             __syncthreads();
         }
-        y = buf[d] * 0.08838834764831845f;
+        if (lead) y = buf[d] * 0.08838834764831845f;
     }
+    if (!lead) return;
     p.out[(b * p.hq + hqi) * 128 + d] = (uint16_t)r2o_f32_to_bf16(y);
 
     if (p.do_append && hqi < p.hkv) {  // fused Recent-FP append (triton_fourq_splitk.py:1007-1020)
@@ -486,7 +662,7 @@ int r2o_decode_partial(const r2o_decode_params* params, void* stream) {
 int r2o_decode_combine(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)params->hq, (unsigned)params->batch), dim3(128), 0,
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)params->hq, (unsigned)params->batch), dim3(1024), 0,
                        (hipStream_t)stream, *params);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
