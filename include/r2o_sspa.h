@@ -43,6 +43,7 @@ typedef struct r2o_request_desc {
     const uint8_t* k_zero;        /* u8   [Hkv, k_superblocks, 128]                              */
     int64_t k_capacity;
     int64_t k_superblocks;
+    const uint32_t* k_operands;   /* u32  [Hkv, k_superblocks, 128]  QK MFMA operands (see pack) */
     const uint16_t* fp_v;         /* bf16 [Hkv, fp_stride, 128]  (FP-V pool)                     */
     int64_t fp_stride;
     const uint8_t* i4_v;          /* u8   [Hkv, i4_stride, 64]   (per-token symmetric INT4-V)   */
@@ -64,7 +65,8 @@ typedef struct r2o_request_desc {
 /* One unit of split-K work: a run of 32-token tiles of one pool segment of one (request,
  * kv head).  Tiles are aligned to 32 positions of the compact K arena so that every tile lies
  * in one K superblock; positions outside [lo, hi) are masked.  For the Recent-FP ring, arena
- * positions are ring slots.  V row = arena position - v_delta.  All fields are 8 bytes. */
+ * positions are ring slots.  V row = arena position - v_delta.  Items may be launched in any
+ * order (largest first); each writes its partial to `slot`.  All fields are 8 bytes. */
 typedef struct r2o_work_item {
     int64_t req;
     int64_t kvh;
@@ -74,12 +76,13 @@ typedef struct r2o_work_item {
     int64_t lo;        /* valid arena positions [lo, hi)                                          */
     int64_t hi;
     int64_t v_delta;
+    int64_t slot;      /* partial-state slot; slots of one (request, kv head) are contiguous     */
 } r2o_work_item;
 
 typedef struct r2o_decode_params {
     const r2o_request_desc* reqs;   /* device [batch]                                  */
-    const r2o_work_item* items;     /* device [n_items], grouped by (req, kvh)         */
-    const int32_t* group_begin;     /* device [batch*hkv + 1] item range of each group */
+    const r2o_work_item* items;     /* device [n_items] in launch order                */
+    const int32_t* group_begin;     /* device [batch*hkv + 1] slot range of each group */
     int64_t n_items;
     float* partial_max;             /* device f32 [n_items, 16]      (log2 domain)     */
     float* partial_sum;             /* device f32 [n_items, 16]                        */
@@ -119,11 +122,15 @@ int r2o_decode_combine(const r2o_decode_params* params, void* stream);
  * multiple of `superblock`.  The first `tail` positions are read back from the arena itself
  * (dequantised, rounded to `dtype`) — the flush rule of CompactInt4KeyArena.append_superblock
  * (compact_int4_key.py:210-220); the next n come from src[h, index[i]] (index NULL: i).
+ * `operands` (nullable) receives, per superblock, the QK MFMA operands derived from the
+ * stored scale/zero: for lane group g (channels 32g..32g+31), MFMA j and pair u, dword
+ * g*32 + 4j + u = fp16 (s[c], s[c+4]) and dword g*32 + 16 + 4j + u = fp16 (-(1024 + z[c]),
+ * -(1024 + z[c+4])) with c = 32g + 8j + u.
  * Replaces _gather_pack_int4_key_kernel (compact_int4_key.py:22-76) and the torch flush path. */
 int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
                     const int64_t* index, int64_t n, int64_t tail, int64_t dst_start,
-                    uint8_t* packed, uint16_t* scale, uint8_t* zero, int64_t capacity,
-                    int64_t superblocks, int64_t superblock, void* stream);
+                    uint8_t* packed, uint16_t* scale, uint8_t* zero, uint32_t* operands,
+                    int64_t capacity, int64_t superblocks, int64_t superblock, void* stream);
 
 /* Per-token symmetric INT4-V: packed[h, dst+i] / scale[h, dst+i] from src[h, index[i]].
  * Replaces _gather_pack_int4_value_kernel (fused_value_pack.py:28-70). */

@@ -146,15 +146,31 @@ __device__ __forceinline__ VConst make_vconst() {
 }
 
 // ------------------------------------------------------------------ pool segment tiles
-// LDS stage of one wave (one tile): V rows in natural row order (bf16 256 B, INT4 64 B, INT2
-// 32 B per row), filled by global->LDS copies of 16 B per lane.  K codes, K superblock metadata
-// and the per-token V metadata of the lane's 8 tokens are prefetched into registers.
-struct TileRegs {
-    r2o_u4 kx[2];     // INT4-K codes of tokens a0 + 16 mg + l16, channels 32g .. 32g+31
-    r2o_u4 ks[4];     // fp16 K scales of the tile's superblock, channels 32g .. 32g+31
-    r2o_u4 kz[2];     // u8 K zero points, same channels
-    uint32_t vm[8];   // INT4-V: f32 scale bits of tokens tile_token(g, k); INT2-V: fp16 scale bits
-    uint32_t vz[8];   // INT2-V: u8 zero point of tokens tile_token(g, k)
+// Per tile, every lane loads straight into registers exactly what its MFMA operands need:
+// the INT4-K codes of token a0 + 16 mg + l16 (channels 32g ..), and for each of its 8 tokens
+// tile_token(g, k) the 8 V dims 8*l16 .. 8*l16+7 (bf16: 16 B, INT4: 4 B, INT2: 2 B) plus the
+// token's V metadata.  The K superblock operands of the wave's whole tile range are copied into
+// LDS once per work item.  INT4/INT2 tiles are prefetched two tiles ahead (three rotating
+// register sets), bf16 tiles one tile ahead.
+template <int KIND>
+struct TileRegs;
+template <>
+struct TileRegs<kFP> {
+    r2o_u4 kx[2];
+    r2o_u4 v[8];
+};
+template <>
+struct TileRegs<kI4> {
+    r2o_u4 kx[2];
+    uint32_t v[8];
+    uint32_t vm[8];  // f32 scale bits
+};
+template <>
+struct TileRegs<kI2> {
+    r2o_u4 kx[2];
+    uint32_t v[8];
+    uint32_t vm[8];  // fp16 scale bits (group of dims 8*l16)
+    uint32_t vz[8];  // u8 zero point
 };
 
 __device__ __forceinline__ void lds_copy16(const void* gsrc, unsigned char* lds_base, int offset) {
@@ -162,54 +178,45 @@ __device__ __forceinline__ void lds_copy16(const void* gsrc, unsigned char* lds_
                                      (__attribute__((address_space(3))) void*)(lds_base + offset), 16, 0, 0);
 }
 
-// Per-item, per-lane addressing of one pool segment (32-bit positions; one head's arena).
+// Per-item, per-lane addressing of one pool segment (32-bit positions within one head).
 struct SegCtx {
     const uint8_t* kcode;    // k_packed of this head + l16*64 + 16g   (+ a0*64 + mg*1024)
-    const uint16_t* kscale;  // k_scale of this head + 32g              (+ sb*128)
-    const uint8_t* kzero;
-    const uint8_t* vrows;    // V rows of this head (byte pointer)
-    const void* vmeta;       // INT4: f32 scales of this head; INT2: fp16 scales
-    const uint8_t* vzero;    // INT2: u8 zero points
+    const uint8_t* vrows;    // V rows of this head + lane column offset
+    const void* vmeta;       // INT4: f32 scales of this head; INT2: fp16 scales (+ gamma)
+    const uint8_t* vzero;    // INT2: u8 zero points (+ gamma)
     int lo, hi, vdelta;      // valid arena positions, V row = arena - vdelta
-    int sb_shift, groups, gamma;
+    int sb_shift, groups;
 };
 
 template <int KIND>
-__device__ __forceinline__ void issue_seg_tile(const SegCtx& c, int a0, int lane, int g, unsigned char* stage,
-                                               TileRegs& tr) {
+__device__ __forceinline__ void issue_seg_tile(const SegCtx& c, int a0, int g, TileRegs<KIND>& tr) {
     constexpr int kRow = KIND == kFP ? 256 : (KIND == kI4 ? 64 : 32);
     tr.kx[0] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64));
     tr.kx[1] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64 + 1024));
-    const int meta = (a0 >> c.sb_shift) * 128;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) tr.ks[w] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kscale + meta) + w);
-#pragma unroll
-    for (int w = 0; w < 2; ++w) tr.kz[w] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kzero + meta) + w);
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
-    const int row0 = a0 - c.vdelta;
-    // V rows; rows outside [lo, hi) read a clamped valid row (finite data, probability 0)
-    auto vrow = [&](int r) -> int {
-        if (full) return row0 + r;
-        const int pos = min(max(a0 + r, c.lo), c.hi - 1);
-        return pos - c.vdelta;
-    };
-    constexpr int kChunks = 32 * kRow / 1024;  // 16-byte chunks per lane per tile
+    int row[8];
+    if (full) {
 #pragma unroll
-    for (int itn = 0; itn < kChunks; ++itn) {
-        const int ch = itn * 64 + lane;               // chunk ch covers row ch*16/kRow
-        const int r = ch * 16 / kRow, col = ch * 16 % kRow;
-        lds_copy16(c.vrows + vrow(r) * kRow + col, stage, itn * 1024);
+        for (int k = 0; k < 8; ++k) row[k] = a0 - c.vdelta + tile_token(g, k);
+    } else {  // rows outside [lo, hi) read a clamped valid row (finite data, probability 0)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) row[k] = min(max(a0 + tile_token(g, k), c.lo), c.hi - 1) - c.vdelta;
     }
-    if (KIND == kI4) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            tr.vm[k] = r2o_ldg(reinterpret_cast<const uint32_t*>(c.vmeta) + vrow(tile_token(g, k)));
-    } else if (KIND == kI2) {
+    for (int k = 0; k < 8; ++k) {
+        const uint8_t* src = c.vrows + row[k] * kRow;
+        if constexpr (KIND == kFP) tr.v[k] = r2o_ldg(reinterpret_cast<const r2o_u4*>(src));
+        else if constexpr (KIND == kI4) tr.v[k] = r2o_ldg(reinterpret_cast<const uint32_t*>(src));
+        else tr.v[k] = r2o_ldg(reinterpret_cast<const uint16_t*>(src));
+    }
+    if constexpr (KIND == kI4) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) tr.vm[k] = r2o_ldg(reinterpret_cast<const uint32_t*>(c.vmeta) + row[k]);
+    } else if constexpr (KIND == kI2) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const int m = vrow(tile_token(g, k)) * c.groups + c.gamma;
-            tr.vm[k] = r2o_ldg(reinterpret_cast<const uint16_t*>(c.vmeta) + m);
-            tr.vz[k] = r2o_ldg(c.vzero + m);
+            tr.vm[k] = r2o_ldg(reinterpret_cast<const uint16_t*>(c.vmeta) + row[k] * c.groups);
+            tr.vz[k] = r2o_ldg(c.vzero + row[k] * c.groups);
         }
     }
 }
@@ -217,75 +224,35 @@ __device__ __forceinline__ void issue_seg_tile(const SegCtx& c, int a0, int lane
 template <int KIND>
 struct SegState {
     uint32_t qp[4][4];   // q (scaled), f16 pairs in the K-unpack channel order
-    uint32_t qs[4][4];   // Q' = q * s of the current superblock
-    r2o_f4 negcorr;      // -sum_c Q'(1024 + z_c), identical in all rows
-    int cur_sb;
     r2o_f4 bias;         // INT4-V: sum_k P'_k * 1032 per head row (removed at the end)
 };
 
 template <int KIND>
-__device__ __forceinline__ void seg_step(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
-                                         int a0, bool has_next, int lane, int l16, int g, bool head_ok,
-                                         unsigned char* stage, const TileRegs& cur, TileRegs& nxt) {
-    __builtin_amdgcn_s_waitcnt(0);  // tile a0: registers and LDS copies complete
-    __builtin_amdgcn_wave_barrier();
-    // ---- transposed V reads: 8 tokens x 8 dims (8*l16 ..) per lane
-    r2o_u4 R[8];
-    uint32_t X[8], Y[8];
-    if (KIND == kFP) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) R[k] = *reinterpret_cast<const r2o_u4*>(stage + tile_token(g, k) * 256 + 16 * l16);
-    } else if (KIND == kI4) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) X[k] = *reinterpret_cast<const uint32_t*>(stage + tile_token(g, k) * 64 + 4 * l16);
-    } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) Y[k] = *reinterpret_cast<const uint16_t*>(stage + tile_token(g, k) * 32 + 2 * l16);
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage reads done before it is refilled
-    __builtin_amdgcn_wave_barrier();
-    if (has_next) issue_seg_tile<KIND>(c, a0 + 32, lane, g, stage, nxt);
-
-    // ---- QK^T: Q' and -sum Q'(1024 + z) for the tile's superblock
+__device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
+                                            int a0, int l16, int g, bool head_ok, const unsigned char* kops,
+                                            int sb0, const TileRegs<KIND>& cur) {
+    // ---- QK^T per MFMA j: Q'_j = q * s (superblock scale pairs from LDS), the correction
+    //      -sum Q'_j (1024 + z) as the C operand, then the two 16-token groups.
     const int sb = a0 >> c.sb_shift;
-    if (sb != ss.cur_sb) {
-        ss.cur_sb = sb;
-        uint32_t sd[16], zd[8];
+    const r2o_u4* ko = reinterpret_cast<const r2o_u4*>(kops + (sb - sb0) * 512 + g * 128);
+    r2o_f4 s[2] = {r2o_f4{0, 0, 0, 0}, r2o_f4{0, 0, 0, 0}};
+    r2o_f4 corr = {0, 0, 0, 0};
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            sd[4 * w] = cur.ks[w].x; sd[4 * w + 1] = cur.ks[w].y; sd[4 * w + 2] = cur.ks[w].z; sd[4 * w + 3] = cur.ks[w].w;
-        }
+    for (int j = 0; j < 4; ++j) {
+        const r2o_u4 sj = ko[j], zj = ko[4 + j];
+        const r2o_u4 qj = {r2o_h2_mul(ss.qp[j][0], sj[0]), r2o_h2_mul(ss.qp[j][1], sj[1]),
+                           r2o_h2_mul(ss.qp[j][2], sj[2]), r2o_h2_mul(ss.qp[j][3], sj[3])};
+        corr = r2o_mfma_f16(zj, qj, corr);
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            zd[4 * w] = cur.kz[w].x; zd[4 * w + 1] = cur.kz[w].y; zd[4 * w + 2] = cur.kz[w].z; zd[4 * w + 3] = cur.kz[w].w;
-        }
-        ss.negcorr = r2o_f4{0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r2o_u4 zop;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t sp = r2o_perm(sd[4 * j + 2 + u / 2], sd[4 * j + u / 2], (u & 1) ? 0x07060302u : 0x05040100u);
-                ss.qs[j][u] = r2o_h2_mul(ss.qp[j][u], sp);
-                const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + u) << 16) | (uint32_t)u;
-                zop[u] = r2o_perm(zd[2 * j + 1], zd[2 * j], sel) | 0xE400E400u;  // -(1024 + z)
-            }
-            ss.negcorr = r2o_mfma_f16(zop, r2o_u4{ss.qs[j][0], ss.qs[j][1], ss.qs[j][2], ss.qs[j][3]}, ss.negcorr);
-        }
-    }
-    r2o_f4 s[2];
-#pragma unroll
-    for (int mg = 0; mg < 2; ++mg) {
-        r2o_f4 acc = ss.negcorr;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int mg = 0; mg < 2; ++mg) {
             const uint32_t w = cur.kx[mg][j];
             const r2o_u4 a = {(w & vc.nib) | vc.magic, ((w >> 4) & vc.nib) | vc.magic, ((w >> 8) & vc.nib) | vc.magic,
                               ((w >> 12) & vc.nib) | vc.magic};
-            acc = r2o_mfma_f16(a, r2o_u4{ss.qs[j][0], ss.qs[j][1], ss.qs[j][2], ss.qs[j][3]}, acc);
+            s[mg] = r2o_mfma_f16(a, qj, s[mg]);
         }
-        s[mg] = acc;
     }
+    s[0] += corr;
+    s[1] += corr;
 
     // ---- softmax (masks only on partial tiles and padded heads)
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);
@@ -305,19 +272,20 @@ __device__ __forceinline__ void seg_step(const SegCtx& c, WaveState& st, SegStat
 
     // ---- PV
     r2o_u4 ap;
-    if (KIND == kFP) {
+    if constexpr (KIND == kFP) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
-        pv_bf16(st, ap, R);
-    } else if (KIND == kI4) {
+        pv_bf16(st, ap, cur.v);
+    } else if constexpr (KIND == kI4) {
         // P' = p * s_t; codes enter as (1032 + c) and sum_k P'_k * 1032 is accumulated by one
         // more MFMA on the same A operand (so both see identical f16 inputs).
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             ap[u] = r2o_pack_h2(pk[2 * u] * __uint_as_float(cur.vm[2 * u]), pk[2 * u + 1] * __uint_as_float(cur.vm[2 * u + 1]));
         ss.bias = r2o_mfma_f16(ap, r2o_u4{0x64086408u, 0x64086408u, 0x64086408u, 0x64086408u}, ss.bias);
+        uint32_t X[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) X[k] ^= 0x88888888u;
+        for (int k = 0; k < 8; ++k) X[k] = cur.v[k] ^ 0x88888888u;
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
             const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + bb) << 16) | (uint32_t)bb;
@@ -337,7 +305,7 @@ __device__ __forceinline__ void seg_step(const SegCtx& c, WaveState& st, SegStat
         uint32_t yp[4], zp[4], sp[4];
 #pragma unroll
         for (int pr = 0; pr < 4; ++pr) {
-            yp[pr] = Y[2 * pr] | (Y[2 * pr + 1] << 16);
+            yp[pr] = cur.v[2 * pr] | (cur.v[2 * pr + 1] << 16);
             zp[pr] = (cur.vz[2 * pr] | (cur.vz[2 * pr + 1] << 16)) | vc.magic;
             sp[pr] = cur.vm[2 * pr] | (cur.vm[2 * pr + 1] << 16);
         }
@@ -366,49 +334,79 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int t_begin = wave * per;
     const int t_end = min((int)it.ntiles, t_begin + per);
     if (t_begin >= t_end) return;
-    unsigned char* stage = smem + wave * kStageBytes;
+    unsigned char* kops = smem + wave * kStageBytes;
     const bool head_ok = l16 < gqa;
 
     SegCtx c;
     c.kcode = rq.k_packed + (kvh * rq.k_capacity + l16) * 64 + 16 * g;
-    c.kscale = rq.k_scale + kvh * rq.k_superblocks * 128 + 32 * g;
-    c.kzero = rq.k_zero + kvh * rq.k_superblocks * 128 + 32 * g;
     c.lo = (int)it.lo;
     c.hi = (int)it.hi;
     c.vdelta = (int)it.v_delta;
     c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
     c.groups = (int)(128 / p.int2_group);
-    c.gamma = (8 * l16) / (int)p.int2_group;
+    const int gamma = (8 * l16) / (int)p.int2_group;
     if (KIND == kFP) {
-        c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128);
+        c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128) + 16 * l16;
     } else if (KIND == kI4) {
-        c.vrows = rq.i4_v + kvh * rq.i4_stride * 64;
+        c.vrows = rq.i4_v + kvh * rq.i4_stride * 64 + 4 * l16;
         c.vmeta = rq.i4_scale + kvh * rq.i4_stride;
     } else {
-        c.vrows = rq.i2_v + kvh * rq.i2_stride * 32;
-        c.vmeta = rq.i2_scale + kvh * rq.i2_stride * c.groups;
-        c.vzero = rq.i2_zero + kvh * rq.i2_stride * c.groups;
+        c.vrows = rq.i2_v + kvh * rq.i2_stride * 32 + 2 * l16;
+        c.vmeta = rq.i2_scale + kvh * rq.i2_stride * c.groups + gamma;
+        c.vzero = rq.i2_zero + kvh * rq.i2_stride * c.groups + gamma;
+    }
+    // ---- K superblock operands of the wave's tile range -> LDS (one copy per item)
+    const int base = (int)it.tile0;
+    const int sb0 = (base + 32 * t_begin) >> c.sb_shift;
+    const int sb1 = (base + 32 * t_end - 1) >> c.sb_shift;
+    {
+        const uint32_t* src = rq.k_operands + kvh * rq.k_superblocks * 128 + (int64_t)sb0 * 128;
+        const int nchunks = (sb1 - sb0 + 1) * 32;  // 16-byte chunks
+        for (int ch0 = 0; ch0 < nchunks; ch0 += 64) {
+            const int ch = min(ch0 + lane, nchunks - 1);
+            lds_copy16(src + ch * 4, kops, ch0 * 16);
+        }
     }
     const VConst vc = make_vconst();
     SegState<KIND> ss;
     load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
-    ss.cur_sb = -1;
-    ss.negcorr = r2o_f4{0, 0, 0, 0};
     ss.bias = r2o_f4{0, 0, 0, 0};
 
-    TileRegs ra, rb;
-    const int base = (int)it.tile0;
-    issue_seg_tile<KIND>(c, base + 32 * t_begin, lane, g, stage, ra);
-    for (int t = t_begin; t < t_end; t += 2) {
-        seg_step<KIND>(c, st, ss, vc, base + 32 * t, t + 1 < t_end, lane, l16, g, head_ok, stage, ra, rb);
-        if (t + 1 >= t_end) break;
-        seg_step<KIND>(c, st, ss, vc, base + 32 * (t + 1), t + 2 < t_end, lane, l16, g, head_ok, stage, rb, ra);
+    const int n = t_end - t_begin;
+    const int a_first = base + 32 * t_begin;
+    if constexpr (KIND == kFP) {
+        TileRegs<KIND> r0, r1;
+        issue_seg_tile<KIND>(c, a_first, g, r0);
+        __builtin_amdgcn_s_waitcnt(0);  // K operands (and tile 0) in LDS / registers
+        __builtin_amdgcn_wave_barrier();
+        for (int i = 0; i < n; i += 2) {
+            if (i + 1 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 1), g, r1);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, head_ok, kops, sb0, r0);
+            if (i + 1 >= n) break;
+            if (i + 2 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 2), g, r0);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, head_ok, kops, sb0, r1);
+        }
+    } else {
+        TileRegs<KIND> r0, r1, r2;
+        issue_seg_tile<KIND>(c, a_first, g, r0);
+        if (n > 1) issue_seg_tile<KIND>(c, a_first + 32, g, r1);
+        __builtin_amdgcn_s_waitcnt(0);  // K operands (and tiles 0, 1) in LDS / registers
+        __builtin_amdgcn_wave_barrier();
+        for (int i = 0; i < n; i += 3) {
+            if (i + 2 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 2), g, r2);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, head_ok, kops, sb0, r0);
+            if (i + 1 >= n) break;
+            if (i + 3 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 3), g, r0);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, head_ok, kops, sb0, r1);
+            if (i + 2 >= n) break;
+            if (i + 4 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 4), g, r1);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 2), l16, g, head_ok, kops, sb0, r2);
+        }
     }
-    if (KIND == kI4) {
+    if constexpr (KIND == kI4) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) st.acc[q] -= ss.bias;
     }
-    __builtin_amdgcn_s_waitcnt(0);
 }
 
 // Recent-FP ring tiles (bf16 K and V, plus the fused-append token): at most a few tiles per
@@ -525,7 +523,7 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
                 A += base[w * kMergeFloats + 32 + h * 128 + d] * sc;
             }
         }
-        const int64_t slot = (int64_t)blockIdx.x * 16 + h;
+        const int64_t slot = it.slot * 16 + h;
         p.partial_out[slot * 128 + d] = A;
         if (d == 0) {
             p.partial_max[slot] = M;

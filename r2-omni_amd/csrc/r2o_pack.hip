@@ -15,7 +15,9 @@ constexpr float kEps = 1.0e-6f;
 __global__ __launch_bounds__(64) void pack_int4_k_kernel(
     const uint16_t* __restrict__ src, int dtype, int64_t src_tokens, const int64_t* __restrict__ index,
     int64_t n, int64_t tail, int64_t dst_start, uint8_t* packed, uint16_t* scale, uint8_t* zero,
-    int64_t capacity, int64_t superblocks, int sb) {
+    uint32_t* operands, int64_t capacity, int64_t superblocks, int sb) {
+    __shared__ uint16_t s_half[128];
+    __shared__ uint8_t s_zero[128];
     const int t = threadIdx.x;
     const int64_t h = blockIdx.y;
     const int64_t total = tail + n;
@@ -61,10 +63,23 @@ __global__ __launch_bounds__(64) void pack_int4_k_kernel(
         const float c1 = fminf(fmaxf(__builtin_rintf(__fdiv_rn(x1, st1) + zp1), 0.f), 15.f);
         prow[j * 64] = (uint8_t)((uint32_t)c0 | ((uint32_t)c1 << 4));
     }
-    srow[0] = (uint16_t)r2o_f32_to_f16(st0);
-    srow[1] = (uint16_t)r2o_f32_to_f16(st1);
+    const uint16_t h0 = (uint16_t)r2o_f32_to_f16(st0), h1 = (uint16_t)r2o_f32_to_f16(st1);
+    srow[0] = h0;
+    srow[1] = h1;
     zrow[0] = (uint8_t)zp0;
     zrow[1] = (uint8_t)zp1;
+    if (operands) {  // QK MFMA operands of this superblock (layout in r2o_sspa.h)
+        s_half[2 * t] = h0;
+        s_half[2 * t + 1] = h1;
+        s_zero[2 * t] = (uint8_t)zp0;
+        s_zero[2 * t + 1] = (uint8_t)zp1;
+        __syncthreads();
+        const int g = t >> 4, j = (t >> 2) & 3, u = t & 3;
+        const int c = 32 * g + 8 * j + u;
+        uint32_t* orow = operands + (h * superblocks + block_row) * 128 + g * 32 + 4 * j + u;
+        orow[0] = (uint32_t)s_half[c] | ((uint32_t)s_half[c + 4] << 16);
+        orow[16] = (0xE400u | s_zero[c]) | ((0xE400u | (uint32_t)s_zero[c + 4]) << 16);
+    }
 }
 
 // ---------------------------------------------------------------------------- INT4 values
@@ -219,7 +234,7 @@ extern "C" {
 
 int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens, const int64_t* index,
                     int64_t n, int64_t tail, int64_t dst_start, uint8_t* packed, uint16_t* scale, uint8_t* zero,
-                    int64_t capacity, int64_t superblocks, int64_t superblock, void* stream) {
+                    uint32_t* operands, int64_t capacity, int64_t superblocks, int64_t superblock, void* stream) {
     if (!(superblock == 32 || superblock == 64 || superblock == 128) || (dtype != 0 && dtype != 1)) return R2O_EINVAL;
     if (hkv <= 0 || n < 0 || tail < 0 || tail >= superblock || dst_start < 0 || dst_start % superblock) return R2O_EINVAL;
     if (dst_start + tail + n > capacity || capacity % superblock || superblocks * superblock != capacity) return R2O_EINVAL;
@@ -228,8 +243,8 @@ int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src
     if (total == 0) return R2O_OK;
     const int64_t blocks = (total + superblock - 1) / superblock;
     hipLaunchKernelGGL(pack_int4_k_kernel, dim3((unsigned)blocks, (unsigned)hkv), dim3(64), 0, (hipStream_t)stream,
-                       src, (int)dtype, src_tokens, index, n, tail, dst_start, packed, scale, zero, capacity,
-                       superblocks, (int)superblock);
+                       src, (int)dtype, src_tokens, index, n, tail, dst_start, packed, scale, zero, operands,
+                       capacity, superblocks, (int)superblock);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
 }

@@ -52,23 +52,24 @@ class DecodeParams(ctypes.Structure):
     ]
 
 
-# r2o_request_desc: 21 eight-byte words, in header order.
+# r2o_request_desc: 22 eight-byte words, in header order.
 REQUEST_FIELDS = (
-    "k_packed", "k_scale", "k_zero", "k_capacity", "k_superblocks",
+    "k_packed", "k_scale", "k_zero", "k_capacity", "k_superblocks", "k_operands",
     "fp_v", "fp_stride",
     "i4_v", "i4_scale", "i4_stride",
     "i2_v", "i2_scale", "i2_zero", "i2_stride",
     "recent_k", "recent_v", "recent_capacity", "recent_length",
     "recent_global", "recent_logical", "recent_page_lengths",
 )
-# r2o_work_item: 8 eight-byte words.
-WORK_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta")
+# r2o_work_item: 9 eight-byte words.
+WORK_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta", "slot")
 KIND_FP, KIND_INT4, KIND_INT2, KIND_RECENT = 0, 1, 2, 3
 
 _SIGNATURES = {
     "r2o_decode_partial": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_combine": (ctypes.POINTER(DecodeParams), c_vp),
-    "r2o_pack_int4_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp),
+    "r2o_pack_int4_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+                        c_vp),
     "r2o_pack_int4_v": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp),
     "r2o_pack_int2_v": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp),
     "r2o_gather_rows": (c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp),

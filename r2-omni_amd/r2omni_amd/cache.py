@@ -57,6 +57,9 @@ class CompactInt4KeyArena:
     original_dtype: torch.dtype
     superblock_size: int = 128
     bit_width: int = 4
+    # u32 [H, capacity/SB, 128]: per superblock, the fp16 scale pairs and -(1024 + zero) pairs in
+    # the channel order of the decode kernel's QK MFMA (derived from scale/zero by the packer)
+    kernel_operands: torch.Tensor | None = None
 
     def __post_init__(self) -> None:
         if self.packed.ndim != 3 or self.packed.dtype != torch.uint8:
@@ -75,6 +78,9 @@ class CompactInt4KeyArena:
             raise ValueError("compact INT4 K metadata dtypes are invalid")
         if tuple(sorted(self.segment_offsets)) != tuple(self.segment_offsets):
             raise ValueError("compact INT4 K segment offsets must be monotonic")
+        if self.kernel_operands is not None and (tuple(self.kernel_operands.shape) != (h, blocks, 128)
+                                                 or self.kernel_operands.dtype != torch.int32):
+            raise ValueError("compact INT4 K kernel operands must be int32 [H,blocks,128]")
 
     @property
     def head_count(self) -> int:
@@ -102,7 +108,9 @@ class CompactInt4KeyArena:
                    + per_block * self.scale.element_size() + per_block * self.zero_point.element_size())
 
     def allocation_tensors(self):
-        return self.packed, self.scale, self.zero_point
+        if self.kernel_operands is None:
+            return self.packed, self.scale, self.zero_point
+        return self.packed, self.scale, self.zero_point, self.kernel_operands
 
     def dequantize_range(self, start: int, length: int) -> torch.Tensor:
         """fp32 (code - z) * s of arena positions [start, start+length) (inspection only)."""
@@ -137,7 +145,8 @@ class CompactInt4KeyArena:
         tail = self.active_length - prefix
         _lib.call("r2o_pack_int4_k", _lib.ptr(key_block), _lib.dtype_code(key_block.dtype), self.head_count, rows,
                   None, 128, tail, prefix, _lib.ptr(self.packed), _lib.ptr(self.scale), _lib.ptr(self.zero_point),
-                  self.capacity, self.superblock_count, self.superblock_size, _lib.stream_of(key_block.device))
+                  _lib.ptr(self.kernel_operands), self.capacity, self.superblock_count, self.superblock_size,
+                  _lib.stream_of(key_block.device))
         self.active_length += 128
         return tail
 
@@ -162,13 +171,14 @@ def build_compact_int4_key_arena(key: torch.Tensor, segment_token_indices, *, ap
         zero_point=torch.zeros((h, blocks, d), device=dev, dtype=torch.uint8),
         active_length=active, capacity=capacity, segment_offsets=offsets,
         original_dtype=key.dtype, superblock_size=superblock_size,
+        kernel_operands=torch.zeros((h, blocks, 128), device=dev, dtype=torch.int32),
     )
     if active:
         key = key.contiguous()
         ordered = torch.cat([ix.to(device=dev, dtype=torch.long) for ix in segment_token_indices]).contiguous()
         _lib.call("r2o_pack_int4_k", _lib.ptr(key), _lib.dtype_code(key.dtype), h, s, _lib.ptr(ordered), active,
-                  0, 0, _lib.ptr(arena.packed), _lib.ptr(arena.scale), _lib.ptr(arena.zero_point), capacity,
-                  blocks, superblock_size, _lib.stream_of(dev))
+                  0, 0, _lib.ptr(arena.packed), _lib.ptr(arena.scale), _lib.ptr(arena.zero_point),
+                  _lib.ptr(arena.kernel_operands), capacity, blocks, superblock_size, _lib.stream_of(dev))
     return arena
 
 

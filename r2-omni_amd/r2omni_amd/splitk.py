@@ -24,7 +24,7 @@ from .cache import ThreePrecisionCache
 
 TILE = 32
 _MIN_TILES_PER_ITEM = 4      # one tile per wave of the 4-wave workgroup
-_MAX_TILES_PER_ITEM = 256
+_MAX_TILES_PER_ITEM = 64       # 16 tiles per wave: K operands of <= 16 superblocks fit the LDS stage
 
 
 @dataclass
@@ -65,16 +65,19 @@ def _tiles(lo: int, hi: int) -> tuple[int, int]:
 
 
 def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_int2: int = 0):
-    """Split every (request, kv head, pool segment) into runs of tiles for ~3 workgroups per CU.
+    """Split every (request, kv head, pool segment) into runs of 32-token tiles.
 
-    Returns (items [n, 8] int64, group_begin [B*hkv + 1] int32) on the host, items grouped by
-    (request, kv head).
+    About two equal workgroups per CU (the partial kernel runs two 4-wave workgroups per CU),
+    at least one tile per wave.  Items keep a partial slot in (request, kv head) order, so the
+    combine reads one contiguous slot range per group, and are launched largest first so the
+    segment-boundary fragments fill in behind the full-size items.
+    Returns (items [n, 9] int64 in launch order, group_begin [B*hkv + 1] int32) on the host.
     """
     segs = [_segments(c, extra_int2) for c in caches]
     total_tiles = 0
     for c, ss in zip(caches, segs):
         total_tiles += hkv * (sum(_tiles(lo, hi)[1] for _, lo, hi, _ in ss) + c.recent_fp_pool.capacity // TILE)
-    target = 3 * max(1, num_cus)
+    target = 2 * max(1, num_cus)
     tpi = -(-total_tiles // target)
     tpi = max(_MIN_TILES_PER_ITEM, min(_MAX_TILES_PER_ITEM, -(-tpi // 4) * 4))
     items = []
@@ -87,10 +90,12 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
             for kind, lo, hi, vd in ss:
                 t0, nt = _tiles(lo, hi)
                 for first in range(0, nt, tpi):
-                    items.append((r, h, kind, t0 + TILE * first, min(tpi, nt - first), lo, hi, vd))
+                    items.append([r, h, kind, t0 + TILE * first, min(tpi, nt - first), lo, hi, vd, len(items)])
             for first in range(0, rcap // TILE, tpi):
-                items.append((r, h, _lib.KIND_RECENT, TILE * first, min(tpi, rcap // TILE - first), 0, rcap, 0))
+                items.append([r, h, _lib.KIND_RECENT, TILE * first, min(tpi, rcap // TILE - first), 0, rcap, 0,
+                              len(items)])
             begins.append(len(items))
+    items.sort(key=lambda it: -it[4])  # stable: largest first, ties keep slot order
     return torch.tensor(items, dtype=torch.int64), torch.tensor(begins, dtype=torch.int32)
 
 
@@ -148,6 +153,7 @@ def _request_desc(cache: ThreePrecisionCache) -> list[int]:
     words = {
         "k_packed": ck.packed.data_ptr(), "k_scale": ck.scale.data_ptr(), "k_zero": ck.zero_point.data_ptr(),
         "k_capacity": ck.capacity, "k_superblocks": ck.superblock_count,
+        "k_operands": ck.kernel_operands.data_ptr(),
         "fp_v": fp.fp_v.data_ptr() if fp.token_count else 0, "fp_stride": fp.token_count,
         "i4_v": i4_packed.data_ptr() if i4_packed is not None else 0,
         "i4_scale": i4_scale.data_ptr() if i4_scale is not None else 0, "i4_stride": i4.token_count,

@@ -43,7 +43,7 @@ def test_params_struct_layout_matches_header():
 def test_host_side_validation_rejects_bad_arguments_without_a_gpu():
     lib = _lib.load()
     # superblock 48 is rejected before any launch
-    rc = lib.r2o_pack_int4_k(None, 0, 2, 10, None, 10, 0, 0, None, None, None, 128, 3, 48, None)
+    rc = lib.r2o_pack_int4_k(None, 0, 2, 10, None, 10, 0, 0, None, None, None, None, 128, 3, 48, None)
     assert rc == 1
     rc = lib.r2o_pack_int2_v(None, 0, 2, 10, None, 10, 0, 48, None, None, None, 128, None)
     assert rc == 1
