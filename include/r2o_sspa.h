@@ -86,7 +86,7 @@ typedef struct r2o_decode_params {
     int64_t n_items;
     float* partial_max;             /* device f32 [n_items, 16]      (log2 domain)     */
     float* partial_sum;             /* device f32 [n_items, 16]                        */
-    float* partial_out;             /* device f32 [n_items, 16, 128]                   */
+    float* partial_out;             /* device f32 [n_items, 16, 128], 16-byte aligned  */
     const uint16_t* query;          /* device [batch, hq, 128] (dtype q_dtype)         */
     uint16_t* out;                  /* device bf16 [batch, hq, 128]                    */
     const uint16_t* append_k;       /* device bf16 [batch, hkv, 128] or NULL           */

@@ -532,96 +532,103 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     }
 }
 
-// One 1024-thread block per (request, query head): 8 slices x 128 dims.  Slice s merges the
-// partials beg+s, beg+s+8, ... (loads of independent partials in flight together), then the
-// slices are merged through LDS.  All merges are the exact fp32 softmax-state merge.
-constexpr int kCombineSlices = 8;
+// One 512-thread block per (request, query head): 16 slices of 32 lanes, lane l owning dims
+// 4l..4l+3.  Slice s merges partials beg+s, beg+s+16, ... four at a time with every load of a
+// round issued before any is used, so a group of up to 64 partials costs one memory round trip;
+// the 16 slice states then merge through LDS in wave 0, which also runs the output FWHT with
+// lane shuffles.  Every merge is the exact fp32 softmax-state merge
+// (triton_fourq_attention.py:58-69; triton_fourq_splitk.py:977-999).
+constexpr int kCombineSlices = 16;
+constexpr int kCombineUnroll = 4;
 
-__global__ __launch_bounds__(1024) void decode_combine_kernel(r2o_decode_params p) {
-    __shared__ float red_m[32];
-    __shared__ float sl_l[kCombineSlices];
-    __shared__ float sl_a[kCombineSlices][128];
-    __shared__ float buf[128];
+__global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p) {
+    __shared__ float sl_m[kCombineSlices], sl_l[kCombineSlices];
+    __shared__ __align__(16) float sl_a[kCombineSlices][128];
     const int64_t b = blockIdx.y;
     const int hqi = blockIdx.x;
-    const int tid = threadIdx.x, d = tid & 127, slice = tid >> 7;
+    const int tid = threadIdx.x, lane = tid & 31, slice = tid >> 5;
     const int gqa = (int)(p.hq / p.hkv);
     const int kvh = hqi / gqa, h = hqi % gqa;
     const int beg = r2o_ldg(p.group_begin + b * p.hkv + kvh), end = r2o_ldg(p.group_begin + b * p.hkv + kvh + 1);
-    // ---- global max over the group's partials
-    float m = -INFINITY;
-    for (int i = beg + tid; i < end; i += 1024) m = fmaxf(m, r2o_ldg(p.partial_max + (int64_t)i * 16 + h));
-    m = r2o_wave_max(m);
-    if ((tid & 63) == 0) red_m[tid >> 6] = m;
-    __syncthreads();
-    float M = red_m[0];
+    float m = -INFINITY, l = 0.f;
+    r2o_f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int base = beg + slice; base < end; base += kCombineUnroll * kCombineSlices) {
+        float mm[kCombineUnroll], ll[kCombineUnroll];
+        r2o_f4 aa[kCombineUnroll];
 #pragma unroll
-    for (int w = 1; w < 16; ++w) M = fmaxf(M, red_m[w]);
-    // ---- per-slice weighted sums
-    float L = 0.f, A = 0.f;
-    if (M != -INFINITY) {
-        int i = beg + slice;
-        for (; i + kCombineSlices < end; i += 2 * kCombineSlices) {
-            const int64_t s0 = (int64_t)i * 16 + h, s1 = (int64_t)(i + kCombineSlices) * 16 + h;
-            const float m0 = r2o_ldg(p.partial_max + s0), m1 = r2o_ldg(p.partial_max + s1);
-            const float l0 = r2o_ldg(p.partial_sum + s0), l1 = r2o_ldg(p.partial_sum + s1);
-            const float a0 = r2o_ldg(p.partial_out + s0 * 128 + d), a1 = r2o_ldg(p.partial_out + s1 * 128 + d);
-            const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - M);
-            const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
-            L += l0 * w0 + l1 * w1;
-            A += a0 * w0 + a1 * w1;
+        for (int k = 0; k < kCombineUnroll; ++k) {  // all loads of the round first
+            const int i = base + k * kCombineSlices;
+            const int64_t slot = (int64_t)(i < end ? i : base) * 16 + h;
+            mm[k] = r2o_ldg(p.partial_max + slot);
+            ll[k] = r2o_ldg(p.partial_sum + slot);
+            aa[k] = r2o_ldg(reinterpret_cast<const r2o_f4*>(p.partial_out + slot * 128) + lane);
         }
-        if (i < end) {
-            const int64_t s0 = (int64_t)i * 16 + h;
-            const float m0 = r2o_ldg(p.partial_max + s0);
-            const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - M);
-            L += r2o_ldg(p.partial_sum + s0) * w0;
-            A += r2o_ldg(p.partial_out + s0 * 128 + d) * w0;
-        }
-    }
-    sl_a[slice][d] = A;
-    if (d == 0) sl_l[slice] = L;
-    __syncthreads();
-    const bool lead = tid < 128;  // the first 128 threads finish the head (all threads meet the barriers)
-    float y = 0.f;
-    if (lead) {
-        float At = 0.f, Lt = 0.f;
+        float mn = m;
 #pragma unroll
-        for (int s2 = 0; s2 < kCombineSlices; ++s2) {
-            At += sl_a[s2][d];
-            Lt += sl_l[s2];
+        for (int k = 0; k < kCombineUnroll; ++k) {
+            if (base + k * kCombineSlices >= end) mm[k] = -INFINITY;
+            mn = fmaxf(mn, mm[k]);
         }
-        y = r2o_bf16_to_f32(r2o_f32_to_bf16(At / Lt));
-    }
-    if (p.output_hadamard) {
-        if (lead) buf[d] = y;
-        __syncthreads();
-        for (int stride = 1; stride < 128; stride <<= 1) {
-            float a = 0.f, c = 0.f;
-            int i0 = 0;
-            if (tid < 64) {
-                i0 = (d / stride) * 2 * stride + (d & (stride - 1));
-                a = buf[i0];
-                c = buf[i0 + stride];
-            }
-            __syncthreads();
-            if (tid < 64) {
-                buf[i0] = a + c;
-                buf[i0 + stride] = a - c;
-            }
-            __syncthreads();
+        const float keep = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+        l *= keep;
+        acc *= keep;
+#pragma unroll
+        for (int k = 0; k < kCombineUnroll; ++k) {
+            const float w = (mm[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mm[k] - mn);
+            l += ll[k] * w;
+            acc += aa[k] * w;
         }
-        if (lead) y = buf[d] * 0.08838834764831845f;
+        m = mn;
     }
-    if (!lead) return;
-    p.out[(b * p.hq + hqi) * 128 + d] = (uint16_t)r2o_f32_to_bf16(y);
+    reinterpret_cast<r2o_f4*>(sl_a[slice])[lane] = acc;
+    if (lane == 0) {
+        sl_m[slice] = m;
+        sl_l[slice] = l;
+    }
+    __syncthreads();
+    if (tid >= 64) return;
+    // ---- wave 0: lane t owns dims t and t + 64
+    float M = -INFINITY;
+#pragma unroll
+    for (int s2 = 0; s2 < kCombineSlices; ++s2) M = fmaxf(M, sl_m[s2]);
+    float L = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < kCombineSlices; ++s2) {
+        const float ms = sl_m[s2];
+        const float w = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+        L += sl_l[s2] * w;
+        a0 += sl_a[s2][tid] * w;
+        a1 += sl_a[s2][tid + 64] * w;
+    }
+    float y0 = r2o_bf16_to_f32(r2o_f32_to_bf16(a0 / L));
+    float y1 = r2o_bf16_to_f32(r2o_f32_to_bf16(a1 / L));
+    if (p.output_hadamard) {  // FWHT-128 of the bf16-rounded row (triton_fourq_splitk.py:1000-1006)
+        const float s0 = y0 + y1, s1 = y0 - y1;  // stride 64: within the lane
+        y0 = s0;
+        y1 = s1;
+#pragma unroll
+        for (int stride = 1; stride < 64; stride <<= 1) {
+            const float o0 = __shfl_xor(y0, stride, R2O_WAVE), o1 = __shfl_xor(y1, stride, R2O_WAVE);
+            const bool upper = (tid & stride) != 0;
+            y0 = upper ? o0 - y0 : y0 + o0;
+            y1 = upper ? o1 - y1 : y1 + o1;
+        }
+        y0 *= 0.08838834764831845f;
+        y1 *= 0.08838834764831845f;
+    }
+    uint16_t* orow = p.out + (b * p.hq + hqi) * 128;
+    orow[tid] = (uint16_t)r2o_f32_to_bf16(y0);
+    orow[tid + 64] = (uint16_t)r2o_f32_to_bf16(y1);
 
     if (p.do_append && hqi < p.hkv) {  // fused Recent-FP append (triton_fourq_splitk.py:1007-1020)
         const r2o_request_desc& rq = p.reqs[b];
         const int64_t pos = p.recent_len[b];
-        rq.recent_k[(hqi * rq.recent_capacity + pos) * 128 + d] = p.append_k[(b * p.hkv + hqi) * 128 + d];
-        rq.recent_v[(hqi * rq.recent_capacity + pos) * 128 + d] = p.append_v[(b * p.hkv + hqi) * 128 + d];
-        if (hqi == 0 && d == 0) {
+        const int64_t dst = (hqi * rq.recent_capacity + pos) * 128, src = (b * p.hkv + hqi) * 128;
+        rq.recent_k[dst + tid] = p.append_k[src + tid];
+        rq.recent_k[dst + tid + 64] = p.append_k[src + tid + 64];
+        rq.recent_v[dst + tid] = p.append_v[src + tid];
+        rq.recent_v[dst + tid + 64] = p.append_v[src + tid + 64];
+        if (hqi == 0 && tid == 0) {
             rq.recent_global[pos] = p.append_global[b];
             rq.recent_logical[pos] = p.append_logical[b];
             *rq.recent_length = (int32_t)(pos + 1);
@@ -641,6 +648,7 @@ int validate(const r2o_decode_params* p) {
     if (p->q_dtype != 0 && p->q_dtype != 1) return R2O_EINVAL;
     if (p->page_size <= 0) return R2O_EINVAL;
     if (p->do_append && (!p->append_k || !p->append_v)) return R2O_EINVAL;
+    if (reinterpret_cast<uintptr_t>(p->partial_out) % 16) return R2O_EINVAL;  // 16-byte vector rows
     return R2O_OK;
 }
 
@@ -660,7 +668,7 @@ int r2o_decode_partial(const r2o_decode_params* params, void* stream) {
 int r2o_decode_combine(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)params->hq, (unsigned)params->batch), dim3(1024), 0,
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)params->hq, (unsigned)params->batch), dim3(512), 0,
                        (hipStream_t)stream, *params);
     R2O_CHECK_LAUNCH();
     return R2O_OK;

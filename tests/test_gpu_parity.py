@@ -159,6 +159,30 @@ def test_decode_matches_oracle(case, hadamard):
     _compare(out, want, f"case {case} hadamard {hadamard}")
 
 
+def test_decode_long_group_combine():
+    """One KV head over 40k tokens: several hundred partial slots merged by one combine group."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    cfg = DecodeConfig("long", 8, 1, (40960 + 128,), (0.15, 0.45, 0.4), recent=128, superblock=32, group=32)
+    data = make_request(cfg, 40960 + 128, seed=77, device=dev)
+    cache = build_request_cache(cfg, data)
+    ws = ro.allocate_splitk_workspace(cache, num_query_heads=8)
+    ex = ro.prepare_splitk_executor(cache, ws, output_hadamard=True)
+    sizes = torch.diff(ex.group_begin.cpu())
+    print(f"long group: {int(sizes.max())} slots", flush=True)
+    oc = _oracle_for(data, cfg)
+    q = bf16_bits_to_f32(_bf16_np(data.query))
+    want = output_transform(mixed_reference(q, oc), True)
+    for call in range(2):
+        out = ex(data.query.contiguous())
+        torch.cuda.synchronize()
+        _compare(out, want, f"long group call {call}")
+
+
 def test_fused_append_then_flush_matches_oracle():
     import r2omni_amd as ro
     from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
