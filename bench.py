@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 SSPA packed-KV decode attention (one line of JSON on stdout).
 
-Workload (the north-star shape): Qwen2.5-Omni-7B attention geometry
+Workload (the headline decode shape): Qwen2.5-Omni-7B attention geometry
 (28 query / 4 KV heads, head_dim 128), batch 4 with ragged contexts 8k/16k/32k/64k, INT4 keys,
 BF16/INT4/INT2 value pages at 15/45/40 %, 128-token BF16 Recent-FP window.  Synthetic seeded
 data.  A step is one decode-attention layer call (split-K partial + combine) over the batch.
@@ -114,7 +114,7 @@ def main() -> int:
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the decode path "
                                    "shards by (request, kv head) or token range across GPUs by design, "
-                                   "see DESIGN.md, but no multi-GPU run is implemented)"}))
+                                   "but no multi-GPU run is implemented)"}))
         return 2
 
     import torch

@@ -10,7 +10,8 @@
  *   - launches asynchronously on that stream and allocates nothing;
  *   - returns 0 on success, R2O_EINVAL for an argument the kernel's grid cannot honour
  *     (checked on the host before any launch), R2O_ELAUNCH if the launch itself failed.
- * Tensor layouts are the reference's "wire format"  so caches built by the
+ * Tensor layouts are the reference's "wire format" (compact_int4_key.py:83-110, quantization.py:19-116,
+ * int2_reference.py:96-151) so caches built by the
  * reference and by this library are byte-identical.
  *
  * dtype codes: 0 = bfloat16, 1 = float16 (element type of K/V/Q rows).
@@ -72,7 +73,8 @@ typedef struct r2o_work_item {
     int64_t kvh;
     int64_t kind;      /* 0 = FP-V (bf16), 1 = INT4-V, 2 = INT2-V, 3 = Recent-FP (bf16 K and V) */
     int64_t tile0;     /* arena position of the first tile (multiple of 32)                      */
-    int64_t ntiles;
+    int64_t ntiles;    /* <= 64 / 120 / 240 tiles at superblock 32 / 64 / 128 (each wave's quarter */
+                       /* must touch at most 16 K superblocks, whose operands are staged in LDS)  */
     int64_t lo;        /* valid arena positions [lo, hi)                                          */
     int64_t hi;
     int64_t v_delta;

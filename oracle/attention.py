@@ -8,11 +8,11 @@ then divide.  The fused output transform of the split-K reduce
 (triton_fourq_splitk.py:1000-1006) rounds to bf16, applies the orthonormal 128-point FWHT in
 fp32 and rounds to bf16 again.
 
-Pinning (tests/test_oracle_attention.py, tests/test_oracle_golden.py):
+Pinning (tests/test_oracle_golden.py, tests/test_oracle_quant.py):
   * the reference's own outputs on three golden caches (before and after a flush);
-  * brute force: a single softmax over the concatenated tokens equals the pool merge, and any
+  * brute force: a float64 softmax over the concatenated tokens with the GQA head map
+    kv = h // GQA (reference tests/test_gqa_contract.py:6-13) equals the pool merge, and any
     partition of the tokens gives the same result (merge invariance);
-  * the GQA head map kv = h // GQA (reference tests/test_gqa_contract.py:6-13);
   * FWHT: H.H = I and FWHT(e0) = 1/sqrt(128) * ones.
 """
 from __future__ import annotations

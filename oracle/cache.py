@@ -9,7 +9,7 @@ Follows, for the released ``v_fourq_k_int4_compact`` cache with INT2 generated v
 
 Pinning: tests/test_oracle_golden.py compares every arena byte, scale, zero point, ring row and
 pool count against fixtures written by the reference's own CPU path (tests/golden/make_golden.py),
-before and after a flush with a partial K tail.  tests/test_oracle_cache.py checks the
+before and after a flush with a partial K tail.  tests/test_oracle_quant.py checks the
 reference's own invariants (tests/test_active_cache_storage.py:72-94: 129 appends on a 128-token
 ring give 128 flushed tokens and one active token) and the FP/INT4/INT2 token-order partition.
 """

@@ -7,19 +7,22 @@
 //   QK  S^T[tok, h] = sum_c K[tok, c] * Q'[h, c]  as f16 MFMA on the raw INT4 codes:
 //       the A operand is (1024 + code) built with one and-or per two nibbles, the B operand is
 //       Q' = q * s (per-channel scale of the tile's K superblock, scaled by D^-1/2 * log2 e),
-//       and the C operand starts at -sum_c Q'[h, c] * (1024 + z_c), itself one MFMA per
-//       superblock, so the MFMA chain returns q . (code - z) * s exactly as the dequantised dot.
+//       and -sum_c Q'[h, c] * (1024 + z_c) is added by one more MFMA per channel block, so the
+//       MFMA chain returns q . (code - z) * s exactly as the dequantised dot.  The per-superblock
+//       (s, -(1024 + z)) operand pairs are written at pack time and staged in LDS per item.
 //       Recent-FP tiles use a bf16 MFMA on the bf16 K rows.
-//   PV  O[h, d] += sum_tok P[h, tok] V[tok, d]: V rows are staged in LDS in their packed form
-//       and read back transposed per lane (8 tokens of 8 adjacent dims) so that the MFMA B
-//       operand holds consecutive tokens.  BF16 V: bf16 MFMA.  INT4 V: the per-token scale is
-//       folded into P (P' = p * s) and the signed codes enter exactly as f16 ((1032 + c) built
-//       with one and-or, minus 1032).  INT2 V: (c - z) * s is formed in f16 per element.
+//   PV  O[h, d] += sum_tok P[h, tok] V[tok, d]: every lane loads, straight into registers, the
+//       8 adjacent dims 8*l16.. of its 8 tokens, which is the MFMA B operand of 8 consecutive
+//       tokens after a byte permute (output dim 8*l16 + q of MFMA q).  BF16 V: bf16 MFMA.
+//       INT4 V: the per-token scale is folded into P (P' = p * s) and the signed codes enter
+//       exactly as f16 (1032 + c, built with one xor and one and-or), the 1032 bias being
+//       removed by one more MFMA.  INT2 V: (c - z) * s is formed in f16 per element.
+//   Pool tiles are prefetched into registers one (BF16) or two (INT4/INT2) tiles ahead.
 // The 4 waves' states are merged in LDS and one (max, sum, acc[GQA][128]) partial is written.
 //
-// Combine pass: one 128-thread block per (request, query head) merges the partials of its
-// (request, kv head) group, divides, rounds to bf16, optionally applies the 128-point FWHT and
-// performs the fused Recent-FP append of the step's K/V row and metadata.
+// Combine pass: one block per (request, query head) merges the partials of its (request,
+// kv head) group, divides, rounds to bf16, optionally applies the 128-point FWHT and performs
+// the fused Recent-FP append of the step's K/V row and metadata.
 //
 // Semantics follow triton_fourq_splitk.py:456-1020 (tile attention, exact state merge, fused
 // append :1007-1020, output Hadamard :1000-1006) and the oracle triton_fourq_attention.py:72-125.
@@ -30,20 +33,11 @@ namespace {
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kStageBytes = 8192;                   // per wave: 32 rows x 256 B (bf16 V)
-constexpr int kRowI4 = 80;                          // padded LDS row stride for INT4 V (64 B)
-constexpr int kRowI2 = 48;                          // padded LDS row stride for INT2 V (32 B)
 constexpr int kMergeFloats = 16 + 16 + 16 * 128;    // per wave: m, l, acc
 constexpr int kSmemBytes = (kWaves * kMergeFloats * 4 > kWaves * kStageBytes) ? kWaves * kMergeFloats * 4
                                                                                 : kWaves * kStageBytes;
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
-
-__device__ __forceinline__ void wave_lds_fence() {
-    // LDS traffic of one wave is processed in order; keep the compiler from reordering the
-    // staging writes and the transposed reads across this point and drain outstanding ops.
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-}
 
 // Lane's 8 tokens of a 32-token tile, in MFMA K order: tokens 4g..4g+3 then 16+4g..16+4g+3.
 __device__ __forceinline__ int tile_token(int g, int k) { return (k < 4) ? 4 * g + k : 16 + 4 * g + (k - 4); }
@@ -90,14 +84,19 @@ __device__ __forceinline__ float head_max(float x) {
 }
 
 // Online-softmax update for one tile: sv are the lane's 8 logits (log2 domain, -inf = masked).
-// Returns the probabilities in pk and rescales the running state (and `extra`, a 4-row
-// accumulator in the PV output layout) when the max grows.
+// Returns the probabilities in pk.  The running max is raised lazily: only when a tile's max
+// exceeds it by more than kRescaleSlack (log2 units) are the state and `extra` (a 4-row
+// accumulator in the PV output layout) rescaled, so p = exp2(s - m) stays below
+// 2^kRescaleSlack while the rescale branch is taken only a few times per work item.  (m, l, acc)
+// always refer to the same m, so the state and its later merges are exact.
+constexpr float kRescaleSlack = 4.f;
+
 __device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8], float (&pk)[8], int g,
                                              r2o_f4* extra = nullptr) {
     float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
     tmax = head_max(tmax);
-    const float m_new = fmaxf(st.m, tmax);
-    if (__any(m_new > st.m)) {
+    if (__any(tmax > st.m + kRescaleSlack)) {  // -inf + slack = -inf: the first valid tile rescales
+        const float m_new = fmaxf(st.m, tmax);
         // exp2(-inf) = 0 when the state was empty; a head with no valid token keeps alpha = 1
         const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
         st.l *= alpha;
@@ -229,7 +228,7 @@ struct SegState {
 
 template <int KIND>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
-                                            int a0, int l16, int g, bool head_ok, const unsigned char* kops,
+                                            int a0, int l16, int g, const unsigned char* kops,
                                             int sb0, const TileRegs<KIND>& cur) {
     // ---- QK^T per MFMA j: Q'_j = q * s (superblock scale pairs from LDS), the correction
     //      -sum Q'_j (1024 + z) as the C operand, then the two 16-token groups.
@@ -254,18 +253,18 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
     s[0] += corr;
     s[1] += corr;
 
-    // ---- softmax (masks only on partial tiles and padded heads)
+    // ---- softmax (masks only on partial tiles; padded heads have q = 0, so their logits are
+    //      0: harmless, and their rows are never written out)
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);
     float sv[8], pk[8];
     if (full) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) sv[k] = head_ok ? s[k >> 2][k & 3] : -INFINITY;
+        for (int k = 0; k < 8; ++k) sv[k] = s[k >> 2][k & 3];
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int pos = a0 + tile_token(g, k);
-            const bool ok = head_ok & (pos >= c.lo) & (pos < c.hi);
-            sv[k] = ok ? s[k >> 2][k & 3] : -INFINITY;
+            sv[k] = ((pos >= c.lo) & (pos < c.hi)) ? s[k >> 2][k & 3] : -INFINITY;
         }
     }
     softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
@@ -335,7 +334,6 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int t_end = min((int)it.ntiles, t_begin + per);
     if (t_begin >= t_end) return;
     unsigned char* kops = smem + wave * kStageBytes;
-    const bool head_ok = l16 < gqa;
 
     SegCtx c;
     c.kcode = rq.k_packed + (kvh * rq.k_capacity + l16) * 64 + 16 * g;
@@ -361,7 +359,8 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int sb1 = (base + 32 * t_end - 1) >> c.sb_shift;
     {
         const uint32_t* src = rq.k_operands + kvh * rq.k_superblocks * 128 + (int64_t)sb0 * 128;
-        const int nchunks = (sb1 - sb0 + 1) * 32;  // 16-byte chunks
+        // 16-byte chunks; items larger than the stage (a planner contract) are clamped, not overrun
+        const int nchunks = min((sb1 - sb0 + 1) * 32, kStageBytes / 16);
         for (int ch0 = 0; ch0 < nchunks; ch0 += 64) {
             const int ch = min(ch0 + lane, nchunks - 1);
             lds_copy16(src + ch * 4, kops, ch0 * 16);
@@ -381,10 +380,10 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
         __builtin_amdgcn_wave_barrier();
         for (int i = 0; i < n; i += 2) {
             if (i + 1 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 1), g, r1);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, head_ok, kops, sb0, r0);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, kops, sb0, r0);
             if (i + 1 >= n) break;
             if (i + 2 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 2), g, r0);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, head_ok, kops, sb0, r1);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, kops, sb0, r1);
         }
     } else {
         TileRegs<KIND> r0, r1, r2;
@@ -394,13 +393,13 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
         __builtin_amdgcn_wave_barrier();
         for (int i = 0; i < n; i += 3) {
             if (i + 2 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 2), g, r2);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, head_ok, kops, sb0, r0);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, kops, sb0, r0);
             if (i + 1 >= n) break;
             if (i + 3 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 3), g, r0);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, head_ok, kops, sb0, r1);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, kops, sb0, r1);
             if (i + 2 >= n) break;
             if (i + 4 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 4), g, r1);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 2), l16, g, head_ok, kops, sb0, r2);
+            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 2), l16, g, kops, sb0, r2);
         }
     }
     if constexpr (KIND == kI4) {
@@ -409,10 +408,11 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     }
 }
 
-// Recent-FP ring tiles (bf16 K and V, plus the fused-append token): at most a few tiles per
-// item, loaded synchronously.
+// Recent-FP ring tiles (bf16 K and V, plus the fused-append token).  Every load of a tile is
+// issued before any is used (rows past the valid end read the last valid row, whose
+// probability is 0); a tile with no valid token is skipped.
 __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
-                           unsigned char* smem, WaveState& st) {
+                           WaveState& st) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
@@ -420,38 +420,42 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     const int per = (int)((it.ntiles + kWaves - 1) / kWaves);
     const int t_begin = wave * per;
     const int t_end = min((int)it.ntiles, t_begin + per);
-    unsigned char* stage = smem + wave * kStageBytes;
+    const int recent_len = p.recent_len[b];
+    const bool app = p.do_append != 0;
+    const int valid_end = recent_len + (app ? 1 : 0);
+    if (t_begin >= t_end || valid_end == 0) return;
     const float qscale = p.sm_scale * kLog2e;
     const bool head_ok = l16 < gqa;
     uint32_t qp[4][4];
     load_query<true>(p, b, kvh, gqa, l16, g, qscale, qp);
-    const int recent_len = p.recent_len[b];
-    const bool app = p.do_append != 0;
-    const int valid_end = recent_len + (app ? 1 : 0);
+    const uint16_t* ring_k = rq.recent_k + kvh * rq.recent_capacity * 128;
+    const uint16_t* ring_v = rq.recent_v + kvh * rq.recent_capacity * 128;
+    const uint16_t* new_k = app ? p.append_k + (b * p.hkv + kvh) * 128 : ring_k;
+    const uint16_t* new_v = app ? p.append_v + (b * p.hkv + kvh) * 128 : ring_v;
     for (int t = t_begin; t < t_end; ++t) {
         const int a0 = (int)it.tile0 + 32 * t;
+        if (a0 >= valid_end) break;  // wave-uniform
+        r2o_u4 kr[2][4], R[8];
+#pragma unroll
+        for (int mg = 0; mg < 2; ++mg) {
+            const int slot = min(a0 + 16 * mg + l16, valid_end - 1);
+            const uint16_t* krow = slot == recent_len ? new_k : ring_k + slot * 128;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kr[mg][j] = r2o_ldg(reinterpret_cast<const r2o_u4*>(krow + 32 * g) + j);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int slot = min(a0 + tile_token(g, k), valid_end - 1);
+            const uint16_t* vrow = slot == recent_len ? new_v : ring_v + slot * 128;
+            R[k] = r2o_ldg(reinterpret_cast<const r2o_u4*>(vrow + 8 * l16));
+        }
         r2o_f4 s[2];
 #pragma unroll
         for (int mg = 0; mg < 2; ++mg) {
-            const int slot = a0 + 16 * mg + l16;
-            const uint16_t* krow = nullptr;
-            if (slot < recent_len) krow = rq.recent_k + (kvh * rq.recent_capacity + slot) * 128;
-            else if (app && slot == recent_len) krow = p.append_k + (b * p.hkv + kvh) * 128;
             r2o_f4 acc = {0, 0, 0, 0};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const r2o_u4 a = krow ? r2o_ldg(reinterpret_cast<const r2o_u4*>(krow + 32 * g) + j) : r2o_u4{0, 0, 0, 0};
-                acc = r2o_mfma_bf16(a, r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
-            }
+            for (int j = 0; j < 4; ++j) acc = r2o_mfma_bf16(kr[mg][j], r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
             s[mg] = acc * qscale;
-        }
-#pragma unroll
-        for (int itn = 0; itn < 8; ++itn) {
-            const int c = itn * 64 + lane, r = c >> 4, col = c & 15;
-            r2o_u4 v = {0, 0, 0, 0};
-            if (a0 + r < recent_len) v = r2o_ldg(reinterpret_cast<const r2o_u4*>(rq.recent_v + (kvh * rq.recent_capacity + a0 + r) * 128) + col);
-            else if (a0 + r < valid_end) v = r2o_ldg(reinterpret_cast<const r2o_u4*>(p.append_v + (b * p.hkv + kvh) * 128) + col);
-            *reinterpret_cast<r2o_u4*>(stage + r * 256 + col * 16) = v;
         }
         float sv[8], pk[8];
 #pragma unroll
@@ -460,12 +464,7 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
         r2o_u4 ap;
 #pragma unroll
         for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
-        wave_lds_fence();
-        r2o_u4 R[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) R[k] = *reinterpret_cast<const r2o_u4*>(stage + tile_token(g, k) * 256 + 16 * l16);
         pv_bf16(st, ap, R);
-        wave_lds_fence();
     }
 }
 
@@ -487,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
         case kFP: run_segment<kFP>(p, it, rq, smem, st); break;
         case kI4: run_segment<kI4>(p, it, rq, smem, st); break;
         case kI2: run_segment<kI2>(p, it, rq, smem, st); break;
-        default: run_recent(p, it, rq, smem, st); break;
+        default: run_recent(p, it, rq, st); break;
     }
 
     // ---- per-wave epilogue: reduce l (and u) over the 4 lane groups of each head

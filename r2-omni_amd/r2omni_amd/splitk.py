@@ -13,6 +13,8 @@ workspace is one split-K work item (a run of 32-token tiles handled by one workg
 """
 from __future__ import annotations
 
+import heapq
+
 import ctypes
 from dataclasses import dataclass, field
 from typing import Sequence
@@ -24,7 +26,12 @@ from .cache import ThreePrecisionCache
 
 TILE = 32
 _MIN_TILES_PER_ITEM = 4      # one tile per wave of the 4-wave workgroup
-_MAX_TILES_PER_ITEM = 64       # 16 tiles per wave: K operands of <= 16 superblocks fit the LDS stage
+
+
+def _max_tiles_per_item(superblock: int) -> int:
+    """Largest item whose per-wave share of K superblock operands (<= 16 blocks) fits in LDS."""
+    per_wave = 16 if superblock == TILE else 15 * superblock // TILE  # +1 block when unaligned
+    return 4 * per_wave
 
 
 @dataclass
@@ -64,24 +71,25 @@ def _tiles(lo: int, hi: int) -> tuple[int, int]:
     return t0, -(-(hi - t0) // TILE)
 
 
+# Relative cost of one 32-token tile per kind (partial kernel, measured on MI355X): the
+# planner sizes items so that every workgroup slot gets about the same amount of work.
+_TILE_COST = {_lib.KIND_FP: 1.2, _lib.KIND_INT4: 1.0, _lib.KIND_INT2: 1.3, _lib.KIND_RECENT: 2.0}
+
+
 def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_int2: int = 0):
     """Split every (request, kv head, pool segment) into runs of 32-token tiles.
 
-    About two equal workgroups per CU (the partial kernel runs two 4-wave workgroups per CU),
-    at least one tile per wave.  Items keep a partial slot in (request, kv head) order, so the
-    combine reads one contiguous slot range per group, and are launched largest first so the
-    segment-boundary fragments fill in behind the full-size items.
+    The partial kernel runs two 4-wave workgroups per CU, so the plan aims at no more than
+    2 x CUs items of about equal cost (tiles weighted by kind), each a multiple of 4 tiles (one
+    share per wave): all items then start together and finish together.  Items keep a partial
+    slot in (request, kv head) order, so the combine reads one contiguous slot range per group,
+    and are launched largest first.
     Returns (items [n, 9] int64 in launch order, group_begin [B*hkv + 1] int32) on the host.
     """
     segs = [_segments(c, extra_int2) for c in caches]
-    total_tiles = 0
-    for c, ss in zip(caches, segs):
-        total_tiles += hkv * (sum(_tiles(lo, hi)[1] for _, lo, hi, _ in ss) + c.recent_fp_pool.capacity // TILE)
-    target = 2 * max(1, num_cus)
-    tpi = -(-total_tiles // target)
-    tpi = max(_MIN_TILES_PER_ITEM, min(_MAX_TILES_PER_ITEM, -(-tpi // 4) * 4))
-    items = []
-    begins = [0]
+    ck = getattr(caches[0], "compact_key", None)
+    max_tiles = _max_tiles_per_item(ck.superblock_size if ck is not None else TILE)
+    runs = []  # (req, head, kind, first tile position, tiles, lo, hi, v_delta)
     for r, (c, ss) in enumerate(zip(caches, segs)):
         rcap = c.recent_fp_pool.capacity
         if rcap % TILE:
@@ -89,13 +97,40 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
         for h in range(hkv):
             for kind, lo, hi, vd in ss:
                 t0, nt = _tiles(lo, hi)
-                for first in range(0, nt, tpi):
-                    items.append([r, h, kind, t0 + TILE * first, min(tpi, nt - first), lo, hi, vd, len(items)])
-            for first in range(0, rcap // TILE, tpi):
-                items.append([r, h, _lib.KIND_RECENT, TILE * first, min(tpi, rcap // TILE - first), 0, rcap, 0,
-                              len(items)])
+                runs.append((r, h, kind, t0, nt, lo, hi, vd))
+            runs.append((r, h, _lib.KIND_RECENT, 0, rcap // TILE, 0, rcap, 0))
+    # Water-filling: give one more item to the run whose items are currently the most
+    # expensive until the workgroup slots are used up (or no run can be split further).
+    target = 2 * max(1, num_cus)
+    counts = [max(1, -(-run[4] // max_tiles)) for run in runs]
+
+    def item_cost(i: int) -> float:
+        nt = runs[i][4]
+        per = -(-nt // counts[i])
+        return (-(-per // 4) * 4) * _TILE_COST[runs[i][2]]
+
+    heap = [(-item_cost(i), i) for i in range(len(runs))]
+    heapq.heapify(heap)
+    total = sum(counts)
+    while total < target and heap:
+        _, i = heapq.heappop(heap)
+        if -(-runs[i][4] // (counts[i] + 1)) < _MIN_TILES_PER_ITEM:
+            continue  # already at the smallest useful item size
+        counts[i] += 1
+        total += 1
+        heapq.heappush(heap, (-item_cost(i), i))
+    items = []
+    begins = [0]
+    group = (0, 0)
+    for (r, h, kind, t0, nt, lo, hi, vd), n_items in zip(runs, counts):
+        if (r, h) != group:
             begins.append(len(items))
-    items.sort(key=lambda it: -it[4])  # stable: largest first, ties keep slot order
+            group = (r, h)
+        n = -(-(-(-nt // n_items)) // 4) * 4  # tiles per item: even split, rounded up to 4
+        for first in range(0, nt, n):
+            items.append([r, h, kind, t0 + TILE * first, min(n, nt - first), lo, hi, vd, len(items)])
+    begins.append(len(items))
+    items.sort(key=lambda it: -it[4] * _TILE_COST[it[2]])  # stable: largest first, ties keep slot order
     return torch.tensor(items, dtype=torch.int64), torch.tensor(begins, dtype=torch.int32)
 
 

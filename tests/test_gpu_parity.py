@@ -1,6 +1,6 @@
 """GPU parity of the HIP path against the CPU oracle and the reference-written golden fixtures.
 
-Bars (BASELINE north star): packing and quantisation bit-exact; attention output within
+Bars: packing and quantisation bit-exact; attention output within
 max-abs 2e-2 and mean-abs 2e-3 of the fp32 dequantise-then-softmax oracle.
 """
 import numpy as np
