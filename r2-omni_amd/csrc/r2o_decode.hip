@@ -32,10 +32,15 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kStageBytes = 8192;                   // per wave: 32 rows x 256 B (bf16 V)
+constexpr int kOpsBytes = 8192;                     // BF16 tiles: K operands of <= 16 superblocks
+constexpr int kDmaStages = 4;                       // INT4/INT2 tiles: LDS ring depth per wave
+constexpr int kDmaStage = 4736;                     // bytes of one INT4/INT2 tile stage
+constexpr int kDmaPerTile = 6;                      // LDS DMA instructions per INT4/INT2 tile
+constexpr int kWaveLds = kDmaStages * kDmaStage;    // per-wave LDS area (>= kOpsBytes)
 constexpr int kMergeFloats = 16 + 16 + 16 * 128;    // per wave: m, l, acc
-constexpr int kSmemBytes = (kWaves * kMergeFloats * 4 > kWaves * kStageBytes) ? kWaves * kMergeFloats * 4
-                                                                                : kWaves * kStageBytes;
+constexpr int kSmemBytes = (kWaves * kMergeFloats * 4 > kWaves * kWaveLds) ? kWaves * kMergeFloats * 4
+                                                                             : kWaves * kWaveLds;
+static_assert(kWaveLds >= kOpsBytes, "BF16 operand stage must fit the per-wave LDS area");
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
 
@@ -333,7 +338,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int t_begin = wave * per;
     const int t_end = min((int)it.ntiles, t_begin + per);
     if (t_begin >= t_end) return;
-    unsigned char* kops = smem + wave * kStageBytes;
+    unsigned char* kops = smem + wave * kWaveLds;
 
     SegCtx c;
     c.kcode = rq.k_packed + (kvh * rq.k_capacity + l16) * 64 + 16 * g;
@@ -360,7 +365,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     {
         const uint32_t* src = rq.k_operands + kvh * rq.k_superblocks * 128 + (int64_t)sb0 * 128;
         // 16-byte chunks; items larger than the stage (a planner contract) are clamped, not overrun
-        const int nchunks = min((sb1 - sb0 + 1) * 32, kStageBytes / 16);
+        const int nchunks = min((sb1 - sb0 + 1) * 32, kOpsBytes / 16);
         for (int ch0 = 0; ch0 < nchunks; ch0 += 64) {
             const int ch = min(ch0 + lane, nchunks - 1);
             lds_copy16(src + ch * 4, kops, ch0 * 16);
@@ -401,6 +406,197 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
             if (i + 4 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 4), g, r1);
             seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 2), l16, g, kops, sb0, r2);
         }
+    }
+    if constexpr (KIND == kI4) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st.acc[q] -= ss.bias;
+    }
+}
+
+// ------------------------------------------------------------------ INT4 / INT2 tiles via LDS DMA
+// Every INT4/INT2 tile is moved by six global->LDS DMA instructions (no VGPRs held while in
+// flight) into one stage of a per-wave ring of kDmaStages stages, issued kDmaStages - 1 tiles
+// ahead.  Stage layout (bytes): K codes [0, 2048) | V payload from 2048 | K superblock operands
+// (512) | V metadata.  The 16-byte chunks of K and V are placed so that the transposed
+// per-lane reads of the compute hit distinct LDS banks (see the slot functions).  A DMA of 16
+// bytes per lane fills LDS at lane * 16; one of 1, 2 or 4 bytes per lane fills the low bytes of
+// the dword at lane * 4, so sub-dword metadata rows sit in dword slots.
+template <int KIND>
+struct DmaLayout {
+    static constexpr int kV = 2048;
+    static constexpr int kOps = KIND == kI4 ? 4096 : 3072;
+    static constexpr int kScale = kOps + 512;
+    static constexpr int kZero = kScale + 256;  // INT2 only
+};
+
+// K codes: token t (0..31), 16-byte chunk c (0..3) of its 64-byte row.  Reads: 8 lanes take 8
+// consecutive tokens of one chunk, so the chunk is rotated by (t >> 1) & 3.
+__device__ __forceinline__ int k_slot(int t, int c) { return 4 * t + (c ^ ((t >> 1) & 3)); }
+// INT4 V: token t, chunk c (0..3) of its 64-byte row.  Reads: 32 lanes take chunks 0..3 of
+// tokens t and t + 4, which land in distinct 16-byte bank groups.
+__device__ __forceinline__ int v4_slot(int t, int c) { return 8 * ((t & 3) + 4 * (t >> 3)) + 2 * c + ((t >> 2) & 1); }
+// INT2 V: token t, chunk c (0..1) of its 32-byte row; tokens t, t+4, t+8, t+12 share 8 slots.
+__device__ __forceinline__ int v2_slot(int t, int c) { return 8 * (t & 3) + 32 * (t >> 4) + 2 * ((t >> 2) & 3) + c; }
+
+template <int SIZE>
+__device__ __forceinline__ void dma(const void* gsrc, unsigned char* lds) {
+    const auto g = (const __attribute__((address_space(1))) void*)gsrc;
+    const auto l = (__attribute__((address_space(3))) void*)lds;
+    if constexpr (SIZE == 16) __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+    else if constexpr (SIZE == 4) __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
+    else if constexpr (SIZE == 2) __builtin_amdgcn_global_load_lds(g, l, 2, 0, 0);
+    else __builtin_amdgcn_global_load_lds(g, l, 1, 0, 0);
+}
+
+__device__ __forceinline__ void wait_dma_tiles(int later) {
+    // vmcnt(later * kDmaPerTile): every DMA of the oldest outstanding tile has landed in LDS
+    switch (later) {
+        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // vmcnt(0)
+        case 1: __builtin_amdgcn_s_waitcnt(0x0F76); break;   // vmcnt(6)
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F7C); break;   // vmcnt(12)
+        default: __builtin_amdgcn_s_waitcnt(0x4F72); break;  // vmcnt(18)
+    }
+    static_assert(kDmaStages == 4 && kDmaPerTile == 6, "wait counts assume 4 stages of 6 DMAs");
+}
+
+struct DmaCtx {
+    const uint8_t* kcode;   // K codes of this head
+    const uint32_t* kops;   // K superblock operands of this head
+    const uint8_t* vrows;   // V rows of this head
+    const uint8_t* vscale;  // V scales of this head (bytes)
+    const uint8_t* vzero;   // INT2 zero points of this head
+    int lo, hi, vdelta, sb_shift, groups;
+    int koff0, koff1;       // this lane's K source offset (bytes) for the two K DMAs
+    int vt0, vt1, vc0, vc1; // this lane's V source token / chunk for the V DMAs
+};
+
+template <int KIND>
+__device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char* stage, int lane) {
+    using Lay = DmaLayout<KIND>;
+    dma<16>(c.kcode + a0 * 64 + c.koff0, stage);
+    dma<16>(c.kcode + a0 * 64 + c.koff1, stage + 1024);
+    const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
+    auto row = [&](int t) { return (full ? a0 + t : min(max(a0 + t, c.lo), c.hi - 1)) - c.vdelta; };
+    if constexpr (KIND == kI4) {
+        dma<16>(c.vrows + row(c.vt0) * 64 + c.vc0 * 16, stage + Lay::kV);
+        dma<16>(c.vrows + row(c.vt1) * 64 + c.vc1 * 16, stage + Lay::kV + 1024);
+    } else {
+        dma<16>(c.vrows + row(c.vt0) * 32 + c.vc0 * 16, stage + Lay::kV);
+    }
+    if (lane < 32) dma<16>(c.kops + (a0 >> c.sb_shift) * 128 + lane * 4, stage + Lay::kOps);
+    if constexpr (KIND == kI4) {
+        if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
+    } else if (c.groups == 4) {  // G = 32: 8-byte scale rows, 4-byte zero rows
+        dma<4>(c.vscale + row(lane >> 1) * 8 + (lane & 1) * 4, stage + Lay::kScale);
+        if (lane < 32) dma<4>(c.vzero + row(lane) * 4, stage + Lay::kZero);
+    } else if (c.groups == 2) {
+        if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
+        if (lane < 32) dma<2>(c.vzero + row(lane) * 2, stage + Lay::kZero);
+    } else {
+        if (lane < 32) dma<2>(c.vscale + row(lane) * 2, stage + Lay::kScale);
+        if (lane < 32) dma<1>(c.vzero + row(lane), stage + Lay::kZero);
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void read_stage(const unsigned char* stage, int l16, int g, int gamma, int groups,
+                                           TileRegs<KIND>& tr) {
+    using Lay = DmaLayout<KIND>;
+#pragma unroll
+    for (int mg = 0; mg < 2; ++mg) {
+        const int t = 16 * mg + l16;
+        tr.kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(t, g));
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int t = tile_token(g, k);
+        if constexpr (KIND == kI4) {
+            tr.v[k] = *reinterpret_cast<const uint32_t*>(stage + Lay::kV + 16 * v4_slot(t, l16 >> 2) + 4 * (l16 & 3));
+            tr.vm[k] = *reinterpret_cast<const uint32_t*>(stage + Lay::kScale + 4 * t);
+        } else {  // scale rows: 8 bytes (G = 32) or one dword slot; zero rows: one dword slot
+            tr.v[k] = *reinterpret_cast<const uint16_t*>(stage + Lay::kV + 16 * v2_slot(t, l16 >> 3) + 2 * (l16 & 7));
+            tr.vm[k] = *reinterpret_cast<const uint16_t*>(stage + Lay::kScale + t * (groups == 4 ? 8 : 4) + 2 * gamma);
+            tr.vz[k] = *(stage + Lay::kZero + 4 * t + gamma);
+        }
+    }
+}
+
+template <int KIND>
+__device__ void run_segment_dma(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
+                                unsigned char* smem, WaveState& st) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+    const int gqa = (int)(p.hq / p.hkv);
+    const int64_t kvh = it.kvh, b = it.req;
+    const int per = (int)((it.ntiles + kWaves - 1) / kWaves);
+    const int t_begin = wave * per;
+    const int t_end = min((int)it.ntiles, t_begin + per);
+    if (t_begin >= t_end) return;
+    unsigned char* ring = smem + wave * kWaveLds;
+
+    DmaCtx c;
+    c.kcode = rq.k_packed + kvh * rq.k_capacity * 64;
+    c.kops = rq.k_operands + kvh * rq.k_superblocks * 128;
+    c.lo = (int)it.lo;
+    c.hi = (int)it.hi;
+    c.vdelta = (int)it.v_delta;
+    c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
+    c.groups = (int)(128 / p.int2_group);
+    const int gamma = (8 * l16) / (int)p.int2_group;
+    if constexpr (KIND == kI4) {
+        c.vrows = rq.i4_v + kvh * rq.i4_stride * 64;
+        c.vscale = reinterpret_cast<const uint8_t*>(rq.i4_scale + kvh * rq.i4_stride);
+        c.vzero = nullptr;
+    } else {
+        c.vrows = rq.i2_v + kvh * rq.i2_stride * 32;
+        c.vscale = reinterpret_cast<const uint8_t*>(rq.i2_scale + kvh * rq.i2_stride * c.groups);
+        c.vzero = rq.i2_zero + kvh * rq.i2_stride * c.groups;
+    }
+    {  // lane -> (token, chunk) sources of the K and V DMAs (inverse of the slot functions)
+        const int s0 = lane, s1 = 64 + lane;
+        const int t0 = s0 >> 2, t1 = s1 >> 2;
+        c.koff0 = t0 * 64 + 16 * ((s0 & 3) ^ ((t0 >> 1) & 3));
+        c.koff1 = t1 * 64 + 16 * ((s1 & 3) ^ ((t1 >> 1) & 3));
+        if constexpr (KIND == kI4) {
+            c.vt0 = 8 * (s0 >> 5) + 4 * (s0 & 1) + ((s0 >> 3) & 3);
+            c.vc0 = (s0 >> 1) & 3;
+            c.vt1 = 8 * (s1 >> 5) + 4 * (s1 & 1) + ((s1 >> 3) & 3);
+            c.vc1 = (s1 >> 1) & 3;
+        } else {
+            c.vt0 = 16 * (s0 >> 5) + 4 * ((s0 >> 1) & 3) + ((s0 >> 3) & 3);
+            c.vc0 = s0 & 1;
+            c.vt1 = c.vt0;
+            c.vc1 = c.vc0;
+        }
+    }
+    const int n = t_end - t_begin;
+    const int a_first = (int)it.tile0 + 32 * t_begin;
+#pragma unroll
+    for (int j = 0; j < kDmaStages - 1; ++j)
+        if (j < n) dma_tile<KIND>(c, a_first + 32 * j, ring + j * kDmaStage, lane);
+
+    const VConst vc = make_vconst();
+    SegState<KIND> ss;
+    load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
+    ss.bias = r2o_f4{0, 0, 0, 0};
+    SegCtx sc;  // the mask / superblock fields seg_compute reads
+    sc.lo = c.lo;
+    sc.hi = c.hi;
+    sc.sb_shift = c.sb_shift;
+    for (int i = 0; i < n; ++i) {
+        if (i + kDmaStages - 1 < n) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage being refilled has been read
+            __builtin_amdgcn_wave_barrier();
+            dma_tile<KIND>(c, a_first + 32 * (i + kDmaStages - 1), ring + ((i + kDmaStages - 1) % kDmaStages) * kDmaStage,
+                           lane);
+        }
+        wait_dma_tiles(min(kDmaStages - 1, n - 1 - i));
+        __builtin_amdgcn_wave_barrier();
+        const unsigned char* stage = ring + (i % kDmaStages) * kDmaStage;
+        TileRegs<KIND> cur;
+        read_stage<KIND>(stage, l16, g, gamma, c.groups, cur);
+        const int a0 = a_first + 32 * i;
+        seg_compute<KIND>(sc, st, ss, vc, a0, l16, g, stage + DmaLayout<KIND>::kOps, a0 >> c.sb_shift, cur);
     }
     if constexpr (KIND == kI4) {
 #pragma unroll
@@ -484,8 +680,8 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
 
     switch (it.kind) {
         case kFP: run_segment<kFP>(p, it, rq, smem, st); break;
-        case kI4: run_segment<kI4>(p, it, rq, smem, st); break;
-        case kI2: run_segment<kI2>(p, it, rq, smem, st); break;
+        case kI4: run_segment_dma<kI4>(p, it, rq, smem, st); break;
+        case kI2: run_segment_dma<kI2>(p, it, rq, smem, st); break;
         default: run_recent(p, it, rq, st); break;
     }
 
