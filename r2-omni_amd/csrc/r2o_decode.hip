@@ -96,9 +96,12 @@ __device__ __forceinline__ float head_max(float x) {
 // always refer to the same m, so the state and its later merges are exact.
 constexpr float kRescaleSlack = 4.f;
 
-__device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8], float (&pk)[8], int g,
+template <int N>
+__device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N], float (&pk)[N], int g,
                                              r2o_f4* extra = nullptr) {
-    float tmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+    float tmax = sv[0];
+#pragma unroll
+    for (int k = 1; k < N; ++k) tmax = fmaxf(tmax, sv[k]);
     tmax = head_max(tmax);
     if (__any(tmax > st.m + kRescaleSlack)) {  // -inf + slack = -inf: the first valid tile rescales
         const float m_new = fmaxf(st.m, tmax);
@@ -116,10 +119,15 @@ __device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8]
     }
     const float m_use = st.m == -INFINITY ? 0.f : st.m;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < N; ++k) {
         pk[k] = __builtin_amdgcn_exp2f(sv[k] - m_use);  // exp2(-inf) = 0 for masked tokens
         st.l += pk[k];
     }
+}
+
+__device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8], float (&pk)[8], int g,
+                                             r2o_f4* extra = nullptr) {
+    softmax_step<8>(st, sv, pk, g, extra);
 }
 
 // PV for bf16 V rows held as R[k] = 8 dims (8*l16 ..) of token tile_token(g, k).
@@ -182,19 +190,17 @@ __device__ __forceinline__ void lds_copy16(const void* gsrc, unsigned char* lds_
                                      (__attribute__((address_space(3))) void*)(lds_base + offset), 16, 0, 0);
 }
 
-// Per-item, per-lane addressing of one pool segment (32-bit positions within one head).
+// Per-item, per-lane addressing of a BF16-V segment (32-bit positions within one head).
 struct SegCtx {
     const uint8_t* kcode;    // k_packed of this head + l16*64 + 16g   (+ a0*64 + mg*1024)
     const uint8_t* vrows;    // V rows of this head + lane column offset
-    const void* vmeta;       // INT4: f32 scales of this head; INT2: fp16 scales (+ gamma)
-    const uint8_t* vzero;    // INT2: u8 zero points (+ gamma)
     int lo, hi, vdelta;      // valid arena positions, V row = arena - vdelta
-    int sb_shift, groups;
+    int sb_shift;
 };
 
-template <int KIND>
-__device__ __forceinline__ void issue_seg_tile(const SegCtx& c, int a0, int g, TileRegs<KIND>& tr) {
-    constexpr int kRow = KIND == kFP ? 256 : (KIND == kI4 ? 64 : 32);
+// BF16-V tile straight into registers: the INT4-K codes of token a0 + 16 mg + l16 and, for each
+// of the lane's 8 tokens tile_token(g, k), the 8 V dims 8*l16 .. 8*l16+7 (16 bytes).
+__device__ __forceinline__ void issue_fp_tile(const SegCtx& c, int a0, int g, TileRegs<kFP>& tr) {
     tr.kx[0] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64));
     tr.kx[1] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64 + 1024));
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
@@ -207,22 +213,7 @@ __device__ __forceinline__ void issue_seg_tile(const SegCtx& c, int a0, int g, T
         for (int k = 0; k < 8; ++k) row[k] = min(max(a0 + tile_token(g, k), c.lo), c.hi - 1) - c.vdelta;
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint8_t* src = c.vrows + row[k] * kRow;
-        if constexpr (KIND == kFP) tr.v[k] = r2o_ldg(reinterpret_cast<const r2o_u4*>(src));
-        else if constexpr (KIND == kI4) tr.v[k] = r2o_ldg(reinterpret_cast<const uint32_t*>(src));
-        else tr.v[k] = r2o_ldg(reinterpret_cast<const uint16_t*>(src));
-    }
-    if constexpr (KIND == kI4) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) tr.vm[k] = r2o_ldg(reinterpret_cast<const uint32_t*>(c.vmeta) + row[k]);
-    } else if constexpr (KIND == kI2) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            tr.vm[k] = r2o_ldg(reinterpret_cast<const uint16_t*>(c.vmeta) + row[k] * c.groups);
-            tr.vz[k] = r2o_ldg(c.vzero + row[k] * c.groups);
-        }
-    }
+    for (int k = 0; k < 8; ++k) tr.v[k] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.vrows + row[k] * 256));
 }
 
 template <int KIND>
@@ -231,25 +222,23 @@ struct SegState {
     r2o_f4 bias;         // INT4-V: sum_k P'_k * 1032 per head row (removed at the end)
 };
 
-template <int KIND>
-__device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
-                                            int a0, int l16, int g, const unsigned char* kops,
-                                            int sb0, const TileRegs<KIND>& cur) {
-    // ---- QK^T per MFMA j: Q'_j = q * s (superblock scale pairs from LDS), the correction
-    //      -sum Q'_j (1024 + z) as the C operand, then the two 16-token groups.
-    const int sb = a0 >> c.sb_shift;
-    const r2o_u4* ko = reinterpret_cast<const r2o_u4*>(kops + (sb - sb0) * 512 + g * 128);
-    r2o_f4 s[2] = {r2o_f4{0, 0, 0, 0}, r2o_f4{0, 0, 0, 0}};
+// QK^T of one INT4-K tile: per MFMA j, Q'_j = q * s (superblock scale pairs from LDS), the
+// correction -sum Q'_j (1024 + z) by one MFMA, then the two 16-token groups.
+__device__ __forceinline__ void qk_int4k(const uint32_t (&qp)[4][4], const VConst& vc, const unsigned char* kops_sb,
+                                         int g, const r2o_u4 (&kx)[2], r2o_f4 (&s)[2]) {
+    const r2o_u4* ko = reinterpret_cast<const r2o_u4*>(kops_sb + g * 128);
+    s[0] = r2o_f4{0, 0, 0, 0};
+    s[1] = r2o_f4{0, 0, 0, 0};
     r2o_f4 corr = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const r2o_u4 sj = ko[j], zj = ko[4 + j];
-        const r2o_u4 qj = {r2o_h2_mul(ss.qp[j][0], sj[0]), r2o_h2_mul(ss.qp[j][1], sj[1]),
-                           r2o_h2_mul(ss.qp[j][2], sj[2]), r2o_h2_mul(ss.qp[j][3], sj[3])};
+        const r2o_u4 qj = {r2o_h2_mul(qp[j][0], sj[0]), r2o_h2_mul(qp[j][1], sj[1]), r2o_h2_mul(qp[j][2], sj[2]),
+                           r2o_h2_mul(qp[j][3], sj[3])};
         corr = r2o_mfma_f16(zj, qj, corr);
 #pragma unroll
         for (int mg = 0; mg < 2; ++mg) {
-            const uint32_t w = cur.kx[mg][j];
+            const uint32_t w = kx[mg][j];
             const r2o_u4 a = {(w & vc.nib) | vc.magic, ((w >> 4) & vc.nib) | vc.magic, ((w >> 8) & vc.nib) | vc.magic,
                               ((w >> 12) & vc.nib) | vc.magic};
             s[mg] = r2o_mfma_f16(a, qj, s[mg]);
@@ -257,11 +246,12 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
     }
     s[0] += corr;
     s[1] += corr;
+}
 
-    // ---- softmax (masks only on partial tiles; padded heads have q = 0, so their logits are
-    //      0: harmless, and their rows are never written out)
+// Logits of a tile in the lane's token order (masks only on partial tiles; padded heads have
+// q = 0, so their logits are 0: harmless, and their rows are never written out).
+__device__ __forceinline__ void tile_logits(const SegCtx& c, int a0, int g, const r2o_f4 (&s)[2], float (&sv)[8]) {
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);
-    float sv[8], pk[8];
     if (full) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) sv[k] = s[k >> 2][k & 3];
@@ -272,9 +262,12 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
             sv[k] = ((pos >= c.lo) & (pos < c.hi)) ? s[k >> 2][k & 3] : -INFINITY;
         }
     }
-    softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
+}
 
-    // ---- PV
+// PV of one tile with probabilities pk (the lane's 8 tokens).
+template <int KIND>
+__device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const VConst& vc, const float (&pk)[8],
+                                        const TileRegs<KIND>& cur) {
     r2o_u4 ap;
     if constexpr (KIND == kFP) {
 #pragma unroll
@@ -327,9 +320,22 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
     }
 }
 
+// One tile: QK, masks, online softmax, PV.  `kops_sb` = the tile's superblock operands in LDS.
 template <int KIND>
-__device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
-                            unsigned char* smem, WaveState& st) {
+__device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
+                                            int a0, int g, const unsigned char* kops_sb, const TileRegs<KIND>& cur) {
+    r2o_f4 s[2];
+    qk_int4k(ss.qp, vc, kops_sb, g, cur.kx, s);
+    float sv[8], pk[8];
+    tile_logits(c, a0, g, s, sv);
+    softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
+    pv_tile<KIND>(st, ss, vc, pk, cur);
+}
+
+// BF16-V segment: tiles prefetched one ahead into registers; the K superblock operands of the
+// wave's whole tile range are copied into LDS once per item.
+__device__ void run_segment_fp(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
+                               unsigned char* smem, WaveState& st) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
@@ -342,23 +348,11 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
 
     SegCtx c;
     c.kcode = rq.k_packed + (kvh * rq.k_capacity + l16) * 64 + 16 * g;
+    c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128) + 16 * l16;
     c.lo = (int)it.lo;
     c.hi = (int)it.hi;
     c.vdelta = (int)it.v_delta;
     c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
-    c.groups = (int)(128 / p.int2_group);
-    const int gamma = (8 * l16) / (int)p.int2_group;
-    if (KIND == kFP) {
-        c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128) + 16 * l16;
-    } else if (KIND == kI4) {
-        c.vrows = rq.i4_v + kvh * rq.i4_stride * 64 + 4 * l16;
-        c.vmeta = rq.i4_scale + kvh * rq.i4_stride;
-    } else {
-        c.vrows = rq.i2_v + kvh * rq.i2_stride * 32 + 2 * l16;
-        c.vmeta = rq.i2_scale + kvh * rq.i2_stride * c.groups + gamma;
-        c.vzero = rq.i2_zero + kvh * rq.i2_stride * c.groups + gamma;
-    }
-    // ---- K superblock operands of the wave's tile range -> LDS (one copy per item)
     const int base = (int)it.tile0;
     const int sb0 = (base + 32 * t_begin) >> c.sb_shift;
     const int sb1 = (base + 32 * t_end - 1) >> c.sb_shift;
@@ -372,44 +366,24 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
         }
     }
     const VConst vc = make_vconst();
-    SegState<KIND> ss;
+    SegState<kFP> ss;
     load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
     ss.bias = r2o_f4{0, 0, 0, 0};
 
     const int n = t_end - t_begin;
     const int a_first = base + 32 * t_begin;
-    if constexpr (KIND == kFP) {
-        TileRegs<KIND> r0, r1;
-        issue_seg_tile<KIND>(c, a_first, g, r0);
-        __builtin_amdgcn_s_waitcnt(0);  // K operands (and tile 0) in LDS / registers
-        __builtin_amdgcn_wave_barrier();
-        for (int i = 0; i < n; i += 2) {
-            if (i + 1 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 1), g, r1);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, kops, sb0, r0);
-            if (i + 1 >= n) break;
-            if (i + 2 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 2), g, r0);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, kops, sb0, r1);
-        }
-    } else {
-        TileRegs<KIND> r0, r1, r2;
-        issue_seg_tile<KIND>(c, a_first, g, r0);
-        if (n > 1) issue_seg_tile<KIND>(c, a_first + 32, g, r1);
-        __builtin_amdgcn_s_waitcnt(0);  // K operands (and tiles 0, 1) in LDS / registers
-        __builtin_amdgcn_wave_barrier();
-        for (int i = 0; i < n; i += 3) {
-            if (i + 2 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 2), g, r2);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * i, l16, g, kops, sb0, r0);
-            if (i + 1 >= n) break;
-            if (i + 3 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 3), g, r0);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 1), l16, g, kops, sb0, r1);
-            if (i + 2 >= n) break;
-            if (i + 4 < n) issue_seg_tile<KIND>(c, a_first + 32 * (i + 4), g, r1);
-            seg_compute<KIND>(c, st, ss, vc, a_first + 32 * (i + 2), l16, g, kops, sb0, r2);
-        }
-    }
-    if constexpr (KIND == kI4) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) st.acc[q] -= ss.bias;
+    auto ops = [&](int a0) { return kops + ((a0 >> c.sb_shift) - sb0) * 512; };
+    TileRegs<kFP> r0, r1;
+    issue_fp_tile(c, a_first, g, r0);
+    __builtin_amdgcn_s_waitcnt(0);  // K operands (and tile 0) in LDS / registers
+    __builtin_amdgcn_wave_barrier();
+    for (int i = 0; i < n; i += 2) {
+        const int a0 = a_first + 32 * i;
+        if (i + 1 < n) issue_fp_tile(c, a0 + 32, g, r1);
+        seg_compute<kFP>(c, st, ss, vc, a0, g, ops(a0), r0);
+        if (i + 1 >= n) break;
+        if (i + 2 < n) issue_fp_tile(c, a0 + 64, g, r0);
+        seg_compute<kFP>(c, st, ss, vc, a0 + 32, g, ops(a0 + 32), r1);
     }
 }
 
@@ -498,15 +472,15 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
     }
 }
 
-template <int KIND>
-__device__ __forceinline__ void read_stage(const unsigned char* stage, int l16, int g, int gamma, int groups,
-                                           TileRegs<KIND>& tr) {
-    using Lay = DmaLayout<KIND>;
+__device__ __forceinline__ void read_k(const unsigned char* stage, int l16, int g, r2o_u4 (&kx)[2]) {
 #pragma unroll
-    for (int mg = 0; mg < 2; ++mg) {
-        const int t = 16 * mg + l16;
-        tr.kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(t, g));
-    }
+    for (int mg = 0; mg < 2; ++mg) kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(16 * mg + l16, g));
+}
+
+template <int KIND>
+__device__ __forceinline__ void read_v(const unsigned char* stage, int l16, int g, int gamma, int groups,
+                                       TileRegs<KIND>& tr) {
+    using Lay = DmaLayout<KIND>;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int t = tile_token(g, k);
@@ -579,24 +553,45 @@ __device__ void run_segment_dma(const r2o_decode_params& p, const r2o_work_item&
     SegState<KIND> ss;
     load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
     ss.bias = r2o_f4{0, 0, 0, 0};
-    SegCtx sc;  // the mask / superblock fields seg_compute reads
+    SegCtx sc;  // the mask fields the compute reads
     sc.lo = c.lo;
     sc.hi = c.hi;
     sc.sb_shift = c.sb_shift;
+    // Software pipeline: the QK MFMAs of tile i + 1 are issued before the softmax and PV of
+    // tile i, so the matrix core and the VALU work on different tiles.
+    r2o_f4 s_cur[2];
+    wait_dma_tiles(min(n, kDmaStages - 1) - 1);  // tile 0 has landed
+    __builtin_amdgcn_wave_barrier();
+    {
+        r2o_u4 kx[2];
+        read_k(ring, l16, g, kx);
+        qk_int4k(ss.qp, vc, ring + DmaLayout<KIND>::kOps, g, kx, s_cur);
+    }
     for (int i = 0; i < n; ++i) {
-        if (i + kDmaStages - 1 < n) {
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stage being refilled has been read
+        if (i + kDmaStages - 1 < n) {  // refill the stage tile i - 1 used
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): that stage has been read
             __builtin_amdgcn_wave_barrier();
             dma_tile<KIND>(c, a_first + 32 * (i + kDmaStages - 1), ring + ((i + kDmaStages - 1) % kDmaStages) * kDmaStage,
                            lane);
         }
-        wait_dma_tiles(min(kDmaStages - 1, n - 1 - i));
-        __builtin_amdgcn_wave_barrier();
+        r2o_f4 s_nxt[2];
+        if (i + 1 < n) {
+            wait_dma_tiles(min(n, i + kDmaStages) - (i + 2));  // tile i + 1 has landed
+            __builtin_amdgcn_wave_barrier();
+            const unsigned char* nstage = ring + ((i + 1) % kDmaStages) * kDmaStage;
+            r2o_u4 kx[2];
+            read_k(nstage, l16, g, kx);
+            qk_int4k(ss.qp, vc, nstage + DmaLayout<KIND>::kOps, g, kx, s_nxt);
+        }
         const unsigned char* stage = ring + (i % kDmaStages) * kDmaStage;
         TileRegs<KIND> cur;
-        read_stage<KIND>(stage, l16, g, gamma, c.groups, cur);
-        const int a0 = a_first + 32 * i;
-        seg_compute<KIND>(sc, st, ss, vc, a0, l16, g, stage + DmaLayout<KIND>::kOps, a0 >> c.sb_shift, cur);
+        read_v<KIND>(stage, l16, g, gamma, c.groups, cur);
+        float sv[8], pk[8];
+        tile_logits(sc, a_first + 32 * i, g, s_cur, sv);
+        softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
+        pv_tile<KIND>(st, ss, vc, pk, cur);
+        s_cur[0] = s_nxt[0];
+        s_cur[1] = s_nxt[1];
     }
     if constexpr (KIND == kI4) {
 #pragma unroll
@@ -679,7 +674,7 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP>(p, it, rq, smem, st); break;
+        case kFP: run_segment_fp(p, it, rq, smem, st); break;
         case kI4: run_segment_dma<kI4>(p, it, rq, smem, st); break;
         case kI2: run_segment_dma<kI2>(p, it, rq, smem, st); break;
         default: run_recent(p, it, rq, st); break;
