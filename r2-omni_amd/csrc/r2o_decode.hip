@@ -430,7 +430,7 @@ __device__ __forceinline__ void wait_dma_tiles(int later) {
         case 2: __builtin_amdgcn_s_waitcnt(0x0F7C); break;   // vmcnt(12)
         default: __builtin_amdgcn_s_waitcnt(0x4F72); break;  // vmcnt(18)
     }
-    static_assert(kDmaStages == 4 && kDmaPerTile == 6, "wait counts assume 4 stages of 6 DMAs");
+    static_assert(kDmaStages <= 4 && kDmaPerTile == 6, "wait counts assume at most 4 stages of 6 DMAs");
 }
 
 struct DmaCtx {
@@ -557,41 +557,58 @@ __device__ void run_segment_dma(const r2o_decode_params& p, const r2o_work_item&
     sc.lo = c.lo;
     sc.hi = c.hi;
     sc.sb_shift = c.sb_shift;
+    if constexpr (kDmaStages == 2) {
+        for (int i = 0; i < n; ++i) {
+            if (i + 1 < n) {
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): that stage has been read
+                __builtin_amdgcn_wave_barrier();
+                dma_tile<KIND>(c, a_first + 32 * (i + 1), ring + ((i + 1) & 1) * kDmaStage, lane);
+            }
+            wait_dma_tiles(i + 1 < n ? 1 : 0);
+            __builtin_amdgcn_wave_barrier();
+            const unsigned char* stage = ring + (i & 1) * kDmaStage;
+            TileRegs<KIND> cur;
+            read_k(stage, l16, g, cur.kx);
+            read_v<KIND>(stage, l16, g, gamma, c.groups, cur);
+            seg_compute<KIND>(sc, st, ss, vc, a_first + 32 * i, g, stage + DmaLayout<KIND>::kOps, cur);
+        }
+    } else {
     // Software pipeline: the QK MFMAs of tile i + 1 are issued before the softmax and PV of
-    // tile i, so the matrix core and the VALU work on different tiles.
-    r2o_f4 s_cur[2];
-    wait_dma_tiles(min(n, kDmaStages - 1) - 1);  // tile 0 has landed
-    __builtin_amdgcn_wave_barrier();
-    {
-        r2o_u4 kx[2];
-        read_k(ring, l16, g, kx);
-        qk_int4k(ss.qp, vc, ring + DmaLayout<KIND>::kOps, g, kx, s_cur);
-    }
-    for (int i = 0; i < n; ++i) {
-        if (i + kDmaStages - 1 < n) {  // refill the stage tile i - 1 used
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): that stage has been read
-            __builtin_amdgcn_wave_barrier();
-            dma_tile<KIND>(c, a_first + 32 * (i + kDmaStages - 1), ring + ((i + kDmaStages - 1) % kDmaStages) * kDmaStage,
-                           lane);
-        }
-        r2o_f4 s_nxt[2];
-        if (i + 1 < n) {
-            wait_dma_tiles(min(n, i + kDmaStages) - (i + 2));  // tile i + 1 has landed
-            __builtin_amdgcn_wave_barrier();
-            const unsigned char* nstage = ring + ((i + 1) % kDmaStages) * kDmaStage;
+        // tile i, so the matrix core and the VALU work on different tiles.
+        r2o_f4 s_cur[2];
+        wait_dma_tiles(min(n, kDmaStages - 1) - 1);  // tile 0 has landed
+        __builtin_amdgcn_wave_barrier();
+        {
             r2o_u4 kx[2];
-            read_k(nstage, l16, g, kx);
-            qk_int4k(ss.qp, vc, nstage + DmaLayout<KIND>::kOps, g, kx, s_nxt);
+            read_k(ring, l16, g, kx);
+            qk_int4k(ss.qp, vc, ring + DmaLayout<KIND>::kOps, g, kx, s_cur);
         }
-        const unsigned char* stage = ring + (i % kDmaStages) * kDmaStage;
-        TileRegs<KIND> cur;
-        read_v<KIND>(stage, l16, g, gamma, c.groups, cur);
-        float sv[8], pk[8];
-        tile_logits(sc, a_first + 32 * i, g, s_cur, sv);
-        softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
-        pv_tile<KIND>(st, ss, vc, pk, cur);
-        s_cur[0] = s_nxt[0];
-        s_cur[1] = s_nxt[1];
+        for (int i = 0; i < n; ++i) {
+            if (i + kDmaStages - 1 < n) {  // refill the stage tile i - 1 used
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): that stage has been read
+                __builtin_amdgcn_wave_barrier();
+                dma_tile<KIND>(c, a_first + 32 * (i + kDmaStages - 1), ring + ((i + kDmaStages - 1) % kDmaStages) * kDmaStage,
+                               lane);
+            }
+            r2o_f4 s_nxt[2];
+            if (i + 1 < n) {
+                wait_dma_tiles(min(n, i + kDmaStages) - (i + 2));  // tile i + 1 has landed
+                __builtin_amdgcn_wave_barrier();
+                const unsigned char* nstage = ring + ((i + 1) % kDmaStages) * kDmaStage;
+                r2o_u4 kx[2];
+                read_k(nstage, l16, g, kx);
+                qk_int4k(ss.qp, vc, nstage + DmaLayout<KIND>::kOps, g, kx, s_nxt);
+            }
+            const unsigned char* stage = ring + (i % kDmaStages) * kDmaStage;
+            TileRegs<KIND> cur;
+            read_v<KIND>(stage, l16, g, gamma, c.groups, cur);
+            float sv[8], pk[8];
+            tile_logits(sc, a_first + 32 * i, g, s_cur, sv);
+            softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
+            pv_tile<KIND>(st, ss, vc, pk, cur);
+            s_cur[0] = s_nxt[0];
+            s_cur[1] = s_nxt[1];
+        }
     }
     if constexpr (KIND == kI4) {
 #pragma unroll

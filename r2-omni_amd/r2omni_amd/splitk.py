@@ -26,6 +26,7 @@ from .cache import ThreePrecisionCache
 
 TILE = 32
 _MIN_TILES_PER_ITEM = 4      # one tile per wave of the 4-wave workgroup
+_BLOCKS_PER_CU = 2           # resident partial-kernel workgroups per CU (LDS / VGPR bound)
 
 
 def _max_tiles_per_item(superblock: int) -> int:
@@ -101,7 +102,7 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
             runs.append((r, h, _lib.KIND_RECENT, 0, rcap // TILE, 0, rcap, 0))
     # Water-filling: give one more item to the run whose items are currently the most
     # expensive until the workgroup slots are used up (or no run can be split further).
-    target = 2 * max(1, num_cus)
+    target = _BLOCKS_PER_CU * max(1, num_cus)
     counts = [max(1, -(-run[4] // max_tiles)) for run in runs]
 
     def item_cost(i: int) -> float:
