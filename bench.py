@@ -95,9 +95,45 @@ def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
         reps += 1
     med = sorted(times)[len(times) // 2]
     nbytes = algorithmic_bytes(caches, hq)
+    what = "request" if len(caches) == 1 else f"{len(caches)} ragged requests"
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"one decode-attention call over the same 4 ragged requests (layer 0), median of {reps} "
-                      f"after 1 warm-up: {med * 1e6:.0f} us/call on {threads} threads (torch CPU fp32 oracle)"}
+            "sample": f"one decode-attention call over the same {what} (layer 0 of the GPU run), median of "
+                      f"{reps} after 1 warm-up: {med * 1e6:.0f} us/call on {threads} threads (torch CPU fp32 "
+                      "oracle: dequantise every pool, softmax, merge)"}
+
+
+def summarize_pmc(directory: str) -> dict:
+    """Mean per-dispatch counter values of a rocprofv3 --pmc CSV run, keyed by kernel then counter."""
+    import collections
+    import csv
+    import glob
+
+    acc = collections.defaultdict(list)
+    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                name = row["Kernel_Name"]
+                kernel = ("decode_partial_kernel" if "decode_partial_kernel" in name else
+                          "decode_combine_kernel" if "decode_combine_kernel" in name else
+                          "copy" if "copyBuffer" in name else None)
+                if kernel:
+                    acc[(kernel, row["Counter_Name"])].append(float(row["Counter_Value"]))
+    out: dict = {}
+    for (kernel, counter), vals in sorted(acc.items()):
+        out.setdefault(kernel, {})[counter] = {"mean": sum(vals) / len(vals), "dispatches": len(vals)}
+    return out
+
+
+def traffic_from_profile() -> tuple[int | None, str | None]:
+    """HBM bytes per partial-kernel launch recorded in the committed PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", "decode_partial_cfg2_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip()), "profiles/decode_partial_cfg2_hbm_traffic.md"
+    return None, None
 
 
 def main() -> int:
@@ -110,7 +146,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (HBM counter calibration)")
+    ap.add_argument("--summarize-pmc", metavar="DIR",
+                    help="only print the mean per-dispatch value of every counter in a rocprofv3 --pmc CSV "
+                         "output directory, per decode kernel (and the calibration copy kernel)")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(args.summarize_pmc)))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the decode path "
                                    "shards by (request, kv head) or token range across GPUs by design, "
@@ -178,6 +220,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         cpu = cpu_baseline(layers[0][0], [layers[0][1][r : r + 1] for r in range(len(cfg.lengths))], cfg.hq)
+    traffic, traffic_src = traffic_from_profile() if args.config == 2 else (None, None)
     line = {
         "metric": "packed-KV decode attn: HBM GB/s (% peak), us/layer @32k ctx; decode tok/s",
         "value": round(gbs, 2),
@@ -198,7 +241,8 @@ def main() -> int:
                    "recent_window": cfg.recent, "k_superblock": cfg.superblock, "int2_group": cfg.group,
                    "rotated_layer_caches": L, "algorithmic_bytes_per_call": nbytes, "output_hadamard": True},
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "decode_partial_kernel", "avg_us": round(ms_partial * 1e3, 3)},
         "cpu_baseline": cpu,
     }
