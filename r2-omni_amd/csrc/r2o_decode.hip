@@ -32,15 +32,18 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kOpsBytes = 8192;                     // BF16 tiles: K operands of <= 16 superblocks
-constexpr int kDmaStages = 4;                       // INT4/INT2 tiles: LDS ring depth per wave
-constexpr int kDmaStage = 4736;                     // bytes of one INT4/INT2 tile stage
-constexpr int kDmaPerTile = 6;                      // LDS DMA instructions per INT4/INT2 tile
-constexpr int kWaveLds = kDmaStages * kDmaStage;    // per-wave LDS area (>= kOpsBytes)
+// Build-time tuning knob (the default is the measured best on MI355X).
+#ifndef R2O_DMA_STAGES
+#define R2O_DMA_STAGES 1          // LDS stages per wave: tiles in flight while one is computed
+#endif
+constexpr int kDmaStages = R2O_DMA_STAGES;
+static_assert(kDmaStages >= 1 && kDmaStages <= 3, "1 to 3 LDS stages per wave");
+constexpr int kStageBytes = 10752;                  // one tile stage (sized for BF16 V, see StageLayout)
+constexpr int kWaveLds = kDmaStages * kStageBytes;  // per-wave LDS ring
 constexpr int kMergeFloats = 16 + 16 + 16 * 128;    // per wave: m, l, acc
 constexpr int kSmemBytes = (kWaves * kMergeFloats * 4 > kWaves * kWaveLds) ? kWaves * kMergeFloats * 4
                                                                              : kWaves * kWaveLds;
-static_assert(kWaveLds >= kOpsBytes, "BF16 operand stage must fit the per-wave LDS area");
+constexpr int kBlocksPerCU = 3;                     // resident partial workgroups per CU
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
 
@@ -164,57 +167,38 @@ __device__ __forceinline__ VConst make_vconst() {
 // token's V metadata.  The K superblock operands of the wave's whole tile range are copied into
 // LDS once per work item.  INT4/INT2 tiles are prefetched two tiles ahead (three rotating
 // register sets), bf16 tiles one tile ahead.
+// Registers of one tile, read from its LDS stage: INT4-K codes of tokens 16 mg + l16 (channels
+// 32g ..), the tile's K superblock operands of lane group g, and for each of the lane's 8 tokens
+// tile_token(g, k) the 8 V dims 8*l16 .. 8*l16+7 (bf16: 16 B, INT4: 4 B, INT2: 2 B) plus the
+// token's V metadata.
 template <int KIND>
 struct TileRegs;
 template <>
 struct TileRegs<kFP> {
     r2o_u4 kx[2];
+    r2o_u4 ops[8];
     r2o_u4 v[8];
 };
 template <>
 struct TileRegs<kI4> {
     r2o_u4 kx[2];
+    r2o_u4 ops[8];
     uint32_t v[8];
     uint32_t vm[8];  // f32 scale bits
 };
 template <>
 struct TileRegs<kI2> {
     r2o_u4 kx[2];
+    r2o_u4 ops[8];
     uint32_t v[8];
     uint32_t vm[8];  // fp16 scale bits (group of dims 8*l16)
     uint32_t vz[8];  // u8 zero point
 };
 
-__device__ __forceinline__ void lds_copy16(const void* gsrc, unsigned char* lds_base, int offset) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
-                                     (__attribute__((address_space(3))) void*)(lds_base + offset), 16, 0, 0);
-}
-
-// Per-item, per-lane addressing of a BF16-V segment (32-bit positions within one head).
+// Valid arena positions of the segment (partial tiles mask the rest).
 struct SegCtx {
-    const uint8_t* kcode;    // k_packed of this head + l16*64 + 16g   (+ a0*64 + mg*1024)
-    const uint8_t* vrows;    // V rows of this head + lane column offset
-    int lo, hi, vdelta;      // valid arena positions, V row = arena - vdelta
-    int sb_shift;
+    int lo, hi;
 };
-
-// BF16-V tile straight into registers: the INT4-K codes of token a0 + 16 mg + l16 and, for each
-// of the lane's 8 tokens tile_token(g, k), the 8 V dims 8*l16 .. 8*l16+7 (16 bytes).
-__device__ __forceinline__ void issue_fp_tile(const SegCtx& c, int a0, int g, TileRegs<kFP>& tr) {
-    tr.kx[0] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64));
-    tr.kx[1] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.kcode + a0 * 64 + 1024));
-    const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
-    int row[8];
-    if (full) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) row[k] = a0 - c.vdelta + tile_token(g, k);
-    } else {  // rows outside [lo, hi) read a clamped valid row (finite data, probability 0)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) row[k] = min(max(a0 + tile_token(g, k), c.lo), c.hi - 1) - c.vdelta;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) tr.v[k] = r2o_ldg(reinterpret_cast<const r2o_u4*>(c.vrows + row[k] * 256));
-}
 
 template <int KIND>
 struct SegState {
@@ -222,11 +206,11 @@ struct SegState {
     r2o_f4 bias;         // INT4-V: sum_k P'_k * 1032 per head row (removed at the end)
 };
 
-// QK^T of one INT4-K tile: per MFMA j, Q'_j = q * s (superblock scale pairs from LDS), the
-// correction -sum Q'_j (1024 + z) by one MFMA, then the two 16-token groups.
-__device__ __forceinline__ void qk_int4k(const uint32_t (&qp)[4][4], const VConst& vc, const unsigned char* kops_sb,
-                                         int g, const r2o_u4 (&kx)[2], r2o_f4 (&s)[2]) {
-    const r2o_u4* ko = reinterpret_cast<const r2o_u4*>(kops_sb + g * 128);
+// QK^T of one INT4-K tile: per MFMA j, Q'_j = q * s (superblock scale pairs), the correction
+// -sum Q'_j (1024 + z) by one MFMA, then the two 16-token groups.  ko = the 4 scale-pair and the
+// 4 zero-pair operand vectors of the lane's channel group.
+__device__ __forceinline__ void qk_int4k(const uint32_t (&qp)[4][4], const VConst& vc, const r2o_u4 (&ko)[8],
+                                         const r2o_u4 (&kx)[2], r2o_f4 (&s)[2]) {
     s[0] = r2o_f4{0, 0, 0, 0};
     s[1] = r2o_f4{0, 0, 0, 0};
     r2o_f4 corr = {0, 0, 0, 0};
@@ -320,88 +304,39 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
     }
 }
 
-// One tile: QK, masks, online softmax, PV.  `kops_sb` = the tile's superblock operands in LDS.
+// One tile: QK, masks, online softmax, PV.
 template <int KIND>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
-                                            int a0, int g, const unsigned char* kops_sb, const TileRegs<KIND>& cur) {
+                                            int a0, int g, const TileRegs<KIND>& cur) {
     r2o_f4 s[2];
-    qk_int4k(ss.qp, vc, kops_sb, g, cur.kx, s);
+    qk_int4k(ss.qp, vc, cur.ops, cur.kx, s);
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
     softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
     pv_tile<KIND>(st, ss, vc, pk, cur);
 }
 
-// BF16-V segment: tiles prefetched one ahead into registers; the K superblock operands of the
-// wave's whole tile range are copied into LDS once per item.
-__device__ void run_segment_fp(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
-                               unsigned char* smem, WaveState& st) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
-    const int gqa = (int)(p.hq / p.hkv);
-    const int64_t kvh = it.kvh, b = it.req;
-    const int per = (int)((it.ntiles + kWaves - 1) / kWaves);
-    const int t_begin = wave * per;
-    const int t_end = min((int)it.ntiles, t_begin + per);
-    if (t_begin >= t_end) return;
-    unsigned char* kops = smem + wave * kWaveLds;
-
-    SegCtx c;
-    c.kcode = rq.k_packed + (kvh * rq.k_capacity + l16) * 64 + 16 * g;
-    c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128) + 16 * l16;
-    c.lo = (int)it.lo;
-    c.hi = (int)it.hi;
-    c.vdelta = (int)it.v_delta;
-    c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
-    const int base = (int)it.tile0;
-    const int sb0 = (base + 32 * t_begin) >> c.sb_shift;
-    const int sb1 = (base + 32 * t_end - 1) >> c.sb_shift;
-    {
-        const uint32_t* src = rq.k_operands + kvh * rq.k_superblocks * 128 + (int64_t)sb0 * 128;
-        // 16-byte chunks; items larger than the stage (a planner contract) are clamped, not overrun
-        const int nchunks = min((sb1 - sb0 + 1) * 32, kOpsBytes / 16);
-        for (int ch0 = 0; ch0 < nchunks; ch0 += 64) {
-            const int ch = min(ch0 + lane, nchunks - 1);
-            lds_copy16(src + ch * 4, kops, ch0 * 16);
-        }
-    }
-    const VConst vc = make_vconst();
-    SegState<kFP> ss;
-    load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
-    ss.bias = r2o_f4{0, 0, 0, 0};
-
-    const int n = t_end - t_begin;
-    const int a_first = base + 32 * t_begin;
-    auto ops = [&](int a0) { return kops + ((a0 >> c.sb_shift) - sb0) * 512; };
-    TileRegs<kFP> r0, r1;
-    issue_fp_tile(c, a_first, g, r0);
-    __builtin_amdgcn_s_waitcnt(0);  // K operands (and tile 0) in LDS / registers
-    __builtin_amdgcn_wave_barrier();
-    for (int i = 0; i < n; i += 2) {
-        const int a0 = a_first + 32 * i;
-        if (i + 1 < n) issue_fp_tile(c, a0 + 32, g, r1);
-        seg_compute<kFP>(c, st, ss, vc, a0, g, ops(a0), r0);
-        if (i + 1 >= n) break;
-        if (i + 2 < n) issue_fp_tile(c, a0 + 64, g, r0);
-        seg_compute<kFP>(c, st, ss, vc, a0 + 32, g, ops(a0 + 32), r1);
-    }
-}
-
-// ------------------------------------------------------------------ INT4 / INT2 tiles via LDS DMA
-// Every INT4/INT2 tile is moved by six global->LDS DMA instructions (no VGPRs held while in
-// flight) into one stage of a per-wave ring of kDmaStages stages, issued kDmaStages - 1 tiles
-// ahead.  Stage layout (bytes): K codes [0, 2048) | V payload from 2048 | K superblock operands
-// (512) | V metadata.  The 16-byte chunks of K and V are placed so that the transposed
-// per-lane reads of the compute hit distinct LDS banks (see the slot functions).  A DMA of 16
+// ------------------------------------------------------------------ pool tiles via LDS DMA
+// Every pool tile is moved by global->LDS DMA (16-byte chunks; no VGPRs held while in flight)
+// into one stage of a per-wave ring of kDmaStages stages.  The wave waits for tile i, reads the
+// whole stage into registers, refills the stage with tile i + kDmaStages, then computes tile i,
+// so kDmaStages tiles stay in flight during the compute.  The 16-byte chunks are placed so that
+// the transposed per-lane reads hit distinct LDS banks (see the slot functions).  A DMA of 16
 // bytes per lane fills LDS at lane * 16; one of 1, 2 or 4 bytes per lane fills the low bytes of
 // the dword at lane * 4, so sub-dword metadata rows sit in dword slots.
 template <int KIND>
-struct DmaLayout {
+struct StageLayout {  // byte offsets within a stage: K codes | V payload | K operands | V metadata
     static constexpr int kV = 2048;
-    static constexpr int kOps = KIND == kI4 ? 4096 : 3072;
+    static constexpr int kVBytes = KIND == kFP ? 8192 : (KIND == kI4 ? 2048 : 1024);
+    static constexpr int kOps = kV + kVBytes;
     static constexpr int kScale = kOps + 512;
-    static constexpr int kZero = kScale + 256;  // INT2 only
+    static constexpr int kZero = kScale + 256;                 // INT2 only
+    static constexpr int kDma = 2 + kVBytes / 1024 + 1 + (KIND == kFP ? 0 : (KIND == kI4 ? 1 : 2));
+    static constexpr int kEnd = KIND == kFP ? kOps + 512 : (KIND == kI4 ? kScale + 128 : kZero + 128);
 };
+static_assert(StageLayout<kFP>::kEnd <= kStageBytes && StageLayout<kI4>::kEnd <= kStageBytes &&
+                  StageLayout<kI2>::kEnd <= kStageBytes,
+              "every tile stage fits kStageBytes");
 
 // K codes: token t (0..31), 16-byte chunk c (0..3) of its 64-byte row.  Reads: 8 lanes take 8
 // consecutive tokens of one chunk, so the chunk is rotated by (t >> 1) & 3.
@@ -411,6 +346,7 @@ __device__ __forceinline__ int k_slot(int t, int c) { return 4 * t + (c ^ ((t >>
 __device__ __forceinline__ int v4_slot(int t, int c) { return 8 * ((t & 3) + 4 * (t >> 3)) + 2 * c + ((t >> 2) & 1); }
 // INT2 V: token t, chunk c (0..1) of its 32-byte row; tokens t, t+4, t+8, t+12 share 8 slots.
 __device__ __forceinline__ int v2_slot(int t, int c) { return 8 * (t & 3) + 32 * (t >> 4) + 2 * ((t >> 2) & 3) + c; }
+// BF16 V rows stay in natural order: 8 lanes read 8 consecutive chunks of one 256-byte row.
 
 template <int SIZE>
 __device__ __forceinline__ void dma(const void* gsrc, unsigned char* lds) {
@@ -422,15 +358,15 @@ __device__ __forceinline__ void dma(const void* gsrc, unsigned char* lds) {
     else __builtin_amdgcn_global_load_lds(g, l, 1, 0, 0);
 }
 
-__device__ __forceinline__ void wait_dma_tiles(int later) {
-    // vmcnt(later * kDmaPerTile): every DMA of the oldest outstanding tile has landed in LDS
-    switch (later) {
-        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // vmcnt(0)
-        case 1: __builtin_amdgcn_s_waitcnt(0x0F76); break;   // vmcnt(6)
-        case 2: __builtin_amdgcn_s_waitcnt(0x0F7C); break;   // vmcnt(12)
-        default: __builtin_amdgcn_s_waitcnt(0x4F72); break;  // vmcnt(18)
-    }
-    static_assert(kDmaStages <= 4 && kDmaPerTile == 6, "wait counts assume at most 4 stages of 6 DMAs");
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// Wait until at most `later` tiles of PER DMAs each are still in flight.
+template <int PER>
+__device__ __forceinline__ void wait_tiles(int later) {
+    static_assert(kDmaStages <= 3 && 2 * PER < 64, "vmcnt holds the DMAs of two later tiles");
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
 
 struct DmaCtx {
@@ -441,17 +377,21 @@ struct DmaCtx {
     const uint8_t* vzero;   // INT2 zero points of this head
     int lo, hi, vdelta, sb_shift, groups;
     int koff0, koff1;       // this lane's K source offset (bytes) for the two K DMAs
-    int vt0, vt1, vc0, vc1; // this lane's V source token / chunk for the V DMAs
+    int vt0, vt1, vc0, vc1; // this lane's V source token / chunk for the INT V DMAs
 };
 
 template <int KIND>
 __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char* stage, int lane) {
-    using Lay = DmaLayout<KIND>;
+    using Lay = StageLayout<KIND>;
     dma<16>(c.kcode + a0 * 64 + c.koff0, stage);
     dma<16>(c.kcode + a0 * 64 + c.koff1, stage + 1024);
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
+    // rows outside [lo, hi) read a clamped valid row (finite data, probability 0)
     auto row = [&](int t) { return (full ? a0 + t : min(max(a0 + t, c.lo), c.hi - 1)) - c.vdelta; };
-    if constexpr (KIND == kI4) {
+    if constexpr (KIND == kFP) {  // 8 x 1 KB: instruction j covers tokens 4j..4j+3 (16 chunks each)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma<16>(c.vrows + row(4 * j + (lane >> 4)) * 256 + (lane & 15) * 16, stage + Lay::kV + 1024 * j);
+    } else if constexpr (KIND == kI4) {
         dma<16>(c.vrows + row(c.vt0) * 64 + c.vc0 * 16, stage + Lay::kV);
         dma<16>(c.vrows + row(c.vt1) * 64 + c.vc1 * 16, stage + Lay::kV + 1024);
     } else {
@@ -460,31 +400,34 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
     if (lane < 32) dma<16>(c.kops + (a0 >> c.sb_shift) * 128 + lane * 4, stage + Lay::kOps);
     if constexpr (KIND == kI4) {
         if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
-    } else if (c.groups == 4) {  // G = 32: 8-byte scale rows, 4-byte zero rows
-        dma<4>(c.vscale + row(lane >> 1) * 8 + (lane & 1) * 4, stage + Lay::kScale);
-        if (lane < 32) dma<4>(c.vzero + row(lane) * 4, stage + Lay::kZero);
-    } else if (c.groups == 2) {
-        if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
-        if (lane < 32) dma<2>(c.vzero + row(lane) * 2, stage + Lay::kZero);
-    } else {
-        if (lane < 32) dma<2>(c.vscale + row(lane) * 2, stage + Lay::kScale);
-        if (lane < 32) dma<1>(c.vzero + row(lane), stage + Lay::kZero);
+    } else if constexpr (KIND == kI2) {
+        if (c.groups == 4) {  // G = 32: 8-byte scale rows, 4-byte zero rows
+            dma<4>(c.vscale + row(lane >> 1) * 8 + (lane & 1) * 4, stage + Lay::kScale);
+            if (lane < 32) dma<4>(c.vzero + row(lane) * 4, stage + Lay::kZero);
+        } else if (c.groups == 2) {
+            if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
+            if (lane < 32) dma<2>(c.vzero + row(lane) * 2, stage + Lay::kZero);
+        } else {
+            if (lane < 32) dma<2>(c.vscale + row(lane) * 2, stage + Lay::kScale);
+            if (lane < 32) dma<1>(c.vzero + row(lane), stage + Lay::kZero);
+        }
     }
 }
 
-__device__ __forceinline__ void read_k(const unsigned char* stage, int l16, int g, r2o_u4 (&kx)[2]) {
-#pragma unroll
-    for (int mg = 0; mg < 2; ++mg) kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(16 * mg + l16, g));
-}
-
 template <int KIND>
-__device__ __forceinline__ void read_v(const unsigned char* stage, int l16, int g, int gamma, int groups,
-                                       TileRegs<KIND>& tr) {
-    using Lay = DmaLayout<KIND>;
+__device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, int g, int gamma, int groups,
+                                          TileRegs<KIND>& tr) {
+    using Lay = StageLayout<KIND>;
+#pragma unroll
+    for (int mg = 0; mg < 2; ++mg) tr.kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(16 * mg + l16, g));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tr.ops[j] = *reinterpret_cast<const r2o_u4*>(stage + Lay::kOps + g * 128 + 16 * j);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int t = tile_token(g, k);
-        if constexpr (KIND == kI4) {
+        if constexpr (KIND == kFP) {
+            tr.v[k] = *reinterpret_cast<const r2o_u4*>(stage + Lay::kV + 256 * t + 16 * l16);
+        } else if constexpr (KIND == kI4) {
             tr.v[k] = *reinterpret_cast<const uint32_t*>(stage + Lay::kV + 16 * v4_slot(t, l16 >> 2) + 4 * (l16 & 3));
             tr.vm[k] = *reinterpret_cast<const uint32_t*>(stage + Lay::kScale + 4 * t);
         } else {  // scale rows: 8 bytes (G = 32) or one dword slot; zero rows: one dword slot
@@ -496,8 +439,8 @@ __device__ __forceinline__ void read_v(const unsigned char* stage, int l16, int 
 }
 
 template <int KIND>
-__device__ void run_segment_dma(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
-                                unsigned char* smem, WaveState& st) {
+__device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
+                            unsigned char* smem, WaveState& st) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
@@ -517,98 +460,58 @@ __device__ void run_segment_dma(const r2o_decode_params& p, const r2o_work_item&
     c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
     c.groups = (int)(128 / p.int2_group);
     const int gamma = (8 * l16) / (int)p.int2_group;
-    if constexpr (KIND == kI4) {
+    c.vscale = nullptr;
+    c.vzero = nullptr;
+    if constexpr (KIND == kFP) {
+        c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128);
+    } else if constexpr (KIND == kI4) {
         c.vrows = rq.i4_v + kvh * rq.i4_stride * 64;
         c.vscale = reinterpret_cast<const uint8_t*>(rq.i4_scale + kvh * rq.i4_stride);
-        c.vzero = nullptr;
     } else {
         c.vrows = rq.i2_v + kvh * rq.i2_stride * 32;
         c.vscale = reinterpret_cast<const uint8_t*>(rq.i2_scale + kvh * rq.i2_stride * c.groups);
         c.vzero = rq.i2_zero + kvh * rq.i2_stride * c.groups;
     }
-    {  // lane -> (token, chunk) sources of the K and V DMAs (inverse of the slot functions)
+    {  // lane -> (token, chunk) sources of the K and INT V DMAs (inverse of the slot functions)
         const int s0 = lane, s1 = 64 + lane;
         const int t0 = s0 >> 2, t1 = s1 >> 2;
         c.koff0 = t0 * 64 + 16 * ((s0 & 3) ^ ((t0 >> 1) & 3));
         c.koff1 = t1 * 64 + 16 * ((s1 & 3) ^ ((t1 >> 1) & 3));
-        if constexpr (KIND == kI4) {
-            c.vt0 = 8 * (s0 >> 5) + 4 * (s0 & 1) + ((s0 >> 3) & 3);
-            c.vc0 = (s0 >> 1) & 3;
-            c.vt1 = 8 * (s1 >> 5) + 4 * (s1 & 1) + ((s1 >> 3) & 3);
-            c.vc1 = (s1 >> 1) & 3;
-        } else {
+        if constexpr (KIND == kI2) {
             c.vt0 = 16 * (s0 >> 5) + 4 * ((s0 >> 1) & 3) + ((s0 >> 3) & 3);
             c.vc0 = s0 & 1;
             c.vt1 = c.vt0;
             c.vc1 = c.vc0;
+        } else {
+            c.vt0 = 8 * (s0 >> 5) + 4 * (s0 & 1) + ((s0 >> 3) & 3);
+            c.vc0 = (s0 >> 1) & 3;
+            c.vt1 = 8 * (s1 >> 5) + 4 * (s1 & 1) + ((s1 >> 3) & 3);
+            c.vc1 = (s1 >> 1) & 3;
         }
     }
     const int n = t_end - t_begin;
     const int a_first = (int)it.tile0 + 32 * t_begin;
 #pragma unroll
-    for (int j = 0; j < kDmaStages - 1; ++j)
-        if (j < n) dma_tile<KIND>(c, a_first + 32 * j, ring + j * kDmaStage, lane);
+    for (int j = 0; j < kDmaStages; ++j)
+        if (j < n) dma_tile<KIND>(c, a_first + 32 * j, ring + j * kStageBytes, lane);
 
     const VConst vc = make_vconst();
     SegState<KIND> ss;
     load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
     ss.bias = r2o_f4{0, 0, 0, 0};
-    SegCtx sc;  // the mask fields the compute reads
-    sc.lo = c.lo;
-    sc.hi = c.hi;
-    sc.sb_shift = c.sb_shift;
-    if constexpr (kDmaStages == 2) {
-        for (int i = 0; i < n; ++i) {
-            if (i + 1 < n) {
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): that stage has been read
-                __builtin_amdgcn_wave_barrier();
-                dma_tile<KIND>(c, a_first + 32 * (i + 1), ring + ((i + 1) & 1) * kDmaStage, lane);
-            }
-            wait_dma_tiles(i + 1 < n ? 1 : 0);
-            __builtin_amdgcn_wave_barrier();
-            const unsigned char* stage = ring + (i & 1) * kDmaStage;
-            TileRegs<KIND> cur;
-            read_k(stage, l16, g, cur.kx);
-            read_v<KIND>(stage, l16, g, gamma, c.groups, cur);
-            seg_compute<KIND>(sc, st, ss, vc, a_first + 32 * i, g, stage + DmaLayout<KIND>::kOps, cur);
-        }
-    } else {
-    // Software pipeline: the QK MFMAs of tile i + 1 are issued before the softmax and PV of
-        // tile i, so the matrix core and the VALU work on different tiles.
-        r2o_f4 s_cur[2];
-        wait_dma_tiles(min(n, kDmaStages - 1) - 1);  // tile 0 has landed
+    const SegCtx sc = {c.lo, c.hi};
+    for (int i = 0; i < n; ++i) {
+        wait_tiles<StageLayout<KIND>::kDma>(min(kDmaStages, n - i) - 1);  // tile i has landed
         __builtin_amdgcn_wave_barrier();
-        {
-            r2o_u4 kx[2];
-            read_k(ring, l16, g, kx);
-            qk_int4k(ss.qp, vc, ring + DmaLayout<KIND>::kOps, g, kx, s_cur);
+        unsigned char* stage = ring + (i % kDmaStages) * kStageBytes;
+        TileRegs<KIND> cur;
+        read_tile<KIND>(stage, l16, g, gamma, c.groups, cur);
+        if (i + kDmaStages < n) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the whole stage is in registers
+            __builtin_amdgcn_wave_barrier();
+            dma_tile<KIND>(c, a_first + 32 * (i + kDmaStages), stage, lane);
         }
-        for (int i = 0; i < n; ++i) {
-            if (i + kDmaStages - 1 < n) {  // refill the stage tile i - 1 used
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): that stage has been read
-                __builtin_amdgcn_wave_barrier();
-                dma_tile<KIND>(c, a_first + 32 * (i + kDmaStages - 1), ring + ((i + kDmaStages - 1) % kDmaStages) * kDmaStage,
-                               lane);
-            }
-            r2o_f4 s_nxt[2];
-            if (i + 1 < n) {
-                wait_dma_tiles(min(n, i + kDmaStages) - (i + 2));  // tile i + 1 has landed
-                __builtin_amdgcn_wave_barrier();
-                const unsigned char* nstage = ring + ((i + 1) % kDmaStages) * kDmaStage;
-                r2o_u4 kx[2];
-                read_k(nstage, l16, g, kx);
-                qk_int4k(ss.qp, vc, nstage + DmaLayout<KIND>::kOps, g, kx, s_nxt);
-            }
-            const unsigned char* stage = ring + (i % kDmaStages) * kDmaStage;
-            TileRegs<KIND> cur;
-            read_v<KIND>(stage, l16, g, gamma, c.groups, cur);
-            float sv[8], pk[8];
-            tile_logits(sc, a_first + 32 * i, g, s_cur, sv);
-            softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
-            pv_tile<KIND>(st, ss, vc, pk, cur);
-            s_cur[0] = s_nxt[0];
-            s_cur[1] = s_nxt[1];
-        }
+        seg_compute<KIND>(sc, st, ss, vc, a_first + 32 * i, g, cur);
     }
     if constexpr (KIND == kI4) {
 #pragma unroll
@@ -676,7 +579,7 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     }
 }
 
-__global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_params p) {
+__global__ __launch_bounds__(256, kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
     __shared__ __align__(16) unsigned char smem[kSmemBytes];
     const r2o_work_item it = p.items[blockIdx.x];
     const r2o_request_desc rq = p.reqs[it.req];
@@ -691,9 +594,9 @@ __global__ __launch_bounds__(256, 2) void decode_partial_kernel(r2o_decode_param
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment_fp(p, it, rq, smem, st); break;
-        case kI4: run_segment_dma<kI4>(p, it, rq, smem, st); break;
-        case kI2: run_segment_dma<kI2>(p, it, rq, smem, st); break;
+        case kFP: run_segment<kFP>(p, it, rq, smem, st); break;
+        case kI4: run_segment<kI4>(p, it, rq, smem, st); break;
+        case kI2: run_segment<kI2>(p, it, rq, smem, st); break;
         default: run_recent(p, it, rq, st); break;
     }
 

@@ -26,7 +26,7 @@ from .cache import ThreePrecisionCache
 
 TILE = 32
 _MIN_TILES_PER_ITEM = 4      # one tile per wave of the 4-wave workgroup
-_BLOCKS_PER_CU = 2           # resident partial-kernel workgroups per CU (LDS / VGPR bound)
+_BLOCKS_PER_CU = 2           # work items planned per CU (the kernel holds up to 3 resident; 2 keeps the combine short)
 
 
 def _max_tiles_per_item(superblock: int) -> int:
@@ -74,7 +74,7 @@ def _tiles(lo: int, hi: int) -> tuple[int, int]:
 
 # Relative cost of one 32-token tile per kind (partial kernel, measured on MI355X): the
 # planner sizes items so that every workgroup slot gets about the same amount of work.
-_TILE_COST = {_lib.KIND_FP: 1.2, _lib.KIND_INT4: 1.0, _lib.KIND_INT2: 1.3, _lib.KIND_RECENT: 2.0}
+_TILE_COST = {_lib.KIND_FP: 1.35, _lib.KIND_INT4: 1.0, _lib.KIND_INT2: 1.1, _lib.KIND_RECENT: 2.0}
 
 
 def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_int2: int = 0):
