@@ -125,9 +125,10 @@ int r2o_decode_combine(const r2o_decode_params* params, void* stream);
  * (dequantised, rounded to `dtype`) — the flush rule of CompactInt4KeyArena.append_superblock
  * (compact_int4_key.py:210-220); the next n come from src[h, index[i]] (index NULL: i).
  * `operands` (nullable) receives, per superblock, the QK MFMA operands derived from the
- * stored scale/zero: for lane group g (channels 32g..32g+31), MFMA j and pair u, dword
- * g*32 + 4j + u = fp16 (s[c], s[c+4]) and dword g*32 + 16 + 4j + u = fp16 (-(1024 + z[c]),
- * -(1024 + z[c+4])) with c = 32g + 8j + u.
+ * stored scale/zero: for lane group g (channels 32g..32g+31), MFMA j and pair u, with
+ * c = 32g + 8j + u, dword g*32 + 4j + u = fp16 (s[c], s[c+4]) and dword g*32 + 16 + 4j + u =
+ * fp16 (-(1024 + z[c]), -(1024 + z[c+4])) for even u; for odd u (codes read 4 bits up, as
+ * 1024 + 16 code) the pairs are (s/16) and -(1024 + 16 z).
  * Replaces _gather_pack_int4_key_kernel (compact_int4_key.py:22-76) and the torch flush path. */
 int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
                     const int64_t* index, int64_t n, int64_t tail, int64_t dst_start,

@@ -100,12 +100,12 @@ __device__ __forceinline__ float head_max(float x) {
 constexpr float kRescaleSlack = 4.f;
 
 template <int N>
-__device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N], float (&pk)[N], int g,
-                                             r2o_f4* extra = nullptr) {
+__device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N], float (&pk)[N], int g, float add,
+                                             r2o_f4* extra) {
     float tmax = sv[0];
 #pragma unroll
     for (int k = 1; k < N; ++k) tmax = fmaxf(tmax, sv[k]);
-    tmax = head_max(tmax);
+    tmax = head_max(tmax) + add;  // -inf + add = -inf
     if (__any(tmax > st.m + kRescaleSlack)) {  // -inf + slack = -inf: the first valid tile rescales
         const float m_new = fmaxf(st.m, tmax);
         // exp2(-inf) = 0 when the state was empty; a head with no valid token keeps alpha = 1
@@ -120,17 +120,18 @@ __device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N]
         }
         st.m = m_new;
     }
-    const float m_use = st.m == -INFINITY ? 0.f : st.m;
+    const float d = (st.m == -INFINITY ? 0.f : st.m) - add;
 #pragma unroll
     for (int k = 0; k < N; ++k) {
-        pk[k] = __builtin_amdgcn_exp2f(sv[k] - m_use);  // exp2(-inf) = 0 for masked tokens
+        pk[k] = __builtin_amdgcn_exp2f(sv[k] - d);  // exp2(-inf) = 0 for masked tokens
         st.l += pk[k];
     }
 }
 
+// Online-softmax update for one tile whose logits are sv + add (log2 domain, -inf = masked).
 __device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8], float (&pk)[8], int g,
-                                             r2o_f4* extra = nullptr) {
-    softmax_step<8>(st, sv, pk, g, extra);
+                                             float add = 0.f, r2o_f4* extra = nullptr) {
+    softmax_step<8>(st, sv, pk, g, add, extra);
 }
 
 // PV for bf16 V rows held as R[k] = 8 dims (8*l16 ..) of token tile_token(g, k).
@@ -147,14 +148,16 @@ __device__ __forceinline__ void pv_bf16(WaveState& st, const r2o_u4& ap, const r
 // Constants kept in VGPRs so that (x & mask) | magic selects one v_and_or_b32 (gfx9 VOP3 can
 // take at most one literal/SGPR operand).
 struct VConst {
-    uint32_t nib;    // 0x000F000F
-    uint32_t crumb;  // 0x00030003
-    uint32_t magic;  // 0x64006400 = fp16 (1024, 1024)
+    uint32_t nib;     // 0x000F000F
+    uint32_t nib_hi;  // 0x00F000F0
+    uint32_t crumb;   // 0x00030003
+    uint32_t magic;   // 0x64006400 = fp16 (1024, 1024)
 };
 
 __device__ __forceinline__ VConst make_vconst() {
     VConst c;
     asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(c.nib));
+    asm volatile("v_mov_b32 %0, 0x00F000F0" : "=v"(c.nib_hi));
     asm volatile("v_mov_b32 %0, 0x00030003" : "=v"(c.crumb));
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.magic));
     return c;
@@ -203,33 +206,35 @@ struct SegCtx {
 template <int KIND>
 struct SegState {
     uint32_t qp[4][4];   // q (scaled), f16 pairs in the K-unpack channel order
-    r2o_f4 bias;         // INT4-V: sum_k P'_k * 1032 per head row (removed at the end)
+    r2o_f4 bias;         // INT4-V: sum_k P'_k per head row (code offsets removed at the end)
 };
 
-// QK^T of one INT4-K tile: per MFMA j, Q'_j = q * s (superblock scale pairs), the correction
-// -sum Q'_j (1024 + z) by one MFMA, then the two 16-token groups.  ko = the 4 scale-pair and the
-// 4 zero-pair operand vectors of the lane's channel group.
+// QK^T of one INT4-K tile: per MFMA j, Q'_j = q * s (superblock scale pairs), the codes of the
+// dword read in place (1024 + c for the low nibble of each byte, 1024 + 16 c for the high one,
+// whose operand pairs carry s / 16), and the correction -sum Q'_j (1024 + z) by one more MFMA.
+// The correction is the same for every token of a head, so it is returned as the lane scalar
+// `corr` and added to the logits by the softmax.  ko = the 4 scale-pair and the 4 zero-pair
+// operand vectors of the lane's channel group.
 __device__ __forceinline__ void qk_int4k(const uint32_t (&qp)[4][4], const VConst& vc, const r2o_u4 (&ko)[8],
-                                         const r2o_u4 (&kx)[2], r2o_f4 (&s)[2]) {
+                                         const r2o_u4 (&kx)[2], r2o_f4 (&s)[2], float& corr) {
     s[0] = r2o_f4{0, 0, 0, 0};
     s[1] = r2o_f4{0, 0, 0, 0};
-    r2o_f4 corr = {0, 0, 0, 0};
+    r2o_f4 cz = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const r2o_u4 sj = ko[j], zj = ko[4 + j];
         const r2o_u4 qj = {r2o_h2_mul(qp[j][0], sj[0]), r2o_h2_mul(qp[j][1], sj[1]), r2o_h2_mul(qp[j][2], sj[2]),
                            r2o_h2_mul(qp[j][3], sj[3])};
-        corr = r2o_mfma_f16(zj, qj, corr);
+        cz = r2o_mfma_f16(zj, qj, cz);
 #pragma unroll
         for (int mg = 0; mg < 2; ++mg) {
-            const uint32_t w = kx[mg][j];
-            const r2o_u4 a = {(w & vc.nib) | vc.magic, ((w >> 4) & vc.nib) | vc.magic, ((w >> 8) & vc.nib) | vc.magic,
-                              ((w >> 12) & vc.nib) | vc.magic};
+            const uint32_t w = kx[mg][j], w8 = w >> 8;
+            const r2o_u4 a = {(w & vc.nib) | vc.magic, (w & vc.nib_hi) | vc.magic, (w8 & vc.nib) | vc.magic,
+                              (w8 & vc.nib_hi) | vc.magic};
             s[mg] = r2o_mfma_f16(a, qj, s[mg]);
         }
     }
-    s[0] += corr;
-    s[1] += corr;
+    corr = cz[0];  // every row of the correction product is the same
 }
 
 // Logits of a tile in the lane's token order (masks only on partial tiles; padded heads have
@@ -258,12 +263,13 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
         for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
         pv_bf16(st, ap, cur.v);
     } else if constexpr (KIND == kI4) {
-        // P' = p * s_t; codes enter as (1032 + c) and sum_k P'_k * 1032 is accumulated by one
-        // more MFMA on the same A operand (so both see identical f16 inputs).
+        // P' = p * s_t; the signed codes (xor 8) enter as 1032 + c (low nibble) and, read in
+        // place, 1152 + 16 c (high nibble).  sum_k P'_k is accumulated by one more MFMA on the
+        // same A operand (so both see identical f16 inputs) and the offsets are removed at the end.
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             ap[u] = r2o_pack_h2(pk[2 * u] * __uint_as_float(cur.vm[2 * u]), pk[2 * u + 1] * __uint_as_float(cur.vm[2 * u + 1]));
-        ss.bias = r2o_mfma_f16(ap, r2o_u4{0x64086408u, 0x64086408u, 0x64086408u, 0x64086408u}, ss.bias);
+        ss.bias = r2o_mfma_f16(ap, r2o_u4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}, ss.bias);
         uint32_t X[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) X[k] = cur.v[k] ^ 0x88888888u;
@@ -275,7 +281,7 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
             for (int pr = 0; pr < 4; ++pr) {
                 const uint32_t y = r2o_perm(X[2 * pr + 1], X[2 * pr], sel);
                 lo[pr] = (y & vc.nib) | vc.magic;
-                hi[pr] = ((y >> 4) & vc.nib) | vc.magic;
+                hi[pr] = (y & vc.nib_hi) | vc.magic;
             }
             st.acc[2 * bb] = r2o_mfma_f16(ap, lo, st.acc[2 * bb]);
             st.acc[2 * bb + 1] = r2o_mfma_f16(ap, hi, st.acc[2 * bb + 1]);
@@ -309,10 +315,11 @@ template <int KIND>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
                                             int a0, int g, const TileRegs<KIND>& cur) {
     r2o_f4 s[2];
-    qk_int4k(ss.qp, vc, cur.ops, cur.kx, s);
+    float corr;
+    qk_int4k(ss.qp, vc, cur.ops, cur.kx, s, corr);
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
-    softmax_tile(st, sv, pk, g, KIND == kI4 ? &ss.bias : nullptr);
+    softmax_tile(st, sv, pk, g, corr, KIND == kI4 ? &ss.bias : nullptr);
     pv_tile<KIND>(st, ss, vc, pk, cur);
 }
 
@@ -513,9 +520,12 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
         }
         seg_compute<KIND>(sc, st, ss, vc, a_first + 32 * i, g, cur);
     }
-    if constexpr (KIND == kI4) {
+    if constexpr (KIND == kI4) {  // remove the code offsets: lo dims 1032 * sum P', hi dims (1152 * sum P') / 16
 #pragma unroll
-        for (int q = 0; q < 8; ++q) st.acc[q] -= ss.bias;
+        for (int q = 0; q < 8; q += 2) {
+            st.acc[q] -= 1032.f * ss.bias;
+            st.acc[q + 1] = (st.acc[q + 1] - 1152.f * ss.bias) * 0.0625f;
+        }
     }
 }
 

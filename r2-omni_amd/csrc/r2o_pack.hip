@@ -77,8 +77,14 @@ __global__ __launch_bounds__(64) void pack_int4_k_kernel(
         const int g = t >> 4, j = (t >> 2) & 3, u = t & 3;
         const int c = 32 * g + 8 * j + u;
         uint32_t* orow = operands + (h * superblocks + block_row) * 128 + g * 32 + 4 * j + u;
-        orow[0] = (uint32_t)s_half[c] | ((uint32_t)s_half[c + 4] << 16);
-        orow[16] = (0xE400u | s_zero[c]) | ((0xE400u | (uint32_t)s_zero[c + 4]) << 16);
+        if (u & 1) {  // channel pair read in place 4 bits up: code enters as 1024 + 16 c
+            orow[0] = r2o_f32_to_f16(r2o_f16_to_f32(s_half[c]) * 0.0625f) |
+                      (r2o_f32_to_f16(r2o_f16_to_f32(s_half[c + 4]) * 0.0625f) << 16);
+            orow[16] = (0xE400u | ((uint32_t)s_zero[c] << 4)) | ((0xE400u | ((uint32_t)s_zero[c + 4] << 4)) << 16);
+        } else {
+            orow[0] = (uint32_t)s_half[c] | ((uint32_t)s_half[c + 4] << 16);
+            orow[16] = (0xE400u | s_zero[c]) | ((0xE400u | (uint32_t)s_zero[c + 4]) << 16);
+        }
     }
 }
 
