@@ -172,6 +172,18 @@ int r2o_recent_shift(uint16_t* recent_k, uint16_t* recent_v, int64_t hkv, int64_
  * triton_fwht_128 (triton_qwen_mrope.py:325-346). */
 int r2o_fwht128(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t dtype, void* stream);
 
+/* Decode-step Q/K rotation: Qwen multimodal RoPE (rotate-half, dimension d takes its cos/sin
+ * from table axis 0, 1 or 2 by d % 64 against the sections (section0, section1, 64 - s0 - s1)),
+ * computed in fp32, optionally followed by the orthonormal FWHT-128, rounded once to `dtype`.
+ * q [batch, hq, tokens, 128], k [batch, hkv, tokens, 128] contiguous; cos/sin [3, batch, tokens,
+ * 128] with element strides (axis, batch, token, dim) and table_dtype 0 = bf16, 1 = fp16,
+ * 2 = fp32.  Replaces _qwen_qk_mrope_kernel / _qwen_batched_qk_mrope_kernel
+ * (triton_qwen_mrope.py:45-211, host wrapper qwen_qk_mrope :214-322). */
+int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out, int64_t dtype,
+                 int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, const void* cos, const void* sin,
+                 int64_t table_dtype, const int64_t* cos_strides, const int64_t* sin_strides,
+                 int64_t section0, int64_t section1, int64_t apply_hadamard, void* stream);
+
 /* Library identification: returns the gfx target the code objects were built for. */
 const char* r2o_build_target(void);
 

@@ -102,6 +102,23 @@ __device__ __forceinline__ uint32_t r2o_pack_bf2(float lo, float hi) {
     return r2o_f32_to_bf16(lo) | (r2o_f32_to_bf16(hi) << 16);
 }
 
+// Orthonormal 128-point FWHT of a row held by one wave: lane t holds x[t] in y0 and x[t + 64]
+// in y1.  Stride 64 is a butterfly inside the lane, strides 32 .. 1 are lane-xor butterflies.
+__device__ __forceinline__ void r2o_fwht128_pair(float& y0, float& y1, int t) {
+    const float s0 = y0 + y1, s1 = y0 - y1;
+    y0 = s0;
+    y1 = s1;
+#pragma unroll
+    for (int stride = 1; stride < 64; stride <<= 1) {
+        const float o0 = __shfl_xor(y0, stride, R2O_WAVE), o1 = __shfl_xor(y1, stride, R2O_WAVE);
+        const bool upper = (t & stride) != 0;
+        y0 = upper ? o0 - y0 : y0 + o0;
+        y1 = upper ? o1 - y1 : y1 + o1;
+    }
+    y0 *= 0.08838834764831845f;
+    y1 *= 0.08838834764831845f;
+}
+
 #define R2O_CHECK_LAUNCH()                                      \
     do {                                                        \
         if (hipGetLastError() != hipSuccess) return R2O_ELAUNCH; \

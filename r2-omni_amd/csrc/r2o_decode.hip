@@ -722,20 +722,7 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
     }
     float y0 = r2o_bf16_to_f32(r2o_f32_to_bf16(a0 / L));
     float y1 = r2o_bf16_to_f32(r2o_f32_to_bf16(a1 / L));
-    if (p.output_hadamard) {  // FWHT-128 of the bf16-rounded row (triton_fourq_splitk.py:1000-1006)
-        const float s0 = y0 + y1, s1 = y0 - y1;  // stride 64: within the lane
-        y0 = s0;
-        y1 = s1;
-#pragma unroll
-        for (int stride = 1; stride < 64; stride <<= 1) {
-            const float o0 = __shfl_xor(y0, stride, R2O_WAVE), o1 = __shfl_xor(y1, stride, R2O_WAVE);
-            const bool upper = (tid & stride) != 0;
-            y0 = upper ? o0 - y0 : y0 + o0;
-            y1 = upper ? o1 - y1 : y1 + o1;
-        }
-        y0 *= 0.08838834764831845f;
-        y1 *= 0.08838834764831845f;
-    }
+    if (p.output_hadamard) r2o_fwht128_pair(y0, y1, tid);  // of the bf16-rounded row (triton_fourq_splitk.py:1000-1006)
     uint16_t* orow = p.out + (b * p.hq + hqi) * 128;
     orow[tid] = (uint16_t)r2o_f32_to_bf16(y0);
     orow[tid + 64] = (uint16_t)r2o_f32_to_bf16(y1);

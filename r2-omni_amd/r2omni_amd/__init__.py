@@ -30,6 +30,7 @@ from .policy import (
     plan_from_pages,
     project_token_bits_to_pages,
 )
+from .rope import qwen_qk_mrope
 from .splitk import (
     SplitKExecutor,
     SplitKWorkspace,

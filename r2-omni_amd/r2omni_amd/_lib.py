@@ -76,6 +76,8 @@ _SIGNATURES = {
     "r2o_recent_append": (c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp),
     "r2o_recent_shift": (c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp),
     "r2o_fwht128": (c_vp, c_vp, c_i64, c_i64, c_vp),
+    "r2o_qk_mrope": (c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp,
+                     c_i64, c_i64, c_i64, c_vp),
 }
 EXPORTED = tuple(_SIGNATURES) + ("r2o_build_target",)
 

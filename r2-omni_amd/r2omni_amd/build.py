@@ -19,7 +19,7 @@ CSRC = os.path.join(ROOT_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libr2o_sspa.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ("r2o_decode.hip", "r2o_pack.hip")
+SOURCES = ("r2o_decode.hip", "r2o_pack.hip", "r2o_rope.hip")
 ARCH = "gfx950"
 
 

@@ -1,0 +1,68 @@
+"""Decode-step query/key rotation: ``qwen_qk_mrope`` on the gfx950 HIP kernel ``r2o_qk_mrope``.
+
+Drop-in for ``r2omni.sspa.kernels.triton_qwen_mrope.qwen_qk_mrope`` (triton_qwen_mrope.py:214-322):
+same arguments, same validation messages, one launch for every (request, head, token) row.
+"""
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+
+import torch
+
+from . import _lib
+
+_TABLE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                  mrope_section: Sequence[int], *, output: tuple[torch.Tensor, torch.Tensor] | None = None,
+                  apply_hadamard: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Apply Qwen multimodal RoPE (and optionally the orthonormal FWHT-128) to Q and K in one launch."""
+    if query.ndim != 4 or key.ndim != 4:
+        raise ValueError("Qwen fused mRoPE requires rank-4 Q/K")
+    if query.shape[0] != key.shape[0]:
+        raise ValueError("Qwen fused mRoPE requires equal Q/K batch sizes")
+    if query.shape[2] <= 0 or key.shape[2] != query.shape[2]:
+        raise ValueError("Qwen fused mRoPE requires equal positive Q/K token counts")
+    if query.shape[-1] != 128 or key.shape[-1] != 128:
+        raise ValueError("Qwen fused mRoPE currently requires head_dim=128")
+    if query.device != key.device or query.dtype != key.dtype:
+        raise ValueError("Q/K device and dtype must match")
+    if cos.device != query.device or sin.device != query.device:
+        raise ValueError("Q/K and rotary tensors must share a device")
+    if cos.shape != sin.shape or cos.ndim != 4 or cos.shape[0] != 3:
+        raise ValueError("Qwen fused mRoPE requires cos/sin [3,B,S,D]")
+    tokens = int(query.shape[2])
+    batch_size = int(query.shape[0])
+    if cos.shape[1] != batch_size or cos.shape[-2:] != (tokens, 128):
+        raise ValueError("Qwen fused mRoPE rotary positions must match Q/K tokens")
+    sections = tuple(int(value) for value in mrope_section)
+    if len(sections) != 3 or sum(sections) != 64:
+        raise ValueError("Qwen mRoPE sections must contain three values summing to 64")
+    if min(sections) < 0:
+        raise ValueError("Qwen mRoPE sections must be non-negative")
+    _lib.require_device(query, "fused Qwen mRoPE input")
+    dtype = _lib.dtype_code(query.dtype)
+    if cos.dtype != sin.dtype or cos.dtype not in _TABLE_CODES:
+        raise ValueError("Qwen fused mRoPE cos/sin must share a bf16, fp16 or fp32 dtype")
+    query = query.contiguous()
+    key = key.contiguous()
+    if output is None:
+        query_out, key_out = torch.empty_like(query), torch.empty_like(key)
+    else:
+        query_out, key_out = output
+        if query_out.shape != query.shape or key_out.shape != key.shape:
+            raise ValueError("fused Qwen mRoPE output shapes must match Q/K")
+        if (query_out.device != query.device or key_out.device != key.device or query_out.dtype != query.dtype
+                or key_out.dtype != key.dtype):
+            raise ValueError("fused Qwen mRoPE outputs must match Q/K device and dtype")
+        if not query_out.is_contiguous() or not key_out.is_contiguous():
+            raise ValueError("fused Qwen mRoPE outputs must be contiguous")
+    cos_strides = (ctypes.c_int64 * 4)(*[int(v) for v in cos.stride()])
+    sin_strides = (ctypes.c_int64 * 4)(*[int(v) for v in sin.stride()])
+    _lib.call("r2o_qk_mrope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(query_out), _lib.ptr(key_out), dtype,
+              batch_size, int(query.shape[1]), int(key.shape[1]), tokens, _lib.ptr(cos), _lib.ptr(sin),
+              _TABLE_CODES[cos.dtype], cos_strides, sin_strides, sections[0], sections[1], int(bool(apply_hadamard)),
+              ctypes.c_void_p(_lib.stream_of(query.device)))
+    return query_out, key_out
