@@ -136,6 +136,49 @@ def traffic_from_profile() -> tuple[int | None, str | None]:
     return None, None
 
 
+def prefill_bench(cfg, config_id: int, dev) -> dict:
+    """Time build_three_precision_cache (tier-sorted gather + INT4-K / INT4-V / INT2-V packing) for
+    the longest request of the configuration; bytes = bf16 K and V read + packed arenas written."""
+    import torch
+
+    from r2omni_amd.cache import build_three_precision_cache
+    from r2omni_amd.policy import plan_from_pages
+    from r2omni_amd.workloads import make_request
+
+    total = max(cfg.lengths)
+    data = make_request(cfg, total, seed=7, device=dev)
+    plan = plan_from_pages(data.page_offsets, data.page_lengths, data.page_classes, recent_fp_capacity=128,
+                           device=dev)
+
+    def build():
+        return build_three_precision_cache(data.key, data.value, plan, page_size=cfg.page,
+                                           key_quantization_superblock=cfg.superblock, int2_group_size=cfg.group,
+                                           compact_key_append_capacity=260, recent_flush_size=128)
+
+    for _ in range(2):
+        cache = build()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 5
+    start.record(stream)
+    for _ in range(reps):
+        cache = build()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / reps
+    hist = int(data.key.shape[1])
+    read = 2 * cfg.hkv * hist * 128 * 2
+    h = cfg.hkv
+    sbs = -(-hist // cfg.superblock)
+    written = h * (hist * 64 + sbs * 128 * (2 + 1 + 4) + cache.fp_pool.token_count * 256
+                   + cache.int4_pool.token_count * 68 + cache.compact_value.active_length * (32 + 3 * (128 // cfg.group)))
+    return {"metric": "prefill cache build (quantise + pack)", "config": f"cfg{config_id} {cfg.name}",
+            "tokens": hist, "hkv": cfg.hkv, "us_per_build": round(ms * 1e3, 1),
+            "GBs": round((read + written) / (ms * 1e-3) / 1e9, 1), "bytes_read": read, "bytes_written": written,
+            "note": "one call of build_three_precision_cache on resident bf16 K/V, host launch gaps included"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +189,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (HBM counter calibration)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="only time the prefill-side cache build (quantise + pack on the GPU) of the longest "
+                         "request of --config and print one JSON line")
     ap.add_argument("--summarize-pmc", metavar="DIR",
                     help="only print the mean per-dispatch value of every counter in a rocprofv3 --pmc CSV "
                          "output directory, per decode kernel (and the calibration copy kernel)")
@@ -176,6 +222,9 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
         return 0
     cfg = CONFIGS[args.config]
+    if args.prefill:
+        print(json.dumps(prefill_bench(cfg, args.config, dev)), flush=True)
+        return 0
     _log(f"building {args.layers} layer caches of {cfg.name} ...")
     layers = []
     for layer in range(args.layers):

@@ -505,12 +505,15 @@ def precision_cache_active_storage_breakdown(cache: ThreePrecisionCache) -> dict
             "persistent_allocation_count": int(fields)}
 
 
-def _compact_page_layouts(plan: LayerCompressionPlan):
+def _compact_page_layouts(plan: LayerCompressionPlan, device=None):
     """(tokens, offsets, lengths, page ids) of FP, INT4, INT2, Recent(empty), evicted pools.
 
     Pages are stably sorted by tier FP(+protected, recent) < INT4 < INT2 < evicted and keep
-    their token order (precision_pool.py:611-669).  Computed on the host from the page table.
+    their token order (precision_pool.py:611-669).  The page table (small) is sorted on the host;
+    the token lists are expanded on ``device`` without a per-page loop: token j of a tier is
+    start(page) + (j - physical offset(page)).
     """
+    dev = torch.device("cpu") if device is None else torch.device(device)
     classes = plan.page_classes.detach().to("cpu", torch.long)
     starts = plan.page_offsets.detach().to("cpu", torch.long)
     lens = plan.page_lengths.detach().to("cpu", torch.long)
@@ -524,20 +527,26 @@ def _compact_page_layouts(plan: LayerCompressionPlan):
     for tier in range(4):
         pages = order[cat[order] == tier]
         pl = lens[pages]
-        toks = [torch.arange(int(starts[p]), int(starts[p]) + int(lens[p])) for p in pages.tolist()]
-        tokens = torch.cat(toks) if toks else torch.zeros(0, dtype=torch.long)
-        layouts.append((tokens, pl.cumsum(0) - pl, pl, pages))
+        offsets = pl.cumsum(0) - pl
+        n_tok = int(pl.sum())
+        if n_tok:
+            shift = torch.repeat_interleave((starts[pages] - offsets).to(dev), pl.to(dev), output_size=n_tok)
+            tokens = shift + torch.arange(n_tok, device=dev, dtype=torch.long)
+        else:
+            tokens = torch.zeros(0, dtype=torch.long, device=dev)
+        layouts.append((tokens, offsets, pl, pages))
     empty = torch.zeros(0, dtype=torch.long)
-    return layouts[0], layouts[1], layouts[2], (empty, empty, empty, empty), layouts[3]
+    return layouts[0], layouts[1], layouts[2], (empty.to(dev), empty, empty, empty), layouts[3]
 
 
 def _make_page_index(plan: LayerCompressionPlan, layout, device) -> PhysicalPageIndex:
     tokens, offsets, lengths, pages = layout
-    gi = plan.global_token_indices.detach().to("cpu", torch.long)
-    lp = plan.logical_positions.detach().to("cpu", torch.long)
+    gi = plan.global_token_indices.detach().to(device, torch.long)
+    lp = plan.logical_positions.detach().to(device, torch.long)
+    tokens = tokens.to(device)
     return PhysicalPageIndex(original_page_ids=pages.to(device), physical_offsets=offsets.to(device),
-                             lengths=lengths.to(device), global_token_indices=gi[tokens].to(device),
-                             logical_positions=lp[tokens].to(device))
+                             lengths=lengths.to(device), global_token_indices=gi[tokens],
+                             logical_positions=lp[tokens])
 
 
 def _preallocate_recent_pool(name: str, key: torch.Tensor, *, page_size: int, capacity: int) -> PrecisionPool:
@@ -611,7 +620,7 @@ def build_three_precision_cache(
     key = key.contiguous()
     value = value.contiguous()
     dev = key.device
-    fp_l, i4_l, i2_l, rec_l, ev_l = _compact_page_layouts(plan)
+    fp_l, i4_l, i2_l, rec_l, ev_l = _compact_page_layouts(plan, dev)
     if sum(int(l[0].numel()) for l in (fp_l, i4_l, i2_l, ev_l)) != int(key.shape[1]):
         raise ValueError("compact physical pools must cover every logical token")
     h = int(key.shape[0])
@@ -637,10 +646,10 @@ def build_three_precision_cache(
                                                append_capacity=append_capacity,
                                                superblock_size=key_quantization_superblock)
     recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity)
-    gi = plan.global_token_indices.detach().to("cpu", torch.long)
+    gi = plan.global_token_indices.detach().to(dev, torch.long)
     return ThreePrecisionCache(
         fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent,
-        evicted_global_indices=gi[ev_l[0]].to(dev), page_size=int(page_size),
+        evicted_global_indices=gi[ev_l[0]], page_size=int(page_size),
         quantization_superblock=int(quantization_superblock), matched_fp=False, cache_variant=cache_variant,
         compact_key=compact_key, compact_value=compact_value, recent_flush_size=int(recent_flush_size),
         generated_value_precision="int2", static_int4_tokens=s_i4, generated_k_offset=compact_key.active_length,
