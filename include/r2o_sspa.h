@@ -39,7 +39,8 @@ extern "C" {
  * rebuilt only when the cache layout changes (prefill, flush), like the reference's
  * prepare_splitk_executor (triton_fourq_splitk.py:1695-1907).  All fields are 8 bytes. */
 typedef struct r2o_request_desc {
-    const uint8_t* k_packed;      /* compact INT4-K arena  u8  [Hkv, k_capacity, 64]            */
+    const uint8_t* k_packed;      /* compact INT4-K arena  u8  [Hkv, k_capacity, 64], or with    */
+                                  /* k_bf16 set, bf16 key rows [Hkv, k_capacity, 128]           */
     const uint16_t* k_scale;      /* fp16 [Hkv, k_superblocks, 128]                              */
     const uint8_t* k_zero;        /* u8   [Hkv, k_superblocks, 128]                              */
     int64_t k_capacity;
@@ -73,8 +74,7 @@ typedef struct r2o_work_item {
     int64_t kvh;
     int64_t kind;      /* 0 = FP-V (bf16), 1 = INT4-V, 2 = INT2-V, 3 = Recent-FP (bf16 K and V) */
     int64_t tile0;     /* arena position of the first tile (multiple of 32)                      */
-    int64_t ntiles;    /* <= 64 / 120 / 240 tiles at superblock 32 / 64 / 128 (each wave's quarter */
-                       /* must touch at most 16 K superblocks, whose operands are staged in LDS)  */
+    int64_t ntiles;    /* tiles of the item; each of the 4 waves takes a contiguous quarter       */
     int64_t lo;        /* valid arena positions [lo, hi)                                          */
     int64_t hi;
     int64_t v_delta;
@@ -102,6 +102,8 @@ typedef struct r2o_decode_params {
     int64_t q_dtype;                /* 0 = bf16, 1 = fp16                              */
     int64_t output_hadamard;        /* 1: out = bf16(FWHT128(bf16(out)))               */
     int64_t do_append;              /* 1: fused Recent-FP append of append_k/append_v  */
+    int64_t k_bf16;                 /* 1: k_packed holds bf16 key rows [Hkv, k_capacity, 128] (matched-FP /
+                                       v_fourq_k_bf16 caches; k_scale, k_zero, k_operands unused)      */
     float sm_scale;                 /* softmax scale (head_dim^-1/2 by default)        */
     int32_t recent_len[R2O_MAX_BATCH];     /* host-tracked Recent-FP active length     */
     int64_t append_global[R2O_MAX_BATCH];  /* global token index of the appended token */

@@ -1,6 +1,9 @@
 """numpy restatement of the three-pool SSPA cache and its append/flush (test infrastructure only).
 
-Follows, for the released ``v_fourq_k_int4_compact`` cache with INT2 generated values:
+Follows, for the released ``v_fourq_k_int4_compact`` cache with INT2 generated values (and the
+BF16-K variants: ``v_fourq_k_bf16`` keeps the pools' K rows in the input dtype, and the matched-FP
+cache keeps every surviving page, K and V, in one FP pool in page order, precision_pool.py:834-876,
+with flushes appended to it, dynamic_fourq_cache.py:145-170, 200-204):
   * ``_compact_page_layouts``      precision_pool.py:611-669  (stable FP -> INT4 -> INT2 -> evicted)
   * ``build_three_precision_cache`` precision_pool.py:787-984 (+ arenas in compact_int4_key.py:223-281,
                                    fused_value_pack.py:152-193, 519-575, recent ring :747-784)
@@ -92,17 +95,29 @@ class OracleCache:
     int2_logical: list = field(default_factory=list)
     flushed_tokens: int = 0
     tail_dequant_tokens: int = 0
+    # BF16-K variants: K rows in physical order [H, cap, D] float32 (values of the input dtype)
+    variant: str = "int4k"
+    k_rows: np.ndarray | None = None
 
     @property
     def recent_capacity(self) -> int:
         return int(self.recent_k.shape[1])
 
 
+def survivor_layout(page_offsets, page_lengths, page_classes):
+    """Tokens of every non-evicted page in page order (matched-FP pool, precision_pool.py:834-846)."""
+    classes = np.asarray(page_classes, dtype=np.int64)
+    parts = [np.arange(page_offsets[p], page_offsets[p] + page_lengths[p], dtype=np.int64)
+             for p in np.nonzero(classes != EVICTED_PAGE)[0]]
+    return np.concatenate(parts) if parts else np.zeros(0, np.int64)
+
+
 def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: str,
                 page_size: int = 32, superblock: int = 32, group: int = 32,
                 recent_capacity: int = 128, append_capacity: int = 260,
-                flush_size: int = 128) -> OracleCache:
-    """Restatement of ``build_three_precision_cache`` for ``v_fourq_k_int4_compact``.
+                flush_size: int = 128, variant: str = "int4k") -> OracleCache:
+    """Restatement of ``build_three_precision_cache``: ``variant`` "int4k" (``v_fourq_k_int4_compact``),
+    "bf16k" (``v_fourq_k_bf16``) or "matched" (``matched_fp=True``).
 
     ``key``/``value`` are float32 arrays holding values of ``dtype`` ([Hkv, S, 128]).
     """
@@ -110,6 +125,12 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
     value = np.asarray(value, np.float32)
     h, s, d = key.shape
     fp_t, i4_t, i2_t, ev_t = compact_page_layouts(page_offsets, page_lengths, page_classes)
+    if variant == "matched":
+        fp_t = survivor_layout(page_offsets, page_lengths, page_classes)
+        i4_t = i2_t = np.zeros(0, np.int64)
+        ev_t = np.zeros(s - len(fp_t), np.int64)
+    elif variant not in ("int4k", "bf16k"):
+        raise ValueError(f"unknown variant {variant}")
     if len(fp_t) + len(i4_t) + len(i2_t) + len(ev_t) != s:
         raise ValueError("compact physical pools must cover every logical token")
     # compact INT4-K arena over the physical order FP, INT4, INT2 (compact_int4_key.py:223-281)
@@ -120,12 +141,17 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
     k_packed = np.zeros((h, k_cap, d // 2), np.uint8)
     k_scale = np.zeros((h, blocks, d), np.float16)
     k_zero = np.zeros((h, blocks, d), np.uint8)
-    for start in range(0, active, superblock):
-        toks = ordered[start : start + superblock]
-        p, sc, z = quantize_int4_key_per_channel(key[:, toks], superblock)
-        k_packed[:, start : start + len(toks)] = p
-        k_scale[:, start // superblock] = sc[:, 0]
-        k_zero[:, start // superblock] = z[:, 0]
+    k_rows = None
+    if variant == "int4k":
+        for start in range(0, active, superblock):
+            toks = ordered[start : start + superblock]
+            p, sc, z = quantize_int4_key_per_channel(key[:, toks], superblock)
+            k_packed[:, start : start + len(toks)] = p
+            k_scale[:, start // superblock] = sc[:, 0]
+            k_zero[:, start // superblock] = z[:, 0]
+    else:
+        k_rows = np.zeros((h, k_cap, d), np.float32)
+        k_rows[:, :active] = key[:, ordered]
     # value pools
     fp_v = value[:, fp_t].copy()
     v4_packed, v4_scale = quantize_int4_value(value[:, i4_t])
@@ -156,6 +182,7 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
         recent_page_lengths=np.zeros(pages, np.int64),
         pool_tokens=[len(fp_t), len(i4_t), len(i2_t)],
         int2_global=list(i2_t), int2_logical=list(i2_t),
+        variant=variant, k_rows=k_rows,
     )
 
 
@@ -204,11 +231,24 @@ def append_token(c: OracleCache, new_k, new_v, *, global_index: int, logical_pos
         value_block = c.recent_v[:, :f].copy()
         g_block = c.recent_global[:f].copy()
         l_block = c.recent_logical[:f].copy()
-        c.tail_dequant_tokens += _flush_key_superblock(c, key_block)
-        _flush_value_int2(c, value_block)
-        c.int2_global.extend(g_block.tolist())
-        c.int2_logical.extend(l_block.tolist())
-        c.pool_tokens[2] += f
+        if c.variant == "matched":  # _append_matched_fp_block (dynamic_fourq_cache.py:145-170)
+            if c.k_active + f > c.k_capacity:
+                grown = np.zeros((c.hkv, c.k_capacity + _round_up(f, 128), c.k_rows.shape[2]), np.float32)
+                grown[:, : c.k_active] = c.k_rows[:, : c.k_active]
+                c.k_rows, c.k_capacity = grown, grown.shape[1]
+            c.k_rows[:, c.k_active : c.k_active + f] = key_block
+            c.k_active += f
+            c.fp_v = np.concatenate((c.fp_v, value_block), axis=1)
+            c.pool_tokens[0] += f
+        elif c.variant == "bf16k":  # dynamic_fourq_cache.py:226-230
+            raise RuntimeError("K-BF16/V-FourQ requires an append_fp_only Recent-FP capacity "
+                               "covering the requested generation horizon")
+        else:
+            c.tail_dequant_tokens += _flush_key_superblock(c, key_block)
+            _flush_value_int2(c, value_block)
+            c.int2_global.extend(g_block.tolist())
+            c.int2_logical.extend(l_block.tolist())
+            c.pool_tokens[2] += f
         rem = c.recent_active - f
         c.recent_k[:, :rem] = c.recent_k[:, f : c.recent_active].copy()
         c.recent_v[:, :rem] = c.recent_v[:, f : c.recent_active].copy()
@@ -235,15 +275,20 @@ def pool_kv(c: OracleCache):
     out = []
     s_fp, s_i4, s_i2 = c.pool_tokens
     segs = c.k_segments
+
+    def keys(start, n):
+        if c.k_rows is not None:
+            return c.k_rows[:, start : start + n]
+        return dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, start, n, c.superblock)
+
     if s_fp:
-        out.append((dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, segs[0], s_fp, c.superblock), c.fp_v))
+        out.append((keys(segs[0], s_fp), c.fp_v))
     if s_i4:
         # PackedTensor.dequantize rounds the fp32 product back to the input dtype
         # (packed_kv_layout.py:30-32); the compact INT4-K / INT2-V arenas stay fp32.
-        out.append((dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, segs[1], s_i4, c.superblock),
-                    round_to_dtype(dequantize_int4_value(c.v4_packed, c.v4_scale), c.dtype)))
+        out.append((keys(segs[1], s_i4), round_to_dtype(dequantize_int4_value(c.v4_packed, c.v4_scale), c.dtype)))
     if s_i2:
-        out.append((dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, segs[2], s_i2, c.superblock),
+        out.append((keys(segs[2], s_i2),
                     dequantize_int2_value(c.v2_packed[:, :s_i2], c.v2_scale[:, :s_i2], c.v2_zero[:, :s_i2], c.group)))
     if c.recent_active:
         out.append((c.recent_k[:, : c.recent_active], c.recent_v[:, : c.recent_active]))

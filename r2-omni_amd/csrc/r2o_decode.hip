@@ -38,12 +38,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 #endif
 constexpr int kDmaStages = R2O_DMA_STAGES;
 static_assert(kDmaStages >= 1 && kDmaStages <= 3, "1 to 3 LDS stages per wave");
-constexpr int kStageBytes = 10752;                  // one tile stage (sized for BF16 V, see StageLayout)
-constexpr int kWaveLds = kDmaStages * kStageBytes;  // per-wave LDS ring
 constexpr int kMergeFloats = 16 + 16 + 16 * 128;    // per wave: m, l, acc
-constexpr int kSmemBytes = (kWaves * kMergeFloats * 4 > kWaves * kWaveLds) ? kWaves * kMergeFloats * 4
-                                                                             : kWaves * kWaveLds;
-constexpr int kBlocksPerCU = 3;                     // resident partial workgroups per CU
+
+// Per-kernel LDS / occupancy configuration.  BK = the cache keeps K as bf16 rows (matched-FP and
+// v_fourq_k_bf16 caches); otherwise K is the compact INT4 arena.
+template <bool BK>
+struct KernelCfg {
+    static constexpr int kStage = BK ? 16384 : 10752;  // one tile stage (sized for BF16 V, see StageLayout)
+    static constexpr int kWaveLds = kDmaStages * kStage;
+    static constexpr int kSmem = (kWaves * kMergeFloats * 4 > kWaves * kWaveLds) ? kWaves * kMergeFloats * 4
+                                                                                 : kWaves * kWaveLds;
+    static constexpr int kBlocksPerCU = BK ? 2 : 3;     // resident partial workgroups per CU
+};
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
 
@@ -174,29 +180,36 @@ __device__ __forceinline__ VConst make_vconst() {
 // 32g ..), the tile's K superblock operands of lane group g, and for each of the lane's 8 tokens
 // tile_token(g, k) the 8 V dims 8*l16 .. 8*l16+7 (bf16: 16 B, INT4: 4 B, INT2: 2 B) plus the
 // token's V metadata.
-template <int KIND>
-struct TileRegs;
+template <bool BK>
+struct KRegs;
 template <>
-struct TileRegs<kFP> {
+struct KRegs<false> {  // INT4-K: codes of tokens 16 mg + l16 (channels 32g ..) and the operand vectors
     r2o_u4 kx[2];
     r2o_u4 ops[8];
+};
+template <>
+struct KRegs<true> {  // BF16-K: channels 32g + 8j .. 32g + 8j + 7 of tokens 16 mg + l16
+    r2o_u4 kb[2][4];
+};
+template <int KIND>
+struct VRegs;
+template <>
+struct VRegs<kFP> {
     r2o_u4 v[8];
 };
 template <>
-struct TileRegs<kI4> {
-    r2o_u4 kx[2];
-    r2o_u4 ops[8];
+struct VRegs<kI4> {
     uint32_t v[8];
     uint32_t vm[8];  // f32 scale bits
 };
 template <>
-struct TileRegs<kI2> {
-    r2o_u4 kx[2];
-    r2o_u4 ops[8];
+struct VRegs<kI2> {
     uint32_t v[8];
     uint32_t vm[8];  // fp16 scale bits (group of dims 8*l16)
     uint32_t vz[8];  // u8 zero point
 };
+template <int KIND, bool BK>
+struct TileRegs : KRegs<BK>, VRegs<KIND> {};
 
 // Valid arena positions of the segment (partial tiles mask the rest).
 struct SegCtx {
@@ -256,7 +269,7 @@ __device__ __forceinline__ void tile_logits(const SegCtx& c, int a0, int g, cons
 // PV of one tile with probabilities pk (the lane's 8 tokens).
 template <int KIND>
 __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const VConst& vc, const float (&pk)[8],
-                                        const TileRegs<KIND>& cur) {
+                                        const VRegs<KIND>& cur) {
     r2o_u4 ap;
     if constexpr (KIND == kFP) {
 #pragma unroll
@@ -310,13 +323,27 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
     }
 }
 
+// QK^T of one BF16-K tile: per MFMA j the bf16 key rows (channels 32g + 8j ..) against the bf16
+// query pairs, scaled by D^-1/2 log2(e) afterwards (the recent-ring formulation).
+__device__ __forceinline__ void qk_bf16k(const uint32_t (&qp)[4][4], float qscale, const r2o_u4 (&kb)[2][4],
+                                         r2o_f4 (&s)[2]) {
+#pragma unroll
+    for (int mg = 0; mg < 2; ++mg) {
+        r2o_f4 acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = r2o_mfma_bf16(kb[mg][j], r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
+        s[mg] = acc * qscale;
+    }
+}
+
 // One tile: QK, masks, online softmax, PV.
-template <int KIND>
+template <int KIND, bool BK>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
-                                            int a0, int g, const TileRegs<KIND>& cur) {
+                                            int a0, int g, float qscale, const TileRegs<KIND, BK>& cur) {
     r2o_f4 s[2];
-    float corr;
-    qk_int4k(ss.qp, vc, cur.ops, cur.kx, s, corr);
+    float corr = 0.f;
+    if constexpr (BK) qk_bf16k(ss.qp, qscale, cur.kb, s);
+    else qk_int4k(ss.qp, vc, cur.ops, cur.kx, s, corr);
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
     softmax_tile(st, sv, pk, g, corr, KIND == kI4 ? &ss.bias : nullptr);
@@ -331,19 +358,23 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
 // the transposed per-lane reads hit distinct LDS banks (see the slot functions).  A DMA of 16
 // bytes per lane fills LDS at lane * 16; one of 1, 2 or 4 bytes per lane fills the low bytes of
 // the dword at lane * 4, so sub-dword metadata rows sit in dword slots.
-template <int KIND>
-struct StageLayout {  // byte offsets within a stage: K codes | V payload | K operands | V metadata
-    static constexpr int kV = 2048;
+template <int KIND, bool BK>
+struct StageLayout {  // byte offsets within a stage: K | V payload | K operands (INT4-K) | V metadata
+    static constexpr int kKBytes = BK ? 8192 : 2048;
+    static constexpr int kV = kKBytes;
     static constexpr int kVBytes = KIND == kFP ? 8192 : (KIND == kI4 ? 2048 : 1024);
-    static constexpr int kOps = kV + kVBytes;
-    static constexpr int kScale = kOps + 512;
+    static constexpr int kOps = kV + kVBytes;                  // INT4-K only
+    static constexpr int kScale = BK ? kV + kVBytes : kOps + 512;
     static constexpr int kZero = kScale + 256;                 // INT2 only
-    static constexpr int kDma = 2 + kVBytes / 1024 + 1 + (KIND == kFP ? 0 : (KIND == kI4 ? 1 : 2));
-    static constexpr int kEnd = KIND == kFP ? kOps + 512 : (KIND == kI4 ? kScale + 128 : kZero + 128);
+    static constexpr int kDma = kKBytes / 1024 + kVBytes / 1024 + (BK ? 0 : 1) + (KIND == kFP ? 0 : (KIND == kI4 ? 1 : 2));
+    static constexpr int kEnd = KIND == kFP ? kScale : (KIND == kI4 ? kScale + 128 : kZero + 128);
 };
-static_assert(StageLayout<kFP>::kEnd <= kStageBytes && StageLayout<kI4>::kEnd <= kStageBytes &&
-                  StageLayout<kI2>::kEnd <= kStageBytes,
-              "every tile stage fits kStageBytes");
+template <bool BK>
+constexpr bool stages_fit() {
+    return StageLayout<kFP, BK>::kEnd <= KernelCfg<BK>::kStage && StageLayout<kI4, BK>::kEnd <= KernelCfg<BK>::kStage &&
+           StageLayout<kI2, BK>::kEnd <= KernelCfg<BK>::kStage;
+}
+static_assert(stages_fit<false>() && stages_fit<true>(), "every tile stage fits its kernel's stage size");
 
 // K codes: token t (0..31), 16-byte chunk c (0..3) of its 64-byte row.  Reads: 8 lanes take 8
 // consecutive tokens of one chunk, so the chunk is rotated by (t >> 1) & 3.
@@ -354,6 +385,9 @@ __device__ __forceinline__ int v4_slot(int t, int c) { return 8 * ((t & 3) + 4 *
 // INT2 V: token t, chunk c (0..1) of its 32-byte row; tokens t, t+4, t+8, t+12 share 8 slots.
 __device__ __forceinline__ int v2_slot(int t, int c) { return 8 * (t & 3) + 32 * (t >> 4) + 2 * ((t >> 2) & 3) + c; }
 // BF16 V rows stay in natural order: 8 lanes read 8 consecutive chunks of one 256-byte row.
+// BF16 K: token t, chunk c (0..15) of its 256-byte row.  Reads: 8 lanes take one chunk of 8
+// consecutive tokens, so the chunk is rotated by t.
+__device__ __forceinline__ int kb_slot(int t, int c) { return 16 * t + (c ^ (t & 15)); }
 
 template <int SIZE>
 __device__ __forceinline__ void dma(const void* gsrc, unsigned char* lds) {
@@ -387,11 +421,19 @@ struct DmaCtx {
     int vt0, vt1, vc0, vc1; // this lane's V source token / chunk for the INT V DMAs
 };
 
-template <int KIND>
+template <int KIND, bool BK>
 __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char* stage, int lane) {
-    using Lay = StageLayout<KIND>;
-    dma<16>(c.kcode + a0 * 64 + c.koff0, stage);
-    dma<16>(c.kcode + a0 * 64 + c.koff1, stage + 1024);
+    using Lay = StageLayout<KIND, BK>;
+    if constexpr (BK) {  // 8 x 1 KB of bf16 rows: slot s = 64 j + lane holds chunk c of token t
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int sl = 64 * j + lane, t = sl >> 4, ch = (sl & 15) ^ (t & 15);
+            dma<16>(c.kcode + (a0 + t) * 256 + ch * 16, stage + 1024 * j);
+        }
+    } else {
+        dma<16>(c.kcode + a0 * 64 + c.koff0, stage);
+        dma<16>(c.kcode + a0 * 64 + c.koff1, stage + 1024);
+    }
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
     // rows outside [lo, hi) read a clamped valid row (finite data, probability 0)
     auto row = [&](int t) { return (full ? a0 + t : min(max(a0 + t, c.lo), c.hi - 1)) - c.vdelta; };
@@ -404,7 +446,8 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
     } else {
         dma<16>(c.vrows + row(c.vt0) * 32 + c.vc0 * 16, stage + Lay::kV);
     }
-    if (lane < 32) dma<16>(c.kops + (a0 >> c.sb_shift) * 128 + lane * 4, stage + Lay::kOps);
+    if constexpr (!BK)
+        if (lane < 32) dma<16>(c.kops + (a0 >> c.sb_shift) * 128 + lane * 4, stage + Lay::kOps);
     if constexpr (KIND == kI4) {
         if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
     } else if constexpr (KIND == kI2) {
@@ -421,14 +464,22 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
     }
 }
 
-template <int KIND>
+template <int KIND, bool BK>
 __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, int g, int gamma, int groups,
-                                          TileRegs<KIND>& tr) {
-    using Lay = StageLayout<KIND>;
+                                          TileRegs<KIND, BK>& tr) {
+    using Lay = StageLayout<KIND, BK>;
+    if constexpr (BK) {
 #pragma unroll
-    for (int mg = 0; mg < 2; ++mg) tr.kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(16 * mg + l16, g));
+        for (int mg = 0; mg < 2; ++mg)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) tr.ops[j] = *reinterpret_cast<const r2o_u4*>(stage + Lay::kOps + g * 128 + 16 * j);
+            for (int j = 0; j < 4; ++j)
+                tr.kb[mg][j] = *reinterpret_cast<const r2o_u4*>(stage + 16 * kb_slot(16 * mg + l16, 4 * g + j));
+    } else {
+#pragma unroll
+        for (int mg = 0; mg < 2; ++mg) tr.kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(16 * mg + l16, g));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tr.ops[j] = *reinterpret_cast<const r2o_u4*>(stage + Lay::kOps + g * 128 + 16 * j);
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int t = tile_token(g, k);
@@ -445,9 +496,10 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
     }
 }
 
-template <int KIND>
+template <int KIND, bool BK>
 __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
                             unsigned char* smem, WaveState& st) {
+    using Cfg = KernelCfg<BK>;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
@@ -456,10 +508,10 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int t_begin = wave * per;
     const int t_end = min((int)it.ntiles, t_begin + per);
     if (t_begin >= t_end) return;
-    unsigned char* ring = smem + wave * kWaveLds;
+    unsigned char* ring = smem + wave * Cfg::kWaveLds;
 
     DmaCtx c;
-    c.kcode = rq.k_packed + kvh * rq.k_capacity * 64;
+    c.kcode = rq.k_packed + kvh * rq.k_capacity * (BK ? 256 : 64);
     c.kops = rq.k_operands + kvh * rq.k_superblocks * 128;
     c.lo = (int)it.lo;
     c.hi = (int)it.hi;
@@ -500,25 +552,26 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int a_first = (int)it.tile0 + 32 * t_begin;
 #pragma unroll
     for (int j = 0; j < kDmaStages; ++j)
-        if (j < n) dma_tile<KIND>(c, a_first + 32 * j, ring + j * kStageBytes, lane);
+        if (j < n) dma_tile<KIND, BK>(c, a_first + 32 * j, ring + j * Cfg::kStage, lane);
 
     const VConst vc = make_vconst();
+    const float qscale = p.sm_scale * kLog2e;
     SegState<KIND> ss;
-    load_query<false>(p, b, kvh, gqa, l16, g, p.sm_scale * kLog2e, ss.qp);
+    load_query<BK>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: bf16 pairs, scaled after the MFMA
     ss.bias = r2o_f4{0, 0, 0, 0};
     const SegCtx sc = {c.lo, c.hi};
     for (int i = 0; i < n; ++i) {
-        wait_tiles<StageLayout<KIND>::kDma>(min(kDmaStages, n - i) - 1);  // tile i has landed
+        wait_tiles<StageLayout<KIND, BK>::kDma>(min(kDmaStages, n - i) - 1);  // tile i has landed
         __builtin_amdgcn_wave_barrier();
-        unsigned char* stage = ring + (i % kDmaStages) * kStageBytes;
-        TileRegs<KIND> cur;
-        read_tile<KIND>(stage, l16, g, gamma, c.groups, cur);
+        unsigned char* stage = ring + (i % kDmaStages) * Cfg::kStage;
+        TileRegs<KIND, BK> cur;
+        read_tile<KIND, BK>(stage, l16, g, gamma, c.groups, cur);
         if (i + kDmaStages < n) {
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the whole stage is in registers
             __builtin_amdgcn_wave_barrier();
-            dma_tile<KIND>(c, a_first + 32 * (i + kDmaStages), stage, lane);
+            dma_tile<KIND, BK>(c, a_first + 32 * (i + kDmaStages), stage, lane);
         }
-        seg_compute<KIND>(sc, st, ss, vc, a_first + 32 * i, g, cur);
+        seg_compute<KIND, BK>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
     }
     if constexpr (KIND == kI4) {  // remove the code offsets: lo dims 1032 * sum P', hi dims (1152 * sum P') / 16
 #pragma unroll
@@ -589,8 +642,9 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     }
 }
 
-__global__ __launch_bounds__(256, kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
-    __shared__ __align__(16) unsigned char smem[kSmemBytes];
+template <bool BK>
+__global__ __launch_bounds__(256, KernelCfg<BK>::kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
+    __shared__ __align__(16) unsigned char smem[KernelCfg<BK>::kSmem];
     const r2o_work_item it = p.items[blockIdx.x];
     const r2o_request_desc rq = p.reqs[it.req];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -604,9 +658,9 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void decode_partial_kernel(r2o_d
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP>(p, it, rq, smem, st); break;
-        case kI4: run_segment<kI4>(p, it, rq, smem, st); break;
-        case kI2: run_segment<kI2>(p, it, rq, smem, st); break;
+        case kFP: run_segment<kFP, BK>(p, it, rq, smem, st); break;
+        case kI4: run_segment<kI4, BK>(p, it, rq, smem, st); break;
+        case kI2: run_segment<kI2, BK>(p, it, rq, smem, st); break;
         default: run_recent(p, it, rq, st); break;
     }
 
@@ -766,8 +820,12 @@ extern "C" {
 int r2o_decode_partial(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_partial_kernel, dim3((unsigned)params->n_items), dim3(256), 0, (hipStream_t)stream,
-                       *params);
+    if (params->k_bf16)
+        hipLaunchKernelGGL(decode_partial_kernel<true>, dim3((unsigned)params->n_items), dim3(256), 0,
+                           (hipStream_t)stream, *params);
+    else
+        hipLaunchKernelGGL(decode_partial_kernel<false>, dim3((unsigned)params->n_items), dim3(256), 0,
+                           (hipStream_t)stream, *params);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
 }

@@ -45,6 +45,7 @@ class DecodeParams(ctypes.Structure):
         ("q_dtype", c_i64),
         ("output_hadamard", c_i64),
         ("do_append", c_i64),
+        ("k_bf16", c_i64),
         ("sm_scale", ctypes.c_float),
         ("recent_len", ctypes.c_int32 * MAX_BATCH),
         ("append_global", c_i64 * MAX_BATCH),
@@ -62,6 +63,7 @@ REQUEST_FIELDS = (
     "recent_global", "recent_logical", "recent_page_lengths",
 )
 # r2o_work_item: 9 eight-byte words.
+ITEM_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta", "slot")
 WORK_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta", "slot")
 KIND_FP, KIND_INT4, KIND_INT2, KIND_RECENT = 0, 1, 2, 3
 

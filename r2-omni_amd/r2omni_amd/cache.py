@@ -43,6 +43,34 @@ class PhysicalPageIndex:
     logical_positions: torch.Tensor
 
 
+# ------------------------------------------------------------------------ BF16 K rows
+@dataclass
+class BF16KeyArena:
+    """Key rows kept in bf16 in physical pool order (FP, INT4, INT2) with append capacity.
+
+    Backs the matched-FP cache and the v_fourq_k_bf16 variant: the pools' ``fp_k`` are views of
+    ``rows`` (precision_pool.py:834-906 keeps one bf16 K tensor per pool; one arena serves the
+    decode kernel, which reads K rows by physical position).
+    """
+    rows: torch.Tensor              # bf16 [H, capacity, D]
+    active_length: int
+    capacity: int
+    segment_offsets: tuple[int, int, int]
+
+    def view(self, start: int, length: int) -> torch.Tensor:
+        return self.rows[:, start : start + length]
+
+    def append_block(self, key_block: torch.Tensor) -> None:
+        n = int(key_block.shape[1])
+        if self.active_length + n > self.capacity:
+            grown = torch.zeros((self.rows.shape[0], _round_up(self.active_length + n + 128, 128), self.rows.shape[2]),
+                                device=self.rows.device, dtype=self.rows.dtype)
+            grown[:, : self.active_length].copy_(self.rows[:, : self.active_length])
+            self.rows, self.capacity = grown, int(grown.shape[1])
+        self.rows[:, self.active_length : self.active_length + n].copy_(key_block)
+        self.active_length += n
+
+
 # ------------------------------------------------------------------------ compact INT4 K
 @dataclass
 class CompactInt4KeyArena:
@@ -403,6 +431,7 @@ class ThreePrecisionCache:
     generated_value_precision: str = "int2"
     static_int4_tokens: int = 0
     generated_k_offset: int = 0
+    bf16_key: BF16KeyArena | None = None   # K rows of the matched-FP / v_fourq_k_bf16 caches
 
     @property
     def pools(self):
@@ -410,7 +439,10 @@ class ThreePrecisionCache:
 
     @property
     def payload_bytes(self) -> int:
-        return sum(p.payload_bytes for p in self.pools) + (0 if self.compact_key is None else self.compact_key.nbytes)
+        total = sum(p.payload_bytes for p in self.pools) + (0 if self.compact_key is None else self.compact_key.nbytes)
+        if self.bf16_key is not None:  # the history pools' fp_k are views of one arena: count it once
+            total += _nbytes(self.bf16_key.rows) - sum(_nbytes(p.fp_k) for p in self.pools[:3])
+        return total
 
     @property
     def survivor_count(self) -> int:
@@ -539,6 +571,35 @@ def _compact_page_layouts(plan: LayerCompressionPlan, device=None):
     return layouts[0], layouts[1], layouts[2], (empty.to(dev), empty, empty, empty), layouts[3]
 
 
+def _survivor_layout(plan: LayerCompressionPlan, device):
+    """Every non-evicted page in page order: the single pool of a matched-FP cache (precision_pool.py:834-846)."""
+    classes = plan.page_classes.detach().to("cpu", torch.long)
+    starts = plan.page_offsets.detach().to("cpu", torch.long)
+    lens = plan.page_lengths.detach().to("cpu", torch.long)
+    pages = torch.nonzero(classes != PageClass.EVICTED_PAGE, as_tuple=False).flatten()
+    pl = lens[pages]
+    offsets = pl.cumsum(0) - pl
+    n_tok = int(pl.sum())
+    dev = torch.device(device)
+    if n_tok:
+        shift = torch.repeat_interleave((starts[pages] - offsets).to(dev), pl.to(dev), output_size=n_tok)
+        tokens = shift + torch.arange(n_tok, device=dev, dtype=torch.long)
+    else:
+        tokens = torch.zeros(0, dtype=torch.long, device=dev)
+    return tokens, offsets, pl, pages
+
+
+def _gather_key_rows(key: torch.Tensor, tokens: torch.Tensor, append_capacity: int, segments) -> BF16KeyArena:
+    h, s, d = map(int, key.shape)
+    n = int(tokens.numel())
+    cap = max(128, _round_up(n + int(append_capacity), 128))
+    rows = torch.zeros((h, cap, d), device=key.device, dtype=key.dtype)
+    if n:
+        _lib.call("r2o_gather_rows", _lib.ptr(key), h, s, _lib.ptr(tokens), n, _lib.ptr(rows), cap,
+                  _lib.stream_of(key.device))
+    return BF16KeyArena(rows=rows, active_length=n, capacity=cap, segment_offsets=tuple(segments))
+
+
 def _make_page_index(plan: LayerCompressionPlan, layout, device) -> PhysicalPageIndex:
     tokens, offsets, lengths, pages = layout
     gi = plan.global_token_indices.detach().to(device, torch.long)
@@ -608,15 +669,18 @@ def build_three_precision_cache(
         raise ValueError(f"unsupported cache_variant: {cache_variant}")
     if generated_value_precision not in ("int2", "int4"):
         raise ValueError("generated_value_precision must be int2 or int4")
-    if cache_variant != "v_fourq_k_int4_compact" or matched_fp or generated_value_precision != "int2" \
+    if (cache_variant == "v_fourq_k_int2_compact" and not matched_fp) or generated_value_precision != "int2" \
             or not preallocate_recent:
         raise NotImplementedError(
-            "the gfx950 path implements the released v_fourq_k_int4_compact cache with INT2 generated "
-            "values and a preallocated Recent-FP ring")
+            "the gfx950 path implements the v_fourq_k_int4_compact and v_fourq_k_bf16 caches and the matched-FP "
+            "cache, with INT2 generated values and a preallocated Recent-FP ring")
     if int(key.shape[2]) != 128:
         raise ValueError("the SSPA decode path requires head_dim 128")
     _lib.require_device(key, "key")
     _lib.dtype_code(key.dtype)
+    bf16_keys = matched_fp or cache_variant == "v_fourq_k_bf16"
+    if bf16_keys and key.dtype != torch.bfloat16:
+        raise ValueError("the BF16-K decode path requires bfloat16 K/V")
     key = key.contiguous()
     value = value.contiguous()
     dev = key.device
@@ -624,9 +688,30 @@ def build_three_precision_cache(
     if sum(int(l[0].numel()) for l in (fp_l, i4_l, i2_l, ev_l)) != int(key.shape[1]):
         raise ValueError("compact physical pools must cover every logical token")
     h = int(key.shape[0])
+    stream = _lib.stream_of(dev)
+    append_capacity = plan.recent_fp_capacity if compact_key_append_capacity is None \
+        else int(compact_key_append_capacity)
+    gi = plan.global_token_indices.detach().to(dev, torch.long)
+    common = dict(evicted_global_indices=gi[ev_l[0]], page_size=int(page_size),
+                  quantization_superblock=int(quantization_superblock), cache_variant=cache_variant,
+                  recent_flush_size=int(recent_flush_size), generated_value_precision="int2")
+    if matched_fp:  # every surviving page, K and V in bf16, in one FP pool (precision_pool.py:834-876)
+        surv = _survivor_layout(plan, dev)
+        n = int(surv[0].numel())
+        arena = _gather_key_rows(key, surv[0], append_capacity, (0, n, n))
+        fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(plan, surv, dev), fp_k=arena.view(0, n))
+        fp_pool.fp_v = torch.empty((h, n, 128), device=dev, dtype=value.dtype)
+        if n:
+            _lib.call("r2o_gather_rows", _lib.ptr(value), h, int(value.shape[1]), _lib.ptr(surv[0]), n,
+                      _lib.ptr(fp_pool.fp_v), n, stream)
+        empty = (surv[0][:0], surv[1][:0], surv[2][:0], surv[3][:0])
+        recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity)
+        return ThreePrecisionCache(
+            fp_pool=fp_pool, int4_pool=PrecisionPool(name="int4", page_index=_make_page_index(plan, empty, dev)),
+            int2_pool=PrecisionPool(name="int2", page_index=_make_page_index(plan, empty, dev)),
+            recent_fp_pool=recent, matched_fp=True, bf16_key=arena, generated_k_offset=n, **common)
     fp_tokens, i4_tokens, i2_tokens = (l[0].to(dev) for l in (fp_l, i4_l, i2_l))
     s_fp, s_i4 = int(fp_tokens.numel()), int(i4_tokens.numel())
-    stream = _lib.stream_of(dev)
 
     fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(plan, fp_l, dev))
     if s_fp:
@@ -637,23 +722,26 @@ def build_three_precision_cache(
     if s_i4:
         int4_pool.packed_v = fused_gather_pack_int4_value(value, i4_tokens)
     int2_pool = PrecisionPool(name="int2", page_index=_make_page_index(plan, i2_l, dev))
-    append_capacity = plan.recent_fp_capacity if compact_key_append_capacity is None \
-        else int(compact_key_append_capacity)
     compact_value = build_compact_int2_value_arena(value, i2_tokens, append_capacity=append_capacity,
                                                    group_size=int2_group_size)
     int2_pool.packed_v = compact_value
+    recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity)
+    if bf16_keys:  # v_fourq_k_bf16: every pool keeps bf16 K rows (precision_pool.py:878-906)
+        s_i2 = int(i2_tokens.numel())
+        arena = _gather_key_rows(key, torch.cat((fp_tokens, i4_tokens, i2_tokens)), append_capacity,
+                                 (0, s_fp, s_fp + s_i4))
+        fp_pool.fp_k, int4_pool.fp_k = arena.view(0, s_fp), arena.view(s_fp, s_i4)
+        int2_pool.fp_k = arena.view(s_fp + s_i4, s_i2)
+        return ThreePrecisionCache(
+            fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
+            compact_value=compact_value, static_int4_tokens=s_i4, bf16_key=arena, **common)
     compact_key = build_compact_int4_key_arena(key, (fp_tokens, i4_tokens, i2_tokens),
                                                append_capacity=append_capacity,
                                                superblock_size=key_quantization_superblock)
-    recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity)
-    gi = plan.global_token_indices.detach().to(dev, torch.long)
     return ThreePrecisionCache(
-        fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent,
-        evicted_global_indices=gi[ev_l[0]], page_size=int(page_size),
-        quantization_superblock=int(quantization_superblock), matched_fp=False, cache_variant=cache_variant,
-        compact_key=compact_key, compact_value=compact_value, recent_flush_size=int(recent_flush_size),
-        generated_value_precision="int2", static_int4_tokens=s_i4, generated_k_offset=compact_key.active_length,
-    )
+        fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
+        compact_key=compact_key, compact_value=compact_value, static_int4_tokens=s_i4,
+        generated_k_offset=compact_key.active_length, **common)
 
 
 # ------------------------------------------------------------------------- append / flush
@@ -705,17 +793,29 @@ def append_generated_token(cache: ThreePrecisionCache, new_key: torch.Tensor, ne
     stream = _lib.stream_of(new_key.device)
     flushed = False
     if pool.active_length == pool.capacity:
-        if cache.compact_key is None or cache.compact_value is None:
-            raise RuntimeError("compact INT4 K cache is missing its compact INT2 V arena")
         key_block = pool.fp_k[:, :flush]
         value_block = pool.fp_v[:, :flush]
         # copy the index slices before the ring shift overwrites them
         global_block = pool.global_index_buffer[:flush].clone()
         logical_block = pool.logical_position_buffer[:flush].clone()
-        stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
-            if flush == 128 else _flush_size_error(flush)
-        cache.compact_value.append_superblock(value_block, source_tokens=cap)
-        _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
+        if cache.matched_fp:  # _append_matched_fp_block (dynamic_fourq_cache.py:145-170)
+            _append_int2_page_metadata(cache.fp_pool, global_block, logical_block, cache.page_size)
+            cache.bf16_key.append_block(key_block)
+            n = cache.bf16_key.active_length
+            cache.bf16_key.segment_offsets = (0, n, n)
+            cache.fp_pool.fp_k = cache.bf16_key.view(0, n)
+            cache.fp_pool.fp_v = torch.cat((cache.fp_pool.fp_v, value_block), dim=1)
+            cache.generated_k_offset = n
+        elif cache.bf16_key is not None:  # dynamic_fourq_cache.py:226-230
+            raise RuntimeError("K-BF16/V-FourQ requires an append_fp_only Recent-FP capacity covering the "
+                               "requested generation horizon")
+        else:
+            if cache.compact_key is None or cache.compact_value is None:
+                raise RuntimeError("compact INT4 K cache is missing its compact INT2 V arena")
+            stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
+                if flush == 128 else _flush_size_error(flush)
+            cache.compact_value.append_superblock(value_block, source_tokens=cap)
+            _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
         _lib.call("r2o_recent_shift", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, flush, pool.active_length,
                   _lib.ptr(pool.global_index_buffer), _lib.ptr(pool.logical_position_buffer),
                   _lib.ptr(pool.length_device), _lib.ptr(pool.page_index.lengths), cache.page_size, stream)

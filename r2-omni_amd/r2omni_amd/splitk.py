@@ -13,9 +13,8 @@ workspace is one split-K work item (a run of 32-token tiles handled by one workg
 """
 from __future__ import annotations
 
-import heapq
-
 import ctypes
+import heapq
 from dataclasses import dataclass, field
 from typing import Sequence
 
@@ -27,12 +26,6 @@ from .cache import ThreePrecisionCache
 TILE = 32
 _MIN_TILES_PER_ITEM = 4      # one tile per wave of the 4-wave workgroup
 _BLOCKS_PER_CU = 2           # work items planned per CU (the kernel holds up to 3 resident; 2 keeps the combine short)
-
-
-def _max_tiles_per_item(superblock: int) -> int:
-    """Largest item whose per-wave share of K superblock operands (<= 16 blocks) fits in LDS."""
-    per_wave = 16 if superblock == TILE else 15 * superblock // TILE  # +1 block when unaligned
-    return 4 * per_wave
 
 
 @dataclass
@@ -53,13 +46,14 @@ def _num_cus(device: torch.device) -> int:
 
 def _segments(cache: ThreePrecisionCache, extra_int2: int = 0):
     """(kind, lo, hi, v_delta) arena ranges of the FP, INT4 and INT2(+generated) pools."""
-    ck = cache.compact_key
-    if ck is None or not cache.compact_int4_key:
-        raise NotImplementedError("the gfx950 decode path requires the compact INT4-K arena")
+    ck = cache.compact_key if cache.compact_key is not None else cache.bf16_key
+    if ck is None or (cache.compact_key is not None and not cache.compact_int4_key):
+        raise NotImplementedError("the gfx950 decode path requires a compact INT4-K or a bf16 K arena")
     k_fp, k_i4, k_i2 = ck.segment_offsets
-    s_fp = cache.fp_pool.token_count
+    s_fp = cache.fp_pool.token_count + (int(extra_int2) if cache.matched_fp else 0)
     s_i4 = cache.int4_pool.token_count
-    s_i2 = cache.compact_value.active_length + int(extra_int2)
+    s_i2 = (0 if cache.compact_value is None else cache.compact_value.active_length) \
+        + (0 if cache.matched_fp else int(extra_int2))
     out = []
     for kind, lo, n in ((_lib.KIND_FP, k_fp, s_fp), (_lib.KIND_INT4, k_i4, s_i4), (_lib.KIND_INT2, k_i2, s_i2)):
         if n > 0:
@@ -88,8 +82,6 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
     Returns (items [n, 9] int64 in launch order, group_begin [B*hkv + 1] int32) on the host.
     """
     segs = [_segments(c, extra_int2) for c in caches]
-    ck = getattr(caches[0], "compact_key", None)
-    max_tiles = _max_tiles_per_item(ck.superblock_size if ck is not None else TILE)
     runs = []  # (req, head, kind, first tile position, tiles, lo, hi, v_delta)
     for r, (c, ss) in enumerate(zip(caches, segs)):
         rcap = c.recent_fp_pool.capacity
@@ -103,7 +95,7 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
     # Water-filling: give one more item to the run whose items are currently the most
     # expensive until the workgroup slots are used up (or no run can be split further).
     target = _BLOCKS_PER_CU * max(1, num_cus)
-    counts = [max(1, -(-run[4] // max_tiles)) for run in runs]
+    counts = [1] * len(runs)
 
     def item_cost(i: int) -> float:
         nt = runs[i][4]
@@ -186,15 +178,23 @@ def _request_desc(cache: ThreePrecisionCache) -> list[int]:
         raise ValueError("the gfx950 decode path requires bfloat16 FP-V / Recent-FP rows")
     i4_packed = i4.packed_v.packed if i4.token_count else None
     i4_scale = i4.packed_v.scale if i4.token_count else None
+    if ck is not None:
+        kw = {"k_packed": ck.packed.data_ptr(), "k_scale": ck.scale.data_ptr(), "k_zero": ck.zero_point.data_ptr(),
+              "k_capacity": ck.capacity, "k_superblocks": ck.superblock_count,
+              "k_operands": ck.kernel_operands.data_ptr()}
+    else:  # bf16 key rows: the kernel reads k_packed as rows [Hkv, k_capacity, 128]
+        kb = cache.bf16_key
+        kw = {"k_packed": kb.rows.data_ptr(), "k_scale": 0, "k_zero": 0, "k_capacity": kb.capacity,
+              "k_superblocks": 0, "k_operands": 0}
     words = {
-        "k_packed": ck.packed.data_ptr(), "k_scale": ck.scale.data_ptr(), "k_zero": ck.zero_point.data_ptr(),
-        "k_capacity": ck.capacity, "k_superblocks": ck.superblock_count,
-        "k_operands": ck.kernel_operands.data_ptr(),
+        **kw,
         "fp_v": fp.fp_v.data_ptr() if fp.token_count else 0, "fp_stride": fp.token_count,
         "i4_v": i4_packed.data_ptr() if i4_packed is not None else 0,
         "i4_scale": i4_scale.data_ptr() if i4_scale is not None else 0, "i4_stride": i4.token_count,
-        "i2_v": cv.packed.data_ptr(), "i2_scale": cv.scale.data_ptr(), "i2_zero": cv.zero_point.data_ptr(),
-        "i2_stride": cv.capacity,
+        "i2_v": cv.packed.data_ptr() if cv is not None else 0,
+        "i2_scale": cv.scale.data_ptr() if cv is not None else 0,
+        "i2_zero": cv.zero_point.data_ptr() if cv is not None else 0,
+        "i2_stride": cv.capacity if cv is not None else 0,
         "recent_k": rec.fp_k.data_ptr(), "recent_v": rec.fp_v.data_ptr(), "recent_capacity": rec.capacity,
         "recent_length": rec.length_device.data_ptr(), "recent_global": rec.global_index_buffer.data_ptr(),
         "recent_logical": rec.logical_position_buffer.data_ptr(),
@@ -207,8 +207,8 @@ def _request_desc(cache: ThreePrecisionCache) -> list[int]:
 class SplitKExecutor:
     caches: list
     workspace: SplitKWorkspace
-    reqs: torch.Tensor          # device int64 [B, 21]
-    items: torch.Tensor         # device int64 [n, 8]
+    reqs: torch.Tensor          # device int64 [B, 22]
+    items: torch.Tensor         # device int64 [n, 9]
     group_begin: torch.Tensor   # device int32 [B*Hkv + 1]
     n_items: int
     num_query_heads: int
@@ -243,6 +243,7 @@ class SplitKExecutor:
         p.superblock, p.int2_group, p.page_size = self.superblock, self.int2_group, self.page_size
         p.q_dtype = _lib.dtype_code(query.dtype)
         p.output_hadamard = int(self.output_hadamard)
+        p.k_bf16 = int(self.caches[0].bf16_key is not None)
         p.sm_scale = float(self.head_dim ** -0.5)
         for r, c in enumerate(self.caches):
             p.recent_len[r] = int(c.recent_fp_pool.active_length)
@@ -324,11 +325,12 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
         raise ValueError("split-K executor supports at most 16 GQA heads per KV head")
     if len(caches) > _lib.MAX_BATCH:
         raise ValueError(f"split-K executor supports at most {_lib.MAX_BATCH} requests per launch")
-    sb = first.compact_key.superblock_size
-    group = first.compact_value.group_size
+    bf16k = first.bf16_key is not None
+    sb = 32 if bf16k else first.compact_key.superblock_size
+    group = 32 if first.compact_value is None else first.compact_value.group_size
     for r, c in enumerate(caches):
-        ck = c.compact_key
-        if ck is None or ck.superblock_size != sb or c.compact_value.group_size != group \
+        if (c.bf16_key is not None) != bf16k or (not bf16k and c.compact_key.superblock_size != sb) \
+                or (c.compact_value is not None and c.compact_value.group_size != group) \
                 or int(c.recent_fp_pool.fp_k.shape[0]) != hkv or c.page_size != first.page_size:
             raise ValueError(f"batched split-K geometry differs for request {r}")
     dev = workspace.output.device

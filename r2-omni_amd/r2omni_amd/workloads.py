@@ -29,6 +29,7 @@ class DecodeConfig:
     page: int = 64
     superblock: int = 32
     group: int = 32
+    variant: str = "int4k"     # "int4k" (v_fourq_k_int4_compact), "bf16k" (v_fourq_k_bf16) or "matched"
 
 
 CONFIGS = {
@@ -91,7 +92,9 @@ def build_request_cache(cfg: DecodeConfig, data: RequestData, *, append_capacity
     cache = build_three_precision_cache(
         data.key, data.value, plan, page_size=cfg.page if cfg.page in (16, 32, 64) else 32,
         key_quantization_superblock=cfg.superblock, int2_group_size=cfg.group,
-        compact_key_append_capacity=append_capacity, recent_flush_size=128)
+        compact_key_append_capacity=append_capacity, recent_flush_size=128,
+        matched_fp=cfg.variant == "matched",
+        cache_variant="v_fourq_k_bf16" if cfg.variant == "bf16k" else "v_fourq_k_int4_compact")
     for i in range(int(data.recent_k.shape[0])):
         append_recent_fp_triton(cache, data.recent_k[i][:, None], data.recent_v[i][:, None],
                                 global_token_index=hist + i, logical_position=hist + i)

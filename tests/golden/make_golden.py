@@ -14,7 +14,9 @@ against closed forms and invariants in tests/test_oracle_*.py):
 * ``append_superblock`` dequantise-then-requantise of a partial K tail on a flush
   (compact_int4_key.py:210-220) and the INT2-V flush append (fused_value_pack.py:474-516);
 * the Recent-FP ring state after ``append_generated_token`` (dynamic_fourq_cache.py:172-267);
-* ``triton_mixed_reference`` attention outputs on those caches (triton_fourq_attention.py:72-125).
+* ``triton_mixed_reference`` attention outputs on those caches (triton_fourq_attention.py:72-125);
+* the matched-FP and K-BF16 caches (precision_pool.py:834-980): survivor order, pool K rows,
+  the matched flush append (dynamic_fourq_cache.py:145-170) and the K-BF16 flush refusal (:226-230).
 
 Usage:  python tests/golden/make_golden.py
 """
@@ -167,7 +169,94 @@ def _case(name, *, seq, hkv, dtype, page_size, sb, group, tier_probs, appends, s
     print(f"wrote {path}: flushes at {flushed_at}, tail tokens {stats.local_tail_dequant_tokens}")
 
 
+def _variant_case(name, *, variant, seq, hkv, dtype, page_size, sb, group, tier_probs, appends, seed):
+    """BF16-K caches: ``matched`` (matched_fp=True) or ``bf16k`` (cache_variant v_fourq_k_bf16)."""
+    sys.path.insert(0, REFERENCE)
+    from r2omni.sspa.policy.page_assignment import build_page_table, project_token_bits_to_pages
+    from r2omni.sspa.runtime.cache_plan import build_layer_compression_plan
+    from r2omni.sspa.runtime.precision_pool import build_three_precision_cache
+    from r2omni.sspa.runtime.dynamic_fourq_cache import DynamicCacheStats, append_generated_token
+    from r2omni.sspa.kernels.triton_fourq_attention import triton_mixed_reference
+
+    gen = torch.Generator().manual_seed(seed)
+    d = 128
+    key = torch.randn(hkv, seq, d, generator=gen).to(dtype)
+    value = torch.randn(hkv, seq, d, generator=gen).to(dtype)
+    modality = _modality(seq, gen)
+    table = build_page_table(modality, page_size=page_size, protected_mask=torch.zeros(seq, dtype=torch.bool),
+                             recent_mask=torch.zeros(seq, dtype=torch.bool))
+    probs = torch.tensor(tier_probs, dtype=torch.float)
+    page_tier = torch.multinomial(probs, table.num_pages, replacement=True, generator=gen)
+    bits_per_tier = torch.tensor([16, 4, 2, 0], dtype=torch.int8)  # 0 bits = evicted page
+    bits = torch.empty(seq, dtype=torch.int8)
+    for page, (off, ln) in enumerate(zip(table.offsets.tolist(), table.lengths.tolist())):
+        bits[off : off + ln] = bits_per_tier[page_tier[page]]
+    assignment = project_token_bits_to_pages(table, bits)
+    plan = build_layer_compression_plan(0, assignment, recent_fp_capacity=128)
+    kwargs = dict(page_size=page_size, key_quantization_superblock=sb, int2_group_size=group,
+                  compact_key_append_capacity=260, recent_flush_size=128)
+    if variant == "matched":
+        cache = build_three_precision_cache(key, value, plan, matched_fp=True, **kwargs)
+    else:
+        cache = build_three_precision_cache(key, value, plan, cache_variant="v_fourq_k_bf16", **kwargs)
+    query = torch.randn(1, hkv * 8, d, generator=gen)
+    record = {"key": _np(key), "value": _np(value), "dtype": np.array(str(dtype)),
+              "page_offsets": _np(plan.page_offsets), "page_lengths": _np(plan.page_lengths),
+              "page_classes": _np(plan.page_classes.to(torch.int64)), "page_size": np.array(page_size),
+              "superblock": np.array(sb), "group": np.array(group), "query": _np(query),
+              "variant": np.array(variant)}
+
+    def snapshot(prefix):
+        pools = [cache.fp_pool, cache.int4_pool, cache.int2_pool]
+        record[prefix + "k_rows"] = _np(torch.cat([p.fp_k for p in pools if p.token_count], dim=1))
+        record[prefix + "pool_tokens"] = np.array([p.token_count for p in pools] + [cache.recent_fp_pool.token_count])
+        fp = cache.fp_pool
+        record[prefix + "fp_v"] = _np(fp.fp_v) if fp.token_count else np.zeros((hkv, 0, d), np.uint16)
+        record[prefix + "fp_global"] = _np(fp.page_index.global_token_indices[: fp.token_count])
+        if variant == "bf16k":
+            i4 = cache.int4_pool
+            record[prefix + "v4_packed"] = _np(i4.packed_v.packed) if i4.token_count else np.zeros(0, np.uint8)
+            record[prefix + "v4_scale"] = (_np(i4.packed_v.scale) if i4.token_count
+                                           else np.zeros((hkv, 0, 1), np.float32))
+            cv = cache.compact_value
+            record[prefix + "v2_packed"] = _np(cv.packed[:, : cv.active_length])
+            record[prefix + "v2_scale"] = _np(cv.scale[:, : cv.active_length])
+            record[prefix + "v2_zero"] = _np(cv.zero_point[:, : cv.active_length])
+        rec = cache.recent_fp_pool
+        record[prefix + "recent_k"] = _np(rec.fp_k[:, : rec.active_length])
+        record[prefix + "recent_v"] = _np(rec.fp_v[:, : rec.active_length])
+        record[prefix + "attn"] = _np(triton_mixed_reference(query, cache).float())
+
+    snapshot("build_")
+    stats = DynamicCacheStats()
+    app_k = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
+    app_v = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
+    record["append_k"] = _np(app_k)
+    record["append_v"] = _np(app_v)
+    flushed_at, refused_at = [], -1
+    for step in range(appends):
+        try:
+            if append_generated_token(cache, app_k[step], app_v[step], global_token_index=seq + step,
+                                      logical_position=seq + step, stats=stats):
+                flushed_at.append(step)
+        except RuntimeError:
+            refused_at = step
+            break
+    record["flushed_at"] = np.array(flushed_at, dtype=np.int64)
+    record["refused_at"] = np.array(refused_at)
+    snapshot("after_")
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **record)
+    print(f"wrote {path}: flushes at {flushed_at}, refused at {refused_at}")
+
+
 def main() -> None:
+    only = set(sys.argv[1:])
+    if only:
+        for name, fn in _VARIANTS.items():
+            if name in only:
+                fn()
+        return
     # Qwen profile: 32-token pages (ragged at modality boundaries), K superblock 32, INT2 group 32.
     _case("qwen_ragged_bf16", seq=333, hkv=2, dtype=torch.bfloat16, page_size=32, sb=32,
           group=32, tier_probs=(0.2, 0.5, 0.3), appends=140, seed=11)
@@ -177,7 +266,22 @@ def main() -> None:
     # MiniCPM all-lowbit profile: K superblock 128, INT2 group 128, all INT2 values.
     _case("minicpm_lowbit_bf16", seq=300, hkv=2, dtype=torch.bfloat16, page_size=32, sb=128,
           group=128, tier_probs=(0.0, 0.0, 1.0), appends=129, seed=13)
+    # matched BF16 cache (the 7B profile's first layers): survivors in page order, flush appends.
+    _variant_case("matched_fp_bf16", variant="matched", seq=300, hkv=2, dtype=torch.bfloat16, page_size=32,
+                  sb=32, group=32, tier_probs=(0.3, 0.3, 0.3, 0.1), appends=131, seed=14)
+    # K-BF16 / V-FourQ cache: tiered values, bf16 keys; a flush is refused by the reference.
+    _variant_case("kbf16_tiered_bf16", variant="bf16k", seq=330, hkv=2, dtype=torch.bfloat16, page_size=32,
+                  sb=32, group=32, tier_probs=(0.2, 0.4, 0.4, 0.0), appends=130, seed=15)
 
+
+_VARIANTS = {
+    "matched_fp_bf16": lambda: _variant_case("matched_fp_bf16", variant="matched", seq=300, hkv=2,
+                                             dtype=torch.bfloat16, page_size=32, sb=32, group=32,
+                                             tier_probs=(0.3, 0.3, 0.3, 0.1), appends=131, seed=14),
+    "kbf16_tiered_bf16": lambda: _variant_case("kbf16_tiered_bf16", variant="bf16k", seq=330, hkv=2,
+                                               dtype=torch.bfloat16, page_size=32, sb=32, group=32,
+                                               tier_probs=(0.2, 0.4, 0.4, 0.0), appends=130, seed=15),
+}
 
 if __name__ == "__main__":
     main()

@@ -7,8 +7,18 @@ import numpy as np
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-def fixture_names():
+def _all_names():
     return sorted(os.path.splitext(os.path.basename(p))[0] for p in glob.glob(os.path.join(HERE, "*.npz")))
+
+
+def fixture_names():
+    """Fixtures of the compact INT4-K cache (v_fourq_k_int4_compact)."""
+    return [n for n in _all_names() if "variant" not in np.load(os.path.join(HERE, n + ".npz"), allow_pickle=False)]
+
+
+def variant_fixture_names():
+    """Fixtures of the BF16-K caches (matched-FP and v_fourq_k_bf16)."""
+    return [n for n in _all_names() if "variant" in np.load(os.path.join(HERE, n + ".npz"), allow_pickle=False)]
 
 
 def load(name):

@@ -32,12 +32,33 @@ def test_library_exports_every_declared_symbol():
         assert re.search(rf"\bT {name}\b", out), name
 
 
-def test_params_struct_layout_matches_header():
-    # offsets computed by the C compiler for the same struct, via a tiny host-only probe
+def _c_layout(struct: str, fields, tmp_path):
+    """offsetof() of each field and sizeof() of an include/r2o_sspa.h struct, from the host C compiler."""
+    src = tmp_path / "probe.c"
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "r2o_sspa.h"', "int main(void) {"]
+    for f in fields:
+        lines.append(f'  printf("%zu\\n", offsetof({struct}, {f}));')
+    lines += [f'  printf("%zu\\n", sizeof({struct}));', "  return 0;", "}"]
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    return vals[:-1], vals[-1]
+
+
+def test_params_struct_layout_matches_header(tmp_path):
     p = _lib.DecodeParams
-    assert p.recent_len.offset == p.sm_scale.offset + 4
-    assert p.append_global.offset % 8 == 0
-    assert ctypes.sizeof(p) == p.append_logical.offset + 8 * _lib.MAX_BATCH
+    names = [f[0] for f in p._fields_]
+    offsets, size = _c_layout("r2o_decode_params", names, tmp_path)
+    assert [getattr(p, n).offset for n in names] == offsets
+    assert ctypes.sizeof(p) == size
+
+
+def test_descriptor_word_layouts_match_header(tmp_path):
+    # the request descriptor and work item are rows of int64 words written by the host planner
+    for struct, fields in (("r2o_request_desc", _lib.REQUEST_FIELDS), ("r2o_work_item", _lib.ITEM_FIELDS)):
+        offsets, size = _c_layout(struct, fields, tmp_path)
+        assert offsets == [8 * i for i in range(len(fields))] and size == 8 * len(fields), struct
 
 
 def test_host_side_validation_rejects_bad_arguments_without_a_gpu():

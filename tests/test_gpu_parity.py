@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from golden_io import as_f32, fixture_names, load
+from golden_io import as_f32, fixture_names, load, variant_fixture_names
 
 pytestmark = pytest.mark.gpu
 
@@ -101,14 +101,14 @@ def test_build_and_flush_bit_exact_against_reference_fixtures(name):
 
 
 # ------------------------------------------------------------------------ decode parity
-def _oracle_for(data, cfg, append_steps=0):
+def _oracle_for(data, cfg):
     from oracle.cache import append_token, build_cache
     from oracle.quant import bf16_bits_to_f32
 
     f32 = lambda t: bf16_bits_to_f32(_bf16_np(t))  # noqa: E731
     c = build_cache(f32(data.key), f32(data.value), data.page_offsets.numpy(), data.page_lengths.numpy(),
                     data.page_classes.numpy(), dtype="bfloat16", page_size=cfg.page, superblock=cfg.superblock,
-                    group=cfg.group, recent_capacity=128, append_capacity=260)
+                    group=cfg.group, recent_capacity=128, append_capacity=260, variant=cfg.variant)
     hist = int(data.key.shape[1])
     rk, rv = f32(data.recent_k), f32(data.recent_v)
     for i in range(rk.shape[0]):
@@ -250,3 +250,183 @@ def test_ragged_batch_matches_per_request_oracle():
     for r, d in enumerate(datas):
         want = output_transform(mixed_reference(bf16_bits_to_f32(_bf16_np(d.query)), _oracle_for(d, cfg)), True)
         _compare(out[r : r + 1], want, f"request {r}")
+
+
+# ------------------------------------------------------------- BF16-K cache variants
+VARIANT_CASES = [0, 2, 4]  # mixed tiers with a partial ring, GQA 7 over 4 KV heads, FP-only pages
+
+
+@pytest.mark.parametrize("variant", ["matched", "bf16k"])
+@pytest.mark.parametrize("case", VARIANT_CASES)
+@pytest.mark.parametrize("hadamard", [False, True])
+def test_bf16_key_variants_decode_matches_oracle(variant, case, hadamard):
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    hq, hkv, total, probs, recent, sb, grp = SMALL[case]
+    cfg = DecodeConfig("t", hq, hkv, (total,), probs, recent=recent, superblock=sb, group=grp, variant=variant)
+    hist = ((total - recent) // 64) * 64
+    data = make_request(cfg, hist + recent, seed=300 + case, device=dev)
+    cache = build_request_cache(cfg, data)
+    assert cache.bf16_key is not None and cache.compact_key is None
+    ws = ro.allocate_splitk_workspace(cache, num_query_heads=hq)
+    ex = ro.prepare_splitk_executor(cache, ws, output_hadamard=hadamard)
+    out = ex(data.query.contiguous())
+    torch.cuda.synchronize()
+    oc = _oracle_for(data, cfg)
+    # the bf16 key rows are the oracle's, bit for bit, in the same physical order
+    kb = cache.bf16_key
+    assert kb.active_length == oc.k_active
+    got_rows = bf16_bits_to_f32(_bf16_np(kb.rows[:, : kb.active_length]))
+    np.testing.assert_array_equal(got_rows, oc.k_rows[:, : oc.k_active])
+    q = bf16_bits_to_f32(_bf16_np(data.query))
+    want = output_transform(mixed_reference(q, oc), hadamard)
+    _compare(out, want, f"{variant} case {case} hadamard {hadamard}")
+
+
+def test_matched_fp_fused_append_then_flush_matches_oracle():
+    """Matched-FP: the 129th generated token moves the ring's first 128 rows into the FP pool."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.cache import append_token
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    cfg = DecodeConfig("t", 16, 2, (0,), (0.2, 0.5, 0.3), recent=120, variant="matched")
+    data = make_request(cfg, 1280 + 120, seed=9, device=dev)
+    cache = build_request_cache(cfg, data)
+    oc = _oracle_for(data, cfg)
+    ws = ro.allocate_splitk_workspace(cache, num_query_heads=16, reserve_tokens=260)
+    ex = ro.prepare_splitk_executor(cache, ws)
+    gen = torch.Generator(device=dev).manual_seed(10)
+    stats = ro.DynamicCacheStats()
+    hist = int(data.key.shape[1]) + 120
+    fp_before = cache.fp_pool.token_count
+    for step in range(20):
+        q = torch.randn(1, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn(1, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+        pos = hist + step
+        kf, vf = bf16_bits_to_f32(_bf16_np(k[0])), bf16_bits_to_f32(_bf16_np(v[0]))
+        rec = cache.recent_fp_pool
+        if rec.active_length < rec.capacity:
+            out = ex(q, append=(k, v, pos, pos))
+            rec.active_length += 1
+            want = mixed_reference(bf16_bits_to_f32(_bf16_np(q)), oc, append=(kf, vf))
+            append_token(oc, kf, vf, global_index=pos, logical_position=pos)
+        else:
+            assert ro.append_generated_token(cache, k[0][:, None], v[0][:, None], global_token_index=pos,
+                                             logical_position=pos, stats=stats)
+            ex = ro.prepare_splitk_executor(cache, ws)
+            append_token(oc, kf, vf, global_index=pos, logical_position=pos)
+            out = ex(q)
+            want = mixed_reference(bf16_bits_to_f32(_bf16_np(q)), oc)
+        torch.cuda.synchronize()
+        _compare(out, output_transform(want, False), f"matched step {step}")
+    assert stats.flushed_tokens == 128
+    assert cache.fp_pool.token_count == fp_before + 128 == oc.pool_tokens[0]
+    assert cache.recent_fp_pool.active_length == oc.recent_active
+    kb = cache.bf16_key
+    assert kb.active_length == oc.k_active
+    np.testing.assert_array_equal(bf16_bits_to_f32(_bf16_np(kb.rows[:, : kb.active_length])),
+                                  oc.k_rows[:, : oc.k_active])
+    np.testing.assert_array_equal(bf16_bits_to_f32(_bf16_np(cache.fp_pool.fp_v)), oc.fp_v)
+
+
+def test_bf16k_ring_overflow_is_refused():
+    """v_fourq_k_bf16 has no low-bit flush: a full ring refuses the next token (dynamic_fourq_cache.py:226-230)."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+
+    dev = _cuda()
+    cfg = DecodeConfig("t", 16, 2, (0,), (0.2, 0.5, 0.3), recent=128, variant="bf16k")
+    data = make_request(cfg, 1024 + 128, seed=11, device=dev)
+    cache = build_request_cache(cfg, data)
+    assert cache.recent_fp_pool.active_length == cache.recent_fp_pool.capacity
+    k = torch.zeros(2, 1, 128, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="K-BF16/V-FourQ"):
+        ro.append_generated_token(cache, k, k, global_token_index=5000, logical_position=5000,
+                                  stats=ro.DynamicCacheStats())
+
+
+@pytest.mark.parametrize("name", variant_fixture_names())
+def test_bf16_key_variant_build_and_appends_bit_exact_against_reference_fixtures(name):
+    """BF16-K builds and appends against the reference's own cache state, then decode against the oracle."""
+    import r2omni_amd as ro
+    from oracle.attention import mixed_reference
+    from oracle.cache import append_token, build_cache
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    g = load(name)
+    dt = str(g["dtype"])
+    variant = str(g["variant"])
+    key = _to_torch(g["key"], dt, dev)
+    value = _to_torch(g["value"], dt, dev)
+    plan = ro.plan_from_pages(g["page_offsets"], g["page_lengths"], g["page_classes"], recent_fp_capacity=128,
+                              device=dev)
+    kwargs = dict(page_size=int(g["page_size"]), key_quantization_superblock=int(g["superblock"]),
+                  int2_group_size=int(g["group"]), compact_key_append_capacity=260, recent_flush_size=128)
+    if variant == "matched":
+        cache = ro.build_three_precision_cache(key, value, plan, matched_fp=True, **kwargs)
+    else:
+        cache = ro.build_three_precision_cache(key, value, plan, cache_variant="v_fourq_k_bf16", **kwargs)
+    oc = build_cache(as_f32(g["key"], dt), as_f32(g["value"], dt), g["page_offsets"], g["page_lengths"],
+                     g["page_classes"], dtype=dt.replace("torch.", ""), page_size=int(g["page_size"]), superblock=int(g["superblock"]),
+                     group=int(g["group"]), recent_capacity=128, append_capacity=260, variant=variant)
+    q = torch.from_numpy(g["query"]).to(dev).to(torch.bfloat16)
+    qf = bf16_bits_to_f32(_bf16_np(q))
+
+    def check(prefix):
+        torch.cuda.synchronize()
+        kb = cache.bf16_key
+        rows = kb.rows[:, : kb.active_length].cpu().view(torch.int16).numpy().view(np.uint16)
+        np.testing.assert_array_equal(rows, g[prefix + "k_rows"])
+        pools = [cache.fp_pool.token_count, cache.int4_pool.token_count, cache.int2_pool.token_count,
+                 cache.recent_fp_pool.active_length]
+        assert pools == [int(v) for v in g[prefix + "pool_tokens"]]
+        fp_v = cache.fp_pool.fp_v[:, : cache.fp_pool.token_count] if cache.fp_pool.token_count else None
+        if fp_v is not None:
+            np.testing.assert_array_equal(_bf16_np(fp_v), g[prefix + "fp_v"])
+        if variant == "bf16k":
+            i4 = cache.int4_pool
+            if i4.token_count:
+                np.testing.assert_array_equal(i4.packed_v.packed.cpu().numpy().reshape(-1),
+                                              g[prefix + "v4_packed"].reshape(-1))
+                np.testing.assert_array_equal(i4.packed_v.scale.cpu().numpy().view(np.uint32).reshape(-1),
+                                              g[prefix + "v4_scale"].view(np.uint32).reshape(-1))
+            cv = cache.compact_value
+            a = cv.active_length
+            np.testing.assert_array_equal(cv.packed[:, :a].cpu().numpy(), g[prefix + "v2_packed"])
+            np.testing.assert_array_equal(cv.scale[:, :a].cpu().view(torch.int16).numpy().view(np.uint16),
+                                          g[prefix + "v2_scale"].view(np.uint16))
+            np.testing.assert_array_equal(cv.zero_point[:, :a].cpu().numpy(), g[prefix + "v2_zero"])
+        r = cache.recent_fp_pool.active_length
+        np.testing.assert_array_equal(_bf16_np(cache.recent_fp_pool.fp_k[:, :r]), g[prefix + "recent_k"])
+        ws = ro.allocate_splitk_workspace(cache, num_query_heads=int(q.shape[1]))
+        out = ro.prepare_splitk_executor(cache, ws)(q)
+        torch.cuda.synchronize()
+        _compare(out, mixed_reference(qf, oc), f"{name} {prefix}decode")
+
+    check("build_")
+    stats = ro.DynamicCacheStats()
+    ak = _to_torch(g["append_k"], dt, dev)
+    av = _to_torch(g["append_v"], dt, dev)
+    seq = int(g["key"].shape[1])
+    flushed, refused = [], -1
+    for step in range(int(ak.shape[0])):
+        try:
+            if ro.append_generated_token(cache, ak[step], av[step], global_token_index=seq + step,
+                                         logical_position=seq + step, stats=stats):
+                flushed.append(step)
+        except RuntimeError:
+            refused = step
+            break
+        append_token(oc, as_f32(g["append_k"][step, :, 0], dt), as_f32(g["append_v"][step, :, 0], dt),
+                     global_index=seq + step, logical_position=seq + step)
+    assert flushed == list(g["flushed_at"]) and refused == int(g["refused_at"])
+    check("after_")

@@ -75,3 +75,58 @@ def test_append_and_flush_match_reference(name):
     _check_snapshot(c, g, "after_", dt)
     out = mixed_reference(g["query"], c)
     np.testing.assert_allclose(out, g["after_attn"], rtol=0, atol=2e-6)
+
+
+# ------------------------------------------------------------------ BF16-K cache variants
+from golden_io import variant_fixture_names  # noqa: E402
+
+VARIANTS = variant_fixture_names()
+
+
+def _build_variant(g):
+    dt = _dtype(g)
+    return build_cache(
+        as_f32(g["key"], dt), as_f32(g["value"], dt),
+        g["page_offsets"], g["page_lengths"], g["page_classes"],
+        dtype=dt, page_size=int(g["page_size"]), superblock=int(g["superblock"]),
+        group=int(g["group"]), recent_capacity=128, append_capacity=260, variant=str(g["variant"]),
+    )
+
+
+def _check_variant(c, g, prefix, dt):
+    s = c.k_active
+    np.testing.assert_array_equal(c.k_rows[:, :s], as_f32(g[prefix + "k_rows"], dt))
+    assert list(c.pool_tokens) + [c.recent_active] == [int(v) for v in g[prefix + "pool_tokens"]]
+    np.testing.assert_array_equal(c.fp_v, as_f32(g[prefix + "fp_v"], dt))
+    if str(g["variant"]) == "bf16k":
+        np.testing.assert_array_equal(c.v4_packed.reshape(-1), g[prefix + "v4_packed"].reshape(-1))
+        np.testing.assert_array_equal(c.v4_scale.view(np.uint32), g[prefix + "v4_scale"].view(np.uint32))
+        a = c.v2_active
+        np.testing.assert_array_equal(c.v2_packed[:, :a], g[prefix + "v2_packed"])
+        np.testing.assert_array_equal(c.v2_scale[:, :a].view(np.uint16), g[prefix + "v2_scale"].view(np.uint16))
+        np.testing.assert_array_equal(c.v2_zero[:, :a], g[prefix + "v2_zero"])
+    r = c.recent_active
+    np.testing.assert_array_equal(c.recent_k[:, :r], as_f32(g[prefix + "recent_k"], dt))
+    np.testing.assert_array_equal(c.recent_v[:, :r], as_f32(g[prefix + "recent_v"], dt))
+
+
+@pytest.mark.parametrize("name", VARIANTS)
+def test_bf16k_variants_build_append_and_attention_match_reference(name):
+    g = load(name)
+    dt = _dtype(g)
+    c = _build_variant(g)
+    _check_variant(c, g, "build_", dt)
+    np.testing.assert_allclose(mixed_reference(g["query"], c), g["build_attn"], rtol=0, atol=2e-6)
+    ak, av = as_f32(g["append_k"], dt), as_f32(g["append_v"], dt)
+    seq = g["key"].shape[1]
+    flushed, refused = [], -1
+    for step in range(ak.shape[0]):
+        try:
+            if append_token(c, ak[step, :, 0], av[step, :, 0], global_index=seq + step, logical_position=seq + step):
+                flushed.append(step)
+        except RuntimeError:
+            refused = step
+            break
+    assert flushed == list(g["flushed_at"]) and refused == int(g["refused_at"])
+    _check_variant(c, g, "after_", dt)
+    np.testing.assert_allclose(mixed_reference(g["query"], c), g["after_attn"], rtol=0, atol=2e-6)
