@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import dataclasses
 import json
 import os
 import sys
@@ -59,24 +60,36 @@ def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
     oc_list = []
     for c in caches:
         ck, cv, rec = c.compact_key, c.compact_value, c.recent_fp_pool
-        fp = c.fp_pool.fp_v.float().cpu().numpy() if c.fp_pool.token_count else np.zeros((ck.head_count, 0, 128), np.float32)
+        h = int(rec.fp_k.shape[0])
+        fp = c.fp_pool.fp_v.float().cpu().numpy() if c.fp_pool.token_count else np.zeros((h, 0, 128), np.float32)
         i4 = c.int4_pool
-        h = ck.head_count
+        if ck is not None:
+            kw = dict(variant="int4k", k_packed=ck.packed.cpu().numpy(), k_scale=ck.scale.cpu().numpy(),
+                      k_zero=ck.zero_point.cpu().numpy(), k_active=ck.active_length, k_capacity=ck.capacity,
+                      k_segments=ck.segment_offsets, superblock=ck.superblock_size)
+        else:  # bf16 key rows
+            kb = c.bf16_key
+            kw = dict(variant="matched" if c.matched_fp else "bf16k", k_rows=kb.rows.float().cpu().numpy(),
+                      k_packed=np.zeros((h, 0, 64), np.uint8), k_scale=np.zeros((h, 0, 128), np.float16),
+                      k_zero=np.zeros((h, 0, 128), np.uint8), k_active=kb.active_length, k_capacity=kb.capacity,
+                      k_segments=kb.segment_offsets, superblock=32)
+        if cv is not None:
+            v2 = dict(v2_packed=cv.packed.cpu().numpy(), v2_scale=cv.scale.cpu().numpy(),
+                      v2_zero=cv.zero_point.cpu().numpy(), v2_active=cv.active_length, v2_capacity=cv.capacity,
+                      group=cv.group_size)
+        else:
+            v2 = dict(v2_packed=np.zeros((h, 0, 32), np.uint8), v2_scale=np.zeros((h, 0, 4, 1), np.float16),
+                      v2_zero=np.zeros((h, 0, 4, 1), np.uint8), v2_active=0, v2_capacity=0, group=32)
         oc = OracleCache(
-            dtype="bfloat16", hkv=h, page_size=c.page_size, superblock=ck.superblock_size, group=cv.group_size,
-            flush_size=128, k_packed=ck.packed.cpu().numpy(), k_scale=ck.scale.cpu().numpy(),
-            k_zero=ck.zero_point.cpu().numpy(), k_active=ck.active_length, k_capacity=ck.capacity,
-            k_segments=ck.segment_offsets, fp_v=fp,
+            dtype="bfloat16", hkv=h, page_size=c.page_size, flush_size=128, fp_v=fp,
             v4_packed=i4.packed_v.packed.cpu().numpy().reshape(h, i4.token_count, 64) if i4.token_count
             else np.zeros((h, 0, 64), np.uint8),
             v4_scale=i4.packed_v.scale.cpu().numpy() if i4.token_count else np.zeros((h, 0, 1), np.float32),
-            v2_packed=cv.packed.cpu().numpy(), v2_scale=cv.scale.cpu().numpy(), v2_zero=cv.zero_point.cpu().numpy(),
-            v2_active=cv.active_length, v2_capacity=cv.capacity,
             recent_k=rec.fp_k.float().cpu().numpy(), recent_v=rec.fp_v.float().cpu().numpy(),
             recent_active=rec.active_length, recent_global=rec.global_index_buffer.cpu().numpy(),
             recent_logical=rec.logical_position_buffer.cpu().numpy(),
             recent_page_lengths=rec.page_index.lengths.cpu().numpy(),
-            pool_tokens=[c.fp_pool.token_count, i4.token_count, cv.active_length],
+            pool_tokens=[c.fp_pool.token_count, i4.token_count, v2["v2_active"]], **kw, **v2,
         )
         oc_list.append(oc)
     qs = [q.float().cpu().numpy() for q in queries]
@@ -186,6 +199,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--variant", choices=("int4k", "bf16k", "matched"), default="int4k",
+                    help="K format of the layer caches: compact INT4-K (default), v_fourq_k_bf16 or matched-FP")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (HBM counter calibration)")
@@ -222,6 +237,8 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
         return 0
     cfg = CONFIGS[args.config]
+    if args.variant != "int4k":
+        cfg = dataclasses.replace(cfg, variant=args.variant)
     if args.prefill:
         print(json.dumps(prefill_bench(cfg, args.config, dev)), flush=True)
         return 0
@@ -269,7 +286,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         cpu = cpu_baseline(layers[0][0], [layers[0][1][r : r + 1] for r in range(len(cfg.lengths))], cfg.hq)
-    traffic, traffic_src = traffic_from_profile() if args.config == 2 else (None, None)
+    traffic, traffic_src = traffic_from_profile() if args.config == 2 and args.variant == "int4k" else (None, None)
     line = {
         "metric": "packed-KV decode attn: HBM GB/s (% peak), us/layer @32k ctx; decode tok/s",
         "value": round(gbs, 2),
@@ -285,7 +302,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int4-k/bf16|int4|int2-v, f16/bf16 mfma, f32 accumulate",
         "data": "synthetic (seeded N(0,1) bf16, 4 key outlier channels x8, seeded per-page V tiers)",
-        "config": {"workload": f"cfg{args.config} {cfg.name}", "hq": cfg.hq, "hkv": cfg.hkv,
+        "config": {"workload": f"cfg{args.config} {cfg.name}" + ("" if args.variant == "int4k" else f" {args.variant}"),
+                   "k_format": args.variant, "hq": cfg.hq, "hkv": cfg.hkv,
                    "context_lengths": list(cfg.lengths), "v_tiers_bf16_int4_int2": list(cfg.tier_probs),
                    "recent_window": cfg.recent, "k_superblock": cfg.superblock, "int2_group": cfg.group,
                    "rotated_layer_caches": L, "algorithmic_bytes_per_call": nbytes, "output_hadamard": True},

@@ -105,19 +105,22 @@ def algorithmic_bytes(caches, hq: int, *, fused_append: bool = False) -> int:
     """Compulsory HBM bytes of one decode call over ``caches`` (one per request).
 
     Per request and KV head: INT4-K codes (64 B/token) + K superblock scale/zero
-    (3 B x 128 channels per superblock), BF16-V 256 B, INT4-V 64 + 4 B, INT2-V 32 + 3*128/G B,
+    (3 B x 128 channels per superblock) or BF16-K rows (256 B/token), BF16-V 256 B, INT4-V 64 + 4 B, INT2-V 32 + 3*128/G B,
     Recent K+V 512 B per active token; plus Q and O (bf16) and, with a fused append, the new
     K/V rows read and written.
     """
     total = 0
     for c in caches:
         hkv = int(c.recent_fp_pool.fp_k.shape[0])
-        ck = c.compact_key
-        hist = ck.active_length
-        sbs = -(-hist // ck.superblock_size)
-        g = c.compact_value.group_size
-        per_head = (hist * 64 + sbs * 3 * 128 + c.fp_pool.token_count * 256 + c.int4_pool.token_count * 68
-                    + c.compact_value.active_length * (32 + 3 * (128 // g)) + c.recent_fp_pool.active_length * 512)
+        ck, cv = c.compact_key, c.compact_value
+        if ck is not None:
+            hist = ck.active_length
+            k_bytes = hist * 64 + -(-hist // ck.superblock_size) * 3 * 128
+        else:  # bf16 key rows (matched-FP and v_fourq_k_bf16 caches)
+            k_bytes = c.bf16_key.active_length * 256
+        v2_bytes = 0 if cv is None else cv.active_length * (32 + 3 * (128 // cv.group_size))
+        per_head = (k_bytes + c.fp_pool.token_count * 256 + c.int4_pool.token_count * 68 + v2_bytes
+                    + c.recent_fp_pool.active_length * 512)
         total += hkv * per_head + 2 * hq * 128 * 2
         if fused_append:
             total += 2 * hkv * 128 * 2 * 2
