@@ -64,7 +64,7 @@ def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
         fp = c.fp_pool.fp_v.float().cpu().numpy() if c.fp_pool.token_count else np.zeros((h, 0, 128), np.float32)
         i4 = c.int4_pool
         if ck is not None:
-            kw = dict(variant="int4k", k_packed=ck.packed.cpu().numpy(), k_scale=ck.scale.cpu().numpy(),
+            kw = dict(variant="int2k" if ck.bit_width == 2 else "int4k", k_packed=ck.packed.cpu().numpy(), k_scale=ck.scale.cpu().numpy(),
                       k_zero=ck.zero_point.cpu().numpy(), k_active=ck.active_length, k_capacity=ck.capacity,
                       k_segments=ck.segment_offsets, superblock=ck.superblock_size)
         else:  # bf16 key rows
@@ -199,8 +199,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--variant", choices=("int4k", "bf16k", "matched"), default="int4k",
-                    help="K format of the layer caches: compact INT4-K (default), v_fourq_k_bf16 or matched-FP")
+    ap.add_argument("--variant", choices=("int4k", "int2k", "bf16k", "matched"), default="int4k",
+                    help="K format of the layer caches: compact INT4-K (default), compact INT2-K, "
+                         "v_fourq_k_bf16 or matched-FP")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (HBM counter calibration)")

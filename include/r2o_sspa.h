@@ -33,16 +33,22 @@ extern "C" {
 #define R2O_MAX_GQA 16
 #define R2O_MAX_BATCH 32
 
+/* r2o_decode_params.k_format */
+#define R2O_K_INT4 0
+#define R2O_K_BF16 1
+#define R2O_K_INT2 2
+
 /* ---------------------------------------------------------------- decode (hot path) ---- */
 
 /* One request's static cache geometry; an array of these lives in device memory and is
  * rebuilt only when the cache layout changes (prefill, flush), like the reference's
  * prepare_splitk_executor (triton_fourq_splitk.py:1695-1907).  All fields are 8 bytes. */
 typedef struct r2o_request_desc {
-    const uint8_t* k_packed;      /* compact INT4-K arena  u8  [Hkv, k_capacity, 64], or with    */
-                                  /* k_bf16 set, bf16 key rows [Hkv, k_capacity, 128]           */
+    const uint8_t* k_packed;      /* R2O_K_INT4: compact INT4-K arena u8 [Hkv, k_capacity, 64];  */
+                                  /* R2O_K_INT2: compact INT2-K arena u8 [Hkv, k_capacity, 32];  */
+                                  /* R2O_K_BF16: bf16 key rows [Hkv, k_capacity, 128]            */
     const uint16_t* k_scale;      /* fp16 [Hkv, k_superblocks, 128]                              */
-    const uint8_t* k_zero;        /* u8   [Hkv, k_superblocks, 128]                              */
+    const uint8_t* k_zero;        /* u8 zero points (INT4) or fp16 offsets (INT2) [Hkv, k_sb, 128] */
     int64_t k_capacity;
     int64_t k_superblocks;
     const uint32_t* k_operands;   /* u32  [Hkv, k_superblocks, 128]  QK MFMA operands (see pack) */
@@ -102,8 +108,8 @@ typedef struct r2o_decode_params {
     int64_t q_dtype;                /* 0 = bf16, 1 = fp16                              */
     int64_t output_hadamard;        /* 1: out = bf16(FWHT128(bf16(out)))               */
     int64_t do_append;              /* 1: fused Recent-FP append of append_k/append_v  */
-    int64_t k_bf16;                 /* 1: k_packed holds bf16 key rows [Hkv, k_capacity, 128] (matched-FP /
-                                       v_fourq_k_bf16 caches; k_scale, k_zero, k_operands unused)      */
+    int64_t k_format;               /* R2O_K_INT4 / R2O_K_BF16 / R2O_K_INT2: the history key layout  */
+                                    /* of every request (see r2o_request_desc.k_packed)               */
     float sm_scale;                 /* softmax scale (head_dim^-1/2 by default)        */
     int32_t recent_len[R2O_MAX_BATCH];     /* host-tracked Recent-FP active length     */
     int64_t append_global[R2O_MAX_BATCH];  /* global token index of the appended token */
@@ -135,6 +141,20 @@ int r2o_decode_combine(const r2o_decode_params* params, void* stream);
 int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
                     const int64_t* index, int64_t n, int64_t tail, int64_t dst_start,
                     uint8_t* packed, uint16_t* scale, uint8_t* zero, uint32_t* operands,
+                    int64_t capacity, int64_t superblocks, int64_t superblock, void* stream);
+
+/* Per-channel affine INT2-K (OScaR form) over superblocks of 32/64/128 tokens, same gather /
+ * tail / superblock-aligned-destination contract as r2o_pack_int4_k.  packed u8 [Hkv, capacity, 32]
+ * (byte j = channels 4j..4j+3, low bits first), scale and offset fp16 [Hkv, superblocks, 128]
+ * (dequant = code * scale + offset).  With operands != NULL also writes the QK MFMA operands
+ * u32 [Hkv, superblocks, 128]: per lane group g and MFMA j, pair u covers channels (c, c + 8),
+ * c = 32g + 16(j/2) + 4(j%2) + u, whose codes enter the MFMA as 1024 + 4^u code; words
+ * [32g + 4j + u] hold (scale / 4^u) pairs and [32g + 16 + 4j + u] offset pairs.
+ * Replaces quantize_int2_key_per_channel (int2_reference.py:159-214) in
+ * build_compact_int2_key_arena (compact_int2_key.py:125-153) and append_superblock (:110-122). */
+int r2o_pack_int2_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
+                    const int64_t* index, int64_t n, int64_t tail, int64_t dst_start,
+                    uint8_t* packed, uint16_t* scale, uint16_t* offset, uint32_t* operands,
                     int64_t capacity, int64_t superblocks, int64_t superblock, void* stream);
 
 /* Per-token symmetric INT4-V: packed[h, dst+i] / scale[h, dst+i] from src[h, index[i]].

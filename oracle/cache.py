@@ -1,9 +1,10 @@
 """numpy restatement of the three-pool SSPA cache and its append/flush (test infrastructure only).
 
 Follows, for the released ``v_fourq_k_int4_compact`` cache with INT2 generated values (and the
-BF16-K variants: ``v_fourq_k_bf16`` keeps the pools' K rows in the input dtype, and the matched-FP
-cache keeps every surviving page, K and V, in one FP pool in page order, precision_pool.py:834-876,
-with flushes appended to it, dynamic_fourq_cache.py:145-170, 200-204):
+other K formats: ``v_fourq_k_int2_compact`` keeps K in a per-channel affine INT2 arena,
+compact_int2_key.py:14-153; ``v_fourq_k_bf16`` keeps the pools' K rows in the input dtype; the
+matched-FP cache keeps every surviving page, K and V, in one FP pool in page order,
+precision_pool.py:834-876, with flushes appended to it, dynamic_fourq_cache.py:145-170, 200-204):
   * ``_compact_page_layouts``      precision_pool.py:611-669  (stable FP -> INT4 -> INT2 -> evicted)
   * ``build_three_precision_cache`` precision_pool.py:787-984 (+ arenas in compact_int4_key.py:223-281,
                                    fused_value_pack.py:152-193, 519-575, recent ring :747-784)
@@ -23,7 +24,9 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from .quant import (
+    dequantize_int2_key,
     dequantize_int4_key,
+    quantize_int2_key_per_channel,
     quantize_int2_value,
     quantize_int4_key_per_channel,
     quantize_int4_value,
@@ -66,7 +69,8 @@ class OracleCache:
     superblock: int
     group: int
     flush_size: int
-    # compact INT4 K arena
+    # compact K arena: INT4 (packed [H,cap,D/2], fp16 scale, u8 zero point) or, for the
+    # "int2k" variant, INT2 (packed [H,cap,D/4], fp16 scale, fp16 offset held in k_zero)
     k_packed: np.ndarray
     k_scale: np.ndarray
     k_zero: np.ndarray
@@ -117,7 +121,7 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
                 recent_capacity: int = 128, append_capacity: int = 260,
                 flush_size: int = 128, variant: str = "int4k") -> OracleCache:
     """Restatement of ``build_three_precision_cache``: ``variant`` "int4k" (``v_fourq_k_int4_compact``),
-    "bf16k" (``v_fourq_k_bf16``) or "matched" (``matched_fp=True``).
+    "int2k" (``v_fourq_k_int2_compact``), "bf16k" (``v_fourq_k_bf16``) or "matched" (``matched_fp=True``).
 
     ``key``/``value`` are float32 arrays holding values of ``dtype`` ([Hkv, S, 128]).
     """
@@ -129,7 +133,7 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
         fp_t = survivor_layout(page_offsets, page_lengths, page_classes)
         i4_t = i2_t = np.zeros(0, np.int64)
         ev_t = np.zeros(s - len(fp_t), np.int64)
-    elif variant not in ("int4k", "bf16k"):
+    elif variant not in ("int4k", "int2k", "bf16k"):
         raise ValueError(f"unknown variant {variant}")
     if len(fp_t) + len(i4_t) + len(i2_t) + len(ev_t) != s:
         raise ValueError("compact physical pools must cover every logical token")
@@ -138,11 +142,17 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
     active = len(ordered)
     k_cap = max(128, _round_up(active + append_capacity, 128))
     blocks = k_cap // superblock
-    k_packed = np.zeros((h, k_cap, d // 2), np.uint8)
+    k_packed = np.zeros((h, k_cap, d // (4 if variant == "int2k" else 2)), np.uint8)
     k_scale = np.zeros((h, blocks, d), np.float16)
-    k_zero = np.zeros((h, blocks, d), np.uint8)
+    k_zero = np.zeros((h, blocks, d), np.float16 if variant == "int2k" else np.uint8)
     k_rows = None
-    if variant == "int4k":
+    if variant == "int2k":  # build_compact_int2_key_arena (compact_int2_key.py:125-153): one quantise
+        if active:
+            p, sc, off = quantize_int2_key_per_channel(key[:, ordered], superblock)
+            k_packed[:, :active] = p
+            k_scale[:, : sc.shape[1]] = sc
+            k_zero[:, : off.shape[1]] = off
+    elif variant == "int4k":
         for start in range(0, active, superblock):
             toks = ordered[start : start + superblock]
             p, sc, z = quantize_int4_key_per_channel(key[:, toks], superblock)
@@ -186,8 +196,29 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
     )
 
 
+def _flush_key_superblock_int2(c: OracleCache, key_block: np.ndarray) -> int:
+    """``CompactInt2KeyArena.append_superblock`` (compact_int2_key.py:110-122)."""
+    n = key_block.shape[1]
+    if c.k_active + 128 > c.k_capacity:
+        raise RuntimeError("compact INT2 K capacity exhausted")
+    prefix = c.k_active // c.superblock * c.superblock
+    tail_count = c.k_active - prefix
+    tail = round_to_dtype(dequantize_int2_key(c.k_packed, c.k_scale, c.k_zero, prefix, tail_count, c.superblock),
+                          c.dtype)
+    merged = np.concatenate((tail, key_block), axis=1)
+    p, sc, off = quantize_int2_key_per_channel(merged, c.superblock)
+    c.k_packed[:, prefix : prefix + merged.shape[1]] = p
+    b0 = prefix // c.superblock
+    c.k_scale[:, b0 : b0 + sc.shape[1]] = sc
+    c.k_zero[:, b0 : b0 + off.shape[1]] = off
+    c.k_active += n
+    return tail_count
+
+
 def _flush_key_superblock(c: OracleCache, key_block: np.ndarray) -> int:
     """``CompactInt4KeyArena.append_superblock`` (compact_int4_key.py:210-220)."""
+    if c.variant == "int2k":
+        return _flush_key_superblock_int2(c, key_block)
     n = key_block.shape[1]
     if c.k_active + 128 > c.k_capacity:
         raise RuntimeError("compact INT4 K capacity exhausted")
@@ -279,6 +310,8 @@ def pool_kv(c: OracleCache):
     def keys(start, n):
         if c.k_rows is not None:
             return c.k_rows[:, start : start + n]
+        if c.variant == "int2k":
+            return dequantize_int2_key(c.k_packed, c.k_scale, c.k_zero, start, n, c.superblock)
         return dequantize_int4_key(c.k_packed, c.k_scale, c.k_zero, start, n, c.superblock)
 
     if s_fp:

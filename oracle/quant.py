@@ -92,6 +92,62 @@ def dequantize_int4_key(packed, scale, zero, start: int, length: int, superblock
 
 
 # ---------------------------------------------------------------------------- INT4 values
+def quantize_int2_key_per_channel(key: np.ndarray, superblock_size: int):
+    """Per-channel affine INT2 over ``superblock_size``-token blocks (OScaR form).
+
+    Follows int2_reference.py:159-214 with clip_ratio 1: mn, mx = block min / max (no
+    inclusion of 0); range = mx - mn; for range > 0: scale = range / 3, inv = (1 / range) * 3
+    (how torch evaluates ``3.0 / range``),
+    zero = rne(-mn * inv), offset = -zero * scale; for a constant channel scale = inv = zero = 0
+    and offset = mn.  code = clamp(rne(x * inv + zero), 0, 3) (the product rounded to fp32
+    before the add); scale and offset stored as fp16; byte j = c[4j] | c[4j+1] << 2 |
+    c[4j+2] << 4 | c[4j+3] << 6.  Returns (packed [H,S,D/4] u8, scale, offset [H,blocks,D] f16).
+    """
+    if key.ndim != 3 or key.shape[2] % 4:
+        raise ValueError("INT2 K must be [H,S,D] with D divisible by four")
+    if superblock_size not in (32, 64, 128):
+        raise ValueError("per-channel INT2 K block size must be 32, 64, or 128")
+    h, length, d = key.shape
+    blocks = max(1, -(-length // superblock_size))
+    scale = np.zeros((h, blocks, d), dtype=np.float16)
+    offset = np.zeros((h, blocks, d), dtype=np.float16)
+    codes = np.zeros((h, length, d), dtype=np.uint8)
+    x = np.asarray(key, dtype=F32)
+    for block, start in enumerate(range(0, length, superblock_size)):
+        src = x[:, start : start + superblock_size]
+        mn = src.min(axis=1)
+        mx = src.max(axis=1)
+        rng = (mx - mn).astype(F32)
+        nonconst = rng > 0
+        with np.errstate(divide="ignore", invalid="ignore"):
+            sc = np.where(nonconst, rng / F32(3.0), F32(0)).astype(F32)
+            # torch evaluates ``3.0 / t`` as ``t.reciprocal() * 3.0`` (Tensor.__rtruediv__): two roundings
+            recip = (F32(1.0) / np.maximum(rng, F32(1e-30))).astype(F32)
+            inv = np.where(nonconst, (recip * F32(3.0)).astype(F32), F32(0)).astype(F32)
+        zp = np.where(nonconst, np.rint(-mn * inv), F32(0)).astype(F32)
+        off = np.where(nonconst, -zp * sc, mn).astype(F32)
+        prod = (src * inv[:, None, :]).astype(F32)
+        q = np.clip(np.rint((prod + zp[:, None, :]).astype(F32)), 0, 3)
+        codes[:, start : start + src.shape[1]] = q.astype(np.uint8)
+        scale[:, block] = sc.astype(np.float16)
+        offset[:, block] = off.astype(np.float16)
+    packed = (codes[..., 0::4] | (codes[..., 1::4] << 2) | (codes[..., 2::4] << 4)
+              | (codes[..., 3::4] << 6)).astype(np.uint8)
+    return packed, scale, offset
+
+
+def dequantize_int2_key(packed, scale, offset, start: int, length: int, superblock_size: int):
+    """``CompactInt2KeyArena.dequantize_range`` (compact_int2_key.py:69-96): code * f32(s) + f32(o)."""
+    h = packed.shape[0]
+    d = packed.shape[2] * 4
+    if length == 0:
+        return np.zeros((h, 0, d), dtype=F32)
+    payload = packed[:, start : start + length]
+    codes = np.stack([(payload >> (2 * i)) & 3 for i in range(4)], axis=-1).reshape(h, length, d)
+    blocks = np.arange(start, start + length) // superblock_size
+    return (codes.astype(F32) * scale[:, blocks].astype(F32)).astype(F32) + offset[:, blocks].astype(F32)
+
+
 def quantize_int4_value(value: np.ndarray):
     """Per-token symmetric INT4 (quantization.py:19-50 with dim=2, packing :77-102).
 

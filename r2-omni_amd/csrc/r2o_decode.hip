@@ -40,15 +40,18 @@ constexpr int kDmaStages = R2O_DMA_STAGES;
 static_assert(kDmaStages >= 1 && kDmaStages <= 3, "1 to 3 LDS stages per wave");
 constexpr int kMergeFloats = 16 + 16 + 16 * 128;    // per wave: m, l, acc
 
-// Per-kernel LDS / occupancy configuration.  BK = the cache keeps K as bf16 rows (matched-FP and
-// v_fourq_k_bf16 caches); otherwise K is the compact INT4 arena.
-template <bool BK>
+// History-key formats (r2o_decode_params.k_format): the compact INT4 arena, bf16 rows
+// (matched-FP and v_fourq_k_bf16 caches) or the compact INT2 arena (v_fourq_k_int2_compact).
+enum KFormat { kKInt4 = 0, kKBf16 = 1, kKInt2 = 2 };
+
+// Per-kernel LDS / occupancy configuration.
+template <int KF>
 struct KernelCfg {
-    static constexpr int kStage = BK ? 16384 : 10752;  // one tile stage (sized for BF16 V, see StageLayout)
+    static constexpr int kStage = KF == kKBf16 ? 16384 : 10752;  // one tile stage (sized for BF16 V, see StageLayout)
     static constexpr int kWaveLds = kDmaStages * kStage;
     static constexpr int kSmem = (kWaves * kMergeFloats * 4 > kWaves * kWaveLds) ? kWaves * kMergeFloats * 4
                                                                                  : kWaves * kWaveLds;
-    static constexpr int kBlocksPerCU = BK ? 2 : 3;     // resident partial workgroups per CU
+    static constexpr int kBlocksPerCU = KF == kKBf16 ? 2 : 3;     // resident partial workgroups per CU
 };
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
@@ -62,10 +65,11 @@ struct WaveState {
     r2o_f4 acc[8];  // O[4g+i][8*l16 + q] for q = 0..7
 };
 
-// Query operand of head l16 of the KV group (padded heads are zero), channels 32g .. 32g+31:
-// f16 pairs (channel 8j+u, 8j+u+4) scaled by D^-1/2 log2(e) for the INT4-K MFMA, or bf16
-// pairs in channel order for the Recent-FP bf16 MFMA.
-template <bool BF16_ORDER>
+// Query operand of head l16 of the KV group (padded heads are zero), channels 32g .. 32g+31, in
+// the K operand order of the format: f16 pairs (8j+u, 8j+u+4) for INT4-K, f16 pairs
+// (16(j/2) + 4(j%2) + u, +8) for INT2-K, both scaled by D^-1/2 log2(e), or bf16 pairs in channel
+// order for bf16 keys (BF16-K pools and the Recent-FP ring).
+template <int KF>
 __device__ __forceinline__ void load_query(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa, int l16,
                                            int g, float qscale, uint32_t (&qp)[4][4]) {
     const bool head_ok = l16 < gqa;
@@ -85,8 +89,10 @@ __device__ __forceinline__ void load_query(const r2o_decode_params& p, int64_t b
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            qp[j][u] = BF16_ORDER ? r2o_pack_bf2(qf[8 * j + 2 * u], qf[8 * j + 2 * u + 1])
-                                  : r2o_pack_h2(qf[8 * j + u] * qscale, qf[8 * j + u + 4] * qscale);
+            qp[j][u] = KF == kKBf16 ? r2o_pack_bf2(qf[8 * j + 2 * u], qf[8 * j + 2 * u + 1])
+                     : KF == kKInt4 ? r2o_pack_h2(qf[8 * j + u] * qscale, qf[8 * j + u + 4] * qscale)
+                                    : r2o_pack_h2(qf[16 * (j >> 1) + 4 * (j & 1) + u] * qscale,
+                                                  qf[16 * (j >> 1) + 4 * (j & 1) + u + 8] * qscale);
 }
 
 // Max / sum over the 4 lanes l16 + 16g (g = 0..3) that hold one head, with VALU lane swaps.
@@ -180,16 +186,21 @@ __device__ __forceinline__ VConst make_vconst() {
 // 32g ..), the tile's K superblock operands of lane group g, and for each of the lane's 8 tokens
 // tile_token(g, k) the 8 V dims 8*l16 .. 8*l16+7 (bf16: 16 B, INT4: 4 B, INT2: 2 B) plus the
 // token's V metadata.
-template <bool BK>
+template <int KF>
 struct KRegs;
 template <>
-struct KRegs<false> {  // INT4-K: codes of tokens 16 mg + l16 (channels 32g ..) and the operand vectors
+struct KRegs<kKInt4> {  // INT4-K: codes of tokens 16 mg + l16 (channels 32g ..) and the operand vectors
     r2o_u4 kx[2];
     r2o_u4 ops[8];
 };
 template <>
-struct KRegs<true> {  // BF16-K: channels 32g + 8j .. 32g + 8j + 7 of tokens 16 mg + l16
+struct KRegs<kKBf16> {  // BF16-K: channels 32g + 8j .. 32g + 8j + 7 of tokens 16 mg + l16
     r2o_u4 kb[2][4];
+};
+template <>
+struct KRegs<kKInt2> {  // INT2-K: codes of tokens 16 mg + l16 (channels 32g .., 8 bytes) and the operands
+    uint32_t kx[2][2];
+    r2o_u4 ops[8];
 };
 template <int KIND>
 struct VRegs;
@@ -208,8 +219,8 @@ struct VRegs<kI2> {
     uint32_t vm[8];  // fp16 scale bits (group of dims 8*l16)
     uint32_t vz[8];  // u8 zero point
 };
-template <int KIND, bool BK>
-struct TileRegs : KRegs<BK>, VRegs<KIND> {};
+template <int KIND, int KF>
+struct TileRegs : KRegs<KF>, VRegs<KIND> {};
 
 // Valid arena positions of the segment (partial tiles mask the rest).
 struct SegCtx {
@@ -244,6 +255,36 @@ __device__ __forceinline__ void qk_int4k(const uint32_t (&qp)[4][4], const VCons
             const uint32_t w = kx[mg][j], w8 = w >> 8;
             const r2o_u4 a = {(w & vc.nib) | vc.magic, (w & vc.nib_hi) | vc.magic, (w8 & vc.nib) | vc.magic,
                               (w8 & vc.nib_hi) | vc.magic};
+            s[mg] = r2o_mfma_f16(a, qj, s[mg]);
+        }
+    }
+    corr = cz[0];  // every row of the correction product is the same
+}
+
+// QK^T of one INT2-K tile (k = code * s + o per channel and superblock): per MFMA j the codes of
+// half a dword enter in place as 1024 + 4^u c (crumb u of bytes 0/2 or 1/3), against
+// Q'_j = q * s / 4^u; the correction sum_c q_c o_c - 1024 sum_c Q'_c takes two more MFMAs (the
+// offset pairs against q, and -1024 against Q'_j, the very f16 values the code MFMAs used), and is
+// returned as the lane scalar `corr`.  ko = the 4 scale-pair and the 4 offset-pair vectors.
+__device__ __forceinline__ void qk_int2k(const uint32_t (&qp)[4][4], const VConst& vc, const r2o_u4 (&ko)[8],
+                                         const uint32_t (&kx)[2][2], r2o_f4 (&s)[2], float& corr) {
+    s[0] = r2o_f4{0, 0, 0, 0};
+    s[1] = r2o_f4{0, 0, 0, 0};
+    r2o_f4 cz = {0, 0, 0, 0};
+    const r2o_u4 neg1024 = {0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const r2o_u4 sj = ko[j], oj = ko[4 + j];
+        const r2o_u4 qraw = {qp[j][0], qp[j][1], qp[j][2], qp[j][3]};
+        const r2o_u4 qj = {r2o_h2_mul(qp[j][0], sj[0]), r2o_h2_mul(qp[j][1], sj[1]), r2o_h2_mul(qp[j][2], sj[2]),
+                           r2o_h2_mul(qp[j][3], sj[3])};
+        cz = r2o_mfma_f16(oj, qraw, cz);
+        cz = r2o_mfma_f16(neg1024, qj, cz);
+#pragma unroll
+        for (int mg = 0; mg < 2; ++mg) {
+            const uint32_t w = (j & 1) ? (kx[mg][j >> 1] >> 8) : kx[mg][j >> 1];
+            const r2o_u4 a = {(w & vc.crumb) | vc.magic, (w & (vc.crumb << 2)) | vc.magic,
+                              (w & (vc.crumb << 4)) | vc.magic, (w & (vc.crumb << 6)) | vc.magic};
             s[mg] = r2o_mfma_f16(a, qj, s[mg]);
         }
     }
@@ -337,13 +378,14 @@ __device__ __forceinline__ void qk_bf16k(const uint32_t (&qp)[4][4], float qscal
 }
 
 // One tile: QK, masks, online softmax, PV.
-template <int KIND, bool BK>
+template <int KIND, int KF>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
-                                            int a0, int g, float qscale, const TileRegs<KIND, BK>& cur) {
+                                            int a0, int g, float qscale, const TileRegs<KIND, KF>& cur) {
     r2o_f4 s[2];
     float corr = 0.f;
-    if constexpr (BK) qk_bf16k(ss.qp, qscale, cur.kb, s);
-    else qk_int4k(ss.qp, vc, cur.ops, cur.kx, s, corr);
+    if constexpr (KF == kKBf16) qk_bf16k(ss.qp, qscale, cur.kb, s);
+    else if constexpr (KF == kKInt4) qk_int4k(ss.qp, vc, cur.ops, cur.kx, s, corr);
+    else qk_int2k(ss.qp, vc, cur.ops, cur.kx, s, corr);
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
     softmax_tile(st, sv, pk, g, corr, KIND == kI4 ? &ss.bias : nullptr);
@@ -358,23 +400,25 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
 // the transposed per-lane reads hit distinct LDS banks (see the slot functions).  A DMA of 16
 // bytes per lane fills LDS at lane * 16; one of 1, 2 or 4 bytes per lane fills the low bytes of
 // the dword at lane * 4, so sub-dword metadata rows sit in dword slots.
-template <int KIND, bool BK>
-struct StageLayout {  // byte offsets within a stage: K | V payload | K operands (INT4-K) | V metadata
-    static constexpr int kKBytes = BK ? 8192 : 2048;
+template <int KIND, int KF>
+struct StageLayout {  // byte offsets within a stage: K | V payload | K operands (INT4/INT2-K) | V metadata
+    static constexpr bool kBK = KF == kKBf16;
+    static constexpr int kKBytes = kBK ? 8192 : (KF == kKInt4 ? 2048 : 1024);
     static constexpr int kV = kKBytes;
     static constexpr int kVBytes = KIND == kFP ? 8192 : (KIND == kI4 ? 2048 : 1024);
-    static constexpr int kOps = kV + kVBytes;                  // INT4-K only
-    static constexpr int kScale = BK ? kV + kVBytes : kOps + 512;
+    static constexpr int kOps = kV + kVBytes;                  // INT4-K and INT2-K only
+    static constexpr int kScale = kBK ? kV + kVBytes : kOps + 512;
     static constexpr int kZero = kScale + 256;                 // INT2 only
-    static constexpr int kDma = kKBytes / 1024 + kVBytes / 1024 + (BK ? 0 : 1) + (KIND == kFP ? 0 : (KIND == kI4 ? 1 : 2));
+    static constexpr int kDma = kKBytes / 1024 + kVBytes / 1024 + (kBK ? 0 : 1) + (KIND == kFP ? 0 : (KIND == kI4 ? 1 : 2));
     static constexpr int kEnd = KIND == kFP ? kScale : (KIND == kI4 ? kScale + 128 : kZero + 128);
 };
-template <bool BK>
+template <int KF>
 constexpr bool stages_fit() {
-    return StageLayout<kFP, BK>::kEnd <= KernelCfg<BK>::kStage && StageLayout<kI4, BK>::kEnd <= KernelCfg<BK>::kStage &&
-           StageLayout<kI2, BK>::kEnd <= KernelCfg<BK>::kStage;
+    return StageLayout<kFP, KF>::kEnd <= KernelCfg<KF>::kStage && StageLayout<kI4, KF>::kEnd <= KernelCfg<KF>::kStage &&
+           StageLayout<kI2, KF>::kEnd <= KernelCfg<KF>::kStage;
 }
-static_assert(stages_fit<false>() && stages_fit<true>(), "every tile stage fits its kernel's stage size");
+static_assert(stages_fit<kKInt4>() && stages_fit<kKBf16>() && stages_fit<kKInt2>(),
+              "every tile stage fits its kernel's stage size");
 
 // K codes: token t (0..31), 16-byte chunk c (0..3) of its 64-byte row.  Reads: 8 lanes take 8
 // consecutive tokens of one chunk, so the chunk is rotated by (t >> 1) & 3.
@@ -384,6 +428,9 @@ __device__ __forceinline__ int k_slot(int t, int c) { return 4 * t + (c ^ ((t >>
 __device__ __forceinline__ int v4_slot(int t, int c) { return 8 * ((t & 3) + 4 * (t >> 3)) + 2 * c + ((t >> 2) & 1); }
 // INT2 V: token t, chunk c (0..1) of its 32-byte row; tokens t, t+4, t+8, t+12 share 8 slots.
 __device__ __forceinline__ int v2_slot(int t, int c) { return 8 * (t & 3) + 32 * (t >> 4) + 2 * ((t >> 2) & 3) + c; }
+// INT2-K codes: token t, chunk c (0..1) of its 32-byte row.  Reads: 16 lanes take 8 bytes of one
+// chunk of 16 consecutive tokens, so tokens 8..15 of a group swap their two chunks.
+__device__ __forceinline__ int k2_slot(int t, int c) { return 2 * t + (c ^ ((t >> 3) & 1)); }
 // BF16 V rows stay in natural order: 8 lanes read 8 consecutive chunks of one 256-byte row.
 // BF16 K: token t, chunk c (0..15) of its 256-byte row.  Reads: 8 lanes take one chunk of 8
 // consecutive tokens, so the chunk is rotated by t.
@@ -417,22 +464,24 @@ struct DmaCtx {
     const uint8_t* vscale;  // V scales of this head (bytes)
     const uint8_t* vzero;   // INT2 zero points of this head
     int lo, hi, vdelta, sb_shift, groups;
-    int koff0, koff1;       // this lane's K source offset (bytes) for the two K DMAs
+    int koff0, koff1;       // this lane's K source offset (bytes) for the K DMAs (INT4: two, INT2: one)
     int vt0, vt1, vc0, vc1; // this lane's V source token / chunk for the INT V DMAs
 };
 
-template <int KIND, bool BK>
+template <int KIND, int KF>
 __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char* stage, int lane) {
-    using Lay = StageLayout<KIND, BK>;
-    if constexpr (BK) {  // 8 x 1 KB of bf16 rows: slot s = 64 j + lane holds chunk c of token t
+    using Lay = StageLayout<KIND, KF>;
+    if constexpr (KF == kKBf16) {  // 8 x 1 KB of bf16 rows: slot s = 64 j + lane holds chunk c of token t
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int sl = 64 * j + lane, t = sl >> 4, ch = (sl & 15) ^ (t & 15);
             dma<16>(c.kcode + (a0 + t) * 256 + ch * 16, stage + 1024 * j);
         }
-    } else {
+    } else if constexpr (KF == kKInt4) {
         dma<16>(c.kcode + a0 * 64 + c.koff0, stage);
         dma<16>(c.kcode + a0 * 64 + c.koff1, stage + 1024);
+    } else {
+        dma<16>(c.kcode + a0 * 32 + c.koff0, stage);
     }
     const bool full = __builtin_amdgcn_readfirstlane(a0 >= c.lo && a0 + 32 <= c.hi);  // wave-uniform
     // rows outside [lo, hi) read a clamped valid row (finite data, probability 0)
@@ -446,7 +495,7 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
     } else {
         dma<16>(c.vrows + row(c.vt0) * 32 + c.vc0 * 16, stage + Lay::kV);
     }
-    if constexpr (!BK)
+    if constexpr (KF != kKBf16)
         if (lane < 32) dma<16>(c.kops + (a0 >> c.sb_shift) * 128 + lane * 4, stage + Lay::kOps);
     if constexpr (KIND == kI4) {
         if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
@@ -464,11 +513,11 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
     }
 }
 
-template <int KIND, bool BK>
+template <int KIND, int KF>
 __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, int g, int gamma, int groups,
-                                          TileRegs<KIND, BK>& tr) {
-    using Lay = StageLayout<KIND, BK>;
-    if constexpr (BK) {
+                                          TileRegs<KIND, KF>& tr) {
+    using Lay = StageLayout<KIND, KF>;
+    if constexpr (KF == kKBf16) {
 #pragma unroll
         for (int mg = 0; mg < 2; ++mg)
 #pragma unroll
@@ -476,7 +525,15 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
                 tr.kb[mg][j] = *reinterpret_cast<const r2o_u4*>(stage + 16 * kb_slot(16 * mg + l16, 4 * g + j));
     } else {
 #pragma unroll
-        for (int mg = 0; mg < 2; ++mg) tr.kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(16 * mg + l16, g));
+        for (int mg = 0; mg < 2; ++mg) {
+            if constexpr (KF == kKInt4) {
+                tr.kx[mg] = *reinterpret_cast<const r2o_u4*>(stage + 16 * k_slot(16 * mg + l16, g));
+            } else {
+                const uint2 w = *reinterpret_cast<const uint2*>(stage + 16 * k2_slot(16 * mg + l16, g >> 1) + 8 * (g & 1));
+                tr.kx[mg][0] = w.x;
+                tr.kx[mg][1] = w.y;
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) tr.ops[j] = *reinterpret_cast<const r2o_u4*>(stage + Lay::kOps + g * 128 + 16 * j);
     }
@@ -496,10 +553,10 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
     }
 }
 
-template <int KIND, bool BK>
+template <int KIND, int KF>
 __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
                             unsigned char* smem, WaveState& st) {
-    using Cfg = KernelCfg<BK>;
+    using Cfg = KernelCfg<KF>;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
@@ -511,7 +568,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     unsigned char* ring = smem + wave * Cfg::kWaveLds;
 
     DmaCtx c;
-    c.kcode = rq.k_packed + kvh * rq.k_capacity * (BK ? 256 : 64);
+    c.kcode = rq.k_packed + kvh * rq.k_capacity * (KF == kKBf16 ? 256 : (KF == kKInt4 ? 64 : 32));
     c.kops = rq.k_operands + kvh * rq.k_superblocks * 128;
     c.lo = (int)it.lo;
     c.hi = (int)it.hi;
@@ -534,8 +591,13 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     {  // lane -> (token, chunk) sources of the K and INT V DMAs (inverse of the slot functions)
         const int s0 = lane, s1 = 64 + lane;
         const int t0 = s0 >> 2, t1 = s1 >> 2;
-        c.koff0 = t0 * 64 + 16 * ((s0 & 3) ^ ((t0 >> 1) & 3));
-        c.koff1 = t1 * 64 + 16 * ((s1 & 3) ^ ((t1 >> 1) & 3));
+        if constexpr (KF == kKInt2) {  // one 1 KB DMA: slot s holds chunk (s & 1) ^ ((t >> 3) & 1) of token s >> 1
+            c.koff0 = (s0 >> 1) * 32 + 16 * ((s0 & 1) ^ ((s0 >> 4) & 1));
+            c.koff1 = 0;
+        } else {
+            c.koff0 = t0 * 64 + 16 * ((s0 & 3) ^ ((t0 >> 1) & 3));
+            c.koff1 = t1 * 64 + 16 * ((s1 & 3) ^ ((t1 >> 1) & 3));
+        }
         if constexpr (KIND == kI2) {
             c.vt0 = 16 * (s0 >> 5) + 4 * ((s0 >> 1) & 3) + ((s0 >> 3) & 3);
             c.vc0 = s0 & 1;
@@ -552,26 +614,26 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int a_first = (int)it.tile0 + 32 * t_begin;
 #pragma unroll
     for (int j = 0; j < kDmaStages; ++j)
-        if (j < n) dma_tile<KIND, BK>(c, a_first + 32 * j, ring + j * Cfg::kStage, lane);
+        if (j < n) dma_tile<KIND, KF>(c, a_first + 32 * j, ring + j * Cfg::kStage, lane);
 
     const VConst vc = make_vconst();
     const float qscale = p.sm_scale * kLog2e;
     SegState<KIND> ss;
-    load_query<BK>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: bf16 pairs, scaled after the MFMA
+    load_query<KF>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: bf16 pairs, scaled after the MFMA
     ss.bias = r2o_f4{0, 0, 0, 0};
     const SegCtx sc = {c.lo, c.hi};
     for (int i = 0; i < n; ++i) {
-        wait_tiles<StageLayout<KIND, BK>::kDma>(min(kDmaStages, n - i) - 1);  // tile i has landed
+        wait_tiles<StageLayout<KIND, KF>::kDma>(min(kDmaStages, n - i) - 1);  // tile i has landed
         __builtin_amdgcn_wave_barrier();
         unsigned char* stage = ring + (i % kDmaStages) * Cfg::kStage;
-        TileRegs<KIND, BK> cur;
-        read_tile<KIND, BK>(stage, l16, g, gamma, c.groups, cur);
+        TileRegs<KIND, KF> cur;
+        read_tile<KIND, KF>(stage, l16, g, gamma, c.groups, cur);
         if (i + kDmaStages < n) {
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the whole stage is in registers
             __builtin_amdgcn_wave_barrier();
-            dma_tile<KIND, BK>(c, a_first + 32 * (i + kDmaStages), stage, lane);
+            dma_tile<KIND, KF>(c, a_first + 32 * (i + kDmaStages), stage, lane);
         }
-        seg_compute<KIND, BK>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
+        seg_compute<KIND, KF>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
     }
     if constexpr (KIND == kI4) {  // remove the code offsets: lo dims 1032 * sum P', hi dims (1152 * sum P') / 16
 #pragma unroll
@@ -601,7 +663,7 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     const float qscale = p.sm_scale * kLog2e;
     const bool head_ok = l16 < gqa;
     uint32_t qp[4][4];
-    load_query<true>(p, b, kvh, gqa, l16, g, qscale, qp);
+    load_query<kKBf16>(p, b, kvh, gqa, l16, g, qscale, qp);
     const uint16_t* ring_k = rq.recent_k + kvh * rq.recent_capacity * 128;
     const uint16_t* ring_v = rq.recent_v + kvh * rq.recent_capacity * 128;
     const uint16_t* new_k = app ? p.append_k + (b * p.hkv + kvh) * 128 : ring_k;
@@ -642,9 +704,9 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     }
 }
 
-template <bool BK>
-__global__ __launch_bounds__(256, KernelCfg<BK>::kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
-    __shared__ __align__(16) unsigned char smem[KernelCfg<BK>::kSmem];
+template <int KF>
+__global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
+    __shared__ __align__(16) unsigned char smem[KernelCfg<KF>::kSmem];
     const r2o_work_item it = p.items[blockIdx.x];
     const r2o_request_desc rq = p.reqs[it.req];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -658,9 +720,9 @@ __global__ __launch_bounds__(256, KernelCfg<BK>::kBlocksPerCU) void decode_parti
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP, BK>(p, it, rq, smem, st); break;
-        case kI4: run_segment<kI4, BK>(p, it, rq, smem, st); break;
-        case kI2: run_segment<kI2, BK>(p, it, rq, smem, st); break;
+        case kFP: run_segment<kFP, KF>(p, it, rq, smem, st); break;
+        case kI4: run_segment<kI4, KF>(p, it, rq, smem, st); break;
+        case kI2: run_segment<kI2, KF>(p, it, rq, smem, st); break;
         default: run_recent(p, it, rq, st); break;
     }
 
@@ -808,6 +870,7 @@ int validate(const r2o_decode_params* p) {
     if (!(p->int2_group == 32 || p->int2_group == 64 || p->int2_group == 128)) return R2O_EINVAL;
     if (p->q_dtype != 0 && p->q_dtype != 1) return R2O_EINVAL;
     if (p->page_size <= 0) return R2O_EINVAL;
+    if (p->k_format != kKInt4 && p->k_format != kKBf16 && p->k_format != kKInt2) return R2O_EINVAL;
     if (p->do_append && (!p->append_k || !p->append_v)) return R2O_EINVAL;
     if (reinterpret_cast<uintptr_t>(p->partial_out) % 16) return R2O_EINVAL;  // 16-byte vector rows
     return R2O_OK;
@@ -820,12 +883,12 @@ extern "C" {
 int r2o_decode_partial(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
-    if (params->k_bf16)
-        hipLaunchKernelGGL(decode_partial_kernel<true>, dim3((unsigned)params->n_items), dim3(256), 0,
-                           (hipStream_t)stream, *params);
-    else
-        hipLaunchKernelGGL(decode_partial_kernel<false>, dim3((unsigned)params->n_items), dim3(256), 0,
-                           (hipStream_t)stream, *params);
+    const dim3 grid((unsigned)params->n_items), block(256);
+    switch (params->k_format) {
+        case kKInt4: hipLaunchKernelGGL(decode_partial_kernel<kKInt4>, grid, block, 0, (hipStream_t)stream, *params); break;
+        case kKBf16: hipLaunchKernelGGL(decode_partial_kernel<kKBf16>, grid, block, 0, (hipStream_t)stream, *params); break;
+        default: hipLaunchKernelGGL(decode_partial_kernel<kKInt2>, grid, block, 0, (hipStream_t)stream, *params); break;
+    }
     R2O_CHECK_LAUNCH();
     return R2O_OK;
 }

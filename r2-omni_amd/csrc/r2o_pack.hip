@@ -88,6 +88,108 @@ __global__ __launch_bounds__(64) void pack_int4_k_kernel(
     }
 }
 
+// ----------------------------------------------------------------------------- INT2 keys
+// OScaR per-channel affine INT2 over superblocks (int2_reference.py:159-214, clip ratio 1):
+// block min/max without 0, scale = range / 3, inv = (1 / range) * 3 (torch's ``3.0 / t``),
+// zero = rne(-min * inv), offset = -zero * scale; constant channels keep scale 0 and offset = min.
+// grid (superblocks to write, hkv), block 64: threads 0..31 quantise channels 4t..4t+3 (byte t
+// of the 32-byte row); then all 64 write the QK MFMA operand pairs of the superblock.
+__global__ __launch_bounds__(64) void pack_int2_k_kernel(
+    const uint16_t* __restrict__ src, int dtype, int64_t src_tokens, const int64_t* __restrict__ index,
+    int64_t n, int64_t tail, int64_t dst_start, uint8_t* packed, uint16_t* scale, uint16_t* offset,
+    uint32_t* operands, int64_t capacity, int64_t superblocks, int sb) {
+    __shared__ uint16_t s_half[128];
+    __shared__ uint16_t s_off[128];
+    const int t = threadIdx.x;
+    const int64_t h = blockIdx.y;
+    const int64_t total = tail + n;
+    const int64_t first = (int64_t)blockIdx.x * sb;  // relative to dst_start
+    const int64_t count = min((int64_t)sb, total - first);
+    if (count <= 0) return;
+    const int64_t block_row = dst_start / sb + blockIdx.x;
+    if (t < 32) {
+        uint8_t* prow = packed + (h * capacity + dst_start + first) * 32 + t;
+        uint16_t* srow = scale + (h * superblocks + block_row) * 128 + 4 * t;
+        uint16_t* orow = offset + (h * superblocks + block_row) * 128 + 4 * t;
+        // old metadata of the tail superblock (only block 0 can hold tail positions)
+        float os[4], oo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            os[i] = r2o_f16_to_f32(srow[i]);
+            oo[i] = r2o_f16_to_f32(orow[i]);
+        }
+        auto value = [&](int64_t j, float (&x)[4]) {
+            const int64_t pos = first + j;
+            if (pos < tail) {  // dequantise-then-round the partial tail (compact_int2_key.py:114-121)
+                const uint32_t b = prow[j * 32];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    x[i] = r2o_round_dtype(__fadd_rn(__fmul_rn((float)((b >> (2 * i)) & 3u), os[i]), oo[i]), dtype);
+            } else {
+                const int64_t i0 = pos - tail;
+                const int64_t row = index ? index[i0] : i0;
+                const uint2 q = *reinterpret_cast<const uint2*>(src + (h * src_tokens + row) * 128 + 4 * t);
+                const uint32_t w[4] = {q.x & 0xffffu, q.x >> 16, q.y & 0xffffu, q.y >> 16};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[i] = dtype == 0 ? r2o_bf16_to_f32(w[i]) : r2o_f16_to_f32(w[i]);
+            }
+        };
+        float mn[4], mx[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            mn[i] = INFINITY;
+            mx[i] = -INFINITY;
+        }
+        for (int64_t j = 0; j < count; ++j) {
+            float x[4];
+            value(j, x);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                mn[i] = fminf(mn[i], x[i]);
+                mx[i] = fmaxf(mx[i], x[i]);
+            }
+        }
+        float sc[4], inv[4], zp[4], off[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float rng = __fsub_rn(mx[i], mn[i]);
+            const bool nonconst = rng > 0.f;
+            sc[i] = nonconst ? __fdiv_rn(rng, 3.0f) : 0.f;
+            inv[i] = nonconst ? __fmul_rn(__fdiv_rn(1.0f, fmaxf(rng, 1e-30f)), 3.0f) : 0.f;
+            zp[i] = nonconst ? __builtin_rintf(__fmul_rn(-mn[i], inv[i])) : 0.f;
+            off[i] = nonconst ? __fmul_rn(-zp[i], sc[i]) : mn[i];
+        }
+        for (int64_t j = 0; j < count; ++j) {
+            float x[4];
+            value(j, x);  // reads the old tail code before this thread overwrites it
+            uint32_t byte = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float c = fminf(fmaxf(__builtin_rintf(__fadd_rn(__fmul_rn(x[i], inv[i]), zp[i])), 0.f), 3.f);
+                byte |= (uint32_t)c << (2 * i);
+            }
+            prow[j * 32] = (uint8_t)byte;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint16_t hs = (uint16_t)r2o_f32_to_f16(sc[i]), ho = (uint16_t)r2o_f32_to_f16(off[i]);
+            srow[i] = hs;
+            orow[i] = ho;
+            s_half[4 * t + i] = hs;
+            s_off[4 * t + i] = ho;
+        }
+    }
+    if (operands) {  // QK MFMA operands of this superblock (layout in r2o_sspa.h)
+        __syncthreads();
+        const int g = t >> 4, j = (t >> 2) & 3, u = t & 3;
+        const int c = 32 * g + 16 * (j >> 1) + 4 * (j & 1) + u;  // pair (c, c + 8)
+        const float k = u == 0 ? 1.f : (u == 1 ? 0.25f : (u == 2 ? 0.0625f : 0.015625f));  // crumb u enters x 4^u
+        uint32_t* orow = operands + (h * superblocks + block_row) * 128 + g * 32 + 4 * j + u;
+        orow[0] = r2o_f32_to_f16(r2o_f16_to_f32(s_half[c]) * k) | (r2o_f32_to_f16(r2o_f16_to_f32(s_half[c + 8]) * k) << 16);
+        orow[16] = (uint32_t)s_off[c] | ((uint32_t)s_off[c + 8] << 16);
+    }
+}
+
 // ---------------------------------------------------------------------------- INT4 values
 // grid (n, hkv), block 64: thread t owns channels 2t, 2t+1.
 __global__ __launch_bounds__(64) void pack_int4_v_kernel(
@@ -250,6 +352,23 @@ int r2o_pack_int4_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src
     const int64_t blocks = (total + superblock - 1) / superblock;
     hipLaunchKernelGGL(pack_int4_k_kernel, dim3((unsigned)blocks, (unsigned)hkv), dim3(64), 0, (hipStream_t)stream,
                        src, (int)dtype, src_tokens, index, n, tail, dst_start, packed, scale, zero, operands,
+                       capacity, superblocks, (int)superblock);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int r2o_pack_int2_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens, const int64_t* index,
+                    int64_t n, int64_t tail, int64_t dst_start, uint8_t* packed, uint16_t* scale, uint16_t* offset,
+                    uint32_t* operands, int64_t capacity, int64_t superblocks, int64_t superblock, void* stream) {
+    if (!(superblock == 32 || superblock == 64 || superblock == 128) || (dtype != 0 && dtype != 1)) return R2O_EINVAL;
+    if (hkv <= 0 || n < 0 || tail < 0 || tail >= superblock || dst_start < 0 || dst_start % superblock) return R2O_EINVAL;
+    if (dst_start + tail + n > capacity || capacity % superblock || superblocks * superblock != capacity) return R2O_EINVAL;
+    if (n > 0 && (!src || src_tokens <= 0)) return R2O_EINVAL;
+    const int64_t total = tail + n;
+    if (total == 0) return R2O_OK;
+    const int64_t blocks = (total + superblock - 1) / superblock;
+    hipLaunchKernelGGL(pack_int2_k_kernel, dim3((unsigned)blocks, (unsigned)hkv), dim3(64), 0, (hipStream_t)stream,
+                       src, (int)dtype, src_tokens, index, n, tail, dst_start, packed, scale, offset, operands,
                        capacity, superblocks, (int)superblock);
     R2O_CHECK_LAUNCH();
     return R2O_OK;

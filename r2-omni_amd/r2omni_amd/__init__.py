@@ -5,6 +5,8 @@ Import names mirror the reference modules the Qwen/MiniCPM SSPA manager imports
 (r2omni/sspa/integration/qwen_sspa_attention.py:16-25, 50-59).
 """
 from .cache import (
+    BF16KeyArena,
+    CompactInt2KeyArena,
     CompactInt2ValueArena,
     CompactInt4KeyArena,
     DynamicCacheStats,
@@ -13,6 +15,7 @@ from .cache import (
     PrecisionPool,
     ThreePrecisionCache,
     append_generated_token,
+    build_compact_int2_key_arena,
     build_compact_int2_value_arena,
     build_compact_int4_key_arena,
     build_three_precision_cache,

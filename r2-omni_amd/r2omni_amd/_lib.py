@@ -45,7 +45,7 @@ class DecodeParams(ctypes.Structure):
         ("q_dtype", c_i64),
         ("output_hadamard", c_i64),
         ("do_append", c_i64),
-        ("k_bf16", c_i64),
+        ("k_format", c_i64),
         ("sm_scale", ctypes.c_float),
         ("recent_len", ctypes.c_int32 * MAX_BATCH),
         ("append_global", c_i64 * MAX_BATCH),
@@ -66,11 +66,15 @@ REQUEST_FIELDS = (
 ITEM_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta", "slot")
 WORK_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta", "slot")
 KIND_FP, KIND_INT4, KIND_INT2, KIND_RECENT = 0, 1, 2, 3
+# r2o_decode_params.k_format: how the request descriptors' k_* fields hold the history keys
+K_INT4, K_BF16, K_INT2 = 0, 1, 2
 
 _SIGNATURES = {
     "r2o_decode_partial": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_combine": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_pack_int4_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+                        c_vp),
+    "r2o_pack_int2_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                         c_vp),
     "r2o_pack_int4_v": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp),
     "r2o_pack_int2_v": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp),

@@ -210,6 +210,142 @@ def build_compact_int4_key_arena(key: torch.Tensor, segment_token_indices, *, ap
     return arena
 
 
+@dataclass
+class CompactInt2KeyArena:
+    """Per-channel affine INT2 K (OScaR form) for all FP/INT4/INT2 tokens in physical order
+    (compact_int2_key.py:14-122): dequant = code * scale + offset, the offset kept in the
+    ``zero_point`` field as fp16 like the reference's."""
+
+    packed: torch.Tensor          # u8  [H, capacity, D/4]
+    scale: torch.Tensor           # f16 [H, capacity/SB, D]
+    zero_point: torch.Tensor      # f16 [H, capacity/SB, D] (the offset)
+    active_length: int
+    capacity: int
+    segment_offsets: tuple[int, int, int]
+    original_dtype: torch.dtype
+    superblock_size: int = 128
+    bit_width: int = 2
+    # u32 [H, capacity/SB, 128]: per superblock, the (scale / 4^u) pairs and offset pairs in the
+    # channel order of the decode kernel's INT2-K QK MFMA (derived by the packer)
+    kernel_operands: torch.Tensor | None = None
+
+    def __post_init__(self) -> None:
+        if self.packed.ndim != 3 or self.packed.dtype != torch.uint8:
+            raise ValueError("compact INT2 K storage must be uint8 [H,capacity,D/4]")
+        h, capacity, d4 = map(int, self.packed.shape)
+        if self.superblock_size not in (32, 64, 128):
+            raise ValueError("per-channel INT2 K block size must be 32, 64, or 128")
+        blocks = -(-capacity // self.superblock_size)
+        if capacity != self.capacity or not 0 <= self.active_length <= capacity:
+            raise ValueError("compact INT2 K active length/capacity is invalid")
+        if tuple(self.scale.shape) != (h, blocks, d4 * 4) or self.zero_point.shape != self.scale.shape:
+            raise ValueError("compact INT2 K metadata shape is invalid")
+        if self.scale.dtype != torch.float16 or self.zero_point.dtype != torch.float16:
+            raise ValueError("compact INT2 K metadata dtypes are invalid")
+        if tuple(sorted(self.segment_offsets)) != tuple(self.segment_offsets):
+            raise ValueError("compact INT2 K segment offsets must be monotonic")
+        if self.kernel_operands is not None and (tuple(self.kernel_operands.shape) != (h, blocks, 128)
+                                                 or self.kernel_operands.dtype != torch.int32):
+            raise ValueError("compact INT2 K kernel operands must be int32 [H,blocks,128]")
+
+    @property
+    def head_count(self) -> int:
+        return int(self.packed.shape[0])
+
+    @property
+    def head_dim(self) -> int:
+        return int(self.packed.shape[2]) * 4
+
+    @property
+    def superblock_count(self) -> int:
+        return int(self.scale.shape[1])
+
+    @property
+    def nbytes(self) -> int:
+        return sum(_nbytes(t) for t in self.allocation_tensors())
+
+    @property
+    def active_nbytes(self) -> int:
+        if self.active_length <= 0:
+            return 0
+        blocks = -(-self.active_length // self.superblock_size)
+        per_block = self.head_count * blocks * self.head_dim
+        return int(self.head_count * self.active_length * (self.head_dim // 4)
+                   + per_block * self.scale.element_size() + per_block * self.zero_point.element_size())
+
+    def allocation_tensors(self):
+        if self.kernel_operands is None:
+            return self.packed, self.scale, self.zero_point
+        return self.packed, self.scale, self.zero_point, self.kernel_operands
+
+    def dequantize_range(self, start: int, length: int) -> torch.Tensor:
+        """fp32 code * s + o of arena positions [start, start+length) (inspection only)."""
+        start, length = int(start), int(length)
+        if start < 0 or length < 0 or start + length > self.active_length:
+            raise ValueError("compact INT2 K range is outside the active payload")
+        payload = self.packed[:, start : start + length]
+        codes = torch.stack([(payload >> (2 * i)) & 3 for i in range(4)], dim=-1)
+        codes = codes.reshape(self.head_count, length, self.head_dim)
+        blocks = torch.arange(start, start + length, device=payload.device) // self.superblock_size
+        return codes.float() * self.scale.index_select(1, blocks).float() \
+            + self.zero_point.index_select(1, blocks).float()
+
+    def dequantize(self) -> torch.Tensor:
+        return self.dequantize_range(0, self.active_length)
+
+    def append_superblock(self, key_block: torch.Tensor, *, source_tokens: int | None = None) -> int:
+        """Flush 128 tokens: re-quantise the partial tail superblock together with them
+        (compact_int2_key.py:110-122).  ``key_block`` as in ``CompactInt4KeyArena.append_superblock``."""
+        if tuple(key_block.shape) != (self.head_count, 128, self.head_dim):
+            raise ValueError("compact INT2 K flush requires 128 matching tokens")
+        if self.active_length + 128 > self.capacity:
+            raise RuntimeError("compact INT2 K capacity exhausted")
+        _lib.require_device(key_block, "compact INT2 K flush block")
+        rows = int(source_tokens) if source_tokens is not None else 128
+        if key_block.stride() != (rows * self.head_dim, self.head_dim, 1):
+            raise ValueError("compact INT2 K flush block must have contiguous rows")
+        prefix = self.active_length // self.superblock_size * self.superblock_size
+        tail = self.active_length - prefix
+        _lib.call("r2o_pack_int2_k", _lib.ptr(key_block), _lib.dtype_code(key_block.dtype), self.head_count, rows,
+                  None, 128, tail, prefix, _lib.ptr(self.packed), _lib.ptr(self.scale), _lib.ptr(self.zero_point),
+                  _lib.ptr(self.kernel_operands), self.capacity, self.superblock_count, self.superblock_size,
+                  _lib.stream_of(key_block.device))
+        self.active_length += 128
+        return tail
+
+
+def build_compact_int2_key_arena(key: torch.Tensor, segment_token_indices, *, append_capacity: int = 0,
+                                 superblock_size: int = 128) -> CompactInt2KeyArena:
+    """``build_compact_int2_key_arena`` (compact_int2_key.py:125-153), packed on the GPU."""
+    if key.ndim != 3 or not torch.is_floating_point(key) or int(key.shape[2]) % 4:
+        raise ValueError("key must be floating [H,S,D] with D divisible by four")
+    if superblock_size not in (32, 64, 128):
+        raise ValueError("per-channel INT2 K block size must be 32, 64, or 128")
+    _lib.require_device(key, "key")
+    lengths = tuple(int(ix.numel()) for ix in segment_token_indices)
+    offsets = (0, lengths[0], lengths[0] + lengths[1])
+    active = sum(lengths)
+    capacity = max(128, _round_up(active + int(append_capacity), 128))
+    h, s, d = map(int, key.shape)
+    blocks = capacity // superblock_size
+    dev = key.device
+    arena = CompactInt2KeyArena(
+        packed=torch.zeros((h, capacity, d // 4), device=dev, dtype=torch.uint8),
+        scale=torch.zeros((h, blocks, d), device=dev, dtype=torch.float16),
+        zero_point=torch.zeros((h, blocks, d), device=dev, dtype=torch.float16),
+        active_length=active, capacity=capacity, segment_offsets=offsets,
+        original_dtype=key.dtype, superblock_size=superblock_size,
+        kernel_operands=torch.zeros((h, blocks, 128), device=dev, dtype=torch.int32),
+    )
+    if active:
+        key = key.contiguous()
+        ordered = torch.cat([ix.to(device=dev, dtype=torch.long) for ix in segment_token_indices]).contiguous()
+        _lib.call("r2o_pack_int2_k", _lib.ptr(key), _lib.dtype_code(key.dtype), h, s, _lib.ptr(ordered), active,
+                  0, 0, _lib.ptr(arena.packed), _lib.ptr(arena.scale), _lib.ptr(arena.zero_point),
+                  _lib.ptr(arena.kernel_operands), capacity, blocks, superblock_size, _lib.stream_of(dev))
+    return arena
+
+
 # ---------------------------------------------------------------------- INT4-V pool payload
 @dataclass
 class PackedTensor:
@@ -423,7 +559,7 @@ class ThreePrecisionCache:
     quantization_superblock: int
     matched_fp: bool
     cache_variant: str
-    compact_key: CompactInt4KeyArena | None = None
+    compact_key: CompactInt4KeyArena | CompactInt2KeyArena | None = None
     compact_value: CompactInt2ValueArena | None = None
     compact_int4_value: Any = None
     metadata_arena: Any = None
@@ -669,11 +805,9 @@ def build_three_precision_cache(
         raise ValueError(f"unsupported cache_variant: {cache_variant}")
     if generated_value_precision not in ("int2", "int4"):
         raise ValueError("generated_value_precision must be int2 or int4")
-    if (cache_variant == "v_fourq_k_int2_compact" and not matched_fp) or generated_value_precision != "int2" \
-            or not preallocate_recent:
+    if generated_value_precision != "int2" or not preallocate_recent:
         raise NotImplementedError(
-            "the gfx950 path implements the v_fourq_k_int4_compact and v_fourq_k_bf16 caches and the matched-FP "
-            "cache, with INT2 generated values and a preallocated Recent-FP ring")
+            "the gfx950 path implements the caches with INT2 generated values and a preallocated Recent-FP ring")
     if int(key.shape[2]) != 128:
         raise ValueError("the SSPA decode path requires head_dim 128")
     _lib.require_device(key, "key")
@@ -735,9 +869,10 @@ def build_three_precision_cache(
         return ThreePrecisionCache(
             fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
             compact_value=compact_value, static_int4_tokens=s_i4, bf16_key=arena, **common)
-    compact_key = build_compact_int4_key_arena(key, (fp_tokens, i4_tokens, i2_tokens),
-                                               append_capacity=append_capacity,
-                                               superblock_size=key_quantization_superblock)
+    build_key = build_compact_int2_key_arena if cache_variant == "v_fourq_k_int2_compact" \
+        else build_compact_int4_key_arena
+    compact_key = build_key(key, (fp_tokens, i4_tokens, i2_tokens), append_capacity=append_capacity,
+                            superblock_size=key_quantization_superblock)
     return ThreePrecisionCache(
         fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
         compact_key=compact_key, compact_value=compact_value, static_int4_tokens=s_i4,
@@ -811,7 +946,7 @@ def append_generated_token(cache: ThreePrecisionCache, new_key: torch.Tensor, ne
                                "requested generation horizon")
         else:
             if cache.compact_key is None or cache.compact_value is None:
-                raise RuntimeError("compact INT4 K cache is missing its compact INT2 V arena")
+                raise RuntimeError("compact INT2 K cache is missing its compact INT2 V arena")
             stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
                 if flush == 128 else _flush_size_error(flush)
             cache.compact_value.append_superblock(value_block, source_tokens=cap)
@@ -835,4 +970,4 @@ def append_generated_token(cache: ThreePrecisionCache, new_key: torch.Tensor, ne
 
 
 def _flush_size_error(flush: int) -> int:
-    raise ValueError(f"compact INT4 K flush requires 128 tokens, the cache flushes {flush}")
+    raise ValueError(f"compact K flush requires 128 tokens, the cache flushes {flush}")

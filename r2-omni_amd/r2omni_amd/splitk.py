@@ -47,8 +47,8 @@ def _num_cus(device: torch.device) -> int:
 def _segments(cache: ThreePrecisionCache, extra_int2: int = 0):
     """(kind, lo, hi, v_delta) arena ranges of the FP, INT4 and INT2(+generated) pools."""
     ck = cache.compact_key if cache.compact_key is not None else cache.bf16_key
-    if ck is None or (cache.compact_key is not None and not cache.compact_int4_key):
-        raise NotImplementedError("the gfx950 decode path requires a compact INT4-K or a bf16 K arena")
+    if ck is None:
+        raise NotImplementedError("the gfx950 decode path requires a compact INT4/INT2-K or a bf16 K arena")
     k_fp, k_i4, k_i2 = ck.segment_offsets
     s_fp = cache.fp_pool.token_count + (int(extra_int2) if cache.matched_fp else 0)
     s_i4 = cache.int4_pool.token_count
@@ -171,6 +171,12 @@ def allocated_workspace_bytes(workspace: SplitKWorkspace) -> int:
                                                           workspace.partial_output, workspace.output)))
 
 
+def _k_format(cache: ThreePrecisionCache) -> int:
+    if cache.bf16_key is not None:
+        return _lib.K_BF16
+    return _lib.K_INT2 if cache.compact_key.bit_width == 2 else _lib.K_INT4
+
+
 def _request_desc(cache: ThreePrecisionCache) -> list[int]:
     ck, cv = cache.compact_key, cache.compact_value
     fp, i4, rec = cache.fp_pool, cache.int4_pool, cache.recent_fp_pool
@@ -243,7 +249,7 @@ class SplitKExecutor:
         p.superblock, p.int2_group, p.page_size = self.superblock, self.int2_group, self.page_size
         p.q_dtype = _lib.dtype_code(query.dtype)
         p.output_hadamard = int(self.output_hadamard)
-        p.k_bf16 = int(self.caches[0].bf16_key is not None)
+        p.k_format = _k_format(self.caches[0])
         p.sm_scale = float(self.head_dim ** -0.5)
         for r, c in enumerate(self.caches):
             p.recent_len[r] = int(c.recent_fp_pool.active_length)
@@ -325,11 +331,12 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
         raise ValueError("split-K executor supports at most 16 GQA heads per KV head")
     if len(caches) > _lib.MAX_BATCH:
         raise ValueError(f"split-K executor supports at most {_lib.MAX_BATCH} requests per launch")
-    bf16k = first.bf16_key is not None
+    kf = _k_format(first)
+    bf16k = kf == _lib.K_BF16
     sb = 32 if bf16k else first.compact_key.superblock_size
     group = 32 if first.compact_value is None else first.compact_value.group_size
     for r, c in enumerate(caches):
-        if (c.bf16_key is not None) != bf16k or (not bf16k and c.compact_key.superblock_size != sb) \
+        if _k_format(c) != kf or (not bf16k and c.compact_key.superblock_size != sb) \
                 or (c.compact_value is not None and c.compact_value.group_size != group) \
                 or int(c.recent_fp_pool.fp_k.shape[0]) != hkv or c.page_size != first.page_size:
             raise ValueError(f"batched split-K geometry differs for request {r}")

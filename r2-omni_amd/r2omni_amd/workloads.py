@@ -29,7 +29,8 @@ class DecodeConfig:
     page: int = 64
     superblock: int = 32
     group: int = 32
-    variant: str = "int4k"     # "int4k" (v_fourq_k_int4_compact), "bf16k" (v_fourq_k_bf16) or "matched"
+    variant: str = "int4k"     # "int4k" (v_fourq_k_int4_compact), "int2k" (v_fourq_k_int2_compact),
+                               # "bf16k" (v_fourq_k_bf16) or "matched" (matched-FP)
 
 
 CONFIGS = {
@@ -94,7 +95,8 @@ def build_request_cache(cfg: DecodeConfig, data: RequestData, *, append_capacity
         key_quantization_superblock=cfg.superblock, int2_group_size=cfg.group,
         compact_key_append_capacity=append_capacity, recent_flush_size=128,
         matched_fp=cfg.variant == "matched",
-        cache_variant="v_fourq_k_bf16" if cfg.variant == "bf16k" else "v_fourq_k_int4_compact")
+        cache_variant={"bf16k": "v_fourq_k_bf16", "int2k": "v_fourq_k_int2_compact"}.get(
+            cfg.variant, "v_fourq_k_int4_compact"))
     for i in range(int(data.recent_k.shape[0])):
         append_recent_fp_triton(cache, data.recent_k[i][:, None], data.recent_v[i][:, None],
                                 global_token_index=hist + i, logical_position=hist + i)
@@ -105,7 +107,8 @@ def algorithmic_bytes(caches, hq: int, *, fused_append: bool = False) -> int:
     """Compulsory HBM bytes of one decode call over ``caches`` (one per request).
 
     Per request and KV head: INT4-K codes (64 B/token) + K superblock scale/zero
-    (3 B x 128 channels per superblock) or BF16-K rows (256 B/token), BF16-V 256 B, INT4-V 64 + 4 B, INT2-V 32 + 3*128/G B,
+    (3 B x 128 channels per superblock), INT2-K codes (32 B/token) + scale/offset (4 B x 128 per
+    superblock), or BF16-K rows (256 B/token); BF16-V 256 B, INT4-V 64 + 4 B, INT2-V 32 + 3*128/G B,
     Recent K+V 512 B per active token; plus Q and O (bf16) and, with a fused append, the new
     K/V rows read and written.
     """
@@ -113,9 +116,12 @@ def algorithmic_bytes(caches, hq: int, *, fused_append: bool = False) -> int:
     for c in caches:
         hkv = int(c.recent_fp_pool.fp_k.shape[0])
         ck, cv = c.compact_key, c.compact_value
-        if ck is not None:
+        if ck is not None and ck.bit_width == 4:
             hist = ck.active_length
             k_bytes = hist * 64 + -(-hist // ck.superblock_size) * 3 * 128
+        elif ck is not None:  # INT2-K: 32 B codes per token, fp16 scale and offset per channel and block
+            hist = ck.active_length
+            k_bytes = hist * 32 + -(-hist // ck.superblock_size) * 4 * 128
         else:  # bf16 key rows (matched-FP and v_fourq_k_bf16 caches)
             k_bytes = c.bf16_key.active_length * 256
         v2_bytes = 0 if cv is None else cv.active_length * (32 + 3 * (128 // cv.group_size))

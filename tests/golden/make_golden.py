@@ -143,8 +143,10 @@ def _case(name, *, seq, hkv, dtype, page_size, sb, group, tier_probs, appends, s
         record[prefix + "int2_global"] = _np(cache.int2_pool.page_index.global_token_indices[: cache.int2_pool.token_count])
         record[prefix + "attn"] = _np(triton_mixed_reference(query, cache).float())
 
+    stats_box = []
     snapshot("build_")
     stats = DynamicCacheStats()
+    stats_box.append(stats)
     app_k = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
     app_v = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
     record["append_k"] = _np(app_k)
@@ -170,7 +172,8 @@ def _case(name, *, seq, hkv, dtype, page_size, sb, group, tier_probs, appends, s
 
 
 def _variant_case(name, *, variant, seq, hkv, dtype, page_size, sb, group, tier_probs, appends, seed):
-    """BF16-K caches: ``matched`` (matched_fp=True) or ``bf16k`` (cache_variant v_fourq_k_bf16)."""
+    """Other K formats: ``matched`` (matched_fp=True), ``bf16k`` (cache_variant v_fourq_k_bf16) or
+    ``int2k`` (cache_variant v_fourq_k_int2_compact)."""
     sys.path.insert(0, REFERENCE)
     from r2omni.sspa.policy.page_assignment import build_page_table, project_token_bits_to_pages
     from r2omni.sspa.runtime.cache_plan import build_layer_compression_plan
@@ -197,6 +200,8 @@ def _variant_case(name, *, variant, seq, hkv, dtype, page_size, sb, group, tier_
                   compact_key_append_capacity=260, recent_flush_size=128)
     if variant == "matched":
         cache = build_three_precision_cache(key, value, plan, matched_fp=True, **kwargs)
+    elif variant == "int2k":
+        cache = build_three_precision_cache(key, value, plan, cache_variant="v_fourq_k_int2_compact", **kwargs)
     else:
         cache = build_three_precision_cache(key, value, plan, cache_variant="v_fourq_k_bf16", **kwargs)
     query = torch.randn(1, hkv * 8, d, generator=gen)
@@ -208,12 +213,22 @@ def _variant_case(name, *, variant, seq, hkv, dtype, page_size, sb, group, tier_
 
     def snapshot(prefix):
         pools = [cache.fp_pool, cache.int4_pool, cache.int2_pool]
-        record[prefix + "k_rows"] = _np(torch.cat([p.fp_k for p in pools if p.token_count], dim=1))
+        if variant == "int2k":
+            ck = cache.compact_key
+            blocks = -(-ck.active_length // ck.superblock_size)
+            record[prefix + "k_packed"] = _np(ck.packed[:, : ck.active_length])
+            record[prefix + "k_scale"] = _np(ck.scale[:, :blocks])
+            record[prefix + "k_offset"] = _np(ck.zero_point[:, :blocks])
+            record[prefix + "k_capacity"] = np.array(ck.capacity)
+            record[prefix + "tail_dequant_tokens"] = np.array(stats_box[0].local_tail_dequant_tokens
+                                                              if stats_box else 0)
+        else:
+            record[prefix + "k_rows"] = _np(torch.cat([p.fp_k for p in pools if p.token_count], dim=1))
         record[prefix + "pool_tokens"] = np.array([p.token_count for p in pools] + [cache.recent_fp_pool.token_count])
         fp = cache.fp_pool
         record[prefix + "fp_v"] = _np(fp.fp_v) if fp.token_count else np.zeros((hkv, 0, d), np.uint16)
         record[prefix + "fp_global"] = _np(fp.page_index.global_token_indices[: fp.token_count])
-        if variant == "bf16k":
+        if variant in ("bf16k", "int2k"):
             i4 = cache.int4_pool
             record[prefix + "v4_packed"] = _np(i4.packed_v.packed) if i4.token_count else np.zeros(0, np.uint8)
             record[prefix + "v4_scale"] = (_np(i4.packed_v.scale) if i4.token_count
@@ -227,8 +242,10 @@ def _variant_case(name, *, variant, seq, hkv, dtype, page_size, sb, group, tier_
         record[prefix + "recent_v"] = _np(rec.fp_v[:, : rec.active_length])
         record[prefix + "attn"] = _np(triton_mixed_reference(query, cache).float())
 
+    stats_box = []
     snapshot("build_")
     stats = DynamicCacheStats()
+    stats_box.append(stats)
     app_k = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
     app_v = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
     record["append_k"] = _np(app_k)
@@ -272,9 +289,18 @@ def main() -> None:
     # K-BF16 / V-FourQ cache: tiered values, bf16 keys; a flush is refused by the reference.
     _variant_case("kbf16_tiered_bf16", variant="bf16k", seq=330, hkv=2, dtype=torch.bfloat16, page_size=32,
                   sb=32, group=32, tier_probs=(0.2, 0.4, 0.4, 0.0), appends=130, seed=15)
+    # compact INT2-K caches: Qwen-style 32-token K blocks, and MiniCPM-style 128-token blocks in fp16
+    _VARIANTS["k_int2_tiered_bf16"]()
+    _VARIANTS["k_int2_sb128_fp16"]()
 
 
 _VARIANTS = {
+    "k_int2_tiered_bf16": lambda: _variant_case("k_int2_tiered_bf16", variant="int2k", seq=333, hkv=2,
+                                                dtype=torch.bfloat16, page_size=32, sb=32, group=32,
+                                                tier_probs=(0.2, 0.4, 0.3, 0.1), appends=140, seed=16),
+    "k_int2_sb128_fp16": lambda: _variant_case("k_int2_sb128_fp16", variant="int2k", seq=300, hkv=2,
+                                               dtype=torch.float16, page_size=64, sb=128, group=128,
+                                               tier_probs=(0.1, 0.2, 0.7, 0.0), appends=131, seed=17),
     "matched_fp_bf16": lambda: _variant_case("matched_fp_bf16", variant="matched", seq=300, hkv=2,
                                              dtype=torch.bfloat16, page_size=32, sb=32, group=32,
                                              tier_probs=(0.3, 0.3, 0.3, 0.1), appends=131, seed=14),

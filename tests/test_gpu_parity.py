@@ -31,6 +31,11 @@ def _bf16_np(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
+def _bits16(t):
+    """16-bit payload of a bf16 or fp16 tensor as uint16 bit patterns (fixtures store fp16 as float16)."""
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
 # --------------------------------------------------------------------------- golden builds
 @pytest.mark.parametrize("name", fixture_names())
 def test_build_and_flush_bit_exact_against_reference_fixtures(name):
@@ -85,8 +90,8 @@ def test_build_and_flush_bit_exact_against_reference_fixtures(name):
         np.testing.assert_array_equal(
             cache.int2_pool.page_index.global_token_indices.cpu().numpy(), g[prefix + "int2_global"])
 
-    check("build_")
     stats = ro.DynamicCacheStats()
+    check("build_")
     ak = _to_torch(g["append_k"], dt, dev)
     av = _to_torch(g["append_v"], dt, dev)
     seq = int(g["key"].shape[1])
@@ -183,7 +188,8 @@ def test_decode_long_group_combine():
         _compare(out, want, f"long group call {call}")
 
 
-def test_fused_append_then_flush_matches_oracle():
+@pytest.mark.parametrize("variant", ["int4k", "int2k"])
+def test_fused_append_then_flush_matches_oracle(variant):
     import r2omni_amd as ro
     from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
     from oracle.attention import mixed_reference, output_transform
@@ -191,7 +197,7 @@ def test_fused_append_then_flush_matches_oracle():
     from oracle.quant import bf16_bits_to_f32
 
     dev = _cuda()
-    cfg = DecodeConfig("t", 16, 2, (0,), (0.2, 0.5, 0.3), recent=120)
+    cfg = DecodeConfig("t", 16, 2, (0,), (0.2, 0.5, 0.3), recent=120, variant=variant)
     data = make_request(cfg, 1280 + 120, seed=7, device=dev)
     cache = build_request_cache(cfg, data)
     oc = _oracle_for(data, cfg)
@@ -226,18 +232,18 @@ def test_fused_append_then_flush_matches_oracle():
     # the ring, lengths and arenas agree with the oracle after the flush
     assert cache.recent_fp_pool.active_length == oc.recent_active
     assert int(cache.recent_fp_pool.length_device.item()) == oc.recent_active
-    ck = cache.compact_key
-    np.testing.assert_array_equal(ck.packed[:, : ck.active_length].cpu().numpy(), oc.k_packed[:, : oc.k_active])
+    _check_k_arena(cache, oc)
 
 
-def test_ragged_batch_matches_per_request_oracle():
+@pytest.mark.parametrize("variant", ["int4k", "int2k"])
+def test_ragged_batch_matches_per_request_oracle(variant):
     import r2omni_amd as ro
     from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
     from oracle.attention import mixed_reference, output_transform
     from oracle.quant import bf16_bits_to_f32
 
     dev = _cuda()
-    cfg = DecodeConfig("t", 28, 4, (0,), (0.15, 0.45, 0.4), recent=128)
+    cfg = DecodeConfig("t", 28, 4, (0,), (0.15, 0.45, 0.4), recent=128, variant=variant)
     totals = (512 + 128, 1024 + 128, 2048 + 128, 3072 + 128)
     datas = [make_request(cfg, t, seed=200 + i, device=dev) for i, t in enumerate(totals)]
     caches = [build_request_cache(cfg, d) for d in datas]
@@ -252,14 +258,39 @@ def test_ragged_batch_matches_per_request_oracle():
         _compare(out[r : r + 1], want, f"request {r}")
 
 
-# ------------------------------------------------------------- BF16-K cache variants
+# ------------------------------------------------------- other K formats (BF16-K, INT2-K)
 VARIANT_CASES = [0, 2, 4]  # mixed tiers with a partial ring, GQA 7 over 4 KV heads, FP-only pages
 
 
-@pytest.mark.parametrize("variant", ["matched", "bf16k"])
-@pytest.mark.parametrize("case", VARIANT_CASES)
+def _check_k_arena(cache, oc):
+    """The GPU K arena equals the oracle's, bit for bit, in the same physical order."""
+    from oracle.quant import bf16_bits_to_f32
+
+    if cache.bf16_key is not None:
+        kb = cache.bf16_key
+        assert kb.active_length == oc.k_active
+        got_rows = bf16_bits_to_f32(_bf16_np(kb.rows[:, : kb.active_length]))
+        np.testing.assert_array_equal(got_rows, oc.k_rows[:, : oc.k_active])
+        return
+    ck = cache.compact_key
+    k = ck.active_length
+    blocks = -(-k // ck.superblock_size)
+    assert k == oc.k_active and ck.capacity == oc.k_capacity
+    np.testing.assert_array_equal(ck.packed[:, :k].cpu().numpy(), oc.k_packed[:, :k])
+    np.testing.assert_array_equal(ck.scale[:, :blocks].cpu().view(torch.int16).numpy().view(np.uint16),
+                                  oc.k_scale[:, :blocks].view(np.uint16))
+    zp = ck.zero_point[:, :blocks].cpu()
+    want = oc.k_zero[:, :blocks]
+    if zp.dtype == torch.float16:
+        np.testing.assert_array_equal(zp.view(torch.int16).numpy().view(np.uint16), want.view(np.uint16))
+    else:
+        np.testing.assert_array_equal(zp.numpy(), want)
+
+
+@pytest.mark.parametrize("variant,case", [(v, c) for v in ("matched", "bf16k") for c in VARIANT_CASES]
+                         + [("int2k", c) for c in range(len(SMALL))])
 @pytest.mark.parametrize("hadamard", [False, True])
-def test_bf16_key_variants_decode_matches_oracle(variant, case, hadamard):
+def test_k_format_variants_decode_matches_oracle(variant, case, hadamard):
     import r2omni_amd as ro
     from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
     from oracle.attention import mixed_reference, output_transform
@@ -271,17 +302,16 @@ def test_bf16_key_variants_decode_matches_oracle(variant, case, hadamard):
     hist = ((total - recent) // 64) * 64
     data = make_request(cfg, hist + recent, seed=300 + case, device=dev)
     cache = build_request_cache(cfg, data)
-    assert cache.bf16_key is not None and cache.compact_key is None
+    if variant == "int2k":
+        assert cache.compact_key is not None and cache.compact_key.bit_width == 2
+    else:
+        assert cache.bf16_key is not None and cache.compact_key is None
     ws = ro.allocate_splitk_workspace(cache, num_query_heads=hq)
     ex = ro.prepare_splitk_executor(cache, ws, output_hadamard=hadamard)
     out = ex(data.query.contiguous())
     torch.cuda.synchronize()
     oc = _oracle_for(data, cfg)
-    # the bf16 key rows are the oracle's, bit for bit, in the same physical order
-    kb = cache.bf16_key
-    assert kb.active_length == oc.k_active
-    got_rows = bf16_bits_to_f32(_bf16_np(kb.rows[:, : kb.active_length]))
-    np.testing.assert_array_equal(got_rows, oc.k_rows[:, : oc.k_active])
+    _check_k_arena(cache, oc)
     q = bf16_bits_to_f32(_bf16_np(data.query))
     want = output_transform(mixed_reference(q, oc), hadamard)
     _compare(out, want, f"{variant} case {case} hadamard {hadamard}")
@@ -354,8 +384,9 @@ def test_bf16k_ring_overflow_is_refused():
 
 
 @pytest.mark.parametrize("name", variant_fixture_names())
-def test_bf16_key_variant_build_and_appends_bit_exact_against_reference_fixtures(name):
-    """BF16-K builds and appends against the reference's own cache state, then decode against the oracle."""
+def test_k_format_variant_build_and_appends_bit_exact_against_reference_fixtures(name):
+    """BF16-K / INT2-K builds and appends against the reference's own cache state, then decode
+    against the oracle."""
     import r2omni_amd as ro
     from oracle.attention import mixed_reference
     from oracle.cache import append_token, build_cache
@@ -373,6 +404,8 @@ def test_bf16_key_variant_build_and_appends_bit_exact_against_reference_fixtures
                   int2_group_size=int(g["group"]), compact_key_append_capacity=260, recent_flush_size=128)
     if variant == "matched":
         cache = ro.build_three_precision_cache(key, value, plan, matched_fp=True, **kwargs)
+    elif variant == "int2k":
+        cache = ro.build_three_precision_cache(key, value, plan, cache_variant="v_fourq_k_int2_compact", **kwargs)
     else:
         cache = ro.build_three_precision_cache(key, value, plan, cache_variant="v_fourq_k_bf16", **kwargs)
     oc = build_cache(as_f32(g["key"], dt), as_f32(g["value"], dt), g["page_offsets"], g["page_lengths"],
@@ -383,16 +416,28 @@ def test_bf16_key_variant_build_and_appends_bit_exact_against_reference_fixtures
 
     def check(prefix):
         torch.cuda.synchronize()
-        kb = cache.bf16_key
-        rows = kb.rows[:, : kb.active_length].cpu().view(torch.int16).numpy().view(np.uint16)
-        np.testing.assert_array_equal(rows, g[prefix + "k_rows"])
+        if variant == "int2k":
+            ck = cache.compact_key
+            k = ck.active_length
+            blocks = -(-k // ck.superblock_size)
+            assert ck.capacity == int(g[prefix + "k_capacity"])
+            np.testing.assert_array_equal(ck.packed[:, :k].cpu().numpy(), g[prefix + "k_packed"])
+            np.testing.assert_array_equal(ck.scale[:, :blocks].cpu().view(torch.int16).numpy().view(np.uint16),
+                                          g[prefix + "k_scale"].view(np.uint16))
+            np.testing.assert_array_equal(ck.zero_point[:, :blocks].cpu().view(torch.int16).numpy().view(np.uint16),
+                                          g[prefix + "k_offset"].view(np.uint16))
+            assert stats.local_tail_dequant_tokens == int(g[prefix + "tail_dequant_tokens"])
+        else:
+            kb = cache.bf16_key
+            rows = kb.rows[:, : kb.active_length].cpu().view(torch.int16).numpy().view(np.uint16)
+            np.testing.assert_array_equal(rows, g[prefix + "k_rows"])
         pools = [cache.fp_pool.token_count, cache.int4_pool.token_count, cache.int2_pool.token_count,
                  cache.recent_fp_pool.active_length]
         assert pools == [int(v) for v in g[prefix + "pool_tokens"]]
         fp_v = cache.fp_pool.fp_v[:, : cache.fp_pool.token_count] if cache.fp_pool.token_count else None
         if fp_v is not None:
-            np.testing.assert_array_equal(_bf16_np(fp_v), g[prefix + "fp_v"])
-        if variant == "bf16k":
+            np.testing.assert_array_equal(_bits16(fp_v), g[prefix + "fp_v"].view(np.uint16))
+        if variant in ("bf16k", "int2k"):
             i4 = cache.int4_pool
             if i4.token_count:
                 np.testing.assert_array_equal(i4.packed_v.packed.cpu().numpy().reshape(-1),
@@ -406,14 +451,19 @@ def test_bf16_key_variant_build_and_appends_bit_exact_against_reference_fixtures
                                           g[prefix + "v2_scale"].view(np.uint16))
             np.testing.assert_array_equal(cv.zero_point[:, :a].cpu().numpy(), g[prefix + "v2_zero"])
         r = cache.recent_fp_pool.active_length
-        np.testing.assert_array_equal(_bf16_np(cache.recent_fp_pool.fp_k[:, :r]), g[prefix + "recent_k"])
+        np.testing.assert_array_equal(_bits16(cache.recent_fp_pool.fp_k[:, :r]),
+                                      g[prefix + "recent_k"].view(np.uint16))
         ws = ro.allocate_splitk_workspace(cache, num_query_heads=int(q.shape[1]))
+        if "bfloat16" not in dt:  # the decode kernels read bf16 FP-V / Recent-FP rows only
+            with pytest.raises(ValueError, match="bfloat16"):
+                ro.prepare_splitk_executor(cache, ws)
+            return
         out = ro.prepare_splitk_executor(cache, ws)(q)
         torch.cuda.synchronize()
         _compare(out, mixed_reference(qf, oc), f"{name} {prefix}decode")
 
-    check("build_")
     stats = ro.DynamicCacheStats()
+    check("build_")
     ak = _to_torch(g["append_k"], dt, dev)
     av = _to_torch(g["append_v"], dt, dev)
     seq = int(g["key"].shape[1])

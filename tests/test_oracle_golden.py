@@ -95,10 +95,18 @@ def _build_variant(g):
 
 def _check_variant(c, g, prefix, dt):
     s = c.k_active
-    np.testing.assert_array_equal(c.k_rows[:, :s], as_f32(g[prefix + "k_rows"], dt))
+    if str(g["variant"]) == "int2k":
+        blocks = -(-s // c.superblock)
+        assert c.k_capacity == int(g[prefix + "k_capacity"])
+        np.testing.assert_array_equal(c.k_packed[:, :s], g[prefix + "k_packed"])
+        np.testing.assert_array_equal(c.k_scale[:, :blocks].view(np.uint16), g[prefix + "k_scale"].view(np.uint16))
+        np.testing.assert_array_equal(c.k_zero[:, :blocks].view(np.uint16), g[prefix + "k_offset"].view(np.uint16))
+        assert c.tail_dequant_tokens == int(g[prefix + "tail_dequant_tokens"])
+    else:
+        np.testing.assert_array_equal(c.k_rows[:, :s], as_f32(g[prefix + "k_rows"], dt))
     assert list(c.pool_tokens) + [c.recent_active] == [int(v) for v in g[prefix + "pool_tokens"]]
     np.testing.assert_array_equal(c.fp_v, as_f32(g[prefix + "fp_v"], dt))
-    if str(g["variant"]) == "bf16k":
+    if str(g["variant"]) in ("bf16k", "int2k"):
         np.testing.assert_array_equal(c.v4_packed.reshape(-1), g[prefix + "v4_packed"].reshape(-1))
         np.testing.assert_array_equal(c.v4_scale.view(np.uint32), g[prefix + "v4_scale"].view(np.uint32))
         a = c.v2_active

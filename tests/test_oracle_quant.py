@@ -6,11 +6,13 @@ from oracle.attention import attention_over_pools, merge_state, output_transform
 from oracle.cache import append_token, build_cache, compact_page_layouts
 from oracle.quant import (
     bf16_bits_to_f32,
+    dequantize_int2_key,
     dequantize_int2_value,
     dequantize_int4_key,
     dequantize_int4_value,
     f32_to_bf16_bits,
     normalized_fwht,
+    quantize_int2_key_per_channel,
     quantize_int2_value,
     quantize_int4_key_per_channel,
     quantize_int4_value,
@@ -40,6 +42,43 @@ def test_int4_key_nibble_order_low_bits_are_even_channel():
     x[0, 0, 1] = 15.0  # channel 1 gets range [0, 15] so its zero point is 0 too
     packed, _, _ = quantize_int4_key_per_channel(x, 32)
     assert packed[0, 0, 0] == 0xFF and packed[0, 1, 0] == 0x0F
+
+
+def test_int2_key_constant_channel_keeps_its_value_as_offset():
+    # OScaR form: a constant channel has scale 0 and offset = the value (no 1e-6 clamp, no zero point)
+    x = np.full((1, 32, 4), 2.5, np.float32)
+    x[0, :, 1] = -0.75
+    packed, scale, offset = quantize_int2_key_per_channel(x, 32)
+    assert np.all(scale == 0) and np.all(packed == 0)
+    np.testing.assert_array_equal(offset[0, 0].astype(np.float32), [2.5, -0.75, 2.5, 2.5])
+    np.testing.assert_array_equal(dequantize_int2_key(packed, scale, offset, 0, 32, 32), x)
+
+
+def test_int2_key_range_endpoints_and_crumb_order():
+    # channel c of token t takes the value (t + c) % 4 on a range [0, 3] (0 is not forced into the
+    # range: [1, 4] gives offset 1), so every code is exact and lands in crumb c % 4 of byte c // 4
+    t = np.arange(32)[:, None]
+    c = np.arange(8)[None, :]
+    codes = (t + c) % 4
+    x = codes.astype(np.float32)[None]
+    packed, scale, offset = quantize_int2_key_per_channel(x, 32)
+    assert np.all(scale.astype(np.float32) == 1.0) and np.all(offset == 0)
+    want = (codes[:, 0::4] | codes[:, 1::4] << 2 | codes[:, 2::4] << 4 | codes[:, 3::4] << 6).astype(np.uint8)
+    np.testing.assert_array_equal(packed[0], want)
+    shifted = x + 1.0  # [1, 4]: zero = rne(-1 * 1) -> -1 ... the offset carries the shift exactly
+    p2, s2, o2 = quantize_int2_key_per_channel(shifted, 32)
+    np.testing.assert_array_equal(dequantize_int2_key(p2, s2, o2, 0, 32, 32), shifted)
+
+
+def test_int2_key_round_trip_bound():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((2, 96, 128)) * 3).astype(np.float32)
+    packed, scale, offset = quantize_int2_key_per_channel(x, 32)
+    deq = dequantize_int2_key(packed, scale, offset, 0, 96, 32)
+    s32 = np.repeat(scale.astype(np.float32), 32, axis=1)
+    # half a step plus the fp16 rounding of scale (3 codes) and offset
+    slack = 0.5 * s32 + 3 * np.abs(s32) * 2.0 ** -10 + np.abs(np.repeat(offset.astype(np.float32), 32, axis=1)) * 2.0 ** -10
+    assert np.all(np.abs(deq - x) <= slack + 1e-6)
 
 
 def test_int4_value_absmax_maps_to_plus_minus_seven_and_ties_to_even():
