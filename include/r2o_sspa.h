@@ -99,6 +99,12 @@ typedef struct r2o_decode_params {
     uint16_t* out;                  /* device bf16 [batch, hq, 128]                    */
     const uint16_t* append_k;       /* device bf16 [batch, hkv, 128] or NULL           */
     const uint16_t* append_v;
+    int64_t* step_positions;        /* device int64 [batch, 2] or NULL.  Non-NULL selects device-state
+                                       mode: both kernels read each ring length from
+                                       reqs[b].recent_length (not recent_len[]), the fused append takes
+                                       (global, logical) from here instead of append_global/logical and
+                                       advances them by one, so one captured launch pair replays
+                                       correctly from step to step (until a flush re-plans the items). */
     int64_t batch;
     int64_t hq;
     int64_t hkv;

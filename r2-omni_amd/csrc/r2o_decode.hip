@@ -656,7 +656,9 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     const int per = (int)((it.ntiles + kWaves - 1) / kWaves);
     const int t_begin = wave * per;
     const int t_end = min((int)it.ntiles, t_begin + per);
-    const int recent_len = p.recent_len[b];
+    // device-state mode: the ring length lives in device memory (advanced by the previous step's
+    // combine), so a captured launch stays valid from step to step
+    const int recent_len = p.step_positions ? min(*rq.recent_length, (int)rq.recent_capacity) : p.recent_len[b];
     const bool app = p.do_append != 0;
     const int valid_end = recent_len + (app ? 1 : 0);
     if (t_begin >= t_end || valid_end == 0) return;
@@ -843,19 +845,32 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
     orow[tid] = (uint16_t)r2o_f32_to_bf16(y0);
     orow[tid + 64] = (uint16_t)r2o_f32_to_bf16(y1);
 
-    if (p.do_append && hqi < p.hkv) {  // fused Recent-FP append (triton_fourq_splitk.py:1007-1020)
+    // Fused Recent-FP append (triton_fourq_splitk.py:1007-1020) of every KV head of request b by
+    // the block of query head 0 alone: it is the only reader and writer of the ring length (and, in
+    // device-state mode, of the step positions) during this kernel.
+    if (p.do_append && hqi == 0) {
         const r2o_request_desc& rq = p.reqs[b];
-        const int64_t pos = p.recent_len[b];
-        const int64_t dst = (hqi * rq.recent_capacity + pos) * 128, src = (b * p.hkv + hqi) * 128;
-        rq.recent_k[dst + tid] = p.append_k[src + tid];
-        rq.recent_k[dst + tid + 64] = p.append_k[src + tid + 64];
-        rq.recent_v[dst + tid] = p.append_v[src + tid];
-        rq.recent_v[dst + tid + 64] = p.append_v[src + tid + 64];
-        if (hqi == 0 && tid == 0) {
-            rq.recent_global[pos] = p.append_global[b];
-            rq.recent_logical[pos] = p.append_logical[b];
-            *rq.recent_length = (int32_t)(pos + 1);
-            rq.recent_page_lengths[pos / p.page_size] = pos % p.page_size + 1;
+        const int64_t pos = p.step_positions ? (int64_t)*rq.recent_length : p.recent_len[b];
+        if (pos < rq.recent_capacity) {  // a full ring takes no append (the host flushes first)
+            for (int e = tid; e < p.hkv * 128; e += 64) {  // wave 0 only: the other waves have returned
+                const int64_t hh = e >> 7, d = e & 127;
+                const int64_t dst = (hh * rq.recent_capacity + pos) * 128 + d, src = (b * p.hkv + hh) * 128 + d;
+                rq.recent_k[dst] = p.append_k[src];
+                rq.recent_v[dst] = p.append_v[src];
+            }
+            if (tid == 0) {
+                int64_t gidx = p.append_global[b], lpos = p.append_logical[b];
+                if (p.step_positions) {  // this step's positions, advanced for the next replay
+                    gidx = p.step_positions[2 * b];
+                    lpos = p.step_positions[2 * b + 1];
+                    p.step_positions[2 * b] = gidx + 1;
+                    p.step_positions[2 * b + 1] = lpos + 1;
+                }
+                rq.recent_global[pos] = gidx;
+                rq.recent_logical[pos] = lpos;
+                *rq.recent_length = (int32_t)(pos + 1);
+                rq.recent_page_lengths[pos / p.page_size] = pos % p.page_size + 1;
+            }
         }
     }
 }

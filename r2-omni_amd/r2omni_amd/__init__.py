@@ -4,6 +4,7 @@ split-K attention call surface, backed by the hand-written HIP kernels of libr2o
 Import names mirror the reference modules the Qwen/MiniCPM SSPA manager imports
 (r2omni/sspa/integration/qwen_sspa_attention.py:16-25, 50-59).
 """
+from .batch import BatchedDecoder
 from .cache import (
     BF16KeyArena,
     CompactInt2KeyArena,
@@ -19,6 +20,7 @@ from .cache import (
     build_compact_int2_value_arena,
     build_compact_int4_key_arena,
     build_three_precision_cache,
+    flush_full_recent_pool,
     fused_gather_pack_int4_value,
     precision_cache_active_storage_breakdown,
     precision_cache_storage_breakdown,

@@ -36,6 +36,7 @@ class DecodeParams(ctypes.Structure):
         ("out", c_vp),
         ("append_k", c_vp),
         ("append_v", c_vp),
+        ("step_positions", c_vp),
         ("batch", c_i64),
         ("hq", c_i64),
         ("hkv", c_i64),

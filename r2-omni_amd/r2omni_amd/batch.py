@@ -1,0 +1,136 @@
+"""Batched decode steps with flushes inside the batch and a HIP graph of the per-step launches.
+
+The reference batches decode only for homogeneous requests whose generation fits the Recent-FP
+ring: ``enable_homogeneous_decode_batch`` (r2omni/sspa/integration/qwen_sspa_attention.py:278-317)
+stacks B=1 executors, and a step fuses the ring append into the split-K call while the ring has
+room (:1794-1807); a flush re-prepares that request's executor (:1808-1818).  ``BatchedDecoder``
+runs one (partial + combine) launch pair per step over requests of any lengths, flushes each
+request whose ring is full before the step (``flush_full_recent_pool``, the flush half of
+``append_generated_token``, dynamic_fourq_cache.py:185-253), re-plans the work items only after a
+flush, and can replay the launch pair from a captured HIP graph: the kernels then read the ring
+lengths and advance the (global, logical) positions on the device, so the captured arguments
+stay valid until the next flush.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+
+from .cache import DynamicCacheStats, ThreePrecisionCache, flush_full_recent_pool
+from .splitk import (
+    SplitKExecutor,
+    _build_executor,
+    _num_cus,
+    _per_request,
+    allocate_splitk_workspace,
+    plan_work_items,
+)
+
+
+class BatchedDecoder:
+    """Decode steps over ``caches`` (one per request, same head geometry and K format).
+
+    ``step(query, new_key, new_value, positions)`` returns the workspace's bf16 [B, Hq, 128]
+    attention output of the step (query over history + ring + the new token, whose K/V row is
+    appended to each ring by the same launch).  Inputs are copied into static buffers, so the
+    caller may reuse its tensors; a caller that writes ``query_buffer`` / ``key_buffer`` /
+    ``value_buffer`` directly can call ``step_in_place``.
+    """
+
+    def __init__(self, caches: Sequence[ThreePrecisionCache], *, num_query_heads: int,
+                 output_hadamard: bool = False, reserve_tokens: int = 1024, use_graph: bool = True,
+                 stats: Sequence[DynamicCacheStats] | None = None):
+        self.caches = list(caches)
+        if not self.caches:
+            raise ValueError("a decode batch needs at least one request")
+        first = self.caches[0].recent_fp_pool
+        self.device = first.fp_k.device
+        self.hkv = int(first.fp_k.shape[0])
+        self.hq = int(num_query_heads)
+        self.output_hadamard = bool(output_hadamard)
+        self.use_graph = bool(use_graph)
+        self.stats = list(stats) if stats is not None else [DynamicCacheStats() for _ in self.caches]
+        if len(self.stats) != len(self.caches):
+            raise ValueError("one DynamicCacheStats per request")
+        b = len(self.caches)
+        # workspace sized for every request grown by ``reserve_tokens`` flushed tokens
+        items, _ = plan_work_items(self.caches, self.hkv, _num_cus(self.device), extra_int2=int(reserve_tokens))
+        self.workspace = allocate_splitk_workspace(self.caches[0], num_query_heads=self.hq, batch_size=b,
+                                                   total_blocks=int(items.shape[0]) + 4 * self.hkv * b)
+        self.query_buffer = torch.zeros((b, self.hq, 128), device=self.device, dtype=torch.bfloat16)
+        self.key_buffer = torch.zeros((b, self.hkv, 128), device=self.device, dtype=torch.bfloat16)
+        self.value_buffer = torch.zeros_like(self.key_buffer)
+        self.step_positions = torch.zeros((b, 2), device=self.device, dtype=torch.int64)
+        self._next_positions: list[tuple[int, int]] | None = None  # what the device holds for the next step
+        self.executor: SplitKExecutor | None = None
+        self._graph: torch.cuda.CUDAGraph | None = None
+        self._params = None
+        self.replans = 0
+        self.graph_captures = 0
+        self._replan()
+
+    # ------------------------------------------------------------------ planning and capture
+    def _replan(self) -> None:
+        self._graph = None
+        self.executor = _build_executor(self.caches, self.workspace, output_hadamard=self.output_hadamard,
+                                        block_n=128, batched=len(self.caches) > 1)
+        self._params = self.executor._params(self.query_buffer, self.workspace.output,
+                                             (self.key_buffer, self.value_buffer, [0] * len(self.caches),
+                                              [0] * len(self.caches)),
+                                             step_positions=self.step_positions)
+        self.replans += 1
+
+    def _capture(self) -> None:
+        # one eager launch first (no append, host-provided lengths: it only rewrites the output) so
+        # that nothing is loaded or initialised for the first time while the stream is capturing
+        self.executor._launch(self.executor._params(self.query_buffer, self.workspace.output, None), self.device)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.graph(graph, stream=side):
+            self.executor._launch(self._params, self.device)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        self._graph = graph
+        self.graph_captures += 1
+
+    # ------------------------------------------------------------------------------ steps
+    def step(self, query: torch.Tensor, new_key: torch.Tensor, new_value: torch.Tensor, *,
+             global_token_index, logical_position) -> torch.Tensor:
+        b = len(self.caches)
+        if query.ndim == 4:
+            query = query[:, :, 0]
+        if new_key.ndim == 4:
+            new_key, new_value = new_key[:, :, 0], new_value[:, :, 0]
+        if tuple(query.shape) != (b, self.hq, 128):
+            raise ValueError("query must be [B, Hq, 128] for the prepared batch")
+        if tuple(new_key.shape) != (b, self.hkv, 128) or new_value.shape != new_key.shape:
+            raise ValueError("new K/V must be [B, Hkv, 128] or [B, Hkv, 1, 128]")
+        self.query_buffer.copy_(query)
+        self.key_buffer.copy_(new_key)
+        self.value_buffer.copy_(new_value)
+        return self.step_in_place(global_token_index=global_token_index, logical_position=logical_position)
+
+    def step_in_place(self, *, global_token_index, logical_position) -> torch.Tensor:
+        b = len(self.caches)
+        gl = _per_request(global_token_index, b)
+        lp = _per_request(logical_position, b)
+        flushed = False
+        for cache, stats in zip(self.caches, self.stats):
+            flushed |= flush_full_recent_pool(cache, stats)
+        if flushed:
+            self._replan()
+        want = list(zip(gl, lp))
+        if want != self._next_positions:  # the device positions only advance by one per step
+            self.step_positions.copy_(torch.tensor(want, dtype=torch.int64))
+        if self.use_graph:
+            if self._graph is None:
+                self._capture()
+            self._graph.replay()
+        else:
+            self.executor._launch(self._params, self.device)
+        for cache, stats in zip(self.caches, self.stats):
+            cache.recent_fp_pool.active_length += 1
+            stats.appended_tokens += 1
+        self._next_positions = [(g + 1, l + 1) for g, l in want]
+        return self.workspace.output

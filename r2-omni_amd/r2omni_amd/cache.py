@@ -910,9 +910,55 @@ def _append_int2_page_metadata(pool: PrecisionPool, global_block: torch.Tensor, 
     )
 
 
+def flush_full_recent_pool(cache: ThreePrecisionCache, stats: DynamicCacheStats) -> bool:
+    """If the Recent-FP ring is full, move its oldest ``recent_flush_size`` tokens into the cache
+    (compact INT4/INT2-K + INT2-V arenas, or the matched-FP pool) and shift the ring: the flush half of
+    ``append_generated_token`` (dynamic_fourq_cache.py:185-253).  Returns whether it flushed.  The
+    caller re-prepares its executors afterwards."""
+    pool = cache.recent_fp_pool
+    flush = int(cache.recent_flush_size)
+    if pool.active_length is None or pool.capacity < flush or pool.length_device is None:
+        raise RuntimeError("Recent-FP pool was not preallocated for dynamic generation")
+    if pool.active_length != pool.capacity:
+        return False
+    h, cap = int(pool.fp_k.shape[0]), int(pool.capacity)
+    stream = _lib.stream_of(pool.fp_k.device)
+    key_block = pool.fp_k[:, :flush]
+    value_block = pool.fp_v[:, :flush]
+    # copy the index slices before the ring shift overwrites them
+    global_block = pool.global_index_buffer[:flush].clone()
+    logical_block = pool.logical_position_buffer[:flush].clone()
+    if cache.matched_fp:  # _append_matched_fp_block (dynamic_fourq_cache.py:145-170)
+        _append_int2_page_metadata(cache.fp_pool, global_block, logical_block, cache.page_size)
+        cache.bf16_key.append_block(key_block)
+        n = cache.bf16_key.active_length
+        cache.bf16_key.segment_offsets = (0, n, n)
+        cache.fp_pool.fp_k = cache.bf16_key.view(0, n)
+        cache.fp_pool.fp_v = torch.cat((cache.fp_pool.fp_v, value_block), dim=1)
+        cache.generated_k_offset = n
+    elif cache.bf16_key is not None:  # dynamic_fourq_cache.py:226-230
+        raise RuntimeError("K-BF16/V-FourQ requires an append_fp_only Recent-FP capacity covering the "
+                           "requested generation horizon")
+    else:
+        if cache.compact_key is None or cache.compact_value is None:
+            raise RuntimeError("compact INT2 K cache is missing its compact INT2 V arena")
+        stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
+            if flush == 128 else _flush_size_error(flush)
+        cache.compact_value.append_superblock(value_block, source_tokens=cap)
+        _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
+    _lib.call("r2o_recent_shift", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, flush, pool.active_length,
+              _lib.ptr(pool.global_index_buffer), _lib.ptr(pool.logical_position_buffer),
+              _lib.ptr(pool.length_device), _lib.ptr(pool.page_index.lengths), cache.page_size, stream)
+    pool.active_length -= flush
+    stats.flushed_superblocks += 1
+    stats.flushed_tokens += flush
+    return True
+
+
 def append_generated_token(cache: ThreePrecisionCache, new_key: torch.Tensor, new_value: torch.Tensor, *,
                            global_token_index: int, logical_position: int, stats: DynamicCacheStats) -> bool:
-    """Append one token to the Recent-FP ring; when it is full, flush its oldest chunk first."""
+    """Append one token to the Recent-FP ring; when it is full, flush its oldest chunk first
+    (dynamic_fourq_cache.py:172-267)."""
     pool = cache.recent_fp_pool
     flush = int(cache.recent_flush_size)
     if pool.active_length is None or pool.capacity < flush or pool.length_device is None:
@@ -926,38 +972,7 @@ def append_generated_token(cache: ThreePrecisionCache, new_key: torch.Tensor, ne
         raise ValueError("new K/V dtype must match the Recent-FP ring")
     h, cap = int(pool.fp_k.shape[0]), int(pool.capacity)
     stream = _lib.stream_of(new_key.device)
-    flushed = False
-    if pool.active_length == pool.capacity:
-        key_block = pool.fp_k[:, :flush]
-        value_block = pool.fp_v[:, :flush]
-        # copy the index slices before the ring shift overwrites them
-        global_block = pool.global_index_buffer[:flush].clone()
-        logical_block = pool.logical_position_buffer[:flush].clone()
-        if cache.matched_fp:  # _append_matched_fp_block (dynamic_fourq_cache.py:145-170)
-            _append_int2_page_metadata(cache.fp_pool, global_block, logical_block, cache.page_size)
-            cache.bf16_key.append_block(key_block)
-            n = cache.bf16_key.active_length
-            cache.bf16_key.segment_offsets = (0, n, n)
-            cache.fp_pool.fp_k = cache.bf16_key.view(0, n)
-            cache.fp_pool.fp_v = torch.cat((cache.fp_pool.fp_v, value_block), dim=1)
-            cache.generated_k_offset = n
-        elif cache.bf16_key is not None:  # dynamic_fourq_cache.py:226-230
-            raise RuntimeError("K-BF16/V-FourQ requires an append_fp_only Recent-FP capacity covering the "
-                               "requested generation horizon")
-        else:
-            if cache.compact_key is None or cache.compact_value is None:
-                raise RuntimeError("compact INT2 K cache is missing its compact INT2 V arena")
-            stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
-                if flush == 128 else _flush_size_error(flush)
-            cache.compact_value.append_superblock(value_block, source_tokens=cap)
-            _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
-        _lib.call("r2o_recent_shift", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, flush, pool.active_length,
-                  _lib.ptr(pool.global_index_buffer), _lib.ptr(pool.logical_position_buffer),
-                  _lib.ptr(pool.length_device), _lib.ptr(pool.page_index.lengths), cache.page_size, stream)
-        pool.active_length -= flush
-        stats.flushed_superblocks += 1
-        stats.flushed_tokens += flush
-        flushed = True
+    flushed = flush_full_recent_pool(cache, stats)
     nk = new_key.reshape(h, -1).contiguous()
     nv = new_value.reshape(h, -1).contiguous()
     _lib.call("r2o_recent_append", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, _lib.ptr(nk), _lib.ptr(nv),

@@ -237,8 +237,14 @@ class SplitKExecutor:
     def total(self) -> int:
         return self.n_items
 
-    def _params(self, query: torch.Tensor, out: torch.Tensor, append) -> _lib.DecodeParams:
+    def _params(self, query: torch.Tensor, out: torch.Tensor, append, *,
+                step_positions: torch.Tensor | None = None) -> _lib.DecodeParams:
+        """Launch arguments.  With ``step_positions`` (device int64 [B, 2]) the launch runs in
+        device-state mode: ring lengths and append positions are read (and advanced) on the device,
+        so the same arguments stay valid for every later step (graph capture)."""
         p = _lib.DecodeParams()
+        if step_positions is not None:
+            p.step_positions = step_positions.data_ptr()
         ws = self.workspace
         p.reqs, p.items, p.group_begin = self.reqs.data_ptr(), self.items.data_ptr(), self.group_begin.data_ptr()
         p.n_items = self.n_items
@@ -291,15 +297,19 @@ class SplitKExecutor:
             gl = _per_request(gidx, b)
             lp = _per_request(lpos, b)
             fused = (ak, av, gl, lp)
-        p = self._params(query, out, fused)
-        stream = ctypes.c_void_p(_lib.stream_of(query.device))
-        lib = _lib.load()
-        _lib.check(lib.r2o_decode_partial(ctypes.byref(p), stream), "r2o_decode_partial")
-        _lib.check(lib.r2o_decode_combine(ctypes.byref(p), stream), "r2o_decode_combine")
+        self._launch(self._params(query, out, fused), query.device)
         if fused is not None and self.batched:
             for c in self.caches:
                 c.recent_fp_pool.active_length += 1
         return out
+
+
+    @staticmethod
+    def _launch(p: _lib.DecodeParams, device: torch.device) -> None:
+        stream = ctypes.c_void_p(_lib.stream_of(device))
+        lib = _lib.load()
+        _lib.check(lib.r2o_decode_partial(ctypes.byref(p), stream), "r2o_decode_partial")
+        _lib.check(lib.r2o_decode_combine(ctypes.byref(p), stream), "r2o_decode_combine")
 
 
 def _per_request(value, b: int) -> list[int]:

@@ -232,6 +232,9 @@ def test_fused_append_then_flush_matches_oracle(variant):
     # the ring, lengths and arenas agree with the oracle after the flush
     assert cache.recent_fp_pool.active_length == oc.recent_active
     assert int(cache.recent_fp_pool.length_device.item()) == oc.recent_active
+    rec, r_act = cache.recent_fp_pool, oc.recent_active  # ring rows written by the fused appends
+    np.testing.assert_array_equal(bf16_bits_to_f32(_bf16_np(rec.fp_k[:, :r_act])), oc.recent_k[:, :r_act])
+    np.testing.assert_array_equal(bf16_bits_to_f32(_bf16_np(rec.fp_v[:, :r_act])), oc.recent_v[:, :r_act])
     _check_k_arena(cache, oc)
 
 
