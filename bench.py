@@ -192,6 +192,70 @@ def prefill_bench(cfg, config_id: int, dev) -> dict:
             "note": "one call of build_three_precision_cache on resident bf16 K/V, host launch gaps included"}
 
 
+def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dict:
+    """Per-step wall time of ``layers`` BatchedDecoder layers over the batch of the configuration:
+    eager launches vs one HIP graph per decode step (DecodeStepGraph), flushes inside the run."""
+    import torch
+
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import build_request_cache, make_request
+
+    out = {"metric": "batched decode step (flush inside the batch)", "config": f"cfg{config_id} {cfg.name}",
+           "steps": steps, "layers": layers, "requests": len(cfg.lengths)}
+    for mode in ("eager", "step_graph"):
+        decs, positions = [], None
+        for layer in range(layers):
+            datas = [make_request(cfg, total, seed=1000 * layer + r, device=dev) for r, total in enumerate(cfg.lengths)]
+            caches = [build_request_cache(cfg, d, append_capacity=steps + 512) for d in datas]
+            positions = [int(d.key.shape[1]) + cfg.recent for d in datas]
+            del datas
+            d = ro.BatchedDecoder(caches, num_query_heads=cfg.hq, output_hadamard=True,
+                                  use_graph=False)
+            gen = torch.Generator(device=dev).manual_seed(5 + layer)
+            d.query_buffer.copy_(torch.randn(d.query_buffer.shape, generator=gen, device=dev))
+            d.key_buffer.copy_(torch.randn(d.key_buffer.shape, generator=gen, device=dev))
+            d.value_buffer.copy_(torch.randn(d.value_buffer.shape, generator=gen, device=dev))
+            decs.append(d)
+        graph = ro.DecodeStepGraph(decs) if mode == "step_graph" else None
+
+        def one_step():
+            nonlocal positions
+            if graph is not None:
+                graph.step_in_place(global_token_index=positions, logical_position=positions)
+            else:
+                for d in decs:
+                    d.step_in_place(global_token_index=positions, logical_position=positions)
+            positions = [p + 1 for p in positions]
+
+        for _ in range(4):  # the rings start full: the first step flushes every request of every layer
+            one_step()
+        torch.cuda.synchronize()
+        steady = 100
+        t0 = time.perf_counter()
+        for _ in range(steady):
+            one_step()
+        torch.cuda.synchronize()
+        t_steady = (time.perf_counter() - t0) / steady
+        flushes0 = sum(st.flushed_superblocks for d in decs for st in d.stats)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            one_step()
+        torch.cuda.synchronize()
+        t_all = (time.perf_counter() - t0) / steps
+        out[mode] = {"us_per_step_steady": round(t_steady * 1e6, 2),
+                     "us_per_layer_call_steady": round(t_steady * 1e6 / layers, 2),
+                     "us_per_step_with_flushes": round(t_all * 1e6, 2),
+                     "flush_steps_in_timed_run": (sum(st.flushed_superblocks for d in decs for st in d.stats)
+                                                  - flushes0) // (layers * len(cfg.lengths)),
+                     "graph_captures": graph.graph_captures if graph is not None else 0}
+        del decs, graph
+        torch.cuda.empty_cache()
+    out["note"] = ("host wall clock per decode step (all layers) over back-to-back steps, no per-step sync: "
+                   "launch overhead, flush packing, re-plans and graph re-captures included; 'steady' = 100 "
+                   "steps without a flush")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -208,6 +272,9 @@ def main() -> int:
     ap.add_argument("--prefill", action="store_true",
                     help="only time the prefill-side cache build (quantise + pack on the GPU) of the longest "
                          "request of --config and print one JSON line")
+    ap.add_argument("--decode-steps", type=int, default=0, metavar="N",
+                    help="only time N decode steps of --layers BatchedDecoder layers of --config (eager launches "
+                         "and one HIP graph per step, flushes inside the batch) and print one JSON line")
     ap.add_argument("--summarize-pmc", metavar="DIR",
                     help="only print the mean per-dispatch value of every counter in a rocprofv3 --pmc CSV "
                          "output directory, per decode kernel (and the calibration copy kernel)")
@@ -242,6 +309,9 @@ def main() -> int:
         cfg = dataclasses.replace(cfg, variant=args.variant)
     if args.prefill:
         print(json.dumps(prefill_bench(cfg, args.config, dev)), flush=True)
+        return 0
+    if args.decode_steps:
+        print(json.dumps(decode_steps_bench(cfg, args.config, dev, args.decode_steps, args.layers)), flush=True)
         return 0
     _log(f"building {args.layers} layer caches of {cfg.name} ...")
     layers = []

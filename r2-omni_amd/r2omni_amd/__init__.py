@@ -4,7 +4,7 @@ split-K attention call surface, backed by the hand-written HIP kernels of libr2o
 Import names mirror the reference modules the Qwen/MiniCPM SSPA manager imports
 (r2omni/sspa/integration/qwen_sspa_attention.py:16-25, 50-59).
 """
-from .batch import BatchedDecoder
+from .batch import BatchedDecoder, DecodeStepGraph
 from .cache import (
     BF16KeyArena,
     CompactInt2KeyArena,

@@ -24,7 +24,7 @@ from .splitk import (
     _num_cus,
     _per_request,
     allocate_splitk_workspace,
-    plan_work_items,
+    max_work_items,
 )
 
 
@@ -39,7 +39,7 @@ class BatchedDecoder:
     """
 
     def __init__(self, caches: Sequence[ThreePrecisionCache], *, num_query_heads: int,
-                 output_hadamard: bool = False, reserve_tokens: int = 1024, use_graph: bool = True,
+                 output_hadamard: bool = False, use_graph: bool = True,
                  stats: Sequence[DynamicCacheStats] | None = None):
         self.caches = list(caches)
         if not self.caches:
@@ -54,10 +54,9 @@ class BatchedDecoder:
         if len(self.stats) != len(self.caches):
             raise ValueError("one DynamicCacheStats per request")
         b = len(self.caches)
-        # workspace sized for every request grown by ``reserve_tokens`` flushed tokens
-        items, _ = plan_work_items(self.caches, self.hkv, _num_cus(self.device), extra_int2=int(reserve_tokens))
+        # the planner's item count is bounded whatever the cache sizes: one workspace serves every flush
         self.workspace = allocate_splitk_workspace(self.caches[0], num_query_heads=self.hq, batch_size=b,
-                                                   total_blocks=int(items.shape[0]) + 4 * self.hkv * b)
+                                                   total_blocks=max_work_items(b, self.hkv, _num_cus(self.device)))
         self.query_buffer = torch.zeros((b, self.hq, 128), device=self.device, dtype=torch.bfloat16)
         self.key_buffer = torch.zeros((b, self.hkv, 128), device=self.device, dtype=torch.bfloat16)
         self.value_buffer = torch.zeros_like(self.key_buffer)
@@ -111,7 +110,9 @@ class BatchedDecoder:
         self.value_buffer.copy_(new_value)
         return self.step_in_place(global_token_index=global_token_index, logical_position=logical_position)
 
-    def step_in_place(self, *, global_token_index, logical_position) -> torch.Tensor:
+    def _prepare(self, global_token_index, logical_position) -> bool:
+        """Flush full rings, re-plan after a flush and load the step's positions if they are not the
+        previous step's + 1.  Returns whether the launch arguments changed (a new plan)."""
         b = len(self.caches)
         gl = _per_request(global_token_index, b)
         lp = _per_request(logical_position, b)
@@ -123,14 +124,66 @@ class BatchedDecoder:
         want = list(zip(gl, lp))
         if want != self._next_positions:  # the device positions only advance by one per step
             self.step_positions.copy_(torch.tensor(want, dtype=torch.int64))
+        self._want = want
+        return flushed
+
+    def _advance(self) -> None:
+        """Host bookkeeping after the step's launch pair (the device advanced itself)."""
+        for cache, stats in zip(self.caches, self.stats):
+            cache.recent_fp_pool.active_length += 1
+            stats.appended_tokens += 1
+        self._next_positions = [(g + 1, l + 1) for g, l in self._want]
+
+    def step_in_place(self, *, global_token_index, logical_position) -> torch.Tensor:
+        self._prepare(global_token_index, logical_position)
         if self.use_graph:
             if self._graph is None:
                 self._capture()
             self._graph.replay()
         else:
             self.executor._launch(self._params, self.device)
-        for cache, stats in zip(self.caches, self.stats):
-            cache.recent_fp_pool.active_length += 1
-            stats.appended_tokens += 1
-        self._next_positions = [(g + 1, l + 1) for g, l in want]
+        self._advance()
         return self.workspace.output
+
+
+class DecodeStepGraph:
+    """One HIP graph holding the launch pairs of every layer of a decode step.
+
+    ``layers`` are per-layer ``BatchedDecoder``s over the same requests (their rings fill and flush
+    together, as every layer appends one token per step).  ``step_in_place`` flushes and re-plans the
+    layers that need it, captures the step again only then, and otherwise replays one graph for
+    all layers; each layer's inputs are its decoder's ``query_buffer`` / ``key_buffer`` /
+    ``value_buffer``.
+    """
+
+    def __init__(self, layers: Sequence[BatchedDecoder]):
+        self.layers = list(layers)
+        if not self.layers:
+            raise ValueError("a decode step needs at least one layer")
+        self.device = self.layers[0].device
+        self._graph: torch.cuda.CUDAGraph | None = None
+        self.graph_captures = 0
+
+    def _capture(self) -> None:
+        for d in self.layers:  # eager warm-up without append (rewrites the outputs only)
+            d.executor._launch(d.executor._params(d.query_buffer, d.workspace.output, None), self.device)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.graph(graph, stream=side):
+            for d in self.layers:
+                d.executor._launch(d._params, self.device)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        self._graph = graph
+        self.graph_captures += 1
+
+    def step_in_place(self, *, global_token_index, logical_position) -> list[torch.Tensor]:
+        changed = False
+        for d in self.layers:
+            changed |= d._prepare(global_token_index, logical_position)
+        if changed or self._graph is None:
+            self._capture()
+        self._graph.replay()
+        for d in self.layers:
+            d._advance()
+        return [d.workspace.output for d in self.layers]

@@ -127,16 +127,23 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
     return torch.tensor(items, dtype=torch.int64), torch.tensor(begins, dtype=torch.int32)
 
 
+def max_work_items(num_requests: int, hkv: int, num_cus: int) -> int:
+    """Upper bound of ``plan_work_items`` for any cache sizes: the water-filling stops at
+    _BLOCKS_PER_CU x CUs items unless the runs alone (one per request, KV head and pool segment,
+    at most 4 per head) are more."""
+    return max(_BLOCKS_PER_CU * max(1, num_cus), 4 * int(num_requests) * int(hkv))
+
+
 def required_splitk_blocks(cache: ThreePrecisionCache, *, block_n: int = 128, reserve_tokens: int = 0) -> int:
-    """Partial-state slots a workspace needs for ``cache`` grown by ``reserve_tokens`` low-bit tokens."""
+    """Partial-state slots a workspace needs for ``cache`` at any growth (``reserve_tokens`` is
+    accepted for the reference's signature; the planner's item count is bounded independently of
+    the cache size, so every flush fits)."""
     if block_n < 1:
         raise ValueError("block_n must be positive")
     dev = cache.recent_fp_pool.fp_k.device
     hkv = int(cache.recent_fp_pool.fp_k.shape[0])
     cus = _num_cus(dev) if dev.type == "cuda" else 256
-    now, _ = plan_work_items([cache], hkv, cus)
-    grown, _ = plan_work_items([cache], hkv, cus, extra_int2=max(0, int(reserve_tokens)))
-    return int(max(now.shape[0], grown.shape[0])) + 4 * hkv
+    return max_work_items(1, hkv, cus)
 
 
 def allocate_splitk_workspace(cache: ThreePrecisionCache, *, num_query_heads: int = 16, block_n: int = 128,
@@ -392,10 +399,9 @@ def stack_homogeneous_splitk_executors(executors: Sequence[SplitKExecutor], *,
     hkv = first.num_key_value_heads
     dev = first.workspace.output.device
     if workspace is None:
-        items, _ = plan_work_items(caches, hkv, _num_cus(dev))
         workspace = allocate_splitk_workspace(caches[0], num_query_heads=first.num_query_heads,
                                               block_n=first.block_n, batch_size=len(caches),
-                                              total_blocks=int(items.shape[0]) + 4 * hkv * len(caches))
+                                              total_blocks=max_work_items(len(caches), hkv, _num_cus(dev)))
     if int(workspace.output.shape[0]) != len(caches):
         raise ValueError("batched workspace output must hold one row per request")
     return _build_executor(caches, workspace, output_hadamard=first.output_hadamard, block_n=first.block_n,

@@ -33,7 +33,7 @@ def test_batched_decoder_flushes_inside_the_batch(variant, use_graph):
         datas.append(data)
         caches.append(build_request_cache(cfg, data))
         oracles.append(_oracle_for(data, cfg))
-    dec = ro.BatchedDecoder(caches, num_query_heads=hq, output_hadamard=False, reserve_tokens=256,
+    dec = ro.BatchedDecoder(caches, num_query_heads=hq, output_hadamard=False,
                             use_graph=use_graph)
     gen = torch.Generator(device=dev).manual_seed(9)
     pos = [hist + recent for hist, recent in shapes]
@@ -77,7 +77,7 @@ def test_batched_decoder_positions_that_jump_are_rewritten():
     dev = _cuda()
     cfg = DecodeConfig("b", 16, 2, (0,), (0.2, 0.5, 0.3), recent=64)
     caches = [build_request_cache(cfg, make_request(cfg, 1024 + 64, seed=600 + r, device=dev)) for r in range(2)]
-    dec = ro.BatchedDecoder(caches, num_query_heads=16, reserve_tokens=128, use_graph=True)
+    dec = ro.BatchedDecoder(caches, num_query_heads=16, use_graph=True)
     q = torch.zeros(2, 16, 128, device=dev, dtype=torch.bfloat16)
     k = torch.zeros(2, 2, 128, device=dev, dtype=torch.bfloat16)
     dec.step(q, k, k, global_token_index=[5000, 7000], logical_position=[5000, 7000])
@@ -90,3 +90,50 @@ def test_batched_decoder_positions_that_jump_are_rewritten():
         assert rec.active_length == 67
         assert rec.global_index_buffer[64:67].cpu().tolist() == want_g
         assert rec.logical_position_buffer[64:67].cpu().tolist() == want_l
+
+
+def test_decode_step_graph_over_layers_matches_oracle():
+    """Two layers in one captured step graph, each compared with its own oracle across a flush."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference
+    from oracle.cache import append_token
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    hq, hkv = 16, 2
+    shapes = [(768, 126), (1280, 126)]
+    layers, oracles = [], []
+    for layer in range(2):
+        caches, ocs = [], []
+        for r, (hist, recent) in enumerate(shapes):
+            cfg = DecodeConfig("g", hq, hkv, (0,), (0.2, 0.5, 0.3), recent=recent)
+            data = make_request(cfg, hist + recent, seed=700 + 10 * layer + r, device=dev)
+            caches.append(build_request_cache(cfg, data))
+            ocs.append(_oracle_for(data, cfg))
+        layers.append(ro.BatchedDecoder(caches, num_query_heads=hq, use_graph=False))
+        oracles.append(ocs)
+    step_graph = ro.DecodeStepGraph(layers)
+    gen = torch.Generator(device=dev).manual_seed(11)
+    pos = [hist + recent for hist, recent in shapes]
+    for step in range(5):  # the rings fill at step 2 and flush at step 2 (every layer, every request)
+        qs, ks, vs = [], [], []
+        for d in layers:
+            qs.append(torch.randn(2, hq, 128, generator=gen, device=dev).to(torch.bfloat16))
+            ks.append(torch.randn(2, hkv, 128, generator=gen, device=dev).to(torch.bfloat16))
+            vs.append(torch.randn(2, hkv, 128, generator=gen, device=dev).to(torch.bfloat16))
+            d.query_buffer.copy_(qs[-1])
+            d.key_buffer.copy_(ks[-1])
+            d.value_buffer.copy_(vs[-1])
+        print(f"[step graph] step {step}", flush=True)
+        outs = step_graph.step_in_place(global_token_index=pos, logical_position=pos)
+        torch.cuda.synchronize()
+        for layer in range(2):
+            for r in range(2):
+                kf = bf16_bits_to_f32(_bf16_np(ks[layer][r]))
+                vf = bf16_bits_to_f32(_bf16_np(vs[layer][r]))
+                append_token(oracles[layer][r], kf, vf, global_index=pos[r], logical_position=pos[r])
+                want = mixed_reference(bf16_bits_to_f32(_bf16_np(qs[layer][r : r + 1])), oracles[layer][r])
+                _compare(outs[layer][r : r + 1], want, f"step graph step {step} layer {layer} request {r}")
+        pos = [p + 1 for p in pos]
+    assert step_graph.graph_captures == 2  # the first step and the flush step

@@ -1,0 +1,54 @@
+"""CPU checks of the split-K work-item planner (host logic only, fake cache geometry)."""
+import random
+from types import SimpleNamespace
+
+import pytest
+
+from r2omni_amd import _lib
+from r2omni_amd.splitk import _TILE_COST, TILE, _segments, max_work_items, plan_work_items
+
+
+def _fake_cache(s_fp, s_i4, s_i2, recent_cap=128):
+    n = SimpleNamespace
+    return n(compact_key=n(segment_offsets=(0, s_fp, s_fp + s_i4)), bf16_key=None, matched_fp=False,
+             fp_pool=n(token_count=s_fp), int4_pool=n(token_count=s_i4), compact_value=n(active_length=s_i2),
+             recent_fp_pool=n(capacity=recent_cap))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_items_cover_every_tile_once_and_respect_the_bound(seed):
+    rnd = random.Random(seed)
+    b = rnd.randint(1, 6)
+    hkv = rnd.choice([1, 2, 4, 8])
+    cus = rnd.choice([8, 64, 256])
+    caches = [_fake_cache(rnd.choice([0, rnd.randint(1, 20000)]), rnd.choice([0, rnd.randint(1, 40000)]),
+                          rnd.choice([0, rnd.randint(1, 60000)])) for _ in range(b)]
+    extra = rnd.choice([0, 128, 256])
+    items, begins = plan_work_items(caches, hkv, cus, extra_int2=extra)
+    items = items.tolist()
+    begins = begins.tolist()
+    assert len(items) <= max_work_items(b, hkv, cus)
+    # slots are 0..n-1, contiguous per (request, kv head) group, in group order
+    assert sorted(it[8] for it in items) == list(range(len(items)))
+    assert len(begins) == b * hkv + 1 and begins[0] == 0 and begins[-1] == len(items)
+    by_slot = sorted(items, key=lambda it: it[8])
+    for gi in range(b * hkv):
+        for it in by_slot[begins[gi] : begins[gi + 1]]:
+            assert (it[0], it[1]) == divmod(gi, hkv)
+    # every tile of every segment (and of the Recent-FP ring) is covered exactly once
+    for r, c in enumerate(caches):
+        segs = _segments(c, extra) + [(_lib.KIND_RECENT, 0, c.recent_fp_pool.capacity, 0)]
+        for h in range(hkv):
+            for kind, lo, hi, vd in segs:
+                mine = sorted((it[3], it[4]) for it in items if it[0] == r and it[1] == h and it[2] == kind)
+                t0 = lo // TILE * TILE
+                pos = t0
+                for tile0, ntiles in mine:
+                    assert tile0 == pos and ntiles >= 1
+                    pos += TILE * ntiles
+                assert pos >= hi and pos - TILE < hi
+                assert all(it[5] == lo and it[6] == hi and it[7] == vd
+                           for it in items if it[0] == r and it[1] == h and it[2] == kind)
+    # launch order: largest (cost-weighted) first
+    costs = [it[4] * _TILE_COST[it[2]] for it in items]
+    assert all(a >= b for a, b in zip(costs, costs[1:]))
