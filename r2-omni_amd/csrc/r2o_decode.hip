@@ -771,13 +771,17 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
 }
 
 // One 512-thread block per (request, query head): 16 slices of 32 lanes, lane l owning dims
-// 4l..4l+3.  Slice s merges partials beg+s, beg+s+16, ... four at a time with every load of a
-// round issued before any is used, so a group of up to 64 partials costs one memory round trip;
+// 4l..4l+3.  Slice s merges partials beg+s, beg+s+16, ... kCombineUnroll at a time with every
+// load of a round issued before any is used, so a group of up to 128 partials costs one memory
+// round trip;
 // the 16 slice states then merge through LDS in wave 0, which also runs the output FWHT with
 // lane shuffles.  Every merge is the exact fp32 softmax-state merge
 // (triton_fourq_attention.py:58-69; triton_fourq_splitk.py:977-999).
 constexpr int kCombineSlices = 16;
-constexpr int kCombineUnroll = 4;
+#ifndef R2O_COMBINE_UNROLL
+#define R2O_COMBINE_UNROLL 8
+#endif
+constexpr int kCombineUnroll = R2O_COMBINE_UNROLL;  // partials per slice per round: 16 x 8 = 128 per round trip
 
 __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p) {
     __shared__ float sl_m[kCombineSlices], sl_l[kCombineSlices];
