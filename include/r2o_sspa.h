@@ -74,7 +74,9 @@ typedef struct r2o_request_desc {
  * kv head).  Tiles are aligned to 32 positions of the compact K arena so that every tile lies
  * in one K superblock; positions outside [lo, hi) are masked.  For the Recent-FP ring, arena
  * positions are ring slots.  V row = arena position - v_delta.  Items may be launched in any
- * order (largest first); each writes its partial to `slot`.  All fields are 8 bytes. */
+ * order (largest first); each writes its partial to `slot`.  The item carries the base pointers
+ * of its (request, kv head) rows, so the partial kernel reads nothing else before its first
+ * loads.  All fields are 8 bytes (16 words, 128 bytes). */
 typedef struct r2o_work_item {
     int64_t req;
     int64_t kvh;
@@ -85,6 +87,13 @@ typedef struct r2o_work_item {
     int64_t hi;
     int64_t v_delta;
     int64_t slot;      /* partial-state slot; slots of one (request, kv head) are contiguous     */
+    const void* k_base;          /* K rows of the head: INT4 / INT2 codes, bf16 rows, or ring K   */
+    const uint32_t* k_ops;       /* QK operands of the head's K superblocks (INT4/INT2-K) or NULL */
+    const void* v_base;          /* V rows of the head in this pool, or ring V                    */
+    const void* v_scale;         /* INT4-V f32 / INT2-V fp16 scales of the head, or NULL          */
+    const uint8_t* v_zero;       /* INT2-V zero points of the head, or NULL                       */
+    const int32_t* ring_length;  /* Recent-FP items: the request's device ring length, or NULL    */
+    int64_t reserved;            /* 0                                                             */
 } r2o_work_item;
 
 typedef struct r2o_decode_params {

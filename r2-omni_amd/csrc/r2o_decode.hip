@@ -554,7 +554,7 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
 }
 
 template <int KIND, int KF>
-__device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
+__device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
                             unsigned char* smem, WaveState& st) {
     using Cfg = KernelCfg<KF>;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -568,26 +568,17 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     unsigned char* ring = smem + wave * Cfg::kWaveLds;
 
     DmaCtx c;
-    c.kcode = rq.k_packed + kvh * rq.k_capacity * (KF == kKBf16 ? 256 : (KF == kKInt4 ? 64 : 32));
-    c.kops = rq.k_operands + kvh * rq.k_superblocks * 128;
+    c.kcode = reinterpret_cast<const uint8_t*>(it.k_base);
+    c.kops = it.k_ops;
     c.lo = (int)it.lo;
     c.hi = (int)it.hi;
     c.vdelta = (int)it.v_delta;
     c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
     c.groups = (int)(128 / p.int2_group);
     const int gamma = (8 * l16) / (int)p.int2_group;
-    c.vscale = nullptr;
-    c.vzero = nullptr;
-    if constexpr (KIND == kFP) {
-        c.vrows = reinterpret_cast<const uint8_t*>(rq.fp_v + kvh * rq.fp_stride * 128);
-    } else if constexpr (KIND == kI4) {
-        c.vrows = rq.i4_v + kvh * rq.i4_stride * 64;
-        c.vscale = reinterpret_cast<const uint8_t*>(rq.i4_scale + kvh * rq.i4_stride);
-    } else {
-        c.vrows = rq.i2_v + kvh * rq.i2_stride * 32;
-        c.vscale = reinterpret_cast<const uint8_t*>(rq.i2_scale + kvh * rq.i2_stride * c.groups);
-        c.vzero = rq.i2_zero + kvh * rq.i2_stride * c.groups;
-    }
+    c.vrows = reinterpret_cast<const uint8_t*>(it.v_base);
+    c.vscale = reinterpret_cast<const uint8_t*>(it.v_scale);
+    c.vzero = it.v_zero;
     {  // lane -> (token, chunk) sources of the K and INT V DMAs (inverse of the slot functions)
         const int s0 = lane, s1 = 64 + lane;
         const int t0 = s0 >> 2, t1 = s1 >> 2;
@@ -647,7 +638,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
 // Recent-FP ring tiles (bf16 K and V, plus the fused-append token).  Every load of a tile is
 // issued before any is used (rows past the valid end read the last valid row, whose
 // probability is 0); a tile with no valid token is skipped.
-__device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, const r2o_request_desc& rq,
+__device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
                            WaveState& st) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
@@ -658,7 +649,7 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     const int t_end = min((int)it.ntiles, t_begin + per);
     // device-state mode: the ring length lives in device memory (advanced by the previous step's
     // combine), so a captured launch stays valid from step to step
-    const int recent_len = p.step_positions ? min(*rq.recent_length, (int)rq.recent_capacity) : p.recent_len[b];
+    const int recent_len = p.step_positions ? min(*it.ring_length, (int)it.hi) : p.recent_len[b];
     const bool app = p.do_append != 0;
     const int valid_end = recent_len + (app ? 1 : 0);
     if (t_begin >= t_end || valid_end == 0) return;
@@ -666,8 +657,8 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it, 
     const bool head_ok = l16 < gqa;
     uint32_t qp[4][4];
     load_query<kKBf16>(p, b, kvh, gqa, l16, g, qscale, qp);
-    const uint16_t* ring_k = rq.recent_k + kvh * rq.recent_capacity * 128;
-    const uint16_t* ring_v = rq.recent_v + kvh * rq.recent_capacity * 128;
+    const uint16_t* ring_k = reinterpret_cast<const uint16_t*>(it.k_base);
+    const uint16_t* ring_v = reinterpret_cast<const uint16_t*>(it.v_base);
     const uint16_t* new_k = app ? p.append_k + (b * p.hkv + kvh) * 128 : ring_k;
     const uint16_t* new_v = app ? p.append_v + (b * p.hkv + kvh) * 128 : ring_v;
     for (int t = t_begin; t < t_end; ++t) {
@@ -710,7 +701,6 @@ template <int KF>
 __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
     __shared__ __align__(16) unsigned char smem[KernelCfg<KF>::kSmem];
     const r2o_work_item it = p.items[blockIdx.x];
-    const r2o_request_desc rq = p.reqs[it.req];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = (int)(p.hq / p.hkv);
@@ -722,10 +712,10 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP, KF>(p, it, rq, smem, st); break;
-        case kI4: run_segment<kI4, KF>(p, it, rq, smem, st); break;
-        case kI2: run_segment<kI2, KF>(p, it, rq, smem, st); break;
-        default: run_recent(p, it, rq, st); break;
+        case kFP: run_segment<kFP, KF>(p, it, smem, st); break;
+        case kI4: run_segment<kI4, KF>(p, it, smem, st); break;
+        case kI2: run_segment<kI2, KF>(p, it, smem, st); break;
+        default: run_recent(p, it, st); break;
     }
 
     // ---- per-wave epilogue: reduce l (and u) over the 4 lane groups of each head

@@ -184,7 +184,7 @@ def _k_format(cache: ThreePrecisionCache) -> int:
     return _lib.K_INT2 if cache.compact_key.bit_width == 2 else _lib.K_INT4
 
 
-def _request_desc(cache: ThreePrecisionCache) -> list[int]:
+def _request_words(cache: ThreePrecisionCache) -> dict[str, int]:
     ck, cv = cache.compact_key, cache.compact_value
     fp, i4, rec = cache.fp_pool, cache.int4_pool, cache.recent_fp_pool
     if rec.fp_k.dtype != torch.bfloat16:
@@ -213,7 +213,33 @@ def _request_desc(cache: ThreePrecisionCache) -> list[int]:
         "recent_logical": rec.logical_position_buffer.data_ptr(),
         "recent_page_lengths": rec.page_index.lengths.data_ptr(),
     }
-    return [int(words[f]) for f in _lib.REQUEST_FIELDS]
+    return {k: int(v) for k, v in words.items()}
+
+
+def _request_desc(cache: ThreePrecisionCache) -> list[int]:
+    words = _request_words(cache)
+    return [words[f] for f in _lib.REQUEST_FIELDS]
+
+
+_K_ROW_BYTES = {_lib.K_INT4: 64, _lib.K_INT2: 32, _lib.K_BF16: 256}
+
+
+def _item_pointers(words: dict[str, int], k_format: int, kind: int, h: int, groups: int) -> list[int]:
+    """Base pointers (k_base, k_ops, v_base, v_scale, v_zero, ring_length) of KV head ``h`` for
+    an item of ``kind``: the pointer arithmetic the kernel would otherwise do per item."""
+    if kind == _lib.KIND_RECENT:
+        row = h * words["recent_capacity"] * 256
+        return [words["recent_k"] + row, 0, words["recent_v"] + row, 0, 0, words["recent_length"]]
+    k_base = words["k_packed"] + h * words["k_capacity"] * _K_ROW_BYTES[k_format]
+    k_ops = words["k_operands"] + h * words["k_superblocks"] * 128 * 4 if words["k_operands"] else 0
+    if kind == _lib.KIND_FP:
+        return [k_base, k_ops, words["fp_v"] + h * words["fp_stride"] * 256, 0, 0, 0]
+    if kind == _lib.KIND_INT4:
+        st = words["i4_stride"]
+        return [k_base, k_ops, words["i4_v"] + h * st * 64, words["i4_scale"] + h * st * 4, 0, 0]
+    st = words["i2_stride"]
+    return [k_base, k_ops, words["i2_v"] + h * st * 32, words["i2_scale"] + h * st * groups * 2,
+            words["i2_zero"] + h * st * groups, 0]
 
 
 @dataclass
@@ -221,7 +247,7 @@ class SplitKExecutor:
     caches: list
     workspace: SplitKWorkspace
     reqs: torch.Tensor          # device int64 [B, 22]
-    items: torch.Tensor         # device int64 [n, 9]
+    items: torch.Tensor         # device int64 [n, 16] (r2o_work_item rows)
     group_begin: torch.Tensor   # device int32 [B*Hkv + 1]
     n_items: int
     num_query_heads: int
@@ -362,7 +388,11 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
     n = int(host_items.shape[0])
     if n > workspace.total_blocks:
         raise ValueError("workspace block capacity is smaller than the active cache")
-    reqs = torch.tensor([_request_desc(c) for c in caches], dtype=torch.int64).to(dev)
+    words = [_request_words(c) for c in caches]
+    reqs = torch.tensor([[w[f] for f in _lib.REQUEST_FIELDS] for w in words], dtype=torch.int64).to(dev)
+    groups = 128 // group
+    rows = [it + _item_pointers(words[it[0]], kf, it[2], it[1], groups) + [0] for it in host_items.tolist()]
+    host_items = torch.tensor(rows, dtype=torch.int64)
     return SplitKExecutor(
         caches=list(caches), workspace=workspace, reqs=reqs, items=host_items.to(dev), group_begin=begins.to(dev),
         n_items=n, num_query_heads=hq, num_key_value_heads=hkv, head_dim=head_dim, superblock=sb, int2_group=group,
