@@ -751,11 +751,13 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
                 A += base[w * kMergeFloats + 32 + h * 128 + d] * sc;
             }
         }
+        // streaming stores: the partials are read once, by the combine launch, so they are not left
+        // dirty in this XCD's L2 for the end-of-kernel writeback
         const int64_t slot = it.slot * 16 + h;
-        p.partial_out[slot * 128 + d] = A;
+        __builtin_nontemporal_store(A, p.partial_out + slot * 128 + d);
         if (d == 0) {
-            p.partial_max[slot] = M;
-            p.partial_sum[slot] = L;
+            __builtin_nontemporal_store(M, p.partial_max + slot);
+            __builtin_nontemporal_store(L, p.partial_sum + slot);
         }
     }
 }
