@@ -3,22 +3,28 @@
 // Partial pass: one 256-thread block (4 waves) per work item, i.e. a run of 32-token tiles of
 // one pool segment of one (request, kv head).  Each wave walks its share of the tiles with an
 // online softmax in the log2 domain and keeps a 16 x 128 fp32 accumulator (query heads of the
-// KV group padded to 16 MFMA rows).  Per tile:
-//   QK  S^T[tok, h] = sum_c K[tok, c] * Q'[h, c]  as f16 MFMA on the raw INT4 codes:
-//       the A operand is (1024 + code) built with one and-or per two nibbles, the B operand is
-//       Q' = q * s (per-channel scale of the tile's K superblock, scaled by D^-1/2 * log2 e),
-//       and -sum_c Q'[h, c] * (1024 + z_c) is added by one more MFMA per channel block, so the
-//       MFMA chain returns q . (code - z) * s exactly as the dequantised dot.  The per-superblock
-//       (s, -(1024 + z)) operand pairs are written at pack time and staged in LDS per item.
-//       Recent-FP tiles use a bf16 MFMA on the bf16 K rows.
-//   PV  O[h, d] += sum_tok P[h, tok] V[tok, d]: every lane loads, straight into registers, the
-//       8 adjacent dims 8*l16.. of its 8 tokens, which is the MFMA B operand of 8 consecutive
-//       tokens after a byte permute (output dim 8*l16 + q of MFMA q).  BF16 V: bf16 MFMA.
-//       INT4 V: the per-token scale is folded into P (P' = p * s) and the signed codes enter
-//       exactly as f16 (1032 + c, built with one xor and one and-or), the 1032 bias being
-//       removed by one more MFMA.  INT2 V: (c - z) * s is formed in f16 per element.
-//   Pool tiles are prefetched into registers one (BF16) or two (INT4/INT2) tiles ahead.
-// The 4 waves' states are merged in LDS and one (max, sum, acc[GQA][128]) partial is written.
+// KV group padded to 16 MFMA rows).  The history keys come in one of three formats
+// (r2o_decode_params.k_format), each a template instance of the kernel.  Per tile:
+//   QK  S^T[tok, h] = sum_c K[tok, c] * Q'[h, c]  as f16 MFMA on the raw codes.
+//       INT4-K: the A operand is (1024 + code) built in place from the nibbles, the B operand
+//       is Q' = q * s (per-channel scale of the tile's K superblock, times D^-1/2 * log2 e), and
+//       -sum_c Q'[h, c] * (1024 + z_c) is added by one more MFMA per channel block, so the chain
+//       returns q . (code - z) * s exactly as the dequantised dot.
+//       INT2-K: the crumb at bit position 2u of a 16-bit lane enters as 1024 + 4^u * code, the
+//       B operand carries s / 4^u, and two correction MFMAs add sum_c q * offset_c and remove
+//       the 1024 offsets, so the chain returns q . (code * s + offset).
+//       The per-superblock operand pairs of both are written at pack time and arrive with the
+//       tile.  BF16-K history and Recent-FP tiles use a bf16 MFMA on the bf16 K rows.
+//   PV  O[h, d] += sum_tok P[h, tok] V[tok, d]: each lane holds the 8 adjacent dims 8*l16.. of
+//       its 8 tokens, the MFMA B operand of 8 consecutive tokens after a byte permute (output
+//       dim 8*l16 + q of MFMA q).  BF16 V: bf16 MFMA.  INT4 V: the per-token scale is folded
+//       into P (P' = p * s) and the signed codes enter exactly as f16 (1032 + c, low nibbles,
+//       and 1152 + 16 c in place for the high nibbles), the offsets being removed after the
+//       last tile.  INT2 V: (c - z) * s is formed in f16 per element.
+//   Pool tiles arrive by global->LDS DMA into a one-stage-per-wave ring (no VGPRs held while in
+//   flight); Recent-FP tiles are loaded straight into registers, all loads of a tile first.
+// The 4 waves' states are merged in LDS and one (max, sum, acc[GQA][128]) fp32 partial is
+// written with streaming stores (read once, by the combine).
 //
 // Combine pass: one block per (request, query head) merges the partials of its (request,
 // kv head) group, divides, rounds to bf16, optionally applies the 128-point FWHT and performs
@@ -176,12 +182,6 @@ __device__ __forceinline__ VConst make_vconst() {
 }
 
 // ------------------------------------------------------------------ pool segment tiles
-// Per tile, every lane loads straight into registers exactly what its MFMA operands need:
-// the INT4-K codes of token a0 + 16 mg + l16 (channels 32g ..), and for each of its 8 tokens
-// tile_token(g, k) the 8 V dims 8*l16 .. 8*l16+7 (bf16: 16 B, INT4: 4 B, INT2: 2 B) plus the
-// token's V metadata.  The K superblock operands of the wave's whole tile range are copied into
-// LDS once per work item.  INT4/INT2 tiles are prefetched two tiles ahead (three rotating
-// register sets), bf16 tiles one tile ahead.
 // Registers of one tile, read from its LDS stage: INT4-K codes of tokens 16 mg + l16 (channels
 // 32g ..), the tile's K superblock operands of lane group g, and for each of the lane's 8 tokens
 // tile_token(g, k) the 8 V dims 8*l16 .. 8*l16+7 (bf16: 16 B, INT4: 4 B, INT2: 2 B) plus the
