@@ -728,34 +728,41 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
         mrg[l16] = st.m;
         mrg[16 + l16] = l_h;
     }
+    // rows 4g + i of the accumulator (the padded heads past the KV group are not needed): the
+    // lane's 8 dims 8 l16 .. 8 l16 + 7 of a row are two 16-byte LDS writes
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) mrg[32 + (4 * g + i) * 128 + 8 * l16 + q] = st.acc[q][i];
+    for (int i = 0; i < 4; ++i) {
+        if (4 * g + i < gqa) {
+            r2o_f4* row = reinterpret_cast<r2o_f4*>(mrg + 32 + (4 * g + i) * 128 + 8 * l16);
+            row[0] = r2o_f4{st.acc[0][i], st.acc[1][i], st.acc[2][i], st.acc[3][i]};
+            row[1] = r2o_f4{st.acc[4][i], st.acc[5][i], st.acc[6][i], st.acc[7][i]};
+        }
+    }
     __syncthreads();
 
-    // ---- merge the 4 wave states of this block and write the partial
+    // ---- merge the 4 wave states of this block and write the partial: 4 dims per thread
     const float* base = reinterpret_cast<const float*>(smem);
-    for (int e = threadIdx.x; e < gqa * 128; e += blockDim.x) {
-        const int h = e >> 7, d = e & 127;
+    for (int e = threadIdx.x; e < gqa * 32; e += blockDim.x) {
+        const int h = e >> 5, d4 = (e & 31) * 4;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) M = fmaxf(M, base[w * kMergeFloats + h]);
-        float L = 0.f, A = 0.f;
+        float L = 0.f;
+        r2o_f4 A = {0.f, 0.f, 0.f, 0.f};
         if (M != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
                 const float mw = base[w * kMergeFloats + h];
                 const float sc = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
                 L += base[w * kMergeFloats + 16 + h] * sc;
-                A += base[w * kMergeFloats + 32 + h * 128 + d] * sc;
+                A += *reinterpret_cast<const r2o_f4*>(base + w * kMergeFloats + 32 + h * 128 + d4) * sc;
             }
         }
         // streaming stores: the partials are read once, by the combine launch, so they are not left
         // dirty in this XCD's L2 for the end-of-kernel writeback
         const int64_t slot = it.slot * 16 + h;
-        __builtin_nontemporal_store(A, p.partial_out + slot * 128 + d);
-        if (d == 0) {
+        __builtin_nontemporal_store(A, reinterpret_cast<r2o_f4*>(p.partial_out + slot * 128 + d4));
+        if (d4 == 0) {
             __builtin_nontemporal_store(M, p.partial_max + slot);
             __builtin_nontemporal_store(L, p.partial_sum + slot);
         }
