@@ -221,6 +221,19 @@ int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t
                  int64_t table_dtype, const int64_t* cos_strides, const int64_t* sin_strides,
                  int64_t section0, int64_t section1, int64_t apply_hadamard, void* stream);
 
+/* Decode-step Q/K transform of Qwen3-style attention (MiniCPM-o's LLM): per-head RMSNorm with
+ * weights q_weight / k_weight [128] and epsilon eps (mean of squares in fp32, x * 1/sqrt(v + eps)
+ * rounded to dtype, times the weight rounded to dtype), then rotate-half RoPE with cos/sin
+ * [batch, tokens, 128] of the same dtype (element strides (batch, token, dim); each product and the
+ * sum rounded to dtype, as torch evaluates them), then optionally the orthonormal FWHT-128.
+ * q/k/q_out/k_out as for r2o_qk_mrope; dtype 0 = bf16, 1 = fp16 for every tensor.  Replaces the
+ * q_norm / k_norm / apply_rotary_pos_emb / triton_fwht_128 sequence of the Qwen3 branch
+ * (qwen_sspa_attention.py:1228-1235). */
+int r2o_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out, int64_t dtype,
+                     int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, const uint16_t* q_weight,
+                     const uint16_t* k_weight, float eps, const uint16_t* cos, const uint16_t* sin,
+                     const int64_t* cos_strides, const int64_t* sin_strides, int64_t apply_hadamard, void* stream);
+
 /* Library identification: returns the gfx target the code objects were built for. */
 const char* r2o_build_target(void);
 

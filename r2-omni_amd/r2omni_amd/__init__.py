@@ -35,7 +35,7 @@ from .policy import (
     plan_from_pages,
     project_token_bits_to_pages,
 )
-from .rope import qwen_qk_mrope
+from .rope import qwen3_qk_norm_rope, qwen_qk_mrope
 from .splitk import (
     SplitKExecutor,
     SplitKWorkspace,

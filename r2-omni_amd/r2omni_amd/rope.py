@@ -1,7 +1,12 @@
-"""Decode-step query/key rotation: ``qwen_qk_mrope`` on the gfx950 HIP kernel ``r2o_qk_mrope``.
+"""Decode-step query/key transforms on the gfx950 HIP kernels.
 
-Drop-in for ``r2omni.sspa.kernels.triton_qwen_mrope.qwen_qk_mrope`` (triton_qwen_mrope.py:214-322):
-same arguments, same validation messages, one launch for every (request, head, token) row.
+* ``qwen_qk_mrope`` (``r2o_qk_mrope``): drop-in for ``r2omni.sspa.kernels.triton_qwen_mrope.qwen_qk_mrope``
+  (triton_qwen_mrope.py:214-322): same arguments, same validation messages, one launch for every
+  (request, head, token) row.
+* ``qwen3_qk_norm_rope`` (``r2o_qk_norm_rope``): the Qwen3 branch of the same step
+  (qwen_sspa_attention.py:1228-1235: ``q_norm`` / ``k_norm``, ``apply_rotary_pos_emb``, then
+  ``triton_fwht_128`` of Q and K when keys are Hadamard-rotated) in one launch, with the rounding of
+  every torch op of that sequence.
 """
 from __future__ import annotations
 
@@ -65,4 +70,55 @@ def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin
               batch_size, int(query.shape[1]), int(key.shape[1]), tokens, _lib.ptr(cos), _lib.ptr(sin),
               _TABLE_CODES[cos.dtype], cos_strides, sin_strides, sections[0], sections[1], int(bool(apply_hadamard)),
               ctypes.c_void_p(_lib.stream_of(query.device)))
+    return query_out, key_out
+
+
+def qwen3_qk_norm_rope(query: torch.Tensor, key: torch.Tensor, q_norm_weight: torch.Tensor,
+                       k_norm_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, eps: float = 1e-6,
+                       apply_hadamard: bool = False,
+                       output: tuple[torch.Tensor, torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``q_norm(q)``, ``k_norm(k)`` (Qwen3 per-head RMSNorm), ``apply_rotary_pos_emb`` with
+    ``cos``/``sin`` [B or 1, T, 128] and, with ``apply_hadamard``, the normalised FWHT-128 of both,
+    in one launch.  Q [B, Hq, T, 128] and K [B, Hkv, T, 128] share one dtype (bf16 or fp16) with the
+    norm weights and the rotary tables, as in the model."""
+    if query.ndim != 4 or key.ndim != 4:
+        raise ValueError("Qwen3 fused norm+RoPE requires rank-4 Q/K")
+    if query.shape[0] != key.shape[0] or query.shape[2] != key.shape[2] or query.shape[2] <= 0:
+        raise ValueError("Qwen3 fused norm+RoPE requires equal Q/K batch sizes and positive token counts")
+    if query.shape[-1] != 128 or key.shape[-1] != 128:
+        raise ValueError("Qwen3 fused norm+RoPE currently requires head_dim=128")
+    if query.device != key.device or query.dtype != key.dtype:
+        raise ValueError("Q/K device and dtype must match")
+    batch_size, tokens = int(query.shape[0]), int(query.shape[2])
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w.shape != (128,) or w.dtype != query.dtype or w.device != query.device:
+            raise ValueError(f"{name} must be a [128] tensor of the Q/K dtype on the Q/K device")
+    if cos.shape != sin.shape or cos.ndim != 3 or cos.shape[-2:] != (tokens, 128) \
+            or int(cos.shape[0]) not in (1, batch_size):
+        raise ValueError("Qwen3 fused norm+RoPE requires cos/sin [B,S,D] matching Q/K tokens")
+    if cos.dtype != query.dtype or sin.dtype != query.dtype or cos.device != query.device \
+            or sin.device != query.device:
+        raise ValueError("Qwen3 fused norm+RoPE cos/sin must share the Q/K dtype and device")
+    if not eps >= 0.0:
+        raise ValueError("RMSNorm epsilon must be non-negative")
+    _lib.require_device(query, "fused Qwen3 norm+RoPE input")
+    dtype = _lib.dtype_code(query.dtype)
+    query, key = query.contiguous(), key.contiguous()
+    q_norm_weight, k_norm_weight = q_norm_weight.contiguous(), k_norm_weight.contiguous()
+    cos, sin = cos.expand(batch_size, tokens, 128), sin.expand(batch_size, tokens, 128)
+    if output is None:
+        query_out, key_out = torch.empty_like(query), torch.empty_like(key)
+    else:
+        query_out, key_out = output
+        if query_out.shape != query.shape or key_out.shape != key.shape or query_out.dtype != query.dtype \
+                or key_out.dtype != key.dtype or query_out.device != query.device or key_out.device != key.device:
+            raise ValueError("fused Qwen3 norm+RoPE outputs must match Q/K shape, dtype and device")
+        if not query_out.is_contiguous() or not key_out.is_contiguous():
+            raise ValueError("fused Qwen3 norm+RoPE outputs must be contiguous")
+    cos_strides = (ctypes.c_int64 * 3)(*[int(v) for v in cos.stride()])
+    sin_strides = (ctypes.c_int64 * 3)(*[int(v) for v in sin.stride()])
+    _lib.call("r2o_qk_norm_rope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(query_out), _lib.ptr(key_out), dtype,
+              batch_size, int(query.shape[1]), int(key.shape[1]), tokens, _lib.ptr(q_norm_weight),
+              _lib.ptr(k_norm_weight), float(eps), _lib.ptr(cos), _lib.ptr(sin), cos_strides, sin_strides,
+              int(bool(apply_hadamard)), ctypes.c_void_p(_lib.stream_of(query.device)))
     return query_out, key_out

@@ -1,5 +1,6 @@
 """Pin the mRoPE oracle with closed forms (no reference fixture exists for the Triton kernel)."""
 import numpy as np
+import pytest
 import torch
 
 from oracle.quant import normalized_fwht
@@ -61,3 +62,68 @@ def test_sections_pick_axes_like_the_split_concatenate_formulation():
     want = (tx * c + rot * s).numpy()
     got = qwen_mrope(x, cos, sin, SECTIONS, hadamard=False, dtype="float32")
     np.testing.assert_allclose(got, want, atol=1e-6)
+
+
+# ----------------------------------------------------------- Qwen3 RMSNorm + RoPE branch
+def _ulp_steps(a: np.ndarray, b: np.ndarray, dtype: str) -> np.ndarray:
+    """Distance in representable steps of ``dtype`` between two arrays of ``dtype`` values."""
+    if dtype == "bfloat16":
+        from oracle.quant import f32_to_bf16_bits
+
+        ia, ib = f32_to_bf16_bits(a).astype(np.int64), f32_to_bf16_bits(b).astype(np.int64)
+    else:
+        ia = a.astype(np.float16).view(np.uint16).astype(np.int64)
+        ib = b.astype(np.float16).view(np.uint16).astype(np.int64)
+    mono = lambda i: np.where(i & 0x8000, -(i & 0x7FFF), i)  # noqa: E731  sign-magnitude -> ordered
+    return np.abs(mono(ia) - mono(ib))
+
+
+def _rope_tables_1d(b, t, gen, dt):
+    inv = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
+    pos = torch.randint(0, 40000, (b, t), generator=gen).double()
+    ang = pos[..., None] * inv
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().to(dt), ang.sin().to(dt)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hadamard", [False, True])
+def test_qwen3_norm_rope_matches_the_transformers_ops_on_cpu(dt, hadamard):
+    """The oracle against transformers' own Qwen3RMSNorm and apply_rotary_pos_emb (and the
+    normalised FWHT) evaluated by torch on the CPU in the model dtype."""
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, apply_rotary_pos_emb
+    from oracle.rope import qwen3_norm_rope
+
+    gen = torch.Generator().manual_seed(5)
+    q = (torch.randn(2, 4, 3, 128, generator=gen) * 3).to(dt)
+    k = (torch.randn(2, 2, 3, 128, generator=gen) * 3).to(dt)
+    qn, kn = Qwen3RMSNorm(128, eps=1e-6).to(dt), Qwen3RMSNorm(128, eps=1e-6).to(dt)
+    with torch.no_grad():
+        qn.weight.copy_((torch.rand(128, generator=gen) * 2).to(dt))
+        kn.weight.copy_((torch.rand(128, generator=gen) * 2).to(dt))
+        cos, sin = _rope_tables_1d(2, 3, gen, dt)
+        want_q, want_k = apply_rotary_pos_emb(qn(q.transpose(1, 2)).transpose(1, 2),
+                                              kn(k.transpose(1, 2)).transpose(1, 2), cos, sin)
+        if hadamard:  # the CPU branch of the reference: normalized_fwht(q).to(q.dtype)
+            want_q = torch.from_numpy(normalized_fwht(want_q.float().numpy())).to(dt)
+            want_k = torch.from_numpy(normalized_fwht(want_k.float().numpy())).to(dt)
+    name = "bfloat16" if dt == torch.bfloat16 else "float16"
+    f = lambda t: t.float().numpy()  # noqa: E731
+    for x, w, want in ((q, qn.weight, want_q), (k, kn.weight, want_k)):
+        got = qwen3_norm_rope(f(x), f(w.detach()), f(cos), f(sin), eps=1e-6, hadamard=hadamard, dtype=name)
+        steps = _ulp_steps(got, f(want), name)
+        # torch sums the squares in another order: a last-bit change of the variance may move the
+        # normalised value's rounding by one step, rarely (two after the RoPE sum, in fp16)
+        assert steps.max() <= 2 and (steps == 0).mean() >= 0.995, (steps.max(), (steps == 0).mean())
+
+
+def test_qwen3_norm_rope_unit_weight_zero_angle_is_a_plain_rms_norm():
+    from oracle.rope import qwen3_norm_rope
+
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((1, 2, 2, 128)).astype(np.float32)
+    ones, zeros = np.ones((1, 2, 128), np.float32), np.zeros((1, 2, 128), np.float32)
+    got = qwen3_norm_rope(x, np.ones(128, np.float32), ones, zeros, eps=0.0, hadamard=False, dtype="float32")
+    want = x / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True))
+    np.testing.assert_allclose(got, want, rtol=1e-6)
+    np.testing.assert_allclose((got.astype(np.float64) ** 2).mean(-1), 1.0, rtol=1e-6)
