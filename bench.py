@@ -256,6 +256,201 @@ def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dic
     return out
 
 
+def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int) -> dict:
+    """Configuration 4: greedy decode of a random-init Qwen2.5-Omni-7B language model on this path.
+
+    Model: 28 layers (``n_layers``), hidden 3584, 28 query / 4 KV heads of 128, SwiGLU 18944, vocab
+    152064, RMSNorm 1e-6, mRoPE sections (16, 24, 24) with theta 1e6, bf16 weights N(0, 0.02).  Each of
+    ``batch`` sequences of ``context`` seeded random token ids is prefilled through the whole model
+    (flash attention); per layer its Hadamard-rotated K/V (keys after RoPE) go into an SSPA cache:
+    INT4 keys, BF16/INT4/INT2 value pages drawn per 64-token page at 15/45/40 %, the newest 128 tokens
+    in the Recent-FP ring.  Then ``steps`` greedy steps: fused mRoPE + FWHT of Q/K, FWHT of V, the
+    packed-KV attention with fused append (BatchedDecoder; the first step flushes every ring inside
+    the batch), projections / MLP / lm_head as torch GEMMs.  The decode runs twice from the same
+    caches: eager launches, then the steps after the first replayed from one HIP graph per step (the
+    greedy argmax stays outside the graph); the graph run counts only if its tokens equal the eager
+    run's.
+    """
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, RequestData, TIER_CLASS, build_request_cache
+
+    hid, nh, nkv, hd, inter, vocab, eps = 3584, 28, 4, 128, 18944, 152064, 1e-6
+    sections, recent = (16, 24, 24), 128
+    bf = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(0)
+    cpu = torch.Generator().manual_seed(0)
+
+    def weight(*shape):
+        return (torch.randn(shape, generator=gen, device=dev) * 0.02).to(bf)
+
+    t0 = time.perf_counter()
+    layers = []
+    for _ in range(n_layers):
+        layers.append({"wq": weight(hid, hid), "bq": weight(hid), "wk": weight(nkv * hd, hid), "bk": weight(nkv * hd),
+                       "wv": weight(nkv * hd, hid), "bv": weight(nkv * hd), "wo": weight(hid, hid),
+                       "wg": weight(inter, hid), "wu": weight(inter, hid), "wd": weight(hid, inter),
+                       "n1": torch.ones(hid, device=dev, dtype=bf), "n2": torch.ones(hid, device=dev, dtype=bf)})
+    embed, lm_head, n_final = weight(vocab, hid), weight(vocab, hid), torch.ones(hid, device=dev, dtype=bf)
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
+
+    def rms(x, w):
+        xf = x.float()
+        return w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(bf)
+
+    def tables(pos):  # text positions: the three mRoPE axes are equal; [3, B, T, 128] in bf16
+        ang = pos.float()[..., None] * inv_freq
+        ang = torch.cat([ang, ang], dim=-1)
+        return ang.cos().to(bf)[None].expand(3, *ang.shape), ang.sin().to(bf)[None].expand(3, *ang.shape)
+
+    def mlp(x, lw):
+        h = rms(x, lw["n2"])
+        return x + F.linear(F.silu(F.linear(h, lw["wg"])) * F.linear(h, lw["wu"]), lw["wd"])
+
+    # ---- prefill: every sequence through the model; keep each layer's rotated K/V
+    kv = [[None] * batch for _ in range(n_layers)]
+    first = torch.empty(batch, dtype=torch.int64, device=dev)
+    with torch.no_grad():
+        for s_i in range(batch):
+            tok = torch.randint(0, vocab, (context,), generator=cpu).to(dev)
+            x = embed[tok]
+            cos, sin = tables(torch.arange(context, device=dev)[None])
+            for li, lw in enumerate(layers):
+                h = rms(x, lw["n1"])
+                q = F.linear(h, lw["wq"], lw["bq"]).view(context, nh, hd).transpose(0, 1)[None]
+                k = F.linear(h, lw["wk"], lw["bk"]).view(context, nkv, hd).transpose(0, 1)[None]
+                v = F.linear(h, lw["wv"], lw["bv"]).view(context, nkv, hd).transpose(0, 1)[None].contiguous()
+                q, k = ro.qwen_qk_mrope(q, k, cos, sin, sections)
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                    a = F.scaled_dot_product_attention(q, k.repeat_interleave(nh // nkv, dim=1),
+                                                       v.repeat_interleave(nh // nkv, dim=1), is_causal=True)
+                x = x + F.linear(a[0].transpose(0, 1).reshape(context, hid), lw["wo"])
+                x = mlp(x, lw)
+                kv[li][s_i] = (ro.triton_fwht_128(k[0]), ro.triton_fwht_128(v[0]))
+            first[s_i] = F.linear(rms(x[-1:], n_final), lm_head).argmax(-1)[0]
+            torch.cuda.synchronize()
+            _log(f"e2e prefill sequence {s_i + 1}/{batch} ({time.perf_counter() - t0:.1f} s)")
+    prefill_s = time.perf_counter() - t0
+
+    cfg = DecodeConfig("e2e", nh, nkv, (context,), (0.15, 0.45, 0.4), recent=recent)
+    hist = context - recent
+    pages = hist // cfg.page
+    tiers = [torch.multinomial(torch.tensor(cfg.tier_probs), pages, replacement=True, generator=cpu)
+             for _ in range(n_layers * batch)]
+
+    def build_caches():
+        out = []
+        for li in range(n_layers):
+            row = []
+            for s_i in range(batch):
+                k, v = kv[li][s_i]
+                classes = torch.tensor(TIER_CLASS, dtype=torch.long)[tiers[li * batch + s_i]]
+                data = RequestData(None, k[:, :hist], v[:, :hist], k[:, hist:].transpose(0, 1),
+                                   v[:, hist:].transpose(0, 1), torch.arange(pages, dtype=torch.long) * cfg.page,
+                                   torch.full((pages,), cfg.page, dtype=torch.long), classes, None)
+                row.append(build_request_cache(cfg, data, append_capacity=steps + 256))
+            out.append(row)
+        torch.cuda.synchronize()
+        return out
+
+    def decode(use_graph: bool):
+        caches = build_caches()
+        decs = [ro.BatchedDecoder(c, num_query_heads=nh, output_hadamard=True, use_graph=False) for c in caches]
+        tok = first.clone()
+        pos_dev = torch.full((1, 1), context, dtype=torch.int64, device=dev)
+        logits = torch.empty(batch, vocab, device=dev, dtype=bf)
+        positions = [context] * batch
+        tokens = []
+
+        def body(attend):
+            x = embed[tok]
+            cos, sin = tables(pos_dev.expand(batch, 1))
+            for lw, d in zip(layers, decs):
+                h = rms(x, lw["n1"])
+                q = F.linear(h, lw["wq"], lw["bq"]).view(batch, nh, 1, hd)
+                k = F.linear(h, lw["wk"], lw["bk"]).view(batch, nkv, 1, hd)
+                v = F.linear(h, lw["wv"], lw["bv"]).view(batch, nkv, hd)
+                ro.qwen_qk_mrope(q, k, cos, sin, sections, apply_hadamard=True,
+                                 output=(d.query_buffer.view(batch, nh, 1, hd), d.key_buffer.view(batch, nkv, 1, hd)))
+                ro.triton_fwht_128(v, output=d.value_buffer)
+                attend(d)
+                x = x + F.linear(d.workspace.output.view(batch, hid), lw["wo"])
+                x = mlp(x, lw)
+            logits.copy_(F.linear(rms(x, n_final), lm_head))
+            pos_dev.add_(1)
+
+        def eager_attend(d):
+            d.step_in_place(global_token_index=positions, logical_position=positions)
+
+        def graph_attend(d):
+            d.executor._launch(d._params, dev)
+
+        stream = torch.cuda.current_stream(dev)
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        graph = None
+        with torch.no_grad():
+            torch.cuda.synchronize()
+            e[0].record(stream)
+            body(eager_attend)  # step 1: every ring is full and flushes inside the batch
+            tok.copy_(logits.argmax(-1))
+            e[1].record(stream)
+            tokens.append(tok.clone())
+            positions = [p + 1 for p in positions]
+            if use_graph:
+                for d in decs:  # the step's host bookkeeping; the captured launches advance the device state
+                    assert not d._prepare(positions, positions), "no flush may fall inside the captured steps"
+                graph = torch.cuda.CUDAGraph()
+                side = torch.cuda.Stream(device=dev)
+                side.wait_stream(stream)
+                with torch.cuda.graph(graph, stream=side):
+                    body(graph_attend)
+                stream.wait_stream(side)
+                torch.cuda.synchronize()
+                # the capture recorded the step without running it: replay it as step 2
+            e[2].record(stream)
+            for i in range(1, steps):
+                if use_graph:
+                    if i > 1:
+                        for d in decs:
+                            assert not d._prepare(positions, positions)
+                    graph.replay()
+                    for d in decs:
+                        d._advance()
+                else:
+                    body(eager_attend)
+                tok.copy_(logits.argmax(-1))
+                tokens.append(tok.clone())
+                positions = [p + 1 for p in positions]
+            e[3].record(stream)
+            torch.cuda.synchronize()
+        ms = e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[3])
+        del decs, caches, graph
+        torch.cuda.empty_cache()
+        return ms, torch.stack(tokens)
+
+    eager_ms, eager_tokens = decode(False)
+    _log(f"e2e eager decode: {eager_ms:.1f} ms for {steps} steps")
+    graph_ms, graph_tokens = decode(True)
+    _log(f"e2e graph decode: {graph_ms:.1f} ms for {steps} steps")
+    match = bool(torch.equal(eager_tokens, graph_tokens))
+    best_ms = graph_ms if match else eager_ms
+    return {"metric": "e2e decode tok/s", "value": round(batch * steps / (best_ms * 1e-3), 1), "unit": "tok/s",
+            "higher_is_better": True, "steps": steps, "ms_per_step": round(best_ms / steps, 3),
+            "mode": "hip_graph_per_step" if match else "eager",
+            "eager_tok_s": round(batch * steps / (eager_ms * 1e-3), 1),
+            "graph_tok_s": round(batch * steps / (graph_ms * 1e-3), 1), "graph_matches_eager": match,
+            "dtype": "bf16", "data": "synthetic (random-init weights N(0, 0.02), seeded random token ids)",
+            "config": {"workload": "cfg4 qwen25omni7b e2e decode", "layers": n_layers, "batch": batch,
+                       "prefill_tokens": context, "decode_steps": steps, "value_tiers": "15/45/40 per 64-token page",
+                       "keys": "compact INT4", "hadamard": True},
+            "prefill_s": round(prefill_s, 1),
+            "note": "host clock excluded: HIP events around the decode steps (first step eager with the flush "
+                    "of every ring; graph capture outside the timed span); greedy argmax in eager launches"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,6 +470,13 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=0, metavar="N",
                     help="only time N decode steps of --layers BatchedDecoder layers of --config (eager launches "
                          "and one HIP graph per step, flushes inside the batch) and print one JSON line")
+    ap.add_argument("--e2e", action="store_true",
+                    help="only run configuration 4: prefill and greedy decode of a random-init Qwen2.5-Omni-7B "
+                         "language model on this path, and print one JSON line (decode tok/s)")
+    ap.add_argument("--e2e-batch", type=int, default=8)
+    ap.add_argument("--e2e-context", type=int, default=32768)
+    ap.add_argument("--e2e-steps", type=int, default=128)
+    ap.add_argument("--e2e-layers", type=int, default=28)
     ap.add_argument("--summarize-pmc", metavar="DIR",
                     help="only print the mean per-dispatch value of every counter in a rocprofv3 --pmc CSV "
                          "output directory, per decode kernel (and the calibration copy kernel)")
@@ -295,6 +497,10 @@ def main() -> int:
     from r2omni_amd.workloads import CONFIGS, algorithmic_bytes, build_request_cache, make_request
 
     dev = torch.device("cuda:0")
+    if args.e2e:
+        print(json.dumps(e2e_decode_bench(dev, batch=args.e2e_batch, context=args.e2e_context, steps=args.e2e_steps,
+                                          n_layers=args.e2e_layers)), flush=True)
+        return 0
     if args.copy_calibration:
         n = args.copy_calibration * (1 << 20) // 4
         src = torch.randn(n, device=dev)
