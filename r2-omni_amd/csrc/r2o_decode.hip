@@ -769,6 +769,34 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     }
 }
 
+// Fused Recent-FP append (triton_fourq_splitk.py:1007-1020) of every KV head of request b, by one
+// extra block of the combine grid: no merge block reads the ring, and this block is the only reader
+// and writer of the ring length (and, in device-state mode, of the step positions) during the launch.
+__device__ void fused_append(const r2o_decode_params& p, int64_t b, int tid) {
+    const r2o_request_desc& rq = p.reqs[b];
+    const int64_t pos = p.step_positions ? (int64_t)*rq.recent_length : p.recent_len[b];
+    if (pos >= rq.recent_capacity) return;  // a full ring takes no append (the host flushes first)
+    for (int e = tid; e < p.hkv * 128; e += blockDim.x) {
+        const int64_t hh = e >> 7, d = e & 127;
+        const int64_t dst = (hh * rq.recent_capacity + pos) * 128 + d, src = (b * p.hkv + hh) * 128 + d;
+        rq.recent_k[dst] = p.append_k[src];
+        rq.recent_v[dst] = p.append_v[src];
+    }
+    if (tid == 0) {
+        int64_t gidx = p.append_global[b], lpos = p.append_logical[b];
+        if (p.step_positions) {  // this step's positions, advanced for the next replay
+            gidx = p.step_positions[2 * b];
+            lpos = p.step_positions[2 * b + 1];
+            p.step_positions[2 * b] = gidx + 1;
+            p.step_positions[2 * b + 1] = lpos + 1;
+        }
+        rq.recent_global[pos] = gidx;
+        rq.recent_logical[pos] = lpos;
+        *rq.recent_length = (int32_t)(pos + 1);
+        rq.recent_page_lengths[pos / p.page_size] = pos % p.page_size + 1;
+    }
+}
+
 // One 512-thread block per (request, query head): 16 slices of 32 lanes, lane l owning dims
 // 4l..4l+3.  Slice s merges partials beg+s, beg+s+16, ... kCombineUnroll at a time with every
 // load of a round issued before any is used, so a group of up to 128 partials costs one memory
@@ -788,6 +816,10 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
     const int64_t b = blockIdx.y;
     const int hqi = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 31, slice = tid >> 5;
+    if (hqi == p.hq) {  // the extra block of a fused append: runs beside the merges of request b
+        fused_append(p, b, tid);
+        return;
+    }
     const int gqa = (int)(p.hq / p.hkv);
     const int kvh = hqi / gqa, h = hqi % gqa;
     const int beg = r2o_ldg(p.group_begin + b * p.hkv + kvh), end = r2o_ldg(p.group_begin + b * p.hkv + kvh + 1);
@@ -847,35 +879,6 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
     uint16_t* orow = p.out + (b * p.hq + hqi) * 128;
     orow[tid] = (uint16_t)r2o_f32_to_bf16(y0);
     orow[tid + 64] = (uint16_t)r2o_f32_to_bf16(y1);
-
-    // Fused Recent-FP append (triton_fourq_splitk.py:1007-1020) of every KV head of request b by
-    // the block of query head 0 alone: it is the only reader and writer of the ring length (and, in
-    // device-state mode, of the step positions) during this kernel.
-    if (p.do_append && hqi == 0) {
-        const r2o_request_desc& rq = p.reqs[b];
-        const int64_t pos = p.step_positions ? (int64_t)*rq.recent_length : p.recent_len[b];
-        if (pos < rq.recent_capacity) {  // a full ring takes no append (the host flushes first)
-            for (int e = tid; e < p.hkv * 128; e += 64) {  // wave 0 only: the other waves have returned
-                const int64_t hh = e >> 7, d = e & 127;
-                const int64_t dst = (hh * rq.recent_capacity + pos) * 128 + d, src = (b * p.hkv + hh) * 128 + d;
-                rq.recent_k[dst] = p.append_k[src];
-                rq.recent_v[dst] = p.append_v[src];
-            }
-            if (tid == 0) {
-                int64_t gidx = p.append_global[b], lpos = p.append_logical[b];
-                if (p.step_positions) {  // this step's positions, advanced for the next replay
-                    gidx = p.step_positions[2 * b];
-                    lpos = p.step_positions[2 * b + 1];
-                    p.step_positions[2 * b] = gidx + 1;
-                    p.step_positions[2 * b + 1] = lpos + 1;
-                }
-                rq.recent_global[pos] = gidx;
-                rq.recent_logical[pos] = lpos;
-                *rq.recent_length = (int32_t)(pos + 1);
-                rq.recent_page_lengths[pos / p.page_size] = pos % p.page_size + 1;
-            }
-        }
-    }
 }
 
 int validate(const r2o_decode_params* p) {
@@ -914,8 +917,8 @@ int r2o_decode_partial(const r2o_decode_params* params, void* stream) {
 int r2o_decode_combine(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)params->hq, (unsigned)params->batch), dim3(512), 0,
-                       (hipStream_t)stream, *params);
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(params->hq + (params->do_append ? 1 : 0)),
+                       (unsigned)params->batch), dim3(512), 0, (hipStream_t)stream, *params);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
 }
