@@ -1,0 +1,83 @@
+"""GPU parity at the edges of the decode path's geometry: the largest and smallest GQA groups, a
+one-page cache, and the largest ragged batch the launch accepts (32 requests), each against the CPU
+oracle to the decode bar (max-abs 2e-2, mean-abs 2e-3)."""
+import pytest
+import torch
+
+from test_gpu_parity import _bf16_np, _compare, _cuda, _oracle_for
+
+pytestmark = pytest.mark.gpu
+
+EDGE = [
+    # name, hq, hkv, historical tokens, ring tokens, tier probs (BF16, INT4, INT2), superblock, group
+    ("gqa16", 32, 2, 1536, 50, (0.2, 0.5, 0.3), 32, 32),
+    ("gqa1", 4, 4, 1024, 31, (0.3, 0.4, 0.3), 64, 64),
+    ("gqa2_int2", 8, 4, 2048, 128, (0.0, 0.0, 1.0), 128, 128),
+    ("one_page", 16, 2, 64, 5, (0.0, 1.0, 0.0), 32, 32),
+    ("one_page_bf16", 16, 2, 64, 0, (1.0, 0.0, 0.0), 32, 32),
+]
+
+
+@pytest.mark.parametrize("case", [e[0] for e in EDGE])
+@pytest.mark.parametrize("hadamard", [False, True])
+def test_edge_geometries_match_oracle(case, hadamard):
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    _, hq, hkv, hist, recent, probs, sb, grp = next(e for e in EDGE if e[0] == case)
+    cfg = DecodeConfig(case, hq, hkv, (hist + recent,), probs, recent=recent, superblock=sb, group=grp)
+    data = make_request(cfg, hist + recent, seed=900 + hq + hkv + hist, device=dev)
+    cache = build_request_cache(cfg, data)
+    ws = ro.allocate_splitk_workspace(cache, num_query_heads=hq)
+    ex = ro.prepare_splitk_executor(cache, ws, output_hadamard=hadamard)
+    print(f"[edge] {case} hadamard={hadamard}: {ex.n_items} items", flush=True)
+    out = ex(data.query.contiguous())
+    torch.cuda.synchronize()
+    want = output_transform(mixed_reference(bf16_bits_to_f32(_bf16_np(data.query)), _oracle_for(data, cfg)), hadamard)
+    _compare(out, want, f"{case} hadamard={hadamard}")
+
+
+def test_largest_ragged_batch_matches_per_request_oracle():
+    """32 requests (the launch maximum) of different lengths, tier mixes and ring fills in one launch."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    gen = torch.Generator().manual_seed(31)
+    datas, caches, cfgs = [], [], []
+    for r in range(32):
+        hist = 64 * int(torch.randint(1, 24, (1,), generator=gen))
+        recent = int(torch.randint(0, 129, (1,), generator=gen))
+        probs = [(0.15, 0.45, 0.4), (0.0, 1.0, 0.0), (0.0, 0.0, 1.0), (1.0, 0.0, 0.0)][r % 4]
+        cfg = DecodeConfig("b32", 28, 4, (hist + recent,), probs, recent=recent)
+        data = make_request(cfg, hist + recent, seed=1300 + r, device=dev)
+        cfgs.append(cfg)
+        datas.append(data)
+        caches.append(build_request_cache(cfg, data))
+    wss = [ro.allocate_splitk_workspace(c, num_query_heads=28) for c in caches]
+    exs = [ro.prepare_splitk_executor(c, w, output_hadamard=True) for c, w in zip(caches, wss)]
+    batched = ro.stack_homogeneous_splitk_executors(exs)
+    print(f"[edge] batch of 32: {batched.n_items} items", flush=True)
+    q = torch.cat([d.query for d in datas]).contiguous()
+    out = batched(q)
+    torch.cuda.synchronize()
+    for r, (d, cfg) in enumerate(zip(datas, cfgs)):
+        want = output_transform(mixed_reference(bf16_bits_to_f32(_bf16_np(d.query)), _oracle_for(d, cfg)), True)
+        _compare(out[r : r + 1], want, f"batch of 32, request {r}")
+
+
+def test_batch_above_the_launch_maximum_is_refused():
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+
+    dev = _cuda()
+    cfg = DecodeConfig("b33", 16, 2, (64 + 8,), (0.0, 1.0, 0.0), recent=8)
+    caches = [build_request_cache(cfg, make_request(cfg, 72, seed=1400 + r, device=dev)) for r in range(33)]
+    exs = [ro.prepare_splitk_executor(c, ro.allocate_splitk_workspace(c, num_query_heads=16)) for c in caches]
+    with pytest.raises(ValueError, match="at most 32 requests"):
+        ro.stack_homogeneous_splitk_executors(exs)
