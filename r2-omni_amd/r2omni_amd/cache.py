@@ -17,6 +17,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Any, Literal
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -674,37 +675,48 @@ def precision_cache_active_storage_breakdown(cache: ThreePrecisionCache) -> dict
 
 
 def _compact_page_layouts(plan: LayerCompressionPlan, device=None):
-    """(tokens, offsets, lengths, page ids) of FP, INT4, INT2, Recent(empty), evicted pools.
+    """(tokens, offsets, lengths, page ids) of FP, INT4, INT2, Recent(empty), evicted pools, on ``device``.
 
     Pages are stably sorted by tier FP(+protected, recent) < INT4 < INT2 < evicted and keep
-    their token order (precision_pool.py:611-669).  The page table (small) is sorted on the host;
-    the token lists are expanded on ``device`` without a per-page loop: token j of a tier is
-    start(page) + (j - physical offset(page)).
+    their token order (precision_pool.py:611-669).  The page table (small) is sorted on the host
+    (one copy from the device when the plan lives there), the page tables of every tier go to
+    ``device`` in one copy, and one expansion there yields the token lists of all tiers: token j
+    of the tier-ordered concatenation is start(page) + (j - offset of the page in it).
     """
     dev = torch.device("cpu") if device is None else torch.device(device)
-    classes = plan.page_classes.detach().to("cpu", torch.long)
-    starts = plan.page_offsets.detach().to("cpu", torch.long)
-    lens = plan.page_lengths.detach().to("cpu", torch.long)
-    cat = torch.full_like(classes, 3)
-    cat[(classes == PageClass.FP_PAGE) | (classes == PageClass.PROTECTED_FP_PAGE)
-        | (classes == PageClass.RECENT_FP_PAGE)] = 0
-    cat[classes == PageClass.INT4_PAGE] = 1
-    cat[classes == PageClass.INT2_PAGE] = 2
-    order = torch.argsort(cat, stable=True)
+    table = plan.host_page_table
+    if table is None:
+        table = torch.stack((plan.page_classes.detach().to(torch.long), plan.page_offsets.detach().to(torch.long),
+                             plan.page_lengths.detach().to(torch.long))).to("cpu")
+    classes, starts, lens = table.numpy()
+    cat = np.full(classes.shape, 3, dtype=np.int64)
+    cat[np.isin(classes, (int(PageClass.FP_PAGE), int(PageClass.PROTECTED_FP_PAGE), int(PageClass.RECENT_FP_PAGE)))] = 0
+    cat[classes == int(PageClass.INT4_PAGE)] = 1
+    cat[classes == int(PageClass.INT2_PAGE)] = 2
+    pages = np.argsort(cat, kind="stable")
+    pl = lens[pages]
+    tier = cat[pages]
+    first_page = np.concatenate(([0], np.cumsum(np.bincount(tier, minlength=4)[:4])))
+    glob_off = np.cumsum(pl) - pl  # offset of each page in the tier-ordered concatenation
+    tier_tok = np.bincount(tier, weights=pl, minlength=4)[:4].astype(np.int64)
+    tier_start = np.concatenate(([0], np.cumsum(tier_tok)[:-1]))
+    n_tok = int(tier_tok.sum())
+    dtab = torch.from_numpy(np.stack((pages, glob_off - tier_start[tier], pl, starts[pages] - glob_off)))
+    if dev.type != "cpu":  # pinned staging: a copy from pageable memory would wait for the stream's earlier work
+        dtab = dtab.pin_memory().to(dev, non_blocking=True)
+    if n_tok:
+        tokens = torch.repeat_interleave(dtab[3], dtab[2], output_size=n_tok) + torch.arange(
+            n_tok, device=dev, dtype=torch.long)
+    else:
+        tokens = torch.zeros(0, dtype=torch.long, device=dev)
     layouts = []
-    for tier in range(4):
-        pages = order[cat[order] == tier]
-        pl = lens[pages]
-        offsets = pl.cumsum(0) - pl
-        n_tok = int(pl.sum())
-        if n_tok:
-            shift = torch.repeat_interleave((starts[pages] - offsets).to(dev), pl.to(dev), output_size=n_tok)
-            tokens = shift + torch.arange(n_tok, device=dev, dtype=torch.long)
-        else:
-            tokens = torch.zeros(0, dtype=torch.long, device=dev)
-        layouts.append((tokens, offsets, pl, pages))
-    empty = torch.zeros(0, dtype=torch.long)
-    return layouts[0], layouts[1], layouts[2], (empty.to(dev), empty, empty, empty), layouts[3]
+    t0 = 0
+    for t in range(4):
+        p0, p1, nt = int(first_page[t]), int(first_page[t + 1]), int(tier_tok[t])
+        layouts.append((tokens[t0:t0 + nt], dtab[1, p0:p1], dtab[2, p0:p1], dtab[0, p0:p1]))
+        t0 += nt
+    empty = torch.zeros(0, dtype=torch.long, device=dev)
+    return layouts[0], layouts[1], layouts[2], (empty, empty, empty, empty), layouts[3]
 
 
 def _survivor_layout(plan: LayerCompressionPlan, device):
@@ -736,14 +748,14 @@ def _gather_key_rows(key: torch.Tensor, tokens: torch.Tensor, append_capacity: i
     return BF16KeyArena(rows=rows, active_length=n, capacity=cap, segment_offsets=tuple(segments))
 
 
-def _make_page_index(plan: LayerCompressionPlan, layout, device) -> PhysicalPageIndex:
+def _make_page_index(layout, gi: torch.Tensor, lp: torch.Tensor) -> PhysicalPageIndex:
+    """Page index of one pool; ``gi`` / ``lp`` are the plan's global / logical token indices on the
+    pool's device."""
     tokens, offsets, lengths, pages = layout
-    gi = plan.global_token_indices.detach().to(device, torch.long)
-    lp = plan.logical_positions.detach().to(device, torch.long)
-    tokens = tokens.to(device)
-    return PhysicalPageIndex(original_page_ids=pages.to(device), physical_offsets=offsets.to(device),
-                             lengths=lengths.to(device), global_token_indices=gi[tokens],
-                             logical_positions=lp[tokens])
+    dev = gi.device
+    tokens = tokens.to(dev)
+    return PhysicalPageIndex(original_page_ids=pages.to(dev), physical_offsets=offsets.to(dev),
+                             lengths=lengths.to(dev), global_token_indices=gi[tokens], logical_positions=lp[tokens])
 
 
 def _preallocate_recent_pool(name: str, key: torch.Tensor, *, page_size: int, capacity: int) -> PrecisionPool:
@@ -826,6 +838,7 @@ def build_three_precision_cache(
     append_capacity = plan.recent_fp_capacity if compact_key_append_capacity is None \
         else int(compact_key_append_capacity)
     gi = plan.global_token_indices.detach().to(dev, torch.long)
+    lp = plan.logical_positions.detach().to(dev, torch.long)
     common = dict(evicted_global_indices=gi[ev_l[0]], page_size=int(page_size),
                   quantization_superblock=int(quantization_superblock), cache_variant=cache_variant,
                   recent_flush_size=int(recent_flush_size), generated_value_precision="int2")
@@ -833,7 +846,7 @@ def build_three_precision_cache(
         surv = _survivor_layout(plan, dev)
         n = int(surv[0].numel())
         arena = _gather_key_rows(key, surv[0], append_capacity, (0, n, n))
-        fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(plan, surv, dev), fp_k=arena.view(0, n))
+        fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(surv, gi, lp), fp_k=arena.view(0, n))
         fp_pool.fp_v = torch.empty((h, n, 128), device=dev, dtype=value.dtype)
         if n:
             _lib.call("r2o_gather_rows", _lib.ptr(value), h, int(value.shape[1]), _lib.ptr(surv[0]), n,
@@ -841,21 +854,21 @@ def build_three_precision_cache(
         empty = (surv[0][:0], surv[1][:0], surv[2][:0], surv[3][:0])
         recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity)
         return ThreePrecisionCache(
-            fp_pool=fp_pool, int4_pool=PrecisionPool(name="int4", page_index=_make_page_index(plan, empty, dev)),
-            int2_pool=PrecisionPool(name="int2", page_index=_make_page_index(plan, empty, dev)),
+            fp_pool=fp_pool, int4_pool=PrecisionPool(name="int4", page_index=_make_page_index(empty, gi, lp)),
+            int2_pool=PrecisionPool(name="int2", page_index=_make_page_index(empty, gi, lp)),
             recent_fp_pool=recent, matched_fp=True, bf16_key=arena, generated_k_offset=n, **common)
-    fp_tokens, i4_tokens, i2_tokens = (l[0].to(dev) for l in (fp_l, i4_l, i2_l))
+    fp_tokens, i4_tokens, i2_tokens = fp_l[0], i4_l[0], i2_l[0]
     s_fp, s_i4 = int(fp_tokens.numel()), int(i4_tokens.numel())
 
-    fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(plan, fp_l, dev))
+    fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(fp_l, gi, lp))
     if s_fp:
         fp_pool.fp_v = torch.empty((h, s_fp, 128), device=dev, dtype=value.dtype)
         _lib.call("r2o_gather_rows", _lib.ptr(value), h, int(value.shape[1]), _lib.ptr(fp_tokens), s_fp,
                   _lib.ptr(fp_pool.fp_v), s_fp, stream)
-    int4_pool = PrecisionPool(name="int4", page_index=_make_page_index(plan, i4_l, dev))
+    int4_pool = PrecisionPool(name="int4", page_index=_make_page_index(i4_l, gi, lp))
     if s_i4:
         int4_pool.packed_v = fused_gather_pack_int4_value(value, i4_tokens)
-    int2_pool = PrecisionPool(name="int2", page_index=_make_page_index(plan, i2_l, dev))
+    int2_pool = PrecisionPool(name="int2", page_index=_make_page_index(i2_l, gi, lp))
     compact_value = build_compact_int2_value_arena(value, i2_tokens, append_capacity=append_capacity,
                                                    group_size=int2_group_size)
     int2_pool.packed_v = compact_value

@@ -140,6 +140,9 @@ class LayerCompressionPlan:
     page_offsets: torch.Tensor
     page_lengths: torch.Tensor
     page_classes: torch.Tensor
+    # Host copy of (page_classes, page_offsets, page_lengths) as int64 [3, pages] when the plan was
+    # made from host data: the cache build then sorts the page table without a device round trip.
+    host_page_table: torch.Tensor | None = None
 
 
 def build_layer_compression_plan(layer_id: int, assignment: PageAssignment, *,
@@ -165,6 +168,10 @@ def plan_from_pages(page_offsets, page_lengths, page_classes, *, recent_fp_capac
                     device=None) -> LayerCompressionPlan:
     """Plan from explicit page geometry (synthetic workloads and tests)."""
     dev = torch.device(device) if device is not None else torch.device("cpu")
+    host = None
+    if all(not (isinstance(v, torch.Tensor) and v.device.type != "cpu")
+           for v in (page_offsets, page_lengths, page_classes)):
+        host = torch.stack([torch.as_tensor(v, dtype=torch.long) for v in (page_classes, page_offsets, page_lengths)])
     offs = torch.as_tensor(page_offsets, dtype=torch.long, device=dev)
     lens = torch.as_tensor(page_lengths, dtype=torch.long, device=dev)
     cls = torch.as_tensor(page_classes, dtype=torch.long, device=dev)
@@ -177,5 +184,5 @@ def plan_from_pages(page_offsets, page_lengths, page_classes, *, recent_fp_capac
         int2_pages=pages(cls == PageClass.INT2_PAGE), evicted_pages=pages(cls == PageClass.EVICTED_PAGE),
         protected_pages=pages(cls == PageClass.PROTECTED_FP_PAGE), recent_fp_capacity=int(recent_fp_capacity),
         logical_positions=positions, global_token_indices=positions.clone(), page_offsets=offs,
-        page_lengths=lens, page_classes=cls,
+        page_lengths=lens, page_classes=cls, host_page_table=host,
     )
