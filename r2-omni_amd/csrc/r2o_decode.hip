@@ -20,7 +20,9 @@
 //       dim 8*l16 + q of MFMA q).  BF16 V: bf16 MFMA.  INT4 V: the per-token scale is folded
 //       into P (P' = p * s) and the signed codes enter exactly as f16 (1032 + c, low nibbles,
 //       and 1152 + 16 c in place for the high nibbles), the offsets being removed after the
-//       last tile.  INT2 V: (c - z) * s is formed in f16 per element.
+//       last tile.  INT2 V: (c - z) * s is formed in f16 per element, or, when a group spans all
+//       128 dims (one scale and zero point per token), the scale is folded into P and the crumbs
+//       enter as 1024 + c, sum P' (1024 + z) being removed after the last tile.
 //   Pool tiles arrive by global->LDS DMA into a one-stage-per-wave ring (no VGPRs held while in
 //   flight); Recent-FP tiles are loaded straight into registers, all loads of a tile first.
 // The 4 waves' states are merged in LDS and one (max, sum, acc[GQA][128]) fp32 partial is
@@ -230,7 +232,8 @@ struct SegCtx {
 template <int KIND>
 struct SegState {
     uint32_t qp[4][4];   // q (scaled), f16 pairs in the K-unpack channel order
-    r2o_f4 bias;         // INT4-V: sum_k P'_k per head row (code offsets removed at the end)
+    r2o_f4 bias;         // INT4-V: sum_k P'_k per head row; INT2-V with one group per token:
+                         // sum_k P'_k (1024 + z_k) (code offsets removed at the end)
 };
 
 // QK^T of one INT4-K tile: per MFMA j, Q'_j = q * s (superblock scale pairs), the codes of the
@@ -308,7 +311,7 @@ __device__ __forceinline__ void tile_logits(const SegCtx& c, int a0, int g, cons
 }
 
 // PV of one tile with probabilities pk (the lane's 8 tokens).
-template <int KIND>
+template <int KIND, bool TS>  // TS: INT2 values with one scale and zero point per token (group 128)
 __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const VConst& vc, const float (&pk)[8],
                                         const VRegs<KIND>& cur) {
     r2o_u4 ap;
@@ -339,6 +342,29 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
             }
             st.acc[2 * bb] = r2o_mfma_f16(ap, lo, st.acc[2 * bb]);
             st.acc[2 * bb + 1] = r2o_mfma_f16(ap, hi, st.acc[2 * bb + 1]);
+        }
+    } else if constexpr (TS) {
+        // one scale and zero point per token (a group of all 128 dims): P' = p * s_t, the crumbs
+        // enter exactly as f16 1024 + c, and sum_k P'_k (1024 + z_k) is accumulated by one more
+        // MFMA on the same A operand (removed after the last tile), as for INT4 values
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            ap[u] = r2o_pack_h2(pk[2 * u] * r2o_f16_to_f32(cur.vm[2 * u]), pk[2 * u + 1] * r2o_f16_to_f32(cur.vm[2 * u + 1]));
+        uint32_t yp[4];
+        r2o_u4 zb;
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+            yp[pr] = cur.v[2 * pr] | (cur.v[2 * pr + 1] << 16);
+            zb[pr] = (cur.vz[2 * pr] | (cur.vz[2 * pr + 1] << 16)) | vc.magic;
+        }
+        ss.bias = r2o_mfma_f16(ap, zb, ss.bias);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int shift = (q < 4) ? 2 * q : 8 + 2 * (q - 4);
+            r2o_u4 bop;
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) bop[pr] = ((yp[pr] >> shift) & vc.crumb) | vc.magic;
+            st.acc[q] = r2o_mfma_f16(ap, bop, st.acc[q]);
         }
     } else {
 #pragma unroll
@@ -378,7 +404,7 @@ __device__ __forceinline__ void qk_bf16k(const uint32_t (&qp)[4][4], float qscal
 }
 
 // One tile: QK, masks, online softmax, PV.
-template <int KIND, int KF>
+template <int KIND, int KF, bool TS>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
                                             int a0, int g, float qscale, const TileRegs<KIND, KF>& cur) {
     r2o_f4 s[2];
@@ -388,8 +414,8 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
     else qk_int2k(ss.qp, vc, cur.ops, cur.kx, s, corr);
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
-    softmax_tile(st, sv, pk, g, corr, KIND == kI4 ? &ss.bias : nullptr);
-    pv_tile<KIND>(st, ss, vc, pk, cur);
+    softmax_tile(st, sv, pk, g, corr, (KIND == kI4 || TS) ? &ss.bias : nullptr);
+    pv_tile<KIND, TS>(st, ss, vc, pk, cur);
 }
 
 // ------------------------------------------------------------------ pool tiles via LDS DMA
@@ -553,7 +579,7 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
     }
 }
 
-template <int KIND, int KF>
+template <int KIND, int KF, bool TS>
 __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
                             unsigned char* smem, WaveState& st) {
     using Cfg = KernelCfg<KF>;
@@ -624,7 +650,11 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
             __builtin_amdgcn_wave_barrier();
             dma_tile<KIND, KF>(c, a_first + 32 * (i + kDmaStages), stage, lane);
         }
-        seg_compute<KIND, KF>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
+        seg_compute<KIND, KF, TS>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
+    }
+    if constexpr (TS) {  // remove the code offsets of the per-token-scale form
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st.acc[q] -= ss.bias;
     }
     if constexpr (KIND == kI4) {  // remove the code offsets: lo dims 1032 * sum P', hi dims (1152 * sum P') / 16
 #pragma unroll
@@ -712,9 +742,12 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP, KF>(p, it, smem, st); break;
-        case kI4: run_segment<kI4, KF>(p, it, smem, st); break;
-        case kI2: run_segment<kI2, KF>(p, it, smem, st); break;
+        case kFP: run_segment<kFP, KF, false>(p, it, smem, st); break;
+        case kI4: run_segment<kI4, KF, false>(p, it, smem, st); break;
+        case kI2:  // INT2 values: one scale and zero point per token when a group spans all 128 dims
+            if (p.int2_group == 128) run_segment<kI2, KF, true>(p, it, smem, st);
+            else run_segment<kI2, KF, false>(p, it, smem, st);
+            break;
         default: run_recent(p, it, st); break;
     }
 
