@@ -24,7 +24,8 @@ from . import _lib
 from .cache import ThreePrecisionCache
 
 TILE = 32
-_MIN_TILES_PER_ITEM = 4      # one tile per wave of the 4-wave workgroup
+_WAVES_PER_ITEM = 4          # waves of the partial kernel's workgroup (each takes a contiguous share)
+_MIN_TILES_PER_ITEM = 4      # one tile per wave
 _BLOCKS_PER_CU = 2           # work items planned per CU (the kernel holds up to 3 resident; 2 keeps the combine short)
 # Small caches: fewer, longer items (about two tiles per wave) while every CU still gets one; more
 # items would only add partial states for the combine (measured on MI355X: a 3B layer at 32k
@@ -107,7 +108,7 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
     def item_cost(i: int) -> float:
         nt = runs[i][4]
         per = -(-nt // counts[i])
-        return (-(-per // 4) * 4) * _TILE_COST[runs[i][2]]
+        return (-(-per // _WAVES_PER_ITEM) * _WAVES_PER_ITEM) * _TILE_COST[runs[i][2]]
 
     heap = [(-item_cost(i), i) for i in range(len(runs))]
     heapq.heapify(heap)
@@ -126,7 +127,7 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
         if (r, h) != group:
             begins.append(len(items))
             group = (r, h)
-        n = -(-(-(-nt // n_items)) // 4) * 4  # tiles per item: even split, rounded up to 4
+        n = -(-(-(-nt // n_items)) // _WAVES_PER_ITEM) * _WAVES_PER_ITEM  # even split, a share per wave
         for first in range(0, nt, n):
             items.append([r, h, kind, t0 + TILE * first, min(n, nt - first), lo, hi, vd, len(items)])
     begins.append(len(items))
