@@ -10,6 +10,7 @@ from .cache import (
     CompactInt2KeyArena,
     CompactInt2ValueArena,
     CompactInt4KeyArena,
+    CompactMetadataArena,
     DynamicCacheStats,
     PackedTensor,
     PhysicalPageIndex,

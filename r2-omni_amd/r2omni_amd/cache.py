@@ -6,6 +6,7 @@ Drop-in for the reference runtime (same names, fields, layouts and error message
   PackedTensor (INT4-V pool) packed_kv_layout.py:11-32, fused_value_pack.py:152-193
   CompactInt2ValueArena      fused_value_pack.py:401-516, build :519-575
   PrecisionPool, ThreePrecisionCache, build_three_precision_cache  precision_pool.py:152-274, 787-984
+  CompactMetadataArena       precision_pool.py:45-145, 400-585
   append_generated_token, DynamicCacheStats  dynamic_fourq_cache.py:16-24, 172-267
 All payload bytes are produced by the gfx950 kernels of libr2o_sspa.so (r2o_pack_int4_k,
 r2o_pack_int4_v, r2o_pack_int2_v, r2o_gather_rows, r2o_recent_append, r2o_recent_shift);
@@ -15,7 +16,7 @@ released ``v_fourq_k_int4_compact`` cache with INT2 generated values.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Any, Literal
+from typing import Any, Literal, NamedTuple
 
 import numpy as np
 import torch
@@ -42,6 +43,53 @@ class PhysicalPageIndex:
     lengths: torch.Tensor
     global_token_indices: torch.Tensor
     logical_positions: torch.Tensor
+
+
+@dataclass
+class CompactMetadataArena:
+    """Every page and token index of a compact cache in one int64 allocation
+    (precision_pool.py:45-145, 400-585).
+
+    The INT2 pool's five fields are reserved up to the packed arenas' append capacity, and the page
+    fields of the reserved pages (id -1, offsets continuing the pool, full length) are written at
+    build time, so a flush copies its token indices in place and allocates nothing.  The INT2 pool's
+    ``page_index`` is re-pointed at longer views of the same buffers.  Generated INT4 values are not
+    supported here, so no INT4 reserve exists.
+    """
+
+    storage: torch.Tensor
+    int2_original_page_ids_buffer: torch.Tensor
+    int2_physical_offsets_buffer: torch.Tensor
+    int2_lengths_buffer: torch.Tensor
+    int2_global_index_buffer: torch.Tensor
+    int2_logical_position_buffer: torch.Tensor
+    int2_page_count: int
+    int2_token_count: int
+
+    def append_int2_pages(self, pool: "PrecisionPool", global_indices: torch.Tensor,
+                          logical_positions: torch.Tensor, page_size: int) -> None:
+        n = int(global_indices.numel())
+        if n <= 0 or n != int(logical_positions.numel()) or n % int(page_size):
+            raise ValueError("compact INT2 metadata append requires matching complete pages")
+        if global_indices.dtype != torch.long or logical_positions.dtype != torch.long \
+                or global_indices.device != self.storage.device or logical_positions.device != self.storage.device:
+            raise ValueError("compact INT2 metadata append requires same-device int64 indices")
+        page_end = self.int2_page_count + n // int(page_size)
+        token_end = self.int2_token_count + n
+        if page_end > self.int2_lengths_buffer.numel():
+            raise RuntimeError("compact INT2 page metadata capacity exhausted")
+        if token_end > self.int2_global_index_buffer.numel():
+            raise RuntimeError("compact INT2 token metadata capacity exhausted")
+        self.int2_global_index_buffer[self.int2_token_count:token_end].copy_(global_indices)
+        self.int2_logical_position_buffer[self.int2_token_count:token_end].copy_(logical_positions)
+        self.int2_page_count, self.int2_token_count = page_end, token_end
+        pool.page_index = PhysicalPageIndex(
+            original_page_ids=self.int2_original_page_ids_buffer[:page_end],
+            physical_offsets=self.int2_physical_offsets_buffer[:page_end],
+            lengths=self.int2_lengths_buffer[:page_end],
+            global_token_indices=self.int2_global_index_buffer[:token_end],
+            logical_positions=self.int2_logical_position_buffer[:token_end],
+        )
 
 
 # ------------------------------------------------------------------------ BF16 K rows
@@ -563,7 +611,7 @@ class ThreePrecisionCache:
     compact_key: CompactInt4KeyArena | CompactInt2KeyArena | None = None
     compact_value: CompactInt2ValueArena | None = None
     compact_int4_value: Any = None
-    metadata_arena: Any = None
+    metadata_arena: CompactMetadataArena | None = None
     recent_flush_size: int = 128
     generated_value_precision: str = "int2"
     static_int4_tokens: int = 0
@@ -639,7 +687,8 @@ def precision_cache_storage_breakdown(cache: ThreePrecisionCache) -> dict[str, i
             pay += int(t.untyped_storage().nbytes())
     meta_seen: set[int] = set()
     meta = 0
-    for t in [cache.evicted_global_indices] + [m for p in cache.pools for m in _pool_metadata(p)]:
+    arena = [] if cache.metadata_arena is None else [cache.metadata_arena.storage]
+    for t in [cache.evicted_global_indices] + arena + [m for p in cache.pools for m in _pool_metadata(p)]:
         if t is None:
             continue
         key = t.untyped_storage().data_ptr()
@@ -674,16 +723,22 @@ def precision_cache_active_storage_breakdown(cache: ThreePrecisionCache) -> dict
             "persistent_allocation_count": int(fields)}
 
 
-def _compact_page_layouts(plan: LayerCompressionPlan, device=None):
-    """(tokens, offsets, lengths, page ids) of FP, INT4, INT2, Recent(empty), evicted pools, on ``device``.
+class _TierTable(NamedTuple):
+    """Host page table in tier order FP(+protected, recent) < INT4 < INT2 < evicted."""
+    pages: np.ndarray        # plan page ids, tier order
+    offsets: np.ndarray      # offset of each page inside its tier's pool
+    lengths: np.ndarray      # tokens per page
+    shift: np.ndarray        # plan token index minus position in the tier-ordered concatenation
+    first_page: np.ndarray   # [5] index of each tier's first page (and the end)
+    tier_tokens: np.ndarray  # [4] tokens per tier
 
-    Pages are stably sorted by tier FP(+protected, recent) < INT4 < INT2 < evicted and keep
-    their token order (precision_pool.py:611-669).  The page table (small) is sorted on the host
-    (one copy from the device when the plan lives there), the page tables of every tier go to
-    ``device`` in one copy, and one expansion there yields the token lists of all tiers: token j
-    of the tier-ordered concatenation is start(page) + (j - offset of the page in it).
+
+def _tier_page_table(plan: LayerCompressionPlan) -> _TierTable:
+    """Pages stably sorted by tier, each keeping its token order (precision_pool.py:611-669).
+
+    The page table is small: it is sorted on the host, from the plan's host copy or one copy from
+    the device when the plan lives there.
     """
-    dev = torch.device("cpu") if device is None else torch.device(device)
     table = plan.host_page_table
     if table is None:
         table = torch.stack((plan.page_classes.detach().to(torch.long), plan.page_offsets.detach().to(torch.long),
@@ -700,23 +755,108 @@ def _compact_page_layouts(plan: LayerCompressionPlan, device=None):
     glob_off = np.cumsum(pl) - pl  # offset of each page in the tier-ordered concatenation
     tier_tok = np.bincount(tier, weights=pl, minlength=4)[:4].astype(np.int64)
     tier_start = np.concatenate(([0], np.cumsum(tier_tok)[:-1]))
-    n_tok = int(tier_tok.sum())
-    dtab = torch.from_numpy(np.stack((pages, glob_off - tier_start[tier], pl, starts[pages] - glob_off)))
+    return _TierTable(pages=pages.astype(np.int64), offsets=(glob_off - tier_start[tier]).astype(np.int64),
+                      lengths=pl.astype(np.int64), shift=(starts[pages] - glob_off).astype(np.int64),
+                      first_page=first_page.astype(np.int64), tier_tokens=tier_tok)
+
+
+def _expand_tier_tokens(tab: _TierTable, device) -> torch.Tensor:
+    """Plan token indices of every tier, concatenated in tier order, on ``device``: token j of the
+    concatenation is start(page) + (j - offset of the page in it), one expansion for all tiers."""
+    dev = torch.device(device)
+    n_tok = int(tab.tier_tokens.sum())
+    if not n_tok:
+        return torch.zeros(0, dtype=torch.long, device=dev)
+    d = torch.from_numpy(np.stack((tab.shift, tab.lengths)))
     if dev.type != "cpu":  # pinned staging: a copy from pageable memory would wait for the stream's earlier work
-        dtab = dtab.pin_memory().to(dev, non_blocking=True)
-    if n_tok:
-        tokens = torch.repeat_interleave(dtab[3], dtab[2], output_size=n_tok) + torch.arange(
-            n_tok, device=dev, dtype=torch.long)
-    else:
-        tokens = torch.zeros(0, dtype=torch.long, device=dev)
-    layouts = []
-    t0 = 0
-    for t in range(4):
-        p0, p1, nt = int(first_page[t]), int(first_page[t + 1]), int(tier_tok[t])
-        layouts.append((tokens[t0:t0 + nt], dtab[1, p0:p1], dtab[2, p0:p1], dtab[0, p0:p1]))
-        t0 += nt
-    empty = torch.zeros(0, dtype=torch.long, device=dev)
-    return layouts[0], layouts[1], layouts[2], (empty, empty, empty, empty), layouts[3]
+        d = d.pin_memory().to(dev, non_blocking=True)
+    return torch.repeat_interleave(d[0], d[1], output_size=n_tok) + torch.arange(n_tok, device=dev,
+                                                                                  dtype=torch.long)
+
+
+def _build_metadata_arena(tab: _TierTable, tokens: torch.Tensor, gi: torch.Tensor, lp: torch.Tensor, *,
+                          page_size: int, recent_capacity: int, int2_reserve: int):
+    """One int64 allocation holding the page index of every pool, the evicted global indices, the
+    Recent-FP ring's index buffers and its device length (precision_pool.py:400-585).
+
+    ``tokens`` are the tier-ordered token indices of ``_expand_tier_tokens``; ``gi`` / ``lp`` the
+    plan's global / logical token indices on the same device.  ``int2_reserve`` tokens (whole pages)
+    are reserved after the INT2 pool's fields.  Layout: the page fields of every pool and the length
+    slot (built on the host, one copy), then the token fields: global [FP INT4 INT2 reserve], logical
+    [FP INT4 INT2 reserve], evicted, ring global, ring logical.  Returns the arena, the four pools'
+    page indexes, the evicted indices and the ring's (global, logical, length) buffers.
+    """
+    ps = int(page_size)
+    cap = int(recent_capacity)
+    if int2_reserve % ps or cap % ps:
+        raise ValueError("metadata reserves must be whole pages")
+    dev = tokens.device
+    fp_, i4_, i2_, ev_ = (slice(int(tab.first_page[t]), int(tab.first_page[t + 1])) for t in range(4))
+    reserve_pages = int2_reserve // ps
+    n_i2 = int(tab.tier_tokens[2])
+    ring_pages = cap // ps
+
+    def fields(ids, offs, lens):
+        return np.concatenate((ids, offs, lens))
+
+    page_parts = [fields(tab.pages[t], tab.offsets[t], tab.lengths[t]) for t in (fp_, i4_)]
+    page_parts.append(fields(np.concatenate((tab.pages[i2_], np.full(reserve_pages, -1))),
+                             np.concatenate((tab.offsets[i2_], n_i2 + ps * np.arange(reserve_pages))),
+                             np.concatenate((tab.lengths[i2_], np.full(reserve_pages, ps)))))
+    page_parts.append(fields(np.full(ring_pages, -1), ps * np.arange(ring_pages), np.zeros(ring_pages, np.int64)))
+    page_parts.append(np.zeros(1, np.int64))  # the ring's device length (int32 in the low half)
+    page_block = torch.from_numpy(np.concatenate(page_parts).astype(np.int64))
+    n_pages_total = int(page_block.numel())
+    n_surv = int(tab.tier_tokens[:3].sum())
+    n_ev = int(tab.tier_tokens[3])
+    surv_span = n_surv + int(int2_reserve)
+    storage = torch.empty(n_pages_total + 2 * surv_span + n_ev + 2 * cap, device=dev, dtype=torch.long)
+    if dev.type != "cpu":
+        page_block = page_block.pin_memory()
+    storage[:n_pages_total].copy_(page_block, non_blocking=True)
+    tok = storage[n_pages_total:]
+    tok.fill_(-1)
+    g_all, l_all = tok[:surv_span], tok[surv_span:2 * surv_span]
+    evicted = tok[2 * surv_span:2 * surv_span + n_ev]
+    ring_g = tok[2 * surv_span + n_ev:2 * surv_span + n_ev + cap]
+    ring_l = tok[2 * surv_span + n_ev + cap:]
+    if n_surv:
+        torch.index_select(gi, 0, tokens[:n_surv], out=g_all[:n_surv])
+        torch.index_select(lp, 0, tokens[:n_surv], out=l_all[:n_surv])
+    if n_ev:
+        torch.index_select(gi, 0, tokens[n_surv:], out=evicted)
+
+    cursor = 0
+
+    def take(n):
+        nonlocal cursor
+        v = storage[cursor:cursor + n]
+        cursor += n
+        return v
+
+    indexes = []
+    tok_start = 0
+    for t, extra in ((fp_, 0), (i4_, 0), (i2_, reserve_pages)):
+        npg = t.stop - t.start + extra
+        ids, offs, lens = take(npg), take(npg), take(npg)
+        nt = int(tab.tier_tokens[len(indexes)])
+        span = nt + extra * ps
+        g, l = g_all[tok_start:tok_start + span], l_all[tok_start:tok_start + span]
+        tok_start += span
+        indexes.append((ids, offs, lens, g, l, npg - extra, nt))
+    ring_ids, ring_offs, ring_lens = take(ring_pages), take(ring_pages), take(ring_pages)
+    length = take(1).view(torch.int32)[0]
+    pools = [PhysicalPageIndex(original_page_ids=ids[:np_], physical_offsets=offs[:np_], lengths=lens[:np_],
+                               global_token_indices=g[:nt], logical_positions=l[:nt])
+             for ids, offs, lens, g, l, np_, nt in indexes]
+    pools.append(PhysicalPageIndex(original_page_ids=ring_ids, physical_offsets=ring_offs, lengths=ring_lens,
+                                   global_token_indices=ring_g, logical_positions=ring_l))
+    ids, offs, lens, g, l, np_, nt = indexes[2]
+    arena = CompactMetadataArena(storage=storage, int2_original_page_ids_buffer=ids,
+                                 int2_physical_offsets_buffer=offs, int2_lengths_buffer=lens,
+                                 int2_global_index_buffer=g, int2_logical_position_buffer=l,
+                                 int2_page_count=np_, int2_token_count=nt)
+    return arena, pools, evicted, (ring_g, ring_l, length)
 
 
 def _survivor_layout(plan: LayerCompressionPlan, device):
@@ -758,25 +898,32 @@ def _make_page_index(layout, gi: torch.Tensor, lp: torch.Tensor) -> PhysicalPage
                              lengths=lengths.to(dev), global_token_indices=gi[tokens], logical_positions=lp[tokens])
 
 
-def _preallocate_recent_pool(name: str, key: torch.Tensor, *, page_size: int, capacity: int) -> PrecisionPool:
+def _preallocate_recent_pool(name: str, key: torch.Tensor, *, page_size: int, capacity: int,
+                             metadata=None) -> PrecisionPool:
+    """The Recent-FP ring: bf16/fp16 K and V rows of ``capacity`` tokens and its index buffers.
+    ``metadata`` = (page index, global buffer, logical buffer, int32 length) views of a metadata arena;
+    without it they are allocated here (the matched-FP cache has no arena)."""
     if capacity < page_size or capacity % page_size:
         raise ValueError("Recent-FP capacity must be positive and page aligned")
     h, _, d = map(int, key.shape)
     dev = key.device
-    gbuf = torch.full((capacity,), -1, device=dev, dtype=torch.long)
-    lbuf = torch.full((capacity,), -1, device=dev, dtype=torch.long)
-    pages = capacity // page_size
-    return PrecisionPool(
-        name=name,
-        page_index=PhysicalPageIndex(
+    if metadata is None:
+        gbuf = torch.full((capacity,), -1, device=dev, dtype=torch.long)
+        lbuf = torch.full((capacity,), -1, device=dev, dtype=torch.long)
+        pages = capacity // page_size
+        index = PhysicalPageIndex(
             original_page_ids=torch.full((pages,), -1, device=dev, dtype=torch.long),
             physical_offsets=torch.arange(pages, device=dev, dtype=torch.long) * page_size,
             lengths=torch.zeros(pages, device=dev, dtype=torch.long),
-            global_token_indices=gbuf, logical_positions=lbuf),
+            global_token_indices=gbuf, logical_positions=lbuf)
+        length = torch.zeros((), device=dev, dtype=torch.int32)
+    else:
+        index, gbuf, lbuf, length = metadata
+    return PrecisionPool(
+        name=name, page_index=index,
         fp_k=torch.zeros((h, capacity, d), device=dev, dtype=key.dtype),
         fp_v=torch.zeros((h, capacity, d), device=dev, dtype=key.dtype),
-        active_length=0, capacity=capacity,
-        length_device=torch.zeros((), device=dev, dtype=torch.int32),
+        active_length=0, capacity=capacity, length_device=length,
         global_index_buffer=gbuf, logical_position_buffer=lbuf,
     )
 
@@ -830,18 +977,23 @@ def build_three_precision_cache(
     key = key.contiguous()
     value = value.contiguous()
     dev = key.device
-    fp_l, i4_l, i2_l, rec_l, ev_l = _compact_page_layouts(plan, dev)
-    if sum(int(l[0].numel()) for l in (fp_l, i4_l, i2_l, ev_l)) != int(key.shape[1]):
+    tab = _tier_page_table(plan)
+    if int(tab.tier_tokens.sum()) != int(key.shape[1]):
         raise ValueError("compact physical pools must cover every logical token")
+    if plan.recent_fp_capacity < page_size or plan.recent_fp_capacity % page_size:
+        raise ValueError("Recent-FP capacity must be positive and page aligned")
     h = int(key.shape[0])
     stream = _lib.stream_of(dev)
     append_capacity = plan.recent_fp_capacity if compact_key_append_capacity is None \
         else int(compact_key_append_capacity)
     gi = plan.global_token_indices.detach().to(dev, torch.long)
     lp = plan.logical_positions.detach().to(dev, torch.long)
-    common = dict(evicted_global_indices=gi[ev_l[0]], page_size=int(page_size),
-                  quantization_superblock=int(quantization_superblock), cache_variant=cache_variant,
-                  recent_flush_size=int(recent_flush_size), generated_value_precision="int2")
+    tokens = _expand_tier_tokens(tab, dev)
+    s_fp, s_i4, s_i2 = (int(n) for n in tab.tier_tokens[:3])
+    n_surv = s_fp + s_i4 + s_i2
+    common = dict(page_size=int(page_size), quantization_superblock=int(quantization_superblock),
+                  cache_variant=cache_variant, recent_flush_size=int(recent_flush_size),
+                  generated_value_precision="int2")
     if matched_fp:  # every surviving page, K and V in bf16, in one FP pool (precision_pool.py:834-876)
         surv = _survivor_layout(plan, dev)
         n = int(surv[0].numel())
@@ -856,40 +1008,49 @@ def build_three_precision_cache(
         return ThreePrecisionCache(
             fp_pool=fp_pool, int4_pool=PrecisionPool(name="int4", page_index=_make_page_index(empty, gi, lp)),
             int2_pool=PrecisionPool(name="int2", page_index=_make_page_index(empty, gi, lp)),
-            recent_fp_pool=recent, matched_fp=True, bf16_key=arena, generated_k_offset=n, **common)
-    fp_tokens, i4_tokens, i2_tokens = fp_l[0], i4_l[0], i2_l[0]
-    s_fp, s_i4 = int(fp_tokens.numel()), int(i4_tokens.numel())
+            recent_fp_pool=recent, matched_fp=True, bf16_key=arena, generated_k_offset=n,
+            evicted_global_indices=gi[tokens[n_surv:]], **common)
+    fp_tokens, i4_tokens, i2_tokens = tokens[:s_fp], tokens[s_fp:s_fp + s_i4], tokens[s_fp + s_i4:n_surv]
 
-    fp_pool = PrecisionPool(name="fp", page_index=_make_page_index(fp_l, gi, lp))
+    fp_v = int4_v = None
     if s_fp:
-        fp_pool.fp_v = torch.empty((h, s_fp, 128), device=dev, dtype=value.dtype)
+        fp_v = torch.empty((h, s_fp, 128), device=dev, dtype=value.dtype)
         _lib.call("r2o_gather_rows", _lib.ptr(value), h, int(value.shape[1]), _lib.ptr(fp_tokens), s_fp,
-                  _lib.ptr(fp_pool.fp_v), s_fp, stream)
-    int4_pool = PrecisionPool(name="int4", page_index=_make_page_index(i4_l, gi, lp))
+                  _lib.ptr(fp_v), s_fp, stream)
     if s_i4:
-        int4_pool.packed_v = fused_gather_pack_int4_value(value, i4_tokens)
-    int2_pool = PrecisionPool(name="int2", page_index=_make_page_index(i2_l, gi, lp))
+        int4_v = fused_gather_pack_int4_value(value, i4_tokens)
     compact_value = build_compact_int2_value_arena(value, i2_tokens, append_capacity=append_capacity,
                                                    group_size=int2_group_size)
-    int2_pool.packed_v = compact_value
-    recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity)
+    compact_key = bf16_arena = None
     if bf16_keys:  # v_fourq_k_bf16: every pool keeps bf16 K rows (precision_pool.py:878-906)
-        s_i2 = int(i2_tokens.numel())
-        arena = _gather_key_rows(key, torch.cat((fp_tokens, i4_tokens, i2_tokens)), append_capacity,
-                                 (0, s_fp, s_fp + s_i4))
-        fp_pool.fp_k, int4_pool.fp_k = arena.view(0, s_fp), arena.view(s_fp, s_i4)
-        int2_pool.fp_k = arena.view(s_fp + s_i4, s_i2)
+        bf16_arena = _gather_key_rows(key, tokens[:n_surv], append_capacity, (0, s_fp, s_fp + s_i4))
+        reserve = 0  # no compact K arena to flush into (precision_pool.py:404-408)
+    else:
+        build_key = build_compact_int2_key_arena if cache_variant == "v_fourq_k_int2_compact" \
+            else build_compact_int4_key_arena
+        compact_key = build_key(key, (fp_tokens, i4_tokens, i2_tokens), append_capacity=append_capacity,
+                                superblock_size=key_quantization_superblock)
+        reserve = min(compact_value.capacity - compact_value.active_length,
+                      compact_key.capacity - compact_key.active_length) // page_size * page_size
+    meta, (fp_pi, i4_pi, i2_pi, ring_pi), evicted, (ring_g, ring_l, ring_len) = _build_metadata_arena(
+        tab, tokens, gi, lp, page_size=page_size, recent_capacity=plan.recent_fp_capacity, int2_reserve=reserve)
+    fp_pool = PrecisionPool(name="fp", page_index=fp_pi, fp_v=fp_v)
+    int4_pool = PrecisionPool(name="int4", page_index=i4_pi, packed_v=int4_v)
+    int2_pool = PrecisionPool(name="int2", page_index=i2_pi, packed_v=compact_value)
+    recent = _preallocate_recent_pool("recent_fp", key, page_size=page_size, capacity=plan.recent_fp_capacity,
+                                      metadata=(ring_pi, ring_g, ring_l, ring_len))
+    if bf16_keys:
+        fp_pool.fp_k, int4_pool.fp_k = bf16_arena.view(0, s_fp), bf16_arena.view(s_fp, s_i4)
+        int2_pool.fp_k = bf16_arena.view(s_fp + s_i4, s_i2)
         return ThreePrecisionCache(
             fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
-            compact_value=compact_value, static_int4_tokens=s_i4, bf16_key=arena, **common)
-    build_key = build_compact_int2_key_arena if cache_variant == "v_fourq_k_int2_compact" \
-        else build_compact_int4_key_arena
-    compact_key = build_key(key, (fp_tokens, i4_tokens, i2_tokens), append_capacity=append_capacity,
-                            superblock_size=key_quantization_superblock)
+            compact_value=compact_value, static_int4_tokens=s_i4, bf16_key=bf16_arena, metadata_arena=meta,
+            evicted_global_indices=evicted, **common)
     return ThreePrecisionCache(
         fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
         compact_key=compact_key, compact_value=compact_value, static_int4_tokens=s_i4,
-        generated_k_offset=compact_key.active_length, **common)
+        generated_k_offset=compact_key.active_length, metadata_arena=meta, evicted_global_indices=evicted,
+        **common)
 
 
 # ------------------------------------------------------------------------- append / flush
@@ -938,9 +1099,10 @@ def flush_full_recent_pool(cache: ThreePrecisionCache, stats: DynamicCacheStats)
     stream = _lib.stream_of(pool.fp_k.device)
     key_block = pool.fp_k[:, :flush]
     value_block = pool.fp_v[:, :flush]
-    # copy the index slices before the ring shift overwrites them
-    global_block = pool.global_index_buffer[:flush].clone()
-    logical_block = pool.logical_position_buffer[:flush].clone()
+    # Views of the ring's oldest indices: every consumer below copies them on this stream before
+    # the ring shift is launched, so no snapshot is needed.
+    global_block = pool.global_index_buffer[:flush]
+    logical_block = pool.logical_position_buffer[:flush]
     if cache.matched_fp:  # _append_matched_fp_block (dynamic_fourq_cache.py:145-170)
         _append_int2_page_metadata(cache.fp_pool, global_block, logical_block, cache.page_size)
         cache.bf16_key.append_block(key_block)
@@ -958,7 +1120,10 @@ def flush_full_recent_pool(cache: ThreePrecisionCache, stats: DynamicCacheStats)
         stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
             if flush == 128 else _flush_size_error(flush)
         cache.compact_value.append_superblock(value_block, source_tokens=cap)
-        _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
+        if cache.metadata_arena is not None:  # in place (dynamic_fourq_cache.py:236-239)
+            cache.metadata_arena.append_int2_pages(cache.int2_pool, global_block, logical_block, cache.page_size)
+        else:
+            _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
     _lib.call("r2o_recent_shift", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, flush, pool.active_length,
               _lib.ptr(pool.global_index_buffer), _lib.ptr(pool.logical_position_buffer),
               _lib.ptr(pool.length_device), _lib.ptr(pool.page_index.lengths), cache.page_size, stream)
