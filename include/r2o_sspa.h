@@ -32,6 +32,7 @@ extern "C" {
 #define R2O_HEAD_DIM 128
 #define R2O_MAX_GQA 16
 #define R2O_MAX_BATCH 32
+#define R2O_MAX_HEADS 4096 /* query heads per decode launch */
 
 /* r2o_decode_params.k_format */
 #define R2O_K_INT4 0

@@ -25,6 +25,16 @@ __device__ __forceinline__ T r2o_ldg(const T* p) {
     return *(const R2O_GLOBAL T*)p;
 }
 
+// a / b for 0 <= a < 2^22 and 1 <= b < 2^22 (head counts, head indices): the truncated product
+// with the reciprocal estimate is within one of the quotient (relative error below 2^-22), and one
+// remainder step each way corrects it; a few instructions in place of the integer division sequence.
+__device__ __forceinline__ int r2o_div_small(int a, int b) {
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
+    const int r = a - q * b;
+    q += (r >= b) - (r < 0);
+    return q;
+}
+
 // ------------------------------------------------------------------ element conversions
 __device__ __forceinline__ float r2o_bf16_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
@@ -102,19 +112,78 @@ __device__ __forceinline__ uint32_t r2o_pack_bf2(float lo, float hi) {
     return r2o_f32_to_bf16(lo) | (r2o_f32_to_bf16(hi) << 16);
 }
 
-// Orthonormal 128-point FWHT of a row held by one wave: lane t holds x[t] in y0 and x[t + 64]
-// in y1.  Stride 64 is a butterfly inside the lane, strides 32 .. 1 are lane-xor butterflies.
+// Cross-lane exchanges through the VALU, in place of the LDS-unit permute behind __shfl_xor:
+// DPP within rows of 16 lanes, gfx950's v_permlane16_swap / v_permlane32_swap across rows.
+template <int CTRL>
+__device__ __forceinline__ float r2o_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// The value of lane (lane ^ M), M = 1, 2, 4 or 8.
+template <int M>
+__device__ __forceinline__ float r2o_lane_xor(float x) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8, "in-row exchange");
+    if constexpr (M == 1) return r2o_dpp<0xB1>(x);  // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) return r2o_dpp<0x4E>(x);  // quad_perm [2,3,0,1]
+    else if constexpr (M == 4) return r2o_dpp<0x1B>(r2o_dpp<0x141>(x));  // half-row mirror, then quad reverse
+    else return r2o_dpp<0x128>(x);  // row_ror:8
+}
+
+// x swapped with itself across the M = 16 or 32 boundary: lanes below it get (first, second) =
+// (x, x of lane ^ M), lanes above it (x of lane ^ M, x).
+template <int M>
+__device__ __forceinline__ void r2o_row_swap(float x, float& first, float& second) {
+    static_assert(M == 16 || M == 32, "cross-row exchange");
+    const uint32_t u = __float_as_uint(x);
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        first = __uint_as_float(r[0]);
+        second = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        first = __uint_as_float(r[0]);
+        second = __uint_as_float(r[1]);
+    }
+}
+
+// x + (x of lane ^ M), the same value in both lanes of a pair, for M = 16 or 32.
+template <int M>
+__device__ __forceinline__ float r2o_sum_lane_pair(float x) {
+    float a, b;
+    r2o_row_swap<M>(x, a, b);
+    return a + b;
+}
+
+// One butterfly stage of the FWHT over lanes: lane t without bit M keeps y + y', with it y' - y,
+// where y' is lane t ^ M's value.
+template <int M>
+__device__ __forceinline__ void r2o_fwht_stage(float& y0, float& y1, int t) {
+    const bool upper = (t & M) != 0;
+    if constexpr (M < 16) {
+        const float o0 = r2o_lane_xor<M>(y0), o1 = r2o_lane_xor<M>(y1);
+        y0 = upper ? o0 - y0 : y0 + o0;
+        y1 = upper ? o1 - y1 : y1 + o1;
+    } else {
+        float a0, b0, a1, b1;
+        r2o_row_swap<M>(y0, a0, b0);
+        r2o_row_swap<M>(y1, a1, b1);
+        y0 = upper ? a0 - b0 : a0 + b0;
+        y1 = upper ? a1 - b1 : a1 + b1;
+    }
+}
+
+// Orthonormal 128-point FWHT of a row held by one full wave: lane t holds x[t] in y0 and x[t + 64]
+// in y1.  Stride 64 is a butterfly inside the lane, strides 1 .. 32 are lane-xor butterflies.
 __device__ __forceinline__ void r2o_fwht128_pair(float& y0, float& y1, int t) {
     const float s0 = y0 + y1, s1 = y0 - y1;
     y0 = s0;
     y1 = s1;
-#pragma unroll
-    for (int stride = 1; stride < 64; stride <<= 1) {
-        const float o0 = __shfl_xor(y0, stride, R2O_WAVE), o1 = __shfl_xor(y1, stride, R2O_WAVE);
-        const bool upper = (t & stride) != 0;
-        y0 = upper ? o0 - y0 : y0 + o0;
-        y1 = upper ? o1 - y1 : y1 + o1;
-    }
+    r2o_fwht_stage<1>(y0, y1, t);
+    r2o_fwht_stage<2>(y0, y1, t);
+    r2o_fwht_stage<4>(y0, y1, t);
+    r2o_fwht_stage<8>(y0, y1, t);
+    r2o_fwht_stage<16>(y0, y1, t);
+    r2o_fwht_stage<32>(y0, y1, t);
     y0 *= 0.08838834764831845f;
     y1 *= 0.08838834764831845f;
 }

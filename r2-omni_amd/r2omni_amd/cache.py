@@ -733,6 +733,13 @@ class _TierTable(NamedTuple):
     tier_tokens: np.ndarray  # [4] tokens per tier
 
 
+# tier of each PageClass value: FP (+protected, recent) 0, INT4 1, INT2 2, evicted 3
+_TIER_OF_CLASS = np.zeros(max(int(c) for c in PageClass) + 1, dtype=np.int64)
+for _c, _t in ((PageClass.EVICTED_PAGE, 3), (PageClass.FP_PAGE, 0), (PageClass.PROTECTED_FP_PAGE, 0),
+               (PageClass.RECENT_FP_PAGE, 0), (PageClass.INT4_PAGE, 1), (PageClass.INT2_PAGE, 2)):
+    _TIER_OF_CLASS[int(_c)] = _t
+
+
 def _tier_page_table(plan: LayerCompressionPlan) -> _TierTable:
     """Pages stably sorted by tier, each keeping its token order (precision_pool.py:611-669).
 
@@ -744,20 +751,19 @@ def _tier_page_table(plan: LayerCompressionPlan) -> _TierTable:
         table = torch.stack((plan.page_classes.detach().to(torch.long), plan.page_offsets.detach().to(torch.long),
                              plan.page_lengths.detach().to(torch.long))).to("cpu")
     classes, starts, lens = table.numpy()
-    cat = np.full(classes.shape, 3, dtype=np.int64)
-    cat[np.isin(classes, (int(PageClass.FP_PAGE), int(PageClass.PROTECTED_FP_PAGE), int(PageClass.RECENT_FP_PAGE)))] = 0
-    cat[classes == int(PageClass.INT4_PAGE)] = 1
-    cat[classes == int(PageClass.INT2_PAGE)] = 2
-    pages = np.argsort(cat, kind="stable")
+    if classes.size and (int(classes.min()) < 0 or int(classes.max()) >= _TIER_OF_CLASS.size):
+        raise ValueError("page_classes holds a value that is not a PageClass")
+    cat = _TIER_OF_CLASS[classes]
+    groups = [np.flatnonzero(cat == t) for t in range(4)]
+    counts = np.array([g.size for g in groups], dtype=np.int64)
+    pages = np.concatenate(groups)
+    first_page = np.concatenate(([0], np.cumsum(counts)))
     pl = lens[pages]
-    tier = cat[pages]
-    first_page = np.concatenate(([0], np.cumsum(np.bincount(tier, minlength=4)[:4])))
-    glob_off = np.cumsum(pl) - pl  # offset of each page in the tier-ordered concatenation
-    tier_tok = np.bincount(tier, weights=pl, minlength=4)[:4].astype(np.int64)
-    tier_start = np.concatenate(([0], np.cumsum(tier_tok)[:-1]))
-    return _TierTable(pages=pages.astype(np.int64), offsets=(glob_off - tier_start[tier]).astype(np.int64),
-                      lengths=pl.astype(np.int64), shift=(starts[pages] - glob_off).astype(np.int64),
-                      first_page=first_page.astype(np.int64), tier_tokens=tier_tok)
+    end = np.cumsum(pl)
+    glob_off = end - pl  # offset of each page in the tier-ordered concatenation
+    bounds = np.concatenate(([0], end))[first_page]
+    return _TierTable(pages=pages, offsets=glob_off - np.repeat(bounds[:-1], counts), lengths=pl,
+                      shift=starts[pages] - glob_off, first_page=first_page, tier_tokens=np.diff(bounds))
 
 
 def _expand_tier_tokens(tab: _TierTable, device) -> torch.Tensor:
