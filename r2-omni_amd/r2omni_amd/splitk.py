@@ -31,6 +31,13 @@ _BLOCKS_PER_CU = 2           # work items planned per CU (the kernel holds up to
 # items would only add partial states for the combine (measured on MI355X: a 3B layer at 32k
 # tokens takes 13.0 us per call at 256 items against 14.9 at 512).
 _TILES_PER_ITEM_TARGET = 8
+# Two workgroups share each CU (slots j and j + CUs of the launch), and the hardware favours the
+# older one: with equal work the later-launched sibling ends ~20 % after it (measured on MI355X for
+# an all-INT2 131k-token layer: 6 us of a 30 us kernel with the CU half occupied).  When every item
+# is of one kind, the items split from a run are therefore uneven: the later-launched half gets
+# this share of the work of the earlier half.  Plans that mix kinds already launch their larger
+# items first and keep an even split (an uneven one measured 1 us slower on the mixed-tier layer).
+_LATE_SHARE = 0.7
 
 
 @dataclass
@@ -81,7 +88,8 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
 
     The partial kernel runs two 4-wave workgroups per CU, so the plan aims at no more than
     2 x CUs items of about equal cost (tiles weighted by kind), each a multiple of 4 tiles (one
-    share per wave): all items then start together and finish together.  A small cache aims at
+    share per wave): all items then start together and finish together (a single-kind plan that
+    puts two items on each CU splits its runs unevenly, see _LATE_SHARE).  A small cache aims at
     about _TILES_PER_ITEM_TARGET tiles per item instead, but at no fewer than CUs items.  Items keep a partial
     slot in (request, kv head) order, so the combine reads one contiguous slot range per group,
     and are launched largest first.
@@ -120,6 +128,8 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
         counts[i] += 1
         total += 1
         heapq.heappush(heap, (-item_cost(i), i))
+    uniform = len({r[2] for r in runs if r[2] != _lib.KIND_RECENT}) == 1
+    late_share = _LATE_SHARE if uniform and total > cus else 1.0
     items = []
     begins = [0]
     group = (0, 0)
@@ -127,12 +137,40 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
         if (r, h) != group:
             begins.append(len(items))
             group = (r, h)
-        n = -(-(-(-nt // n_items)) // _WAVES_PER_ITEM) * _WAVES_PER_ITEM  # even split, a share per wave
-        for first in range(0, nt, n):
-            items.append([r, h, kind, t0 + TILE * first, min(n, nt - first), lo, hi, vd, len(items)])
+        for first, size in _split_run(nt, n_items, late_share):
+            items.append([r, h, kind, t0 + TILE * first, size, lo, hi, vd, len(items)])
     begins.append(len(items))
     items.sort(key=lambda it: -it[4] * _TILE_COST[it[2]])  # stable: largest first, ties keep slot order
     return torch.tensor(items, dtype=torch.int64), torch.tensor(begins, dtype=torch.int32)
+
+
+def _split_run(nt: int, n_items: int, late_share: float = 1.0):
+    """(first tile, tiles) of the items of one run: multiples of a wave share each, all but the
+    last; with late_share < 1 the second half of the items gets that share of the first half's."""
+    w = _WAVES_PER_ITEM
+    if late_share >= 1.0 or n_items < 2:
+        n = -(-(-(-nt // n_items)) // w) * w  # even split, a share per wave
+        return [(f, min(n, nt - f)) for f in range(0, nt, n)]
+    big = -(-n_items // 2)
+    small = n_items - big
+    x = nt / (big + late_share * small)
+    bsize = -(-int(round(x)) // w) * w
+    out, f = [], 0
+    for k in range(n_items):
+        if f >= nt:
+            break
+        if k < big:
+            size = bsize
+        else:
+            left = n_items - k
+            size = -(-(-(-(nt - f) // left)) // w) * w
+        size = min(size, nt - f)
+        out.append((f, size))
+        f += size
+    if f < nt:  # rounding left a remainder: extend the last item
+        last_f, last_s = out[-1]
+        out[-1] = (last_f, last_s + nt - f)
+    return out
 
 
 def max_work_items(num_requests: int, hkv: int, num_cus: int) -> int:

@@ -52,3 +52,19 @@ def test_items_cover_every_tile_once_and_respect_the_bound(seed):
     # launch order: largest (cost-weighted) first
     costs = [it[4] * _TILE_COST[it[2]] for it in items]
     assert all(a >= b for a, b in zip(costs, costs[1:]))
+
+
+@pytest.mark.parametrize("nt,n_items,share", [(4096, 64, 0.7), (4097, 63, 0.7), (100, 3, 0.7), (37, 2, 0.7),
+                                              (8, 2, 0.7), (5, 2, 0.7), (4096, 64, 1.0), (130, 7, 0.5)])
+def test_split_run_covers_the_run_with_wave_shares(nt, n_items, share):
+    from r2omni_amd.splitk import _WAVES_PER_ITEM, _split_run
+    items = _split_run(nt, n_items, share)
+    assert 1 <= len(items) <= n_items
+    assert items[0][0] == 0 and sum(s for _, s in items) == nt
+    assert all(f2 == f1 + s1 for (f1, s1), (f2, _) in zip(items, items[1:]))
+    assert all(s > 0 and s % _WAVES_PER_ITEM == 0 for _, s in items[:-1])
+    if share < 1.0 and nt >= 64 * n_items:  # the later half gets about `share` of the earlier half's work
+        big = items[: -(-n_items // 2)]
+        small = items[-(-n_items // 2):-1]
+        ratio = (sum(s for _, s in small) / len(small)) / (sum(s for _, s in big) / len(big))
+        assert abs(ratio - share) < 0.1
