@@ -62,7 +62,7 @@ typedef struct r2o_request_desc {
     const uint16_t* i2_scale;     /* fp16 [Hkv, i2_stride, 128/G]                                */
     const uint8_t* i2_zero;       /* u8   [Hkv, i2_stride, 128/G]                                */
     int64_t i2_stride;
-    uint16_t* recent_k;           /* bf16 [Hkv, recent_capacity, 128]  Recent-FP ring            */
+    uint16_t* recent_k;           /* bf16 [Hkv, recent_capacity, 128]  Recent-FP ring, 16-byte aligned */
     uint16_t* recent_v;
     int64_t recent_capacity;
     int32_t* recent_length;       /* device int32 active length (written by the fused append)   */
@@ -107,7 +107,8 @@ typedef struct r2o_decode_params {
     float* partial_out;             /* device f32 [n_items, 16, 128], 16-byte aligned  */
     const uint16_t* query;          /* device [batch, hq, 128] (dtype q_dtype)         */
     uint16_t* out;                  /* device bf16 [batch, hq, 128]                    */
-    const uint16_t* append_k;       /* device bf16 [batch, hkv, 128] or NULL           */
+    const uint16_t* append_k;       /* device bf16 [batch, hkv, 128] or NULL; 16-byte
+                                       aligned, and hkv <= 128 when do_append is set  */
     const uint16_t* append_v;
     int64_t* step_positions;        /* device int64 [batch, 2] or NULL.  Non-NULL selects device-state
                                        mode: both kernels read each ring length from

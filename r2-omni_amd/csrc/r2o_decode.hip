@@ -815,21 +815,48 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
 // Fused Recent-FP append (triton_fourq_splitk.py:1007-1020) of every KV head of request b, by one
 // extra block of the combine grid: no merge block reads the ring, and this block is the only reader
 // and writer of the ring length (and, in device-state mode, of the step positions) during the launch.
-__device__ void fused_append(const r2o_decode_params& p, int64_t b, int tid) {
+// 16-byte pieces of one token's K (or V) rows of every KV head that each combine thread moves:
+// 4 x 512 threads cover hkv <= 128 (checked on the host).
+constexpr int kAppendPieces = 4;
+
+__device__ __forceinline__ void fused_append(const r2o_decode_params& p, int64_t b, int tid) {
     const r2o_request_desc& rq = p.reqs[b];
-    const int64_t pos = p.step_positions ? (int64_t)*rq.recent_length : p.recent_len[b];
-    if (pos >= rq.recent_capacity) return;  // a full ring takes no append (the host flushes first)
-    for (int e = tid; e < p.hkv * 128; e += blockDim.x) {
-        const int64_t hh = e >> 7, d = e & 127;
-        const int64_t dst = (hh * rq.recent_capacity + pos) * 128 + d, src = (b * p.hkv + hh) * 128 + d;
-        rq.recent_k[dst] = p.append_k[src];
-        rq.recent_v[dst] = p.append_v[src];
+    // Every load that does not depend on the ring position is issued before it is known: the
+    // appended rows (16 bytes a piece) and this step's (global, logical) positions.
+    const int pieces = (int)p.hkv * 16;
+    const r2o_u4* src_k = reinterpret_cast<const r2o_u4*>(p.append_k + b * p.hkv * 128);
+    const r2o_u4* src_v = reinterpret_cast<const r2o_u4*>(p.append_v + b * p.hkv * 128);
+    r2o_u4 rk[kAppendPieces], rv[kAppendPieces];
+#pragma unroll
+    for (int k = 0; k < kAppendPieces; ++k) {  // unconditional loads (clamped index), guarded stores
+        const int e = min(tid + k * (int)blockDim.x, pieces - 1);
+        rk[k] = r2o_ldg(src_k + e);
+        rv[k] = r2o_ldg(src_v + e);
     }
+    int64_t gidx = 0, lpos = 0;
     if (tid == 0) {
-        int64_t gidx = p.append_global[b], lpos = p.append_logical[b];
         if (p.step_positions) {  // this step's positions, advanced for the next replay
             gidx = p.step_positions[2 * b];
             lpos = p.step_positions[2 * b + 1];
+        } else {
+            gidx = p.append_global[b];
+            lpos = p.append_logical[b];
+        }
+    }
+    const int64_t pos = p.step_positions ? (int64_t)*rq.recent_length : p.recent_len[b];
+    if (pos >= rq.recent_capacity) return;  // a full ring takes no append (the host flushes first)
+#pragma unroll
+    for (int k = 0; k < kAppendPieces; ++k) {
+        const int e = tid + k * (int)blockDim.x;
+        if (e < pieces) {
+            const int64_t hh = e >> 4, c = e & 15;
+            const int64_t row = (hh * rq.recent_capacity + pos) * 16 + c;  // in 16-byte pieces
+            reinterpret_cast<r2o_u4*>(rq.recent_k)[row] = rk[k];
+            reinterpret_cast<r2o_u4*>(rq.recent_v)[row] = rv[k];
+        }
+    }
+    if (tid == 0) {
+        if (p.step_positions) {
             p.step_positions[2 * b] = gidx + 1;
             p.step_positions[2 * b + 1] = lpos + 1;
         }
@@ -938,6 +965,10 @@ int validate(const r2o_decode_params* p) {
     if (p->page_size <= 0) return R2O_EINVAL;
     if (p->k_format != kKInt4 && p->k_format != kKBf16 && p->k_format != kKInt2) return R2O_EINVAL;
     if (p->do_append && (!p->append_k || !p->append_v)) return R2O_EINVAL;
+    // the fused append moves the new rows in 16-byte pieces, 4 per thread of a 512-thread block
+    if (p->do_append && (p->hkv > 128 || reinterpret_cast<uintptr_t>(p->append_k) % 16 ||
+                         reinterpret_cast<uintptr_t>(p->append_v) % 16))
+        return R2O_EINVAL;
     if (reinterpret_cast<uintptr_t>(p->partial_out) % 16) return R2O_EINVAL;  // 16-byte vector rows
     return R2O_OK;
 }

@@ -367,6 +367,8 @@ class SplitKExecutor:
                 raise ValueError("append K/V must be contiguous [B,Hkv,1,D] or [B,Hkv,D]")
             if ak.dtype != torch.bfloat16 or av.dtype != torch.bfloat16:
                 raise ValueError("append K/V must be bfloat16 like the Recent-FP ring")
+            if ak.data_ptr() % 16 or av.data_ptr() % 16:  # the kernel moves the rows in 16-byte pieces
+                ak, av = ak.clone(), av.clone()
             for c in self.caches:
                 rec = c.recent_fp_pool
                 if rec.active_length is None or rec.active_length >= rec.capacity:
