@@ -188,6 +188,13 @@ def test_decode_long_group_combine():
         _compare(out, want, f"long group call {call}")
 
 
+def _misaligned(t):
+    """The same values as a contiguous view whose data pointer is one element past t's storage start."""
+    buf = torch.empty(t.numel() + 1, device=t.device, dtype=t.dtype)
+    buf[1:] = t.flatten()
+    return buf[1:].view(t.shape)
+
+
 @pytest.mark.parametrize("variant", ["int4k", "int2k"])
 def test_fused_append_then_flush_matches_oracle(variant):
     import r2omni_amd as ro
@@ -213,7 +220,10 @@ def test_fused_append_then_flush_matches_oracle(variant):
         pos = hist + step
         rec = cache.recent_fp_pool
         if rec.active_length < rec.capacity:
-            out = ex(q, append=(k, v, pos, pos))
+            # odd steps pass the rows as views 2 bytes past a 16-byte boundary (copied by the executor)
+            ka, va = (_misaligned(k), _misaligned(v)) if step % 2 else (k, v)
+            assert (ka.data_ptr() % 16 != 0) == bool(step % 2)
+            out = ex(q, append=(ka, va, pos, pos))
             rec.active_length += 1  # the caller advances the host length after a fused append
             kf, vf = bf16_bits_to_f32(_bf16_np(k[0])), bf16_bits_to_f32(_bf16_np(v[0]))
             want = mixed_reference(bf16_bits_to_f32(_bf16_np(q)), oc, append=(kf, vf))
