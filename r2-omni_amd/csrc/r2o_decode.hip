@@ -872,7 +872,7 @@ __device__ __forceinline__ void fused_append(const r2o_decode_params& p, int64_t
 // load of a round issued before any is used, so a group of up to 128 partials costs one memory
 // round trip;
 // the 16 slice states then merge through LDS in wave 0, which also runs the output FWHT with
-// lane shuffles.  Every merge is the exact fp32 softmax-state merge
+// DPP and permlane butterflies.  Every merge is the exact fp32 softmax-state merge
 // (triton_fourq_attention.py:58-69; triton_fourq_splitk.py:977-999).
 constexpr int kCombineSlices = 16;
 #ifndef R2O_COMBINE_UNROLL

@@ -36,7 +36,7 @@ struct RopeArgs {
 
 __global__ __launch_bounds__(256) void qk_mrope_kernel(RopeArgs a) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= a.rows) return;  // whole-wave exit: the FWHT shuffles stay within live waves
+    if (row >= a.rows) return;  // whole-wave exit: the FWHT's cross-lane butterflies need every lane of a live wave
     const int t = threadIdx.x & 63;
     const int64_t per_req = (a.hq + a.hkv) * a.tokens;
     const int64_t b = row / per_req, local = row % per_req;
@@ -95,7 +95,7 @@ struct NormRopeArgs {
 //   optional FWHT-128 of y in fp32 (triton_fwht_128), rounded to dtype.
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= a.rows) return;  // whole-wave exit: the shuffles stay within live waves
+    if (row >= a.rows) return;  // whole-wave exit: the cross-lane sums and butterflies need every lane of a live wave
     const int t = threadIdx.x & 63;
     const int64_t per_req = (a.hq + a.hkv) * a.tokens;
     const int64_t b = row / per_req, local = row % per_req;
