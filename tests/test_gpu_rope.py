@@ -119,3 +119,68 @@ def test_qwen3_qk_norm_rope_rejects_mismatched_arguments():
         ro.qwen3_qk_norm_rope(q, k, w.float(), w, cs, cs)
     with pytest.raises(ValueError, match="rank-4"):
         ro.qwen3_qk_norm_rope(q[0], k, w, w, cs, cs)
+
+
+def _butterfly_fwht_f32(x):
+    """float32 FWHT-128 in the kernel's stage order: the stride-64 butterfly first (both halves
+    of a row sit in one lane), then strides 1 .. 32 with lane t ^ s as partner, the upper lane
+    taking partner - own; then the 1/sqrt(128) scale.  Every step is one IEEE float32 operation."""
+    y = np.asarray(x, dtype=np.float32)
+    a, b = y[:, :64].copy(), y[:, 64:].copy()
+    y = np.concatenate([a + b, a - b], axis=1)
+    idx = np.arange(128)
+    for s in (1, 2, 4, 8, 16, 32):
+        o = y[:, idx ^ s]
+        y = np.where((idx & s) != 0, o - y, y + o).astype(np.float32)
+    return y * np.float32(0.08838834764831845)
+
+
+def _exact_where_normal(got, want32, dtype):
+    """Bit equality of got with want32 rounded to dtype, outside fp16's subnormal range."""
+    want = torch.from_numpy(np.ascontiguousarray(want32)).to(dtype)
+    normal = torch.from_numpy(np.abs(want32) >= (2.0 ** -14 if dtype == torch.float16 else 0.0))
+    return torch.equal(got.cpu().view(torch.int16)[normal], want.view(torch.int16)[normal])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fwht128_is_the_reference_stage_order_bit_exact(dtype):
+    """triton_fwht_128 (r2o_fwht128) runs the reference's stages (stride 1 .. 64, left + right and
+    left - right, then the float32 scale): bit-exact to the oracle's float32 restatement of
+    that order, rounded once to the dtype."""
+    import r2omni_amd as ro
+    from oracle.quant import normalized_fwht
+
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    gen = torch.Generator().manual_seed(21)
+    x = (torch.randn(1024, 128, generator=gen) * 4).to(dtype)
+    got = ro.triton_fwht_128(x.to("cuda:0"))
+    torch.cuda.synchronize()
+    assert _exact_where_normal(got, normalized_fwht(_np32(x)), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_lane_butterflies_are_bit_exact(dtype):
+    """The in-register FWHT of the mRoPE and combine kernels (DPP within rows, permlane swaps
+    across rows): with identity tables (cos 1, sin 0) the mRoPE output is that FWHT of the input,
+    bit-exact to its stage order (stride 64 in the lane, then strides 1 .. 32) evaluated in
+    float32 on the CPU, and within one output rounding of the reference's order."""
+    import r2omni_amd as ro
+    from oracle.quant import normalized_fwht
+
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(22)
+    q = (torch.randn(2, 28, 3, 128, generator=gen) * 4).to(dtype)
+    k = (torch.randn(2, 4, 3, 128, generator=gen) * 4).to(dtype)
+    cos = torch.ones(3, 2, 3, 128, dtype=torch.float32, device=dev)
+    sin = torch.zeros(3, 2, 3, 128, dtype=torch.float32, device=dev)
+    qo, ko = ro.qwen_qk_mrope(q.to(dev), k.to(dev), cos, sin, (16, 24, 24), apply_hadamard=True)
+    torch.cuda.synchronize()
+    for got, x in ((qo, q), (ko, k)):
+        rows = _np32(x).reshape(-1, 128)
+        assert _exact_where_normal(got.reshape(-1, 128), _butterfly_fwht_f32(rows), dtype)
+        ref = normalized_fwht(rows)
+        step = np.abs(ref) * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-4
+        assert np.all(np.abs(_np32(got).reshape(-1, 128) - ref) <= step)
