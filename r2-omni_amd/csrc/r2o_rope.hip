@@ -24,13 +24,15 @@ __device__ __forceinline__ float load_table(const void* base, int code, int64_t 
 struct RopeArgs {
     const uint16_t* q;
     const uint16_t* k;
+    const uint16_t* v;  // nullable: V rows take the FWHT alone
     uint16_t* q_out;
     uint16_t* k_out;
+    uint16_t* v_out;
     const void* cos;
     const void* sin;
     int64_t cs[4];  // cos strides (axis, batch, token, dim) in elements
     int64_t ss[4];  // sin strides
-    int64_t hq, hkv, tokens, rows;
+    int64_t hq, hkv, hv, tokens, rows;  // hv: V heads (hkv with V rows, else 0)
     int dtype, table_code, s0, s1, hadamard;
 };
 
@@ -38,15 +40,23 @@ __global__ __launch_bounds__(256) void qk_mrope_kernel(RopeArgs a) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.rows) return;  // whole-wave exit: the FWHT's cross-lane butterflies need every lane of a live wave
     const int t = threadIdx.x & 63;
-    const int64_t per_req = (a.hq + a.hkv) * a.tokens;
+    const int64_t per_req = (a.hq + a.hkv + a.hv) * a.tokens;
     const int64_t b = row / per_req, local = row % per_req;
     const int64_t head = local / a.tokens, token = local % a.tokens;
-    const bool is_q = head < a.hq;
-    const int64_t off = is_q ? ((b * a.hq + head) * a.tokens + token) * 128 : ((b * a.hkv + head - a.hq) * a.tokens + token) * 128;
-    const uint16_t* src = is_q ? a.q : a.k;
-    uint16_t* dst = is_q ? a.q_out : a.k_out;
+    const bool is_q = head < a.hq, is_v = head >= a.hq + a.hkv;
+    const int64_t kv_head = is_v ? head - a.hq - a.hkv : head - a.hq;
+    const int64_t off = is_q ? ((b * a.hq + head) * a.tokens + token) * 128 : ((b * a.hkv + kv_head) * a.tokens + token) * 128;
+    const uint16_t* src = is_q ? a.q : (is_v ? a.v : a.k);
+    uint16_t* dst = is_q ? a.q_out : (is_v ? a.v_out : a.k_out);
     const float x0 = a.dtype == 0 ? r2o_bf16_to_f32(src[off + t]) : r2o_f16_to_f32(src[off + t]);
     const float x1 = a.dtype == 0 ? r2o_bf16_to_f32(src[off + t + 64]) : r2o_f16_to_f32(src[off + t + 64]);
+    if (is_v) {  // wave-uniform: a V row is the FWHT of the row alone (triton_fwht_128)
+        float y0 = x0, y1 = x1;
+        r2o_fwht128_pair(y0, y1, t);
+        dst[off + t] = (uint16_t)(a.dtype == 0 ? r2o_f32_to_bf16(y0) : r2o_f32_to_f16(y0));
+        dst[off + t + 64] = (uint16_t)(a.dtype == 0 ? r2o_f32_to_bf16(y1) : r2o_f32_to_f16(y1));
+        return;
+    }
     const int axis = t < a.s0 ? 0 : (t < a.s0 + a.s1 ? 1 : 2);  // section of d % 64 == t
     const int64_t c0 = axis * a.cs[0] + b * a.cs[1] + token * a.cs[2], sn0 = axis * a.ss[0] + b * a.ss[1] + token * a.ss[2];
     const float cos0 = load_table(a.cos, a.table_code, c0 + t * a.cs[3]);
@@ -128,19 +138,23 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
 
 extern "C" {
 
-int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out, int64_t dtype, int64_t batch,
-                 int64_t hq, int64_t hkv, int64_t tokens, const void* cos, const void* sin, int64_t table_dtype,
-                 const int64_t* cos_strides, const int64_t* sin_strides, int64_t section0, int64_t section1,
-                 int64_t apply_hadamard, void* stream) {
+int r2o_qkv_mrope(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* q_out, uint16_t* k_out,
+                  uint16_t* v_out, int64_t dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens,
+                  const void* cos, const void* sin, int64_t table_dtype, const int64_t* cos_strides,
+                  const int64_t* sin_strides, int64_t section0, int64_t section1, int64_t apply_hadamard,
+                  void* stream) {
     if (!q || !k || !q_out || !k_out || !cos || !sin || !cos_strides || !sin_strides) return R2O_EINVAL;
+    if ((v == nullptr) != (v_out == nullptr)) return R2O_EINVAL;
     if ((dtype != 0 && dtype != 1) || table_dtype < 0 || table_dtype > 2) return R2O_EINVAL;
     if (batch <= 0 || hq <= 0 || hkv <= 0 || tokens <= 0) return R2O_EINVAL;
     if (section0 < 0 || section1 < 0 || section0 + section1 > 64) return R2O_EINVAL;
     RopeArgs a;
     a.q = q;
     a.k = k;
+    a.v = v;
     a.q_out = q_out;
     a.k_out = k_out;
+    a.v_out = v_out;
     a.cos = cos;
     a.sin = sin;
     for (int i = 0; i < 4; ++i) {
@@ -149,8 +163,9 @@ int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t
     }
     a.hq = hq;
     a.hkv = hkv;
+    a.hv = v ? hkv : 0;
     a.tokens = tokens;
-    a.rows = batch * (hq + hkv) * tokens;
+    a.rows = batch * (hq + hkv + a.hv) * tokens;
     a.dtype = (int)dtype;
     a.table_code = (int)table_dtype;
     a.s0 = (int)section0;
@@ -160,6 +175,14 @@ int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t
     hipLaunchKernelGGL(qk_mrope_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
+}
+
+int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out, int64_t dtype, int64_t batch,
+                 int64_t hq, int64_t hkv, int64_t tokens, const void* cos, const void* sin, int64_t table_dtype,
+                 const int64_t* cos_strides, const int64_t* sin_strides, int64_t section0, int64_t section1,
+                 int64_t apply_hadamard, void* stream) {
+    return r2o_qkv_mrope(q, k, nullptr, q_out, k_out, nullptr, dtype, batch, hq, hkv, tokens, cos, sin, table_dtype,
+                         cos_strides, sin_strides, section0, section1, apply_hadamard, stream);
 }
 
 int r2o_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out, int64_t dtype,

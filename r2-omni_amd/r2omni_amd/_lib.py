@@ -86,6 +86,8 @@ _SIGNATURES = {
     "r2o_fwht128": (c_vp, c_vp, c_i64, c_i64, c_vp),
     "r2o_qk_mrope": (c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp,
                      c_i64, c_i64, c_i64, c_vp),
+    "r2o_qkv_mrope": (c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp,
+                      c_vp, c_i64, c_i64, c_i64, c_vp),
     "r2o_qk_norm_rope": (c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, ctypes.c_float,
                          c_vp, c_vp, c_vp, c_vp, c_i64, c_vp),
 }

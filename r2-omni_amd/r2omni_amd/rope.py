@@ -21,9 +21,14 @@ _TABLE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
 def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                  mrope_section: Sequence[int], *, output: tuple[torch.Tensor, torch.Tensor] | None = None,
-                  apply_hadamard: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
-    """Apply Qwen multimodal RoPE (and optionally the orthonormal FWHT-128) to Q and K in one launch."""
+                  mrope_section: Sequence[int], *, output: tuple[torch.Tensor, ...] | None = None,
+                  apply_hadamard: bool = False, value: torch.Tensor | None = None):
+    """Apply Qwen multimodal RoPE (and optionally the orthonormal FWHT-128) to Q and K in one launch.
+
+    With ``value`` ([B, Hkv, T, 128], Q/K's dtype), returns (Q, K, V) and, when ``apply_hadamard``
+    is set, folds the decode step's V Hadamard (``triton_fwht_128(value)``,
+    qwen_sspa_attention.py:230-235) into the same launch; without it V is returned unchanged, as the
+    manager rotates V only under Hadamard.  ``output`` then holds three tensors."""
     if query.ndim != 4 or key.ndim != 4:
         raise ValueError("Qwen fused mRoPE requires rank-4 Q/K")
     if query.shape[0] != key.shape[0]:
@@ -51,12 +56,32 @@ def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin
     dtype = _lib.dtype_code(query.dtype)
     if cos.dtype != sin.dtype or cos.dtype not in _TABLE_CODES:
         raise ValueError("Qwen fused mRoPE cos/sin must share a bf16, fp16 or fp32 dtype")
+    if value is not None:
+        if value.shape != key.shape or value.device != key.device or value.dtype != key.dtype:
+            raise ValueError("fused Qwen mRoPE value must match K's shape, device and dtype")
+    fold_v = value is not None and bool(apply_hadamard)
     query = query.contiguous()
     key = key.contiguous()
+    value_out = value
+    if fold_v:
+        value = value.contiguous()
     if output is None:
         query_out, key_out = torch.empty_like(query), torch.empty_like(key)
+        if fold_v:
+            value_out = torch.empty_like(value)
     else:
-        query_out, key_out = output
+        if len(output) != (2 if value is None else 3):
+            raise ValueError("fused Qwen mRoPE output must hold one tensor per input")
+        query_out, key_out = output[0], output[1]
+        if value is not None:
+            if fold_v:
+                value_out = output[2]
+                if value_out.shape != value.shape or value_out.device != value.device \
+                        or value_out.dtype != value.dtype or not value_out.is_contiguous():
+                    raise ValueError("fused Qwen mRoPE value output must match V and be contiguous")
+            else:
+                output[2].copy_(value)
+                value_out = output[2]
         if query_out.shape != query.shape or key_out.shape != key.shape:
             raise ValueError("fused Qwen mRoPE output shapes must match Q/K")
         if (query_out.device != query.device or key_out.device != key.device or query_out.dtype != query.dtype
@@ -66,11 +91,14 @@ def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin
             raise ValueError("fused Qwen mRoPE outputs must be contiguous")
     cos_strides = (ctypes.c_int64 * 4)(*[int(v) for v in cos.stride()])
     sin_strides = (ctypes.c_int64 * 4)(*[int(v) for v in sin.stride()])
-    _lib.call("r2o_qk_mrope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(query_out), _lib.ptr(key_out), dtype,
+    _lib.call("r2o_qkv_mrope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(value) if fold_v else None,
+              _lib.ptr(query_out), _lib.ptr(key_out), _lib.ptr(value_out) if fold_v else None, dtype,
               batch_size, int(query.shape[1]), int(key.shape[1]), tokens, _lib.ptr(cos), _lib.ptr(sin),
               _TABLE_CODES[cos.dtype], cos_strides, sin_strides, sections[0], sections[1], int(bool(apply_hadamard)),
               ctypes.c_void_p(_lib.stream_of(query.device)))
-    return query_out, key_out
+    if value is None:
+        return query_out, key_out
+    return query_out, key_out, value_out
 
 
 def qwen3_qk_norm_rope(query: torch.Tensor, key: torch.Tensor, q_norm_weight: torch.Tensor,

@@ -184,3 +184,46 @@ def test_lane_butterflies_are_bit_exact(dtype):
         ref = normalized_fwht(rows)
         step = np.abs(ref) * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-4
         assert np.all(np.abs(_np32(got).reshape(-1, 128) - ref) <= step)
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_qkv_mrope_folds_the_v_hadamard(case):
+    """qwen_qk_mrope(value=V): Q and K bit-identical to the two-tensor call; with the Hadamard on, V
+    is its FWHT (bit-exact to the in-register butterfly order, within one output rounding of the
+    reference's order), written into a caller's buffer when given; with it off, V is returned as is."""
+    import r2omni_amd as ro
+    from oracle.quant import normalized_fwht
+
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    dev = torch.device("cuda:0")
+    b, hq, hkv, t, qdt, tdt, had, shared = CASES[case]
+    gen = torch.Generator().manual_seed(30 + case)
+    q = torch.randn(b, hq, t, 128, generator=gen).to(qdt).to(dev)
+    k = torch.randn(b, hkv, t, 128, generator=gen).to(qdt).to(dev)
+    v = (torch.randn(b, hkv, t, 128, generator=gen) * 3).to(qdt).to(dev)
+    pos = torch.randint(0, 8000, (3, b, t), generator=gen).double()
+    ang = pos[..., None] * (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128)))
+    ang = torch.cat([ang, ang], dim=-1)
+    cos, sin = ang.cos().to(tdt).to(dev), ang.sin().to(tdt).to(dev)
+    sections = (16, 24, 24)
+    q2, k2 = ro.qwen_qk_mrope(q, k, cos, sin, sections, apply_hadamard=had)
+    vbuf = torch.full_like(v, 7.0)
+    q3, k3, v3 = ro.qwen_qk_mrope(q, k, cos, sin, sections, apply_hadamard=had, value=v,
+                                  output=(torch.empty_like(q), torch.empty_like(k), vbuf))
+    torch.cuda.synchronize()
+    assert torch.equal(q3.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(k3.view(torch.int16), k2.view(torch.int16))
+    assert v3.data_ptr() == vbuf.data_ptr()
+    rows = _np32(v).reshape(-1, 128)
+    if had:
+        assert _exact_where_normal(v3.reshape(-1, 128), _butterfly_fwht_f32(rows), qdt)
+        ref = normalized_fwht(rows)
+        step = np.abs(ref) * (2.0 ** -7 if qdt == torch.bfloat16 else 2.0 ** -10) + 1e-4
+        assert np.all(np.abs(_np32(v3).reshape(-1, 128) - ref) <= step)
+    else:
+        assert torch.equal(v3, v)
+        _, _, same = ro.qwen_qk_mrope(q, k, cos, sin, sections, value=v)
+        assert same is v
+    with pytest.raises(ValueError, match="value"):
+        ro.qwen_qk_mrope(q, k, cos, sin, sections, apply_hadamard=had, value=v[:, :, :, :64])
