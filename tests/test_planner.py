@@ -68,3 +68,30 @@ def test_split_run_covers_the_run_with_wave_shares(nt, n_items, share):
         small = items[-(-n_items // 2):-1]
         ratio = (sum(s for _, s in small) / len(small)) / (sum(s for _, s in big) / len(big))
         assert abs(ratio - share) < 0.1
+
+
+def test_single_kind_plans_give_the_later_launched_half_less_work():
+    """Two workgroups share a CU (launch slots j and j + CUs) and the earlier one runs ahead: an
+    all-INT2 plan that fills both slots gives the later-launched half about _LATE_SHARE of the
+    work, a mixed plan keeps equal items per run, and a plan within one slot per CU is even."""
+    from r2omni_amd.splitk import _LATE_SHARE
+    cus = 256
+    uniform = [_fake_cache(0, 0, 131072)]
+    items = plan_work_items(uniform, 8, cus)[0].tolist()
+    seg = [it for it in items if it[2] == _lib.KIND_INT2]
+    assert len(items) > cus
+    early = [it[4] for it in seg if items.index(it) < cus]
+    late = [it[4] for it in seg if items.index(it) >= cus]
+    ratio = (sum(late) / len(late)) / (sum(early) / len(early))
+    assert abs(ratio - _LATE_SHARE) < 0.06
+    mixed = [_fake_cache(8192, 24576, 32768), _fake_cache(2048, 6144, 8192)]
+    items = plan_work_items(mixed, 4, cus)[0].tolist()
+    for r in range(2):
+        for h in range(4):
+            for kind in (_lib.KIND_FP, _lib.KIND_INT4, _lib.KIND_INT2):
+                sizes = [it[4] for it in items if (it[0], it[1], it[2]) == (r, h, kind)]
+                assert max(sizes[:-1] or [0]) - min(sizes[:-1] or [0]) <= 0  # equal but the last
+    small = plan_work_items([_fake_cache(0, 0, 4096)], 2, cus)[0].tolist()
+    assert len(small) <= cus
+    sizes = sorted(it[4] for it in small if it[2] == _lib.KIND_INT2)
+    assert sizes[-1] - sizes[1] <= 4  # even (one wave share of rounding), the remainder aside
