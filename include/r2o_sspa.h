@@ -248,6 +248,16 @@ int r2o_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint
                      const uint16_t* k_weight, float eps, const uint16_t* cos, const uint16_t* sin,
                      const int64_t* cos_strides, const int64_t* sin_strides, int64_t apply_hadamard, void* stream);
 
+/* r2o_qk_norm_rope plus, when v / v_out are non-NULL, the orthonormal FWHT-128 of the V rows
+ * v [batch, hkv, tokens, 128] (same dtype) into v_out in the same launch: the Qwen3 branch's Q/K
+ * transform and the decode step's V Hadamard (triton_fwht_128 at qwen_sspa_attention.py:230-235)
+ * as one launch, V rows as in r2o_qkv_mrope.  v and v_out must both be NULL or both be set. */
+int r2o_qkv_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* q_out, uint16_t* k_out,
+                      uint16_t* v_out, int64_t dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens,
+                      const uint16_t* q_weight, const uint16_t* k_weight, float eps, const uint16_t* cos,
+                      const uint16_t* sin, const int64_t* cos_strides, const int64_t* sin_strides,
+                      int64_t apply_hadamard, void* stream);
+
 /* Library identification: returns the gfx target the code objects were built for. */
 const char* r2o_build_target(void);
 

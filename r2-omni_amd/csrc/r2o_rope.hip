@@ -83,15 +83,17 @@ __device__ __forceinline__ float load_elem(const uint16_t* p, int64_t i, int dty
 struct NormRopeArgs {
     const uint16_t* q;
     const uint16_t* k;
+    const uint16_t* v;  // nullable: V rows take the FWHT alone
     uint16_t* q_out;
     uint16_t* k_out;
+    uint16_t* v_out;
     const uint16_t* q_weight;  // [128] RMSNorm weights, input dtype
     const uint16_t* k_weight;
     const uint16_t* cos;       // input dtype, strides (batch, token, dim) in elements
     const uint16_t* sin;
     int64_t cs[3];
     int64_t ss[3];
-    int64_t hq, hkv, tokens, rows;
+    int64_t hq, hkv, hv, tokens, rows;  // hv: V heads (hkv with V rows, else 0)
     float eps;
     int dtype, hadamard;
 };
@@ -107,16 +109,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.rows) return;  // whole-wave exit: the cross-lane sums and butterflies need every lane of a live wave
     const int t = threadIdx.x & 63;
-    const int64_t per_req = (a.hq + a.hkv) * a.tokens;
+    const int64_t per_req = (a.hq + a.hkv + a.hv) * a.tokens;
     const int64_t b = row / per_req, local = row % per_req;
     const int64_t head = local / a.tokens, token = local % a.tokens;
-    const bool is_q = head < a.hq;
-    const int64_t off = is_q ? ((b * a.hq + head) * a.tokens + token) * 128 : ((b * a.hkv + head - a.hq) * a.tokens + token) * 128;
-    const uint16_t* src = is_q ? a.q : a.k;
+    const bool is_q = head < a.hq, is_v = head >= a.hq + a.hkv;
+    const int64_t kv_head = is_v ? head - a.hq - a.hkv : head - a.hq;
+    const int64_t off = is_q ? ((b * a.hq + head) * a.tokens + token) * 128 : ((b * a.hkv + kv_head) * a.tokens + token) * 128;
+    const uint16_t* src = is_q ? a.q : (is_v ? a.v : a.k);
     const uint16_t* wt = is_q ? a.q_weight : a.k_weight;
-    uint16_t* dst = is_q ? a.q_out : a.k_out;
+    uint16_t* dst = is_q ? a.q_out : (is_v ? a.v_out : a.k_out);
     const int dt = a.dtype;
     const float x0 = load_elem(src, off + t, dt), x1 = load_elem(src, off + t + 64, dt);
+    if (is_v) {  // wave-uniform: a V row is the FWHT of the row alone (triton_fwht_128)
+        float y0 = x0, y1 = x1;
+        r2o_fwht128_pair(y0, y1, t);
+        dst[off + t] = (uint16_t)(dt == 0 ? r2o_f32_to_bf16(y0) : r2o_f32_to_f16(y0));
+        dst[off + t + 64] = (uint16_t)(dt == 0 ? r2o_f32_to_bf16(y1) : r2o_f32_to_f16(y1));
+        return;
+    }
     float sq = __fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1));
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) sq = __fadd_rn(sq, __shfl_xor(sq, m, R2O_WAVE));
@@ -185,19 +195,23 @@ int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t
                          cos_strides, sin_strides, section0, section1, apply_hadamard, stream);
 }
 
-int r2o_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out, int64_t dtype,
-                     int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, const uint16_t* q_weight,
-                     const uint16_t* k_weight, float eps, const uint16_t* cos, const uint16_t* sin,
-                     const int64_t* cos_strides, const int64_t* sin_strides, int64_t apply_hadamard, void* stream) {
+int r2o_qkv_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* q_out, uint16_t* k_out,
+                      uint16_t* v_out, int64_t dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens,
+                      const uint16_t* q_weight, const uint16_t* k_weight, float eps, const uint16_t* cos,
+                      const uint16_t* sin, const int64_t* cos_strides, const int64_t* sin_strides,
+                      int64_t apply_hadamard, void* stream) {
     if (!q || !k || !q_out || !k_out || !q_weight || !k_weight || !cos || !sin || !cos_strides || !sin_strides)
         return R2O_EINVAL;
+    if ((v == nullptr) != (v_out == nullptr)) return R2O_EINVAL;
     if ((dtype != 0 && dtype != 1) || batch <= 0 || hq <= 0 || hkv <= 0 || tokens <= 0) return R2O_EINVAL;
     if (!(eps >= 0.f)) return R2O_EINVAL;
     NormRopeArgs a;
     a.q = q;
     a.k = k;
+    a.v = v;
     a.q_out = q_out;
     a.k_out = k_out;
+    a.v_out = v_out;
     a.q_weight = q_weight;
     a.k_weight = k_weight;
     a.cos = cos;
@@ -208,8 +222,9 @@ int r2o_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint
     }
     a.hq = hq;
     a.hkv = hkv;
+    a.hv = v ? hkv : 0;
     a.tokens = tokens;
-    a.rows = batch * (hq + hkv) * tokens;
+    a.rows = batch * (hq + hkv + a.hv) * tokens;
     a.eps = eps;
     a.dtype = (int)dtype;
     a.hadamard = apply_hadamard ? 1 : 0;
@@ -217,6 +232,14 @@ int r2o_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
+}
+
+int r2o_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out, int64_t dtype,
+                     int64_t batch, int64_t hq, int64_t hkv, int64_t tokens, const uint16_t* q_weight,
+                     const uint16_t* k_weight, float eps, const uint16_t* cos, const uint16_t* sin,
+                     const int64_t* cos_strides, const int64_t* sin_strides, int64_t apply_hadamard, void* stream) {
+    return r2o_qkv_norm_rope(q, k, nullptr, q_out, k_out, nullptr, dtype, batch, hq, hkv, tokens, q_weight, k_weight,
+                             eps, cos, sin, cos_strides, sin_strides, apply_hadamard, stream);
 }
 
 }  // extern "C"

@@ -88,6 +88,8 @@ _SIGNATURES = {
                      c_i64, c_i64, c_i64, c_vp),
     "r2o_qkv_mrope": (c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp,
                       c_vp, c_i64, c_i64, c_i64, c_vp),
+    "r2o_qkv_norm_rope": (c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp,
+                          ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp),
     "r2o_qk_norm_rope": (c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, ctypes.c_float,
                          c_vp, c_vp, c_vp, c_vp, c_i64, c_vp),
 }

@@ -20,6 +20,29 @@ from . import _lib
 _TABLE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
+def _value_operands(value, output, apply_hadamard, what):
+    """(V input, V output, whether the launch transforms V) for the optional V of a fused rotation:
+    V takes the FWHT only under the Hadamard, and otherwise is returned (or copied into the caller's
+    output) unchanged."""
+    if output is not None and len(output) != (2 if value is None else 3):
+        raise ValueError(f"{what} output must hold one tensor per input")
+    if value is None:
+        return None, None, False
+    fold_v = bool(apply_hadamard)
+    if fold_v:
+        value = value.contiguous()
+    if output is None:
+        return value, (torch.empty_like(value) if fold_v else value), fold_v
+    value_out = output[2]
+    if fold_v:
+        if value_out.shape != value.shape or value_out.device != value.device or value_out.dtype != value.dtype \
+                or not value_out.is_contiguous():
+            raise ValueError(f"{what} value output must match V and be contiguous")
+    else:
+        value_out.copy_(value)
+    return value, value_out, fold_v
+
+
 def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                   mrope_section: Sequence[int], *, output: tuple[torch.Tensor, ...] | None = None,
                   apply_hadamard: bool = False, value: torch.Tensor | None = None):
@@ -59,29 +82,13 @@ def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin
     if value is not None:
         if value.shape != key.shape or value.device != key.device or value.dtype != key.dtype:
             raise ValueError("fused Qwen mRoPE value must match K's shape, device and dtype")
-    fold_v = value is not None and bool(apply_hadamard)
     query = query.contiguous()
     key = key.contiguous()
-    value_out = value
-    if fold_v:
-        value = value.contiguous()
+    value, value_out, fold_v = _value_operands(value, output, apply_hadamard, "fused Qwen mRoPE")
     if output is None:
         query_out, key_out = torch.empty_like(query), torch.empty_like(key)
-        if fold_v:
-            value_out = torch.empty_like(value)
     else:
-        if len(output) != (2 if value is None else 3):
-            raise ValueError("fused Qwen mRoPE output must hold one tensor per input")
         query_out, key_out = output[0], output[1]
-        if value is not None:
-            if fold_v:
-                value_out = output[2]
-                if value_out.shape != value.shape or value_out.device != value.device \
-                        or value_out.dtype != value.dtype or not value_out.is_contiguous():
-                    raise ValueError("fused Qwen mRoPE value output must match V and be contiguous")
-            else:
-                output[2].copy_(value)
-                value_out = output[2]
         if query_out.shape != query.shape or key_out.shape != key.shape:
             raise ValueError("fused Qwen mRoPE output shapes must match Q/K")
         if (query_out.device != query.device or key_out.device != key.device or query_out.dtype != query.dtype
@@ -103,12 +110,13 @@ def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin
 
 def qwen3_qk_norm_rope(query: torch.Tensor, key: torch.Tensor, q_norm_weight: torch.Tensor,
                        k_norm_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, eps: float = 1e-6,
-                       apply_hadamard: bool = False,
-                       output: tuple[torch.Tensor, torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                       apply_hadamard: bool = False, output: tuple[torch.Tensor, ...] | None = None,
+                       value: torch.Tensor | None = None):
     """``q_norm(q)``, ``k_norm(k)`` (Qwen3 per-head RMSNorm), ``apply_rotary_pos_emb`` with
     ``cos``/``sin`` [B or 1, T, 128] and, with ``apply_hadamard``, the normalised FWHT-128 of both,
     in one launch.  Q [B, Hq, T, 128] and K [B, Hkv, T, 128] share one dtype (bf16 or fp16) with the
-    norm weights and the rotary tables, as in the model."""
+    norm weights and the rotary tables, as in the model.  With ``value`` ([B, Hkv, T, 128]), returns
+    (Q, K, V), folding the V Hadamard into the launch as ``qwen_qk_mrope(value=...)`` does."""
     if query.ndim != 4 or key.ndim != 4:
         raise ValueError("Qwen3 fused norm+RoPE requires rank-4 Q/K")
     if query.shape[0] != key.shape[0] or query.shape[2] != key.shape[2] or query.shape[2] <= 0:
@@ -131,13 +139,16 @@ def qwen3_qk_norm_rope(query: torch.Tensor, key: torch.Tensor, q_norm_weight: to
         raise ValueError("RMSNorm epsilon must be non-negative")
     _lib.require_device(query, "fused Qwen3 norm+RoPE input")
     dtype = _lib.dtype_code(query.dtype)
+    if value is not None and (value.shape != key.shape or value.device != key.device or value.dtype != key.dtype):
+        raise ValueError("fused Qwen3 norm+RoPE value must match K's shape, device and dtype")
     query, key = query.contiguous(), key.contiguous()
     q_norm_weight, k_norm_weight = q_norm_weight.contiguous(), k_norm_weight.contiguous()
     cos, sin = cos.expand(batch_size, tokens, 128), sin.expand(batch_size, tokens, 128)
+    value, value_out, fold_v = _value_operands(value, output, apply_hadamard, "fused Qwen3 norm+RoPE")
     if output is None:
         query_out, key_out = torch.empty_like(query), torch.empty_like(key)
     else:
-        query_out, key_out = output
+        query_out, key_out = output[0], output[1]
         if query_out.shape != query.shape or key_out.shape != key.shape or query_out.dtype != query.dtype \
                 or key_out.dtype != key.dtype or query_out.device != query.device or key_out.device != key.device:
             raise ValueError("fused Qwen3 norm+RoPE outputs must match Q/K shape, dtype and device")
@@ -145,8 +156,11 @@ def qwen3_qk_norm_rope(query: torch.Tensor, key: torch.Tensor, q_norm_weight: to
             raise ValueError("fused Qwen3 norm+RoPE outputs must be contiguous")
     cos_strides = (ctypes.c_int64 * 3)(*[int(v) for v in cos.stride()])
     sin_strides = (ctypes.c_int64 * 3)(*[int(v) for v in sin.stride()])
-    _lib.call("r2o_qk_norm_rope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(query_out), _lib.ptr(key_out), dtype,
+    _lib.call("r2o_qkv_norm_rope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(value) if fold_v else None,
+              _lib.ptr(query_out), _lib.ptr(key_out), _lib.ptr(value_out) if fold_v else None, dtype,
               batch_size, int(query.shape[1]), int(key.shape[1]), tokens, _lib.ptr(q_norm_weight),
               _lib.ptr(k_norm_weight), float(eps), _lib.ptr(cos), _lib.ptr(sin), cos_strides, sin_strides,
               int(bool(apply_hadamard)), ctypes.c_void_p(_lib.stream_of(query.device)))
-    return query_out, key_out
+    if value is None:
+        return query_out, key_out
+    return query_out, key_out, value_out

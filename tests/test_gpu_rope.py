@@ -227,3 +227,38 @@ def test_qkv_mrope_folds_the_v_hadamard(case):
         assert same is v
     with pytest.raises(ValueError, match="value"):
         ro.qwen_qk_mrope(q, k, cos, sin, sections, apply_hadamard=had, value=v[:, :, :, :64])
+
+
+@pytest.mark.parametrize("case", range(len(NORM_CASES)))
+def test_qwen3_qkv_norm_rope_folds_the_v_hadamard(case):
+    """qwen3_qk_norm_rope(value=V): Q and K bit-identical to the two-tensor call; with the Hadamard
+    on, V is its in-register-order FWHT (bit-exact) written into the caller's buffer; with it off, V
+    is copied unchanged into that buffer."""
+    import r2omni_amd as ro
+    from test_oracle_rope import _rope_tables_1d
+
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    dev = torch.device("cuda:0")
+    b, hq, hkv, t, dt, had, shared = NORM_CASES[case]
+    gen = torch.Generator().manual_seed(40 + case)
+    q = (torch.randn(b, hq, t, 128, generator=gen) * 3).to(dt).to(dev)
+    k = (torch.randn(b, hkv, t, 128, generator=gen) * 3).to(dt).to(dev)
+    v = (torch.randn(b, hkv, t, 128, generator=gen) * 3).to(dt).to(dev)
+    wq, wk = (torch.rand(128, generator=gen) * 2).to(dt).to(dev), (torch.rand(128, generator=gen) * 2).to(dt).to(dev)
+    cos, sin = _rope_tables_1d(1 if shared else b, t, gen, dt)
+    cos, sin = cos.to(dev), sin.to(dev)
+    q2, k2 = ro.qwen3_qk_norm_rope(q, k, wq, wk, cos, sin, eps=1e-6, apply_hadamard=had)
+    vbuf = torch.full_like(v, 5.0)
+    q3, k3, v3 = ro.qwen3_qk_norm_rope(q, k, wq, wk, cos, sin, eps=1e-6, apply_hadamard=had, value=v,
+                                       output=(torch.empty_like(q), torch.empty_like(k), vbuf))
+    torch.cuda.synchronize()
+    assert torch.equal(q3.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(k3.view(torch.int16), k2.view(torch.int16))
+    assert v3.data_ptr() == vbuf.data_ptr()
+    if had:
+        assert _exact_where_normal(v3.reshape(-1, 128), _butterfly_fwht_f32(_np32(v).reshape(-1, 128)), dt)
+    else:
+        assert torch.equal(v3, v)
+    with pytest.raises(ValueError, match="one tensor per input"):
+        ro.qwen3_qk_norm_rope(q, k, wq, wk, cos, sin, value=v, output=(q2, k2))
