@@ -173,19 +173,19 @@ __device__ __forceinline__ void r2o_fwht_stage(float& y0, float& y1, int t) {
 }
 
 // Orthonormal 128-point FWHT of a row held by one full wave: lane t holds x[t] in y0 and x[t + 64]
-// in y1.  Stride 64 is a butterfly inside the lane, strides 1 .. 32 are lane-xor butterflies.
+// in y1.  Strides 1 .. 32 are lane-xor butterflies, stride 64 is a butterfly inside the lane, in
+// the stage order of triton_fwht_128 (triton_qwen_mrope.py:23-32: stride 1 first, 64 last), so
+// every fp32 sum is formed from the same operands in the same order.
 __device__ __forceinline__ void r2o_fwht128_pair(float& y0, float& y1, int t) {
-    const float s0 = y0 + y1, s1 = y0 - y1;
-    y0 = s0;
-    y1 = s1;
     r2o_fwht_stage<1>(y0, y1, t);
     r2o_fwht_stage<2>(y0, y1, t);
     r2o_fwht_stage<4>(y0, y1, t);
     r2o_fwht_stage<8>(y0, y1, t);
     r2o_fwht_stage<16>(y0, y1, t);
     r2o_fwht_stage<32>(y0, y1, t);
-    y0 *= 0.08838834764831845f;
-    y1 *= 0.08838834764831845f;
+    const float s0 = y0 + y1, s1 = y0 - y1;
+    y0 = s0 * 0.08838834764831845f;
+    y1 = s1 * 0.08838834764831845f;
 }
 
 #define R2O_CHECK_LAUNCH()                                      \

@@ -44,6 +44,11 @@ class BatchedDecoder:
         self.caches = list(caches)
         if not self.caches:
             raise ValueError("a decode batch needs at least one request")
+        # each request appends to (and flushes) its own cache in place: a cache listed twice would
+        # take two appends into one ring per step
+        rings = [c.recent_fp_pool.fp_k.data_ptr() for c in self.caches]
+        if len(set(map(id, self.caches))) != len(self.caches) or len(set(rings)) != len(rings):
+            raise ValueError("BatchedDecoder requests must be distinct caches (a cache appears twice)")
         first = self.caches[0].recent_fp_pool
         self.device = first.fp_k.device
         self.hkv = int(first.fp_k.shape[0])

@@ -23,7 +23,7 @@ _TABLE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 def _value_operands(value, output, apply_hadamard, what):
     """(V input, V output, whether the launch transforms V) for the optional V of a fused rotation:
     V takes the FWHT only under the Hadamard, and otherwise is returned (or copied into the caller's
-    output) unchanged."""
+    output by ``_copy_value``, once every argument has been checked) unchanged.  Writes nothing."""
     if output is not None and len(output) != (2 if value is None else 3):
         raise ValueError(f"{what} output must hold one tensor per input")
     if value is None:
@@ -34,13 +34,16 @@ def _value_operands(value, output, apply_hadamard, what):
     if output is None:
         return value, (torch.empty_like(value) if fold_v else value), fold_v
     value_out = output[2]
-    if fold_v:
-        if value_out.shape != value.shape or value_out.device != value.device or value_out.dtype != value.dtype \
-                or not value_out.is_contiguous():
-            raise ValueError(f"{what} value output must match V and be contiguous")
-    else:
-        value_out.copy_(value)
+    if value_out.shape != value.shape or value_out.device != value.device or value_out.dtype != value.dtype \
+            or (fold_v and not value_out.is_contiguous()):
+        raise ValueError(f"{what} value output must match V" + (" and be contiguous" if fold_v else ""))
     return value, value_out, fold_v
+
+
+def _copy_value(value, value_out, fold_v) -> None:
+    """Without the Hadamard, V reaches the caller's output buffer as a plain copy."""
+    if value is not None and not fold_v and value_out is not value:
+        value_out.copy_(value)
 
 
 def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
@@ -98,6 +101,7 @@ def qwen_qk_mrope(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin
             raise ValueError("fused Qwen mRoPE outputs must be contiguous")
     cos_strides = (ctypes.c_int64 * 4)(*[int(v) for v in cos.stride()])
     sin_strides = (ctypes.c_int64 * 4)(*[int(v) for v in sin.stride()])
+    _copy_value(value, value_out, fold_v)
     _lib.call("r2o_qkv_mrope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(value) if fold_v else None,
               _lib.ptr(query_out), _lib.ptr(key_out), _lib.ptr(value_out) if fold_v else None, dtype,
               batch_size, int(query.shape[1]), int(key.shape[1]), tokens, _lib.ptr(cos), _lib.ptr(sin),
@@ -156,6 +160,7 @@ def qwen3_qk_norm_rope(query: torch.Tensor, key: torch.Tensor, q_norm_weight: to
             raise ValueError("fused Qwen3 norm+RoPE outputs must be contiguous")
     cos_strides = (ctypes.c_int64 * 3)(*[int(v) for v in cos.stride()])
     sin_strides = (ctypes.c_int64 * 3)(*[int(v) for v in sin.stride()])
+    _copy_value(value, value_out, fold_v)
     _lib.call("r2o_qkv_norm_rope", _lib.ptr(query), _lib.ptr(key), _lib.ptr(value) if fold_v else None,
               _lib.ptr(query_out), _lib.ptr(key_out), _lib.ptr(value_out) if fold_v else None, dtype,
               batch_size, int(query.shape[1]), int(key.shape[1]), tokens, _lib.ptr(q_norm_weight),

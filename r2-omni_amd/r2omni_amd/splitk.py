@@ -5,7 +5,8 @@ Same names, arguments, return values and error behaviour as the reference
   allocate_splitk_workspace   :1607-1676   required_splitk_blocks :1679-1692
   prepare_splitk_executor     :1695-1907   SplitKExecutor.__call__ :1243-1547
   append_recent_fp_triton     :1557-1604   (name kept; it launches r2o_recent_append)
-  stack_homogeneous_splitk_executors :1995-2241 (here also for ragged batches: no payload copy)
+  stack_homogeneous_splitk_executors :1995-2241 (here also for ragged batches; the read-only
+                                     payload is shared, each request's Recent-FP ring is copied)
   allocated_workspace_bytes   :2244-2256
 Launch knobs of the Triton kernels (block_n, num_warps, num_stages, tensor-core flags, ...)
 are accepted and ignored: the gfx950 kernels fix their own tiling.  A "block" of the
@@ -230,9 +231,12 @@ def _k_format(cache: ThreePrecisionCache) -> int:
     return _lib.K_INT2 if cache.compact_key.bit_width == 2 else _lib.K_INT4
 
 
-def _request_words(cache: ThreePrecisionCache) -> dict[str, int]:
+def _request_words(cache: ThreePrecisionCache, ring=None) -> dict[str, int]:
+    """Pool pointers of one request; ``ring`` replaces the cache's Recent-FP pool (the private ring
+    copy of a stacked executor)."""
     ck, cv = cache.compact_key, cache.compact_value
-    fp, i4, rec = cache.fp_pool, cache.int4_pool, cache.recent_fp_pool
+    fp, i4 = cache.fp_pool, cache.int4_pool
+    rec = cache.recent_fp_pool if ring is None else ring
     if rec.fp_k.dtype != torch.bfloat16:
         raise ValueError("the gfx950 decode path requires bfloat16 FP-V / Recent-FP rows")
     i4_packed = i4.packed_v.packed if i4.token_count else None
@@ -306,6 +310,11 @@ class SplitKExecutor:
     block_n: int = 128
     batched: bool = False
     host_items: torch.Tensor | None = None
+    # Stacked executors (stack_homogeneous_splitk_executors) own a copy of each request's Recent-FP
+    # ring and track its length here, as the reference's batched_recent / batched_recent_lengths
+    # (triton_fourq_splitk.py:1232-1241, 1543-1546): the source caches are never written.
+    batched_recent: list | None = None
+    batched_recent_lengths: list | None = None
     _keep: list = field(default_factory=list)
 
     @property
@@ -336,8 +345,8 @@ class SplitKExecutor:
         p.output_hadamard = int(self.output_hadamard)
         p.k_format = _k_format(self.caches[0])
         p.sm_scale = float(self.head_dim ** -0.5)
-        for r, c in enumerate(self.caches):
-            p.recent_len[r] = int(c.recent_fp_pool.active_length)
+        for r, n in enumerate(self._ring_lengths()):
+            p.recent_len[r] = n
         if append is not None:
             ak, av, gidx, lpos = append
             p.append_k, p.append_v, p.do_append = ak.data_ptr(), av.data_ptr(), 1
@@ -345,6 +354,11 @@ class SplitKExecutor:
                 p.append_global[r] = int(gidx[r])
                 p.append_logical[r] = int(lpos[r])
         return p
+
+    def _ring_lengths(self) -> list[int]:
+        if self.batched_recent_lengths is not None:
+            return list(self.batched_recent_lengths)
+        return [int(c.recent_fp_pool.active_length) for c in self.caches]
 
     def __call__(self, query: torch.Tensor, append=None) -> torch.Tensor:
         if query.ndim == 4:
@@ -369,19 +383,25 @@ class SplitKExecutor:
                 raise ValueError("append K/V must be bfloat16 like the Recent-FP ring")
             if ak.data_ptr() % 16 or av.data_ptr() % 16:  # the kernel moves the rows in 16-byte pieces
                 ak, av = ak.clone(), av.clone()
-            for c in self.caches:
-                rec = c.recent_fp_pool
-                if rec.active_length is None or rec.active_length >= rec.capacity:
-                    raise RuntimeError(
-                        "prepared batched executor cannot fuse an append into a full Recent-FP pool" if self.batched
-                        else "prepared executor cannot fuse an append into a full Recent-FP pool")
+            capacity = self.caches[0].recent_fp_pool.capacity
+            if self.batched_recent_lengths is not None:
+                if any(n >= capacity for n in self.batched_recent_lengths):
+                    raise RuntimeError("prepared batched executor cannot fuse an append into a full Recent-FP pool")
+            else:
+                for c in self.caches:
+                    rec = c.recent_fp_pool
+                    if rec.active_length is None or rec.active_length >= rec.capacity:
+                        raise RuntimeError(
+                            "prepared batched executor cannot fuse an append into a full Recent-FP pool"
+                            if self.batched else "prepared executor cannot fuse an append into a full Recent-FP pool")
             gl = _per_request(gidx, b)
             lp = _per_request(lpos, b)
             fused = (ak, av, gl, lp)
         self._launch(self._params(query, out, fused), query.device)
-        if fused is not None and self.batched:
-            for c in self.caches:
-                c.recent_fp_pool.active_length += 1
+        # A stacked executor advances its private ring lengths; a B=1 executor leaves the cache's
+        # host length to the caller (qwen_sspa_attention.py:1824-1826), as the reference does.
+        if fused is not None and self.batched_recent_lengths is not None:
+            self.batched_recent_lengths[:] = [n + 1 for n in self.batched_recent_lengths]
         return out
 
 
@@ -405,7 +425,9 @@ def _per_request(value, b: int) -> list[int]:
 
 
 def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWorkspace, *, output_hadamard: bool,
-                    block_n: int, batched: bool) -> SplitKExecutor:
+                    block_n: int, batched: bool, rings: Sequence | None = None) -> SplitKExecutor:
+    """Plan the work items and resolve the pool pointers of ``caches``.  ``rings`` (one Recent-FP
+    pool per request) replaces the caches' own rings: the kernels then read and append to those."""
     first = caches[0]
     rec = first.recent_fp_pool
     if rec.fp_k is None or rec.fp_k.ndim != 3:
@@ -436,7 +458,7 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
     n = int(host_items.shape[0])
     if n > workspace.total_blocks:
         raise ValueError("workspace block capacity is smaller than the active cache")
-    words = [_request_words(c) for c in caches]
+    words = [_request_words(c, None if rings is None else rings[r]) for r, c in enumerate(caches)]
     reqs = torch.tensor([[w[f] for f in _lib.REQUEST_FIELDS] for w in words], dtype=torch.int64).to(dev)
     groups = 128 // group
     rows = [it + _item_pointers(words[it[0]], kf, it[2], it[1], groups) + [0] for it in host_items.tolist()]
@@ -446,6 +468,8 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
         n_items=n, num_query_heads=hq, num_key_value_heads=hkv, head_dim=head_dim, superblock=sb, int2_group=group,
         page_size=first.page_size, output_hadamard=bool(output_hadamard), block_n=block_n, batched=batched,
         host_items=host_items,
+        batched_recent=None if rings is None else list(rings),
+        batched_recent_lengths=None if rings is None else [int(r.active_length) for r in rings],
     )
 
 
@@ -466,7 +490,14 @@ def stack_homogeneous_splitk_executors(executors: Sequence[SplitKExecutor], *,
                                        workspace: SplitKWorkspace | None = None,
                                        throughput_use_tensor_cores_pv: bool = False,
                                        throughput_direct_reduce_max_splits: int = 0) -> SplitKExecutor:
-    """One launch pair over several requests; unlike the reference, lengths may differ (ragged)."""
+    """One launch pair over several requests; unlike the reference, lengths may differ (ragged).
+
+    As in the reference, the stacked executor keeps its own copy of each request's Recent-FP ring
+    (rows, index buffers, page lengths and device length) and its own host lengths, so the same
+    executor may be stacked several times ((ex,) * B) and the source caches stay unchanged.  The
+    packed history is only read, so it is shared instead of copied.  A fused append fills the
+    copies; like the reference, the stacked executor refuses an append into a full ring (a flush is
+    a scheduler boundary: re-stack from the source caches, or use ``BatchedDecoder``)."""
     if len(executors) < 2:
         raise ValueError("batched split-K requires at least two executors")
     caches = [e.cache for e in executors]
@@ -482,8 +513,28 @@ def stack_homogeneous_splitk_executors(executors: Sequence[SplitKExecutor], *,
                                               total_blocks=max_work_items(len(caches), hkv, _num_cus(dev)))
     if int(workspace.output.shape[0]) != len(caches):
         raise ValueError("batched workspace output must hold one row per request")
+    rings = [_copy_ring(e.cache.recent_fp_pool) for e in executors]
     return _build_executor(caches, workspace, output_hadamard=first.output_hadamard, block_n=first.block_n,
-                           batched=True)
+                           batched=True, rings=rings)
+
+
+def _copy_ring(pool):
+    """A private copy of a Recent-FP ring: rows, index buffers, page table and device length."""
+    from .cache import PhysicalPageIndex, PrecisionPool
+
+    if any(t is None for t in (pool.fp_k, pool.fp_v, pool.global_index_buffer, pool.logical_position_buffer,
+                               pool.length_device)) or pool.active_length is None:
+        raise ValueError("batched Recent-FP metadata buffers are incomplete")
+    gbuf = pool.global_index_buffer.clone()
+    lbuf = pool.logical_position_buffer.clone()
+    idx = pool.page_index
+    index = PhysicalPageIndex(original_page_ids=idx.original_page_ids.clone(),
+                              physical_offsets=idx.physical_offsets.clone(), lengths=idx.lengths.clone(),
+                              global_token_indices=gbuf, logical_positions=lbuf)
+    return PrecisionPool(name=pool.name, page_index=index, fp_k=pool.fp_k.clone(), fp_v=pool.fp_v.clone(),
+                         active_length=int(pool.active_length), capacity=pool.capacity,
+                         length_device=pool.length_device.clone(), global_index_buffer=gbuf,
+                         logical_position_buffer=lbuf)
 
 
 def append_recent_fp_triton(cache: ThreePrecisionCache, new_key: torch.Tensor, new_value: torch.Tensor, *,

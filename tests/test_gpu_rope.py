@@ -44,10 +44,8 @@ def test_qk_mrope_matches_oracle(case):
     cs, sn = _np32(cos), _np32(sin)
     for got, x in ((qo, q), (ko, k)):
         want = qwen_mrope(_np32(x), cs, sn, sections, hadamard=had, dtype=name)
-        if had:  # FWHT summation order differs: at most one output ulp
-            np.testing.assert_allclose(_np32(got), want, rtol=2 ** -7, atol=1e-6)
-        else:    # same fp32 operations in the same order: bit-exact
-            np.testing.assert_array_equal(_np32(got), want)
+        # the same fp32 operations in the same order (the FWHT in the reference's stage order): bit-exact
+        np.testing.assert_array_equal(_np32(got), want)
 
 
 def test_qk_mrope_rejects_bad_sections_and_shapes():
@@ -121,20 +119,6 @@ def test_qwen3_qk_norm_rope_rejects_mismatched_arguments():
         ro.qwen3_qk_norm_rope(q[0], k, w, w, cs, cs)
 
 
-def _butterfly_fwht_f32(x):
-    """float32 FWHT-128 in the kernel's stage order: the stride-64 butterfly first (both halves
-    of a row sit in one lane), then strides 1 .. 32 with lane t ^ s as partner, the upper lane
-    taking partner - own; then the 1/sqrt(128) scale.  Every step is one IEEE float32 operation."""
-    y = np.asarray(x, dtype=np.float32)
-    a, b = y[:, :64].copy(), y[:, 64:].copy()
-    y = np.concatenate([a + b, a - b], axis=1)
-    idx = np.arange(128)
-    for s in (1, 2, 4, 8, 16, 32):
-        o = y[:, idx ^ s]
-        y = np.where((idx & s) != 0, o - y, y + o).astype(np.float32)
-    return y * np.float32(0.08838834764831845)
-
-
 def _exact_where_normal(got, want32, dtype):
     """Bit equality of got with want32 rounded to dtype, outside fp16's subnormal range."""
     want = torch.from_numpy(np.ascontiguousarray(want32)).to(dtype)
@@ -162,9 +146,9 @@ def test_fwht128_is_the_reference_stage_order_bit_exact(dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_lane_butterflies_are_bit_exact(dtype):
     """The in-register FWHT of the mRoPE and combine kernels (DPP within rows, permlane swaps
-    across rows): with identity tables (cos 1, sin 0) the mRoPE output is that FWHT of the input,
-    bit-exact to its stage order (stride 64 in the lane, then strides 1 .. 32) evaluated in
-    float32 on the CPU, and within one output rounding of the reference's order."""
+    across rows, stride 64 inside the lane last): with identity tables (cos 1, sin 0) the mRoPE
+    output is that FWHT of the input, bit-exact to the reference's stage order (stride 1 .. 64,
+    triton_qwen_mrope.py:23-32) evaluated in float32 on the CPU."""
     import r2omni_amd as ro
     from oracle.quant import normalized_fwht
 
@@ -180,17 +164,14 @@ def test_lane_butterflies_are_bit_exact(dtype):
     torch.cuda.synchronize()
     for got, x in ((qo, q), (ko, k)):
         rows = _np32(x).reshape(-1, 128)
-        assert _exact_where_normal(got.reshape(-1, 128), _butterfly_fwht_f32(rows), dtype)
-        ref = normalized_fwht(rows)
-        step = np.abs(ref) * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-4
-        assert np.all(np.abs(_np32(got).reshape(-1, 128) - ref) <= step)
+        assert _exact_where_normal(got.reshape(-1, 128), normalized_fwht(rows), dtype)
 
 
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_qkv_mrope_folds_the_v_hadamard(case):
     """qwen_qk_mrope(value=V): Q and K bit-identical to the two-tensor call; with the Hadamard on, V
-    is its FWHT (bit-exact to the in-register butterfly order, within one output rounding of the
-    reference's order), written into a caller's buffer when given; with it off, V is returned as is."""
+    is its FWHT (bit-exact to the reference's stage order), written into a caller's buffer when
+    given; with it off, V is returned as is."""
     import r2omni_amd as ro
     from oracle.quant import normalized_fwht
 
@@ -217,10 +198,7 @@ def test_qkv_mrope_folds_the_v_hadamard(case):
     assert v3.data_ptr() == vbuf.data_ptr()
     rows = _np32(v).reshape(-1, 128)
     if had:
-        assert _exact_where_normal(v3.reshape(-1, 128), _butterfly_fwht_f32(rows), qdt)
-        ref = normalized_fwht(rows)
-        step = np.abs(ref) * (2.0 ** -7 if qdt == torch.bfloat16 else 2.0 ** -10) + 1e-4
-        assert np.all(np.abs(_np32(v3).reshape(-1, 128) - ref) <= step)
+        assert _exact_where_normal(v3.reshape(-1, 128), normalized_fwht(rows), qdt)
     else:
         assert torch.equal(v3, v)
         _, _, same = ro.qwen_qk_mrope(q, k, cos, sin, sections, value=v)
@@ -232,9 +210,10 @@ def test_qkv_mrope_folds_the_v_hadamard(case):
 @pytest.mark.parametrize("case", range(len(NORM_CASES)))
 def test_qwen3_qkv_norm_rope_folds_the_v_hadamard(case):
     """qwen3_qk_norm_rope(value=V): Q and K bit-identical to the two-tensor call; with the Hadamard
-    on, V is its in-register-order FWHT (bit-exact) written into the caller's buffer; with it off, V
-    is copied unchanged into that buffer."""
+    on, V is its FWHT (bit-exact to the reference's stage order) written into the caller's buffer;
+    with it off, V is copied unchanged into that buffer."""
     import r2omni_amd as ro
+    from oracle.quant import normalized_fwht
     from test_oracle_rope import _rope_tables_1d
 
     if not torch.cuda.is_available():
@@ -257,8 +236,34 @@ def test_qwen3_qkv_norm_rope_folds_the_v_hadamard(case):
     assert torch.equal(k3.view(torch.int16), k2.view(torch.int16))
     assert v3.data_ptr() == vbuf.data_ptr()
     if had:
-        assert _exact_where_normal(v3.reshape(-1, 128), _butterfly_fwht_f32(_np32(v).reshape(-1, 128)), dt)
+        assert _exact_where_normal(v3.reshape(-1, 128), normalized_fwht(_np32(v).reshape(-1, 128)), dt)
     else:
         assert torch.equal(v3, v)
     with pytest.raises(ValueError, match="one tensor per input"):
         ro.qwen3_qk_norm_rope(q, k, wq, wk, cos, sin, value=v, output=(q2, k2))
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_rejected_call_leaves_the_value_buffer_untouched(norm):
+    """Every output is checked before the launch or the V copy: a bad Q output raises and the
+    caller's V buffer keeps its contents (apply_hadamard=False copies V into it only on success)."""
+    import r2omni_amd as ro
+
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    dev = torch.device("cuda:0")
+    q = torch.randn(1, 4, 1, 128, device=dev).to(torch.bfloat16)
+    k = torch.randn(1, 2, 1, 128, device=dev).to(torch.bfloat16)
+    v = torch.randn(1, 2, 1, 128, device=dev).to(torch.bfloat16)
+    vbuf = torch.full_like(v, 3.0)
+    bad = (torch.empty(1, 4, 1, 64, device=dev, dtype=torch.bfloat16), torch.empty_like(k), vbuf)
+    with pytest.raises(ValueError):
+        if norm:
+            w = torch.ones(128, device=dev, dtype=torch.bfloat16)
+            cs = torch.zeros(1, 1, 128, device=dev, dtype=torch.bfloat16)
+            ro.qwen3_qk_norm_rope(q, k, w, w, cs, cs, value=v, output=bad)
+        else:
+            cs = torch.zeros(3, 1, 1, 128, device=dev, dtype=torch.float32)
+            ro.qwen_qk_mrope(q, k, cs, cs, (16, 24, 24), value=v, output=bad)
+    torch.cuda.synchronize()
+    assert torch.equal(vbuf, torch.full_like(v, 3.0))
