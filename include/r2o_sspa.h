@@ -226,9 +226,9 @@ int r2o_qk_mrope(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t
 /* r2o_qk_mrope plus, when v / v_out are non-NULL, the orthonormal FWHT-128 of the V rows
  * v [batch, hkv, tokens, 128] (same dtype) into v_out, in the same launch: the decode step's
  * K/V rotation (qwen_sspa_attention.py:1239-1247) and V Hadamard (triton_fwht_128 at :230-235,
- * triton_qwen_mrope.py:325-346) as one launch instead of two.  The V rows' butterflies run in
- * the in-register order of the Q/K FWHT (stride 64, then 1 .. 32), so they may differ from
- * r2o_fwht128 in the last bit.  v and v_out must both be NULL or both be set. */
+ * triton_qwen_mrope.py:325-346) as one launch instead of two.  Every FWHT here (Q, K, V) runs the
+ * reference's stage order (stride 1 .. 64), so V equals r2o_fwht128's result bit for bit.
+ * v and v_out must both be NULL or both be set. */
 int r2o_qkv_mrope(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* q_out, uint16_t* k_out,
                   uint16_t* v_out, int64_t dtype, int64_t batch, int64_t hq, int64_t hkv, int64_t tokens,
                   const void* cos, const void* sin, int64_t table_dtype, const int64_t* cos_strides,
