@@ -142,6 +142,17 @@ int r2o_decode_partial(const r2o_decode_params* params, void* stream);
  * (triton_fourq_splitk.py:1023-1155, :936-1020, launched at :1467-1541). */
 int r2o_decode_combine(const r2o_decode_params* params, void* stream);
 
+/* Workspace-free decode: r2o_decode_partial then r2o_decode_combine on `stream`, with the split-K
+ * partial states held in a library-owned device array (one per GPU, kept until the process ends)
+ * instead of params->partial_max / partial_sum / partial_out, which are ignored and may be NULL.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops).  Allocates nothing (no hipMalloc / hipFree).
+ * Limit: params->n_items <= 1024 work items (8.1 MiB of partial states), else R2O_EINVAL before any
+ * launch.  The array is shared by every call on one GPU and keeps the last call's contents (every
+ * slot a launch reads is written first by that launch): calls that overlap on one GPU (different
+ * streams, or threads without ordering) race on it. */
+int r2o_decode_noalloc(const r2o_decode_params* params, void* stream);
+
 /* ----------------------------------------------------------------- pack / append --------- */
 
 /* Per-channel affine INT4-K over `superblock`-token blocks into the compact arena.

@@ -34,6 +34,8 @@
 //
 // Semantics follow triton_fourq_splitk.py:456-1020 (tile attention, exact state merge, fused
 // append :1007-1020, output Hadamard :1000-1006) and the oracle triton_fourq_attention.py:72-125.
+#include <atomic>
+
 #include "r2o_common.hpp"
 
 namespace {
@@ -784,8 +786,10 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     __syncthreads();
 
     // ---- merge the 4 wave states of this block and write the partial: 4 dims per thread
+    // (the planner numbers the slots 0 .. n_items - 1; a slot outside that range writes nothing)
     const float* base = reinterpret_cast<const float*>(smem);
-    for (int e = threadIdx.x; e < gqa * 32; e += blockDim.x) {
+    const int nmerge = (it.slot >= 0 && it.slot < p.n_items) ? gqa * 32 : 0;
+    for (int e = threadIdx.x; e < nmerge; e += blockDim.x) {
         const int h = e >> 5, d4 = (e & 31) * 4;
         float M = -INFINITY;
 #pragma unroll
@@ -893,7 +897,9 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
     }
     const int gqa = __builtin_amdgcn_readfirstlane(r2o_div_small((int)p.hq, (int)p.hkv));
     const int kvh = __builtin_amdgcn_readfirstlane(r2o_div_small(hqi, gqa)), h = hqi - kvh * gqa;
-    const int beg = r2o_ldg(p.group_begin + b * p.hkv + kvh), end = r2o_ldg(p.group_begin + b * p.hkv + kvh + 1);
+    // slot range of the group, clamped to the slots a launch of n_items items writes
+    const int beg = max(r2o_ldg(p.group_begin + b * p.hkv + kvh), 0);
+    const int end = min(r2o_ldg(p.group_begin + b * p.hkv + kvh + 1), (int)p.n_items);
     float m = -INFINITY, l = 0.f;
     r2o_f4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int base = beg + slice; base < end; base += kCombineUnroll * kCombineSlices) {
@@ -973,6 +979,54 @@ int validate(const r2o_decode_params* p) {
     return R2O_OK;
 }
 
+// ------------------------------------------------------------- workspace-free decode
+// The partial states of r2o_decode_noalloc live in this array: one per GPU for the life of the
+// process, kScratchSlots work items of (acc [16][128], max [16], sum [16]) fp32 = 8.1 MiB.
+constexpr int64_t kScratchSlots = 1024;
+constexpr int64_t kScratchFloats = kScratchSlots * (16 * 128 + 16 + 16);
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+
+}  // namespace
+
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+
+// Device address of this GPU's `scratch` (the host-side name is only a stand-in): looked up once
+// per device, with that device current, on its first r2o_decode_noalloc call.  Returns nullptr if
+// the lookup fails.
+float* scratch_address() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    float* ptr = g_scratch[dev].load(std::memory_order_acquire);
+    if (ptr == nullptr) {
+        void* addr = nullptr;
+        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) return nullptr;
+        ptr = static_cast<float*>(addr);
+        g_scratch[dev].store(ptr, std::memory_order_release);
+    }
+    return ptr;
+}
+
+int launch_decode(const r2o_decode_params& p, hipStream_t stream) {
+    const dim3 grid((unsigned)p.n_items), block(256);
+    switch (p.k_format) {
+        case kKInt4: hipLaunchKernelGGL(decode_partial_kernel<kKInt4>, grid, block, 0, stream, p); break;
+        case kKBf16: hipLaunchKernelGGL(decode_partial_kernel<kKBf16>, grid, block, 0, stream, p); break;
+        default: hipLaunchKernelGGL(decode_partial_kernel<kKInt2>, grid, block, 0, stream, p); break;
+    }
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
+int launch_combine(const r2o_decode_params& p, hipStream_t stream) {
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(p.hq + (p.do_append ? 1 : 0)), (unsigned)p.batch),
+                       dim3(512), 0, stream, p);
+    R2O_CHECK_LAUNCH();
+    return R2O_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -980,23 +1034,29 @@ extern "C" {
 int r2o_decode_partial(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
-    const dim3 grid((unsigned)params->n_items), block(256);
-    switch (params->k_format) {
-        case kKInt4: hipLaunchKernelGGL(decode_partial_kernel<kKInt4>, grid, block, 0, (hipStream_t)stream, *params); break;
-        case kKBf16: hipLaunchKernelGGL(decode_partial_kernel<kKBf16>, grid, block, 0, (hipStream_t)stream, *params); break;
-        default: hipLaunchKernelGGL(decode_partial_kernel<kKInt2>, grid, block, 0, (hipStream_t)stream, *params); break;
-    }
-    R2O_CHECK_LAUNCH();
-    return R2O_OK;
+    return launch_decode(*params, (hipStream_t)stream);
 }
 
 int r2o_decode_combine(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(params->hq + (params->do_append ? 1 : 0)),
-                       (unsigned)params->batch), dim3(512), 0, (hipStream_t)stream, *params);
-    R2O_CHECK_LAUNCH();
-    return R2O_OK;
+    return launch_combine(*params, (hipStream_t)stream);
+}
+
+int r2o_decode_noalloc(const r2o_decode_params* params, void* stream) {
+    if (!params) return R2O_EINVAL;
+    if (params->n_items > kScratchSlots) return R2O_EINVAL;  // more partial states than `scratch` holds
+    float* base = scratch_address();
+    if (base == nullptr) return R2O_ELAUNCH;
+    r2o_decode_params p = *params;  // the caller's partial pointers are ignored
+    p.partial_out = base;
+    p.partial_max = base + kScratchSlots * 16 * 128;
+    p.partial_sum = p.partial_max + kScratchSlots * 16;
+    const int rc = validate(&p);
+    if (rc) return rc;
+    const int lrc = launch_decode(p, (hipStream_t)stream);
+    if (lrc) return lrc;
+    return launch_combine(p, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -16,6 +16,7 @@ LIB_PATH = os.environ.get("R2O_SSPA_LIB", os.path.join(_PKG_DIR, "libr2o_sspa.so
 
 MAX_BATCH = 32
 MAX_GQA = 16
+NOALLOC_MAX_ITEMS = 1024  # work items r2o_decode_noalloc's device array holds
 
 c_i64 = ctypes.c_int64
 c_vp = ctypes.c_void_p
@@ -74,6 +75,7 @@ K_INT4, K_BF16, K_INT2 = 0, 1, 2
 _SIGNATURES = {
     "r2o_decode_partial": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_combine": (ctypes.POINTER(DecodeParams), c_vp),
+    "r2o_decode_noalloc": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_pack_int4_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                         c_vp),
     "r2o_pack_int2_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,

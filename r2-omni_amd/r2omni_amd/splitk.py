@@ -361,10 +361,34 @@ class SplitKExecutor:
         return [int(c.recent_fp_pool.active_length) for c in self.caches]
 
     def __call__(self, query: torch.Tensor, append=None) -> torch.Tensor:
+        p, query, fused = self._prepare_call(query, append, self.workspace.output)
+        self._launch(p, query.device)
+        self._finish_call(fused)
+        return self.workspace.output
+
+    def call_noalloc(self, query: torch.Tensor, append=None, *, out: torch.Tensor | None = None) -> torch.Tensor:
+        """``__call__`` through ``r2o_decode_noalloc``: the partial states live in the library's
+        per-GPU device array instead of the workspace, and nothing is allocated (unless ``append``
+        rows need a 16-byte-aligned copy).  At most ``_lib.NOALLOC_MAX_ITEMS`` work items; calls that
+        overlap on one GPU race on that array.  ``out`` (bf16 [B, Hq, 128]) defaults to the
+        workspace's output."""
+        out = self.workspace.output if out is None else out
+        if out.dtype != torch.bfloat16 or not out.is_contiguous():
+            raise ValueError("split-K output must be a contiguous bfloat16 tensor")
+        if self.n_items > _lib.NOALLOC_MAX_ITEMS:
+            raise ValueError(f"workspace-free decode holds at most {_lib.NOALLOC_MAX_ITEMS} work items")
+        p, query, fused = self._prepare_call(query, append, out)
+        p.partial_max = p.partial_sum = p.partial_out = None
+        _lib.check(_lib.load().r2o_decode_noalloc(ctypes.byref(p), ctypes.c_void_p(_lib.stream_of(query.device))),
+                   "r2o_decode_noalloc")
+        self._finish_call(fused)
+        return out
+
+    def _prepare_call(self, query: torch.Tensor, append, out: torch.Tensor):
+        """Checks of a decode call (before any launch) and its launch arguments."""
         if query.ndim == 4:
             query = query[:, :, 0]
         b = len(self.caches)
-        out = self.workspace.output
         if tuple(query.shape) != (b, self.num_query_heads, self.head_dim) or query.device != out.device \
                 or not query.is_contiguous():
             raise ValueError("query does not match prepared split-K executor")
@@ -397,12 +421,13 @@ class SplitKExecutor:
             gl = _per_request(gidx, b)
             lp = _per_request(lpos, b)
             fused = (ak, av, gl, lp)
-        self._launch(self._params(query, out, fused), query.device)
+        return self._params(query, out, fused), query, fused
+
+    def _finish_call(self, fused) -> None:
         # A stacked executor advances its private ring lengths; a B=1 executor leaves the cache's
         # host length to the caller (qwen_sspa_attention.py:1824-1826), as the reference does.
         if fused is not None and self.batched_recent_lengths is not None:
             self.batched_recent_lengths[:] = [n + 1 for n in self.batched_recent_lengths]
-        return out
 
 
     @staticmethod
