@@ -256,7 +256,7 @@ def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dic
     return out
 
 
-def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int) -> dict:
+class E2EQwenDecoder:
     """Configuration 4: greedy decode of a random-init Qwen2.5-Omni-7B language model on this path.
 
     Model: 28 layers (``n_layers``), hidden 3584, 28 query / 4 KV heads of 128, SwiGLU 18944, vocab
@@ -264,123 +264,172 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
     ``batch`` sequences of ``context`` seeded random token ids is prefilled through the whole model
     (flash attention); per layer its Hadamard-rotated K/V (keys after RoPE) go into an SSPA cache:
     INT4 keys, BF16/INT4/INT2 value pages drawn per 64-token page at 15/45/40 %, the newest 128 tokens
-    in the Recent-FP ring.  Then ``steps`` greedy steps: fused mRoPE + FWHT of Q/K, FWHT of V, the
-    packed-KV attention with fused append (BatchedDecoder; the first step flushes every ring inside
-    the batch), projections / MLP / lm_head as torch GEMMs.  The decode runs twice from the same
-    caches: eager launches, then the steps after the first replayed from one HIP graph per step (the
-    greedy argmax stays outside the graph); the graph run counts only if its tokens equal the eager
-    run's.
+    in the Recent-FP ring.  Then greedy steps: fused mRoPE + FWHT of Q/K and the FWHT of V in one
+    launch, the packed-KV attention with fused append (BatchedDecoder; the first step flushes every ring
+    inside the batch), projections / MLP / lm_head as torch GEMMs.  The greedy loop is the reference's
+    (qwen_r2omni_decode.py:248-292) with the manager's decode step (qwen_sspa_attention.py:1239-1247,
+    1794-1826) in place of HF attention.
     """
-    import torch
-    import torch.nn.functional as F
-    from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    import r2omni_amd as ro
-    from r2omni_amd.workloads import DecodeConfig, RequestData, TIER_CLASS, build_request_cache
+    HID, NH, NKV, HD, INTER, VOCAB, EPS = 3584, 28, 4, 128, 18944, 152064, 1e-6
+    SECTIONS, RECENT, PAGE, TIERS = (16, 24, 24), 128, 64, (0.15, 0.45, 0.4)
 
-    hid, nh, nkv, hd, inter, vocab, eps = 3584, 28, 4, 128, 18944, 152064, 1e-6
-    sections, recent = (16, 24, 24), 128
-    bf = torch.bfloat16
-    gen = torch.Generator(device=dev).manual_seed(0)
-    cpu = torch.Generator().manual_seed(0)
+    def __init__(self, dev, *, batch: int, context: int, n_layers: int):
+        import torch
 
-    def weight(*shape):
-        return (torch.randn(shape, generator=gen, device=dev) * 0.02).to(bf)
+        self.dev, self.batch, self.context, self.n_layers = dev, batch, context, n_layers
+        bf = torch.bfloat16
+        gen = torch.Generator(device=dev).manual_seed(0)
+        self.cpu_gen = torch.Generator().manual_seed(0)
 
-    t0 = time.perf_counter()
-    layers = []
-    for _ in range(n_layers):
-        layers.append({"wq": weight(hid, hid), "bq": weight(hid), "wk": weight(nkv * hd, hid), "bk": weight(nkv * hd),
-                       "wv": weight(nkv * hd, hid), "bv": weight(nkv * hd), "wo": weight(hid, hid),
-                       "wg": weight(inter, hid), "wu": weight(inter, hid), "wd": weight(hid, inter),
-                       "n1": torch.ones(hid, device=dev, dtype=bf), "n2": torch.ones(hid, device=dev, dtype=bf)})
-    embed, lm_head, n_final = weight(vocab, hid), weight(vocab, hid), torch.ones(hid, device=dev, dtype=bf)
-    inv_freq = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
+        def weight(*shape):
+            return (torch.randn(shape, generator=gen, device=dev) * 0.02).to(bf)
 
-    def rms(x, w):
+        hid, nkv, hd, inter = self.HID, self.NKV, self.HD, self.INTER
+        self.layers = []
+        for _ in range(n_layers):
+            self.layers.append({"wq": weight(hid, hid), "bq": weight(hid), "wk": weight(nkv * hd, hid),
+                                "bk": weight(nkv * hd), "wv": weight(nkv * hd, hid), "bv": weight(nkv * hd),
+                                "wo": weight(hid, hid), "wg": weight(inter, hid), "wu": weight(inter, hid),
+                                "wd": weight(hid, inter), "n1": torch.ones(hid, device=dev, dtype=bf),
+                                "n2": torch.ones(hid, device=dev, dtype=bf)})
+        self.embed, self.lm_head = weight(self.VOCAB, hid), weight(self.VOCAB, hid)
+        self.n_final = torch.ones(hid, device=dev, dtype=bf)
+        self.inv_freq = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
+        self.kv = None
+        self.first = None
+        self.prefill_s = 0.0
+        self.tiers = None
+
+    # ------------------------------------------------------------------ model pieces
+    def rms(self, x, w):
+        import torch
+
         xf = x.float()
-        return w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(bf)
+        return w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.EPS)).to(torch.bfloat16)
 
-    def tables(pos):  # text positions: the three mRoPE axes are equal; [3, B, T, 128] in bf16
-        ang = pos.float()[..., None] * inv_freq
+    def tables(self, pos):
+        """Text positions: the three mRoPE axes are equal; cos/sin [3, B, T, 128] in bf16."""
+        import torch
+
+        ang = pos.float()[..., None] * self.inv_freq
         ang = torch.cat([ang, ang], dim=-1)
-        return ang.cos().to(bf)[None].expand(3, *ang.shape), ang.sin().to(bf)[None].expand(3, *ang.shape)
+        return ang.cos().to(torch.bfloat16)[None].expand(3, *ang.shape), \
+            ang.sin().to(torch.bfloat16)[None].expand(3, *ang.shape)
 
-    def mlp(x, lw):
-        h = rms(x, lw["n2"])
+    def mlp(self, x, lw):
+        import torch.nn.functional as F
+
+        h = self.rms(x, lw["n2"])
         return x + F.linear(F.silu(F.linear(h, lw["wg"])) * F.linear(h, lw["wu"]), lw["wd"])
 
-    # ---- prefill: every sequence through the model; keep each layer's rotated K/V
-    kv = [[None] * batch for _ in range(n_layers)]
-    first = torch.empty(batch, dtype=torch.int64, device=dev)
-    with torch.no_grad():
-        for s_i in range(batch):
-            tok = torch.randint(0, vocab, (context,), generator=cpu).to(dev)
-            x = embed[tok]
-            cos, sin = tables(torch.arange(context, device=dev)[None])
-            for li, lw in enumerate(layers):
-                h = rms(x, lw["n1"])
-                q = F.linear(h, lw["wq"], lw["bq"]).view(context, nh, hd).transpose(0, 1)[None]
-                k = F.linear(h, lw["wk"], lw["bk"]).view(context, nkv, hd).transpose(0, 1)[None]
-                v = F.linear(h, lw["wv"], lw["bv"]).view(context, nkv, hd).transpose(0, 1)[None].contiguous()
-                q, k = ro.qwen_qk_mrope(q, k, cos, sin, sections)
-                with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
-                    a = F.scaled_dot_product_attention(q, k.repeat_interleave(nh // nkv, dim=1),
-                                                       v.repeat_interleave(nh // nkv, dim=1), is_causal=True)
-                x = x + F.linear(a[0].transpose(0, 1).reshape(context, hid), lw["wo"])
-                x = mlp(x, lw)
-                kv[li][s_i] = (ro.triton_fwht_128(k[0]), ro.triton_fwht_128(v[0]))
-            first[s_i] = F.linear(rms(x[-1:], n_final), lm_head).argmax(-1)[0]
-            torch.cuda.synchronize()
-            _log(f"e2e prefill sequence {s_i + 1}/{batch} ({time.perf_counter() - t0:.1f} s)")
-    prefill_s = time.perf_counter() - t0
+    # ------------------------------------------------------------------------- prefill
+    def prefill(self) -> None:
+        """Every sequence through the model (flash attention); keeps each layer's rotated K/V and the
+        first greedy token of every sequence."""
+        import torch
+        import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    cfg = DecodeConfig("e2e", nh, nkv, (context,), (0.15, 0.45, 0.4), recent=recent)
-    hist = context - recent
-    pages = hist // cfg.page
-    tiers = [torch.multinomial(torch.tensor(cfg.tier_probs), pages, replacement=True, generator=cpu)
-             for _ in range(n_layers * batch)]
+        import r2omni_amd as ro
 
-    def build_caches():
-        out = []
-        for li in range(n_layers):
-            row = []
-            for s_i in range(batch):
-                k, v = kv[li][s_i]
-                classes = torch.tensor(TIER_CLASS, dtype=torch.long)[tiers[li * batch + s_i]]
-                data = RequestData(None, k[:, :hist], v[:, :hist], k[:, hist:].transpose(0, 1),
-                                   v[:, hist:].transpose(0, 1), torch.arange(pages, dtype=torch.long) * cfg.page,
-                                   torch.full((pages,), cfg.page, dtype=torch.long), classes, None)
-                row.append(build_request_cache(cfg, data, append_capacity=steps + 256))
-            out.append(row)
+        dev, context, nh, nkv, hd, hid = self.dev, self.context, self.NH, self.NKV, self.HD, self.HID
+        t0 = time.perf_counter()
+        self.kv = [[None] * self.batch for _ in range(self.n_layers)]
+        self.first = torch.empty(self.batch, dtype=torch.int64, device=dev)
+        with torch.no_grad():
+            for s_i in range(self.batch):
+                tok = torch.randint(0, self.VOCAB, (context,), generator=self.cpu_gen).to(dev)
+                x = self.embed[tok]
+                cos, sin = self.tables(torch.arange(context, device=dev)[None])
+                for li, lw in enumerate(self.layers):
+                    h = self.rms(x, lw["n1"])
+                    q = F.linear(h, lw["wq"], lw["bq"]).view(context, nh, hd).transpose(0, 1)[None]
+                    k = F.linear(h, lw["wk"], lw["bk"]).view(context, nkv, hd).transpose(0, 1)[None]
+                    v = F.linear(h, lw["wv"], lw["bv"]).view(context, nkv, hd).transpose(0, 1)[None].contiguous()
+                    q, k = ro.qwen_qk_mrope(q, k, cos, sin, self.SECTIONS)
+                    with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                        a = F.scaled_dot_product_attention(q, k.repeat_interleave(nh // nkv, dim=1),
+                                                           v.repeat_interleave(nh // nkv, dim=1), is_causal=True)
+                    x = x + F.linear(a[0].transpose(0, 1).reshape(context, hid), lw["wo"])
+                    x = self.mlp(x, lw)
+                    self.kv[li][s_i] = (ro.triton_fwht_128(k[0]), ro.triton_fwht_128(v[0]))
+                self.first[s_i] = F.linear(self.rms(x[-1:], self.n_final), self.lm_head).argmax(-1)[0]
+                torch.cuda.synchronize()
+                _log(f"e2e prefill sequence {s_i + 1}/{self.batch} ({time.perf_counter() - t0:.1f} s)")
+        self.prefill_s = time.perf_counter() - t0
+        hist = context - self.RECENT
+        pages = hist // self.PAGE
+        self.tiers = [torch.multinomial(torch.tensor(self.TIERS), pages, replacement=True, generator=self.cpu_gen)
+                      for _ in range(self.n_layers * self.batch)]
+
+    def request_data(self, layer: int, seq: int):
+        """The cache inputs of one (layer, sequence): history K/V, the ring's 128 newest rows, pages."""
+        import torch
+
+        from r2omni_amd.workloads import TIER_CLASS, RequestData
+
+        hist = self.context - self.RECENT
+        pages = hist // self.PAGE
+        k, v = self.kv[layer][seq]
+        classes = torch.tensor(TIER_CLASS, dtype=torch.long)[self.tiers[layer * self.batch + seq]]
+        return RequestData(None, k[:, :hist], v[:, :hist], k[:, hist:].transpose(0, 1), v[:, hist:].transpose(0, 1),
+                           torch.arange(pages, dtype=torch.long) * self.PAGE,
+                           torch.full((pages,), self.PAGE, dtype=torch.long), classes, None)
+
+    def cache_config(self):
+        from r2omni_amd.workloads import DecodeConfig
+
+        return DecodeConfig("e2e", self.NH, self.NKV, (self.context,), self.TIERS, recent=self.RECENT, page=self.PAGE)
+
+    def build_caches(self, steps: int):
+        import torch
+
+        from r2omni_amd.workloads import build_request_cache
+
+        cfg = self.cache_config()
+        out = [[build_request_cache(cfg, self.request_data(li, s_i), append_capacity=steps + 256)
+                for s_i in range(self.batch)] for li in range(self.n_layers)]
         torch.cuda.synchronize()
         return out
 
-    def decode(use_graph: bool):
-        caches = build_caches()
+    # -------------------------------------------------------------------------- decode
+    def decode(self, steps: int, use_graph: bool, inspect=None):
+        """``steps`` greedy steps from fresh caches: eager launches, or (``use_graph``) the steps
+        after the first replayed from one HIP graph per step (the argmax stays outside the graph).
+        ``inspect(step, decoders)`` runs after each step's synchronisation (not for timing).
+        Returns (decode ms from HIP events, tokens [steps, B], whether every step's logits were finite)."""
+        import torch
+        import torch.nn.functional as F
+
+        import r2omni_amd as ro
+
+        dev, batch, nh, nkv, hd, hid = self.dev, self.batch, self.NH, self.NKV, self.HD, self.HID
+        caches = self.build_caches(steps)
         decs = [ro.BatchedDecoder(c, num_query_heads=nh, output_hadamard=True, use_graph=False) for c in caches]
-        tok = first.clone()
-        pos_dev = torch.full((1, 1), context, dtype=torch.int64, device=dev)
-        logits = torch.empty(batch, vocab, device=dev, dtype=bf)
-        positions = [context] * batch
+        tok = self.first.clone()
+        pos_dev = torch.full((1, 1), self.context, dtype=torch.int64, device=dev)
+        logits = torch.empty(batch, self.VOCAB, device=dev, dtype=torch.bfloat16)
+        finite = torch.ones((), dtype=torch.bool, device=dev)
+        positions = [self.context] * batch
         tokens = []
 
         def body(attend):
-            x = embed[tok]
-            cos, sin = tables(pos_dev.expand(batch, 1))
-            for lw, d in zip(layers, decs):
-                h = rms(x, lw["n1"])
+            x = self.embed[tok]
+            cos, sin = self.tables(pos_dev.expand(batch, 1))
+            for lw, d in zip(self.layers, decs):
+                h = self.rms(x, lw["n1"])
                 q = F.linear(h, lw["wq"], lw["bq"]).view(batch, nh, 1, hd)
                 k = F.linear(h, lw["wk"], lw["bk"]).view(batch, nkv, 1, hd)
                 v = F.linear(h, lw["wv"], lw["bv"]).view(batch, nkv, hd)
                 # Q/K rotation + FWHT and the V FWHT in one launch
-                ro.qwen_qk_mrope(q, k, cos, sin, sections, apply_hadamard=True, value=v.view(batch, nkv, 1, hd),
+                ro.qwen_qk_mrope(q, k, cos, sin, self.SECTIONS, apply_hadamard=True, value=v.view(batch, nkv, 1, hd),
                                  output=(d.query_buffer.view(batch, nh, 1, hd), d.key_buffer.view(batch, nkv, 1, hd),
                                          d.value_buffer.view(batch, nkv, 1, hd)))
                 attend(d)
                 x = x + F.linear(d.workspace.output.view(batch, hid), lw["wo"])
-                x = mlp(x, lw)
-            logits.copy_(F.linear(rms(x, n_final), lm_head))
+                x = self.mlp(x, lw)
+            logits.copy_(F.linear(self.rms(x, self.n_final), self.lm_head))
             pos_dev.add_(1)
 
         def eager_attend(d):
@@ -389,6 +438,14 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
         def graph_attend(d):
             d.executor._launch(d._params, dev)
 
+        def greedy(step):
+            tok.copy_(logits.argmax(-1))
+            finite.logical_and_(torch.isfinite(logits).all())
+            tokens.append(tok.clone())
+            if inspect is not None:
+                torch.cuda.synchronize()
+                inspect(step, decs)
+
         stream = torch.cuda.current_stream(dev)
         e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         graph = None
@@ -396,9 +453,8 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
             torch.cuda.synchronize()
             e[0].record(stream)
             body(eager_attend)  # step 1: every ring is full and flushes inside the batch
-            tok.copy_(logits.argmax(-1))
+            greedy(0)
             e[1].record(stream)
-            tokens.append(tok.clone())
             positions = [p + 1 for p in positions]
             if use_graph:
                 for d in decs:  # the step's host bookkeeping; the captured launches advance the device state
@@ -422,36 +478,47 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
                         d._advance()
                 else:
                     body(eager_attend)
-                tok.copy_(logits.argmax(-1))
-                tokens.append(tok.clone())
+                greedy(i)
                 positions = [p + 1 for p in positions]
             e[3].record(stream)
             torch.cuda.synchronize()
         ms = e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[3])
         del decs, caches, graph
         torch.cuda.empty_cache()
-        return ms, torch.stack(tokens)
+        return ms, torch.stack(tokens), bool(finite.item())
 
-    eager_ms, eager_tokens = decode(False)
+
+def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int) -> dict:
+    """Configuration 4 decode tok/s: the decode runs twice from the same caches, eager launches and
+    then one HIP graph per step; the faster is reported (a graph run only if its tokens equal the
+    eager run's)."""
+    import torch
+
+    model = E2EQwenDecoder(dev, batch=batch, context=context, n_layers=n_layers)
+    model.prefill()
+    eager_ms, eager_tokens, eager_finite = model.decode(steps, False)
     _log(f"e2e eager decode: {eager_ms:.1f} ms for {steps} steps")
-    graph_ms, graph_tokens = decode(True)
+    graph_ms, graph_tokens, graph_finite = model.decode(steps, True)
     _log(f"e2e graph decode: {graph_ms:.1f} ms for {steps} steps")
     match = bool(torch.equal(eager_tokens, graph_tokens))
-    # both modes run the same decode; the faster one is reported (a graph run only if its tokens match)
     use_graph = match and graph_ms < eager_ms
     best_ms = graph_ms if use_graph else eager_ms
-    return {"metric": "e2e decode tok/s", "value": round(batch * steps / (best_ms * 1e-3), 1), "unit": "tok/s",
-            "higher_is_better": True, "steps": steps, "ms_per_step": round(best_ms / steps, 3),
-            "mode": "hip_graph_per_step" if use_graph else "eager",
-            "eager_tok_s": round(batch * steps / (eager_ms * 1e-3), 1),
-            "graph_tok_s": round(batch * steps / (graph_ms * 1e-3), 1), "graph_matches_eager": match,
-            "dtype": "bf16", "data": "synthetic (random-init weights N(0, 0.02), seeded random token ids)",
-            "config": {"workload": "cfg4 qwen25omni7b e2e decode", "layers": n_layers, "batch": batch,
-                       "prefill_tokens": context, "decode_steps": steps, "value_tiers": "15/45/40 per 64-token page",
-                       "keys": "compact INT4", "hadamard": True},
-            "prefill_s": round(prefill_s, 1),
-            "note": "host clock excluded: HIP events around the decode steps (first step eager with the flush "
-                    "of every ring; graph capture outside the timed span); greedy argmax in eager launches"}
+    result = {"metric": "e2e decode tok/s", "value": round(batch * steps / (best_ms * 1e-3), 1), "unit": "tok/s",
+              "higher_is_better": True, "steps": steps, "ms_per_step": round(best_ms / steps, 3),
+              "mode": "hip_graph_per_step" if use_graph else "eager",
+              "eager_tok_s": round(batch * steps / (eager_ms * 1e-3), 1),
+              "graph_tok_s": round(batch * steps / (graph_ms * 1e-3), 1), "graph_matches_eager": match,
+              "logits_finite": eager_finite and graph_finite,
+              "dtype": "bf16", "data": "synthetic (random-init weights N(0, 0.02), seeded random token ids)",
+              "config": {"workload": "cfg4 qwen25omni7b e2e decode", "layers": n_layers, "batch": batch,
+                         "prefill_tokens": context, "decode_steps": steps, "value_tiers": "15/45/40 per 64-token page",
+                         "keys": "compact INT4", "hadamard": True},
+              "prefill_s": round(model.prefill_s, 1),
+              "note": "HIP events around the decode steps (first step eager with the flush of every ring; graph "
+                      "capture outside the timed span); greedy argmax in eager launches"}
+    del model
+    torch.cuda.empty_cache()
+    return result
 
 
 def main() -> int:
