@@ -9,7 +9,11 @@ To make the bytes come from HBM rather than the 256 MB Infinity Cache, the steps
 
 Reported: ``value`` = algorithmic GB/s of a layer call, ``ms_per_step`` = time per layer call,
 ``roofline`` for the dominant partial kernel (its average duration from HIP events on its
-stream), ``cpu_baseline`` = the CPU oracle's dequantise+attention on the same packed data.
+stream), ``cpu_baseline`` = the reference's CPU dequantise+attention path (restated in torch) on
+the same packed data, ``hbm_copy`` = the box's measured device copy rate, and ``e2e`` = the rest
+of the metric: configuration 4's decode tok/s (a random-init 28-layer Qwen2.5-Omni-7B decoder, batch
+8 x 32k, 128 greedy steps on this path).  Other modes (--prefill, --decode-steps, --sweep, --e2e)
+print their own line instead.
 """
 from __future__ import annotations
 
@@ -47,11 +51,13 @@ def _time_events(fn, steps: int, stream) -> float:
 
 
 def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
-    """Time the CPU oracle (dequantise every pool to fp32, softmax-merge) on the same packed data."""
+    """Time the reference's CPU path restated in torch (oracle/torch_path.py: every pool dequantised
+    with torch ops on each call, as triton_mixed_reference does, then the softmax states merged) on
+    the same packed data, on all of this process's host cores."""
     import numpy as np
     import torch
 
-    from oracle.attention import mixed_reference
+    from oracle import torch_path
     from oracle.cache import OracleCache
     from r2omni_amd.workloads import algorithmic_bytes
 
@@ -91,12 +97,12 @@ def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
             recent_page_lengths=rec.page_index.lengths.cpu().numpy(),
             pool_tokens=[c.fp_pool.token_count, i4.token_count, v2["v2_active"]], **kw, **v2,
         )
-        oc_list.append(oc)
+        oc_list.append(torch_path.from_oracle(oc))  # the packed cache as torch tensors, as the reference holds it
     qs = [q.float().cpu().numpy() for q in queries]
 
     def one_pass():
-        for oc, q in zip(oc_list, qs):
-            mixed_reference(q, oc)
+        for tc, q in zip(oc_list, qs):
+            torch_path.mixed_reference(q, tc)
 
     one_pass()  # warm-up
     reps, t0 = 0, time.perf_counter()
@@ -111,8 +117,37 @@ def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
     what = "request" if len(caches) == 1 else f"{len(caches)} ragged requests"
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"one decode-attention call over the same {what} (layer 0 of the GPU run), median of "
-                      f"{reps} after 1 warm-up: {med * 1e6:.0f} us/call on {threads} threads (torch CPU fp32 "
-                      "oracle: dequantise every pool, softmax, merge)"}
+                      f"{reps} after 1 warm-up: {med * 1e6:.0f} us/call on {threads} threads (torch CPU restatement "
+                      "of triton_mixed_reference: every pool dequantised with torch ops per call, fp32 softmax "
+                      "states per pool, exact merge)"}
+
+
+def copy_bandwidth(dev, mib: int = 1024, reps: int = 20) -> dict:
+    """The box's device-to-device copy rate: a torch copy of ``mib`` MiB, (bytes read + written) /
+    time, median of ``reps`` HIP-event timings."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    stream = torch.cuda.current_stream(dev)
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        dst.copy_(src)
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    ms = sorted(times)[reps // 2]
+    moved = 2 * n * 4
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"GBs": round(moved / (ms * 1e-3) / 1e9, 1), "pct_of_peak": round(100 * moved / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
+            "bytes_per_copy": moved, "method": f"device-to-device torch copy of {mib} MiB, (read + write bytes) / "
+                                             f"time, median of {reps} HIP-event timings"}
 
 
 def summarize_pmc(directory: str) -> dict:
@@ -521,6 +556,86 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
     return result
 
 
+def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed_base: int = 0) -> dict:
+    """Build ``n_layers`` distinct layer caches of ``cfg`` (seeds 1000 * layer + request) and time one
+    decode-attention layer call (partial + combine, no append) rotating over them with HIP events on
+    the launch stream; then the partial kernel alone the same way."""
+    import torch
+
+    import r2omni_amd as ro
+    from r2omni_amd import _lib
+    from r2omni_amd.workloads import algorithmic_bytes, build_request_cache, make_request
+
+    _log(f"building {n_layers} layer caches of {cfg.name} {list(cfg.lengths)} ...")
+    layers = []
+    for layer in range(n_layers):
+        datas = [make_request(cfg, total, seed=seed_base + 1000 * layer + r, device=dev)
+                 for r, total in enumerate(cfg.lengths)]
+        caches = [build_request_cache(cfg, d) for d in datas]
+        q = torch.cat([d.query for d in datas]).contiguous()
+        wss = [ro.allocate_splitk_workspace(c, num_query_heads=cfg.hq) for c in caches]
+        exs = [ro.prepare_splitk_executor(c, w, output_hadamard=True) for c, w in zip(caches, wss)]
+        ex = exs[0] if len(exs) == 1 else ro.stack_homogeneous_splitk_executors(exs)
+        del datas
+        layers.append((caches, q, ex))
+    _log(f"{n_layers} layers ready ({layers[0][2].n_items} work items in layer 0)")
+    torch.cuda.synchronize()
+    nbytes = algorithmic_bytes(layers[0][0], cfg.hq)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    params = [ex._params(q, ex.workspace.output, None) for _, q, ex in layers]
+    n_rot = len(layers)
+
+    def step(i):
+        p = ctypes.byref(params[i % n_rot])
+        lib.r2o_decode_partial(p, sp)
+        lib.r2o_decode_combine(p, sp)
+
+    def partial_only(i):
+        lib.r2o_decode_partial(ctypes.byref(params[i % n_rot]), sp)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ms_step = _time_events(step, steps, stream)
+    ms_partial = _time_events(partial_only, steps, stream)
+    return {"layers": layers, "bytes": nbytes, "ms_step": ms_step, "ms_partial": ms_partial,
+            "n_items": layers[0][2].n_items}
+
+
+def context_sweep(cfg, dev, *, factors, n_layers: int, steps: int, warmup: int) -> dict:
+    """The layer call of ``cfg`` at context lengths scaled by ``factors`` (the recent window kept at
+    128, the history rounded to whole pages), and a least-squares fit time = fixed + bytes / rate of
+    the whole call and of the partial kernel: the fixed part is the per-launch cost (start-up, tail,
+    combine), the rate the sustained streaming rate of the steady state."""
+    import numpy as np
+    import torch
+
+    points = []
+    for f in factors:
+        lengths = tuple(int(round((t - cfg.recent) * f / cfg.page)) * cfg.page + cfg.recent for t in cfg.lengths)
+        c = dataclasses.replace(cfg, lengths=lengths)
+        r = time_decode_layers(c, dev, n_layers=n_layers, steps=steps, warmup=warmup)
+        points.append({"factor": f, "context_lengths": list(lengths), "bytes": r["bytes"], "work_items": r["n_items"],
+                       "us_call": round(r["ms_step"] * 1e3, 3), "us_partial": round(r["ms_partial"] * 1e3, 3),
+                       "call_GBs": round(r["bytes"] / (r["ms_step"] * 1e-3) / 1e9, 1),
+                       "partial_GBs": round(r["bytes"] / (r["ms_partial"] * 1e-3) / 1e9, 1)})
+        _log(f"sweep x{f}: {points[-1]}")
+        del r
+        torch.cuda.empty_cache()
+    b = np.array([p["bytes"] for p in points], dtype=np.float64)
+    fits = {}
+    for key in ("us_call", "us_partial"):
+        t = np.array([p[key] for p in points], dtype=np.float64)
+        slope, fixed = np.polyfit(b, t, 1)
+        fits[key.replace("us_", "")] = {"fixed_us": round(float(fixed), 3),
+                                        "rate_GBs": round(float(1e-3 / slope), 1),
+                                        "rate_pct_of_peak": round(float(1e-3 / slope) / HBM_PEAK_GBS * 100, 1)}
+    return {"metric": "decode-attention layer call vs context (fit: time = fixed + bytes / rate)",
+            "config": f"{cfg.name} geometry, history x {list(factors)}", "points": points, "fit": fits}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -532,6 +647,7 @@ def main() -> int:
                     help="K format of the layer caches: compact INT4-K (default), compact INT2-K, "
                          "v_fourq_k_bf16 or matched-FP")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="leave configuration 4 (decode tok/s) out of the line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (HBM counter calibration)")
     ap.add_argument("--prefill", action="store_true",
@@ -540,6 +656,9 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=0, metavar="N",
                     help="only time N decode steps of --layers BatchedDecoder layers of --config (eager launches "
                          "and one HIP graph per step, flushes inside the batch) and print one JSON line")
+    ap.add_argument("--sweep", type=str, default="", metavar="F1,F2,...",
+                    help="only time the layer call of --config with its history scaled by each factor and print "
+                         "the points and the fit time = fixed + bytes / rate as one JSON line")
     ap.add_argument("--e2e", action="store_true",
                     help="only run configuration 4: prefill and greedy decode of a random-init Qwen2.5-Omni-7B "
                          "language model on this path, and print one JSON line (decode tok/s)")
@@ -562,14 +681,12 @@ def main() -> int:
 
     import torch
 
-    import r2omni_amd as ro
-    from r2omni_amd import _lib
-    from r2omni_amd.workloads import CONFIGS, algorithmic_bytes, build_request_cache, make_request
+    from r2omni_amd.workloads import CONFIGS
 
     dev = torch.device("cuda:0")
+    e2e_kw = dict(batch=args.e2e_batch, context=args.e2e_context, steps=args.e2e_steps, n_layers=args.e2e_layers)
     if args.e2e:
-        print(json.dumps(e2e_decode_bench(dev, batch=args.e2e_batch, context=args.e2e_context, steps=args.e2e_steps,
-                                          n_layers=args.e2e_layers)), flush=True)
+        print(json.dumps(e2e_decode_bench(dev, **e2e_kw)), flush=True)
         return 0
     if args.copy_calibration:
         n = args.copy_calibration * (1 << 20) // 4
@@ -589,42 +706,16 @@ def main() -> int:
     if args.decode_steps:
         print(json.dumps(decode_steps_bench(cfg, args.config, dev, args.decode_steps, args.layers)), flush=True)
         return 0
-    _log(f"building {args.layers} layer caches of {cfg.name} ...")
-    layers = []
-    for layer in range(args.layers):
-        datas = [make_request(cfg, total, seed=1000 * layer + r, device=dev) for r, total in enumerate(cfg.lengths)]
-        caches = [build_request_cache(cfg, d) for d in datas]
-        q = torch.cat([d.query for d in datas]).contiguous()
-        wss = [ro.allocate_splitk_workspace(c, num_query_heads=cfg.hq) for c in caches]
-        exs = [ro.prepare_splitk_executor(c, w, output_hadamard=True) for c, w in zip(caches, wss)]
-        ex = exs[0] if len(exs) == 1 else ro.stack_homogeneous_splitk_executors(exs)
-        del datas
-        layers.append((caches, q, ex))
-        _log(f"layer {layer} ready ({ex.n_items} work items)")
-    torch.cuda.synchronize()
-    nbytes = algorithmic_bytes(layers[0][0], cfg.hq)
-    lib = _lib.load()
-    stream = torch.cuda.current_stream(dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    params = [ex._params(q, ex.workspace.output, None) for _, q, ex in layers]
-    L = len(layers)
-
-    def step(i):
-        p = ctypes.byref(params[i % L])
-        lib.r2o_decode_partial(p, sp)
-        lib.r2o_decode_combine(p, sp)
-
-    def partial_only(i):
-        lib.r2o_decode_partial(ctypes.byref(params[i % L]), sp)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
+    if args.sweep:
+        factors = [float(f) for f in args.sweep.split(",")]
+        print(json.dumps(context_sweep(cfg, dev, factors=factors, n_layers=args.layers, steps=args.steps,
+                                       warmup=args.warmup)), flush=True)
+        return 0
     _log("timing ...")
     t0 = time.perf_counter()
-    ms_step = _time_events(step, args.steps, stream)
+    r = time_decode_layers(cfg, dev, n_layers=args.layers, steps=args.steps, warmup=args.warmup)
     wall = time.perf_counter() - t0
-    ms_partial = _time_events(partial_only, args.steps, stream)
+    nbytes, ms_step, ms_partial = r["bytes"], r["ms_step"], r["ms_partial"]
     gbs = nbytes / (ms_step * 1e-3) / 1e9
     part_gbs = nbytes / (ms_partial * 1e-3) / 1e9
     _log(f"step {ms_step * 1e3:.2f} us ({gbs:.0f} GB/s), partial {ms_partial * 1e3:.2f} us ({part_gbs:.0f} GB/s), "
@@ -632,7 +723,17 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
-        cpu = cpu_baseline(layers[0][0], [layers[0][1][r : r + 1] for r in range(len(cfg.lengths))], cfg.hq)
+        caches0, q0, _ = r["layers"][0]
+        cpu = cpu_baseline(caches0, [q0[i : i + 1] for i in range(len(cfg.lengths))], cfg.hq)
+    del r
+    torch.cuda.empty_cache()
+    _log("copy bandwidth ...")
+    copy = copy_bandwidth(dev)
+    copy["partial_kernel_pct_of_copy"] = round(100 * part_gbs / copy["GBs"], 1)
+    e2e = None
+    if not args.no_e2e:
+        _log("e2e (configuration 4) ...")
+        e2e = e2e_decode_bench(dev, **e2e_kw)
     traffic, traffic_src = traffic_from_profile() if args.config == 2 and args.variant == "int4k" else (None, None)
     line = {
         "metric": "packed-KV decode attn: HBM GB/s (% peak), us/layer @32k ctx; decode tok/s",
@@ -653,12 +754,14 @@ def main() -> int:
                    "k_format": args.variant, "hq": cfg.hq, "hkv": cfg.hkv,
                    "context_lengths": list(cfg.lengths), "v_tiers_bf16_int4_int2": list(cfg.tier_probs),
                    "recent_window": cfg.recent, "k_superblock": cfg.superblock, "int2_group": cfg.group,
-                   "rotated_layer_caches": L, "algorithmic_bytes_per_call": nbytes, "output_hadamard": True},
+                   "rotated_layer_caches": args.layers, "algorithmic_bytes_per_call": nbytes, "output_hadamard": True},
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
                      "kernel": "decode_partial_kernel", "avg_us": round(ms_partial * 1e3, 3)},
         "cpu_baseline": cpu,
+        "hbm_copy": copy,
+        "e2e": e2e,
     }
     print(json.dumps(line), flush=True)
     return 0
