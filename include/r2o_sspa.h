@@ -47,13 +47,13 @@ extern "C" {
 typedef struct r2o_request_desc {
     const uint8_t* k_packed;      /* R2O_K_INT4: compact INT4-K arena u8 [Hkv, k_capacity, 64];  */
                                   /* R2O_K_INT2: compact INT2-K arena u8 [Hkv, k_capacity, 32];  */
-                                  /* R2O_K_BF16: bf16 key rows [Hkv, k_capacity, 128]            */
+                                  /* R2O_K_BF16: 16-bit key rows [Hkv, k_capacity, 128]          */
     const uint16_t* k_scale;      /* fp16 [Hkv, k_superblocks, 128]                              */
     const uint8_t* k_zero;        /* u8 zero points (INT4) or fp16 offsets (INT2) [Hkv, k_sb, 128] */
     int64_t k_capacity;
     int64_t k_superblocks;
     const uint32_t* k_operands;   /* u32  [Hkv, k_superblocks, 128]  QK MFMA operands (see pack) */
-    const uint16_t* fp_v;         /* bf16 [Hkv, fp_stride, 128]  (FP-V pool)                     */
+    const uint16_t* fp_v;         /* 16-bit [Hkv, fp_stride, 128]  (FP-V pool, row_dtype)        */
     int64_t fp_stride;
     const uint8_t* i4_v;          /* u8   [Hkv, i4_stride, 64]   (per-token symmetric INT4-V)   */
     const float* i4_scale;        /* f32  [Hkv, i4_stride]                                       */
@@ -62,7 +62,7 @@ typedef struct r2o_request_desc {
     const uint16_t* i2_scale;     /* fp16 [Hkv, i2_stride, 128/G]                                */
     const uint8_t* i2_zero;       /* u8   [Hkv, i2_stride, 128/G]                                */
     int64_t i2_stride;
-    uint16_t* recent_k;           /* bf16 [Hkv, recent_capacity, 128]  Recent-FP ring, 16-byte aligned */
+    uint16_t* recent_k;           /* 16-bit [Hkv, recent_capacity, 128]  Recent-FP ring (row_dtype), 16-byte aligned */
     uint16_t* recent_v;
     int64_t recent_capacity;
     int32_t* recent_length;       /* device int32 active length (written by the fused append)   */
@@ -131,6 +131,9 @@ typedef struct r2o_decode_params {
     int32_t recent_len[R2O_MAX_BATCH];     /* host-tracked Recent-FP active length     */
     int64_t append_global[R2O_MAX_BATCH];  /* global token index of the appended token */
     int64_t append_logical[R2O_MAX_BATCH]; /* logical position of the appended token   */
+    int64_t row_dtype;              /* 0 = bf16, 1 = fp16: element type of every 16-bit row (FP-V pool,
+                                       Recent-FP ring, BF16-K arena, append_k / append_v); the output
+                                       stays bf16, as the reference's (triton_fourq_splitk.py:1653-1655) */
 } r2o_decode_params;
 
 /* Split-K partial pass.  Replaces _fourq_page_partial_kernel / _full_head_page_partial_kernel

@@ -54,6 +54,21 @@ constexpr int kMergeFloats = 16 + 16 + 16 * 128;    // per wave: m, l, acc
 // (matched-FP and v_fourq_k_bf16 caches) or the compact INT2 arena (v_fourq_k_int2_compact).
 enum KFormat { kKInt4 = 0, kKBf16 = 1, kKInt2 = 2 };
 
+// Element type of the 16-bit rows (FP-V pool, Recent-FP ring, BF16-K arena, appended token):
+// r2o_decode_params.row_dtype.  Their MFMAs take the rows as they are, with P and the query packed to
+// the same type.
+enum RowFormat { kRowBf16 = 0, kRowF16 = 1 };
+
+template <int RF>
+__device__ __forceinline__ uint32_t pack_row2(float lo, float hi) {
+    return RF == kRowF16 ? r2o_pack_h2(lo, hi) : r2o_pack_bf2(lo, hi);
+}
+template <int RF>
+__device__ __forceinline__ r2o_f4 mfma_rows(r2o_u4 a, r2o_u4 b, r2o_f4 c) {
+    if constexpr (RF == kRowF16) return r2o_mfma_f16(a, b, c);
+    else return r2o_mfma_bf16(a, b, c);
+}
+
 // Per-kernel LDS / occupancy configuration.
 template <int KF>
 struct KernelCfg {
@@ -78,8 +93,8 @@ struct WaveState {
 // Query operand of head l16 of the KV group (padded heads are zero), channels 32g .. 32g+31, in
 // the K operand order of the format: f16 pairs (8j+u, 8j+u+4) for INT4-K, f16 pairs
 // (16(j/2) + 4(j%2) + u, +8) for INT2-K, both scaled by D^-1/2 log2(e), or bf16 pairs in channel
-// order for bf16 keys (BF16-K pools and the Recent-FP ring).
-template <int KF>
+// order for bf16 keys (BF16-K pools and the Recent-FP ring; fp16 pairs for fp16 rows).
+template <int KF, int RF>
 __device__ __forceinline__ void load_query(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa, int l16,
                                            int g, float qscale, uint32_t (&qp)[4][4]) {
     const bool head_ok = l16 < gqa;
@@ -99,7 +114,7 @@ __device__ __forceinline__ void load_query(const r2o_decode_params& p, int64_t b
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            qp[j][u] = KF == kKBf16 ? r2o_pack_bf2(qf[8 * j + 2 * u], qf[8 * j + 2 * u + 1])
+            qp[j][u] = KF == kKBf16 ? pack_row2<RF>(qf[8 * j + 2 * u], qf[8 * j + 2 * u + 1])
                      : KF == kKInt4 ? r2o_pack_h2(qf[8 * j + u] * qscale, qf[8 * j + u + 4] * qscale)
                                     : r2o_pack_h2(qf[16 * (j >> 1) + 4 * (j & 1) + u] * qscale,
                                                   qf[16 * (j >> 1) + 4 * (j & 1) + u + 8] * qscale);
@@ -156,14 +171,15 @@ __device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8]
     softmax_step<8>(st, sv, pk, g, add, extra);
 }
 
-// PV for bf16 V rows held as R[k] = 8 dims (8*l16 ..) of token tile_token(g, k).
-__device__ __forceinline__ void pv_bf16(WaveState& st, const r2o_u4& ap, const r2o_u4 (&R)[8]) {
+// PV for 16-bit V rows held as R[k] = 8 dims (8*l16 ..) of token tile_token(g, k).
+template <int RF>
+__device__ __forceinline__ void pv_rows(WaveState& st, const r2o_u4& ap, const r2o_u4 (&R)[8]) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         const uint32_t sel = (q & 1) ? 0x07060302u : 0x05040100u;
         const r2o_u4 bop = {r2o_perm(R[1][q >> 1], R[0][q >> 1], sel), r2o_perm(R[3][q >> 1], R[2][q >> 1], sel),
                             r2o_perm(R[5][q >> 1], R[4][q >> 1], sel), r2o_perm(R[7][q >> 1], R[6][q >> 1], sel)};
-        st.acc[q] = r2o_mfma_bf16(ap, bop, st.acc[q]);
+        st.acc[q] = mfma_rows<RF>(ap, bop, st.acc[q]);
     }
 }
 
@@ -313,14 +329,14 @@ __device__ __forceinline__ void tile_logits(const SegCtx& c, int a0, int g, cons
 }
 
 // PV of one tile with probabilities pk (the lane's 8 tokens).
-template <int KIND, bool TS>  // TS: INT2 values with one scale and zero point per token (group 128)
+template <int KIND, bool TS, int RF>  // TS: INT2 values with one scale and zero point per token (group 128)
 __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const VConst& vc, const float (&pk)[8],
                                         const VRegs<KIND>& cur) {
     r2o_u4 ap;
     if constexpr (KIND == kFP) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
-        pv_bf16(st, ap, cur.v);
+        for (int u = 0; u < 4; ++u) ap[u] = pack_row2<RF>(pk[2 * u], pk[2 * u + 1]);
+        pv_rows<RF>(st, ap, cur.v);
     } else if constexpr (KIND == kI4) {
         // P' = p * s_t; the signed codes (xor 8) enter as 1032 + c (low nibble) and, read in
         // place, 1152 + 16 c (high nibble).  sum_k P'_k is accumulated by one more MFMA on the
@@ -394,30 +410,31 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
 
 // QK^T of one BF16-K tile: per MFMA j the bf16 key rows (channels 32g + 8j ..) against the bf16
 // query pairs, scaled by D^-1/2 log2(e) afterwards (the recent-ring formulation).
+template <int RF>
 __device__ __forceinline__ void qk_bf16k(const uint32_t (&qp)[4][4], float qscale, const r2o_u4 (&kb)[2][4],
                                          r2o_f4 (&s)[2]) {
 #pragma unroll
     for (int mg = 0; mg < 2; ++mg) {
         r2o_f4 acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc = r2o_mfma_bf16(kb[mg][j], r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
+        for (int j = 0; j < 4; ++j) acc = mfma_rows<RF>(kb[mg][j], r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
         s[mg] = acc * qscale;
     }
 }
 
 // One tile: QK, masks, online softmax, PV.
-template <int KIND, int KF, bool TS>
+template <int KIND, int KF, bool TS, int RF>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
                                             int a0, int g, float qscale, const TileRegs<KIND, KF>& cur) {
     r2o_f4 s[2];
     float corr = 0.f;
-    if constexpr (KF == kKBf16) qk_bf16k(ss.qp, qscale, cur.kb, s);
+    if constexpr (KF == kKBf16) qk_bf16k<RF>(ss.qp, qscale, cur.kb, s);
     else if constexpr (KF == kKInt4) qk_int4k(ss.qp, vc, cur.ops, cur.kx, s, corr);
     else qk_int2k(ss.qp, vc, cur.ops, cur.kx, s, corr);
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
     softmax_tile(st, sv, pk, g, corr, (KIND == kI4 || TS) ? &ss.bias : nullptr);
-    pv_tile<KIND, TS>(st, ss, vc, pk, cur);
+    pv_tile<KIND, TS, RF>(st, ss, vc, pk, cur);
 }
 
 // ------------------------------------------------------------------ pool tiles via LDS DMA
@@ -590,7 +607,7 @@ __device__ __forceinline__ void touch_combine_kernarg(const r2o_decode_params& p
     asm volatile("" ::"s"(p.group_begin), "s"(p.hq), "s"(p.output_hadamard));
 }
 
-template <int KIND, int KF, bool TS>
+template <int KIND, int KF, bool TS, int RF>
 __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
                             unsigned char* smem, WaveState& st) {
     using Cfg = KernelCfg<KF>;
@@ -648,7 +665,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const VConst vc = make_vconst();
     const float qscale = p.sm_scale * kLog2e;
     SegState<KIND> ss;
-    load_query<KF>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: bf16 pairs, scaled after the MFMA
+    load_query<KF, RF>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: row-type pairs, scaled after the MFMA
     ss.bias = r2o_f4{0, 0, 0, 0};
     const SegCtx sc = {c.lo, c.hi};
     for (int i = 0; i < n; ++i) {
@@ -662,7 +679,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
             __builtin_amdgcn_wave_barrier();
             dma_tile<KIND, KF>(c, a_first + 32 * (i + kDmaStages), stage, lane);
         }
-        seg_compute<KIND, KF, TS>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
+        seg_compute<KIND, KF, TS, RF>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
     }
     if constexpr (TS) {  // remove the code offsets of the per-token-scale form
 #pragma unroll
@@ -680,6 +697,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
 // Recent-FP ring tiles (bf16 K and V, plus the fused-append token).  Every load of a tile is
 // issued before any is used (rows past the valid end read the last valid row, whose
 // probability is 0); a tile with no valid token is skipped.
+template <int RF>
 __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
                            WaveState& st) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -698,7 +716,7 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
     const float qscale = p.sm_scale * kLog2e;
     const bool head_ok = l16 < gqa;
     uint32_t qp[4][4];
-    load_query<kKBf16>(p, b, kvh, gqa, l16, g, qscale, qp);
+    load_query<kKBf16, RF>(p, b, kvh, gqa, l16, g, qscale, qp);
     const uint16_t* ring_k = reinterpret_cast<const uint16_t*>(it.k_base);
     const uint16_t* ring_v = reinterpret_cast<const uint16_t*>(it.v_base);
     const uint16_t* new_k = app ? p.append_k + (b * p.hkv + kvh) * 128 : ring_k;
@@ -725,7 +743,7 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
         for (int mg = 0; mg < 2; ++mg) {
             r2o_f4 acc = {0, 0, 0, 0};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = r2o_mfma_bf16(kr[mg][j], r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
+            for (int j = 0; j < 4; ++j) acc = mfma_rows<RF>(kr[mg][j], r2o_u4{qp[j][0], qp[j][1], qp[j][2], qp[j][3]}, acc);
             s[mg] = acc * qscale;
         }
         float sv[8], pk[8];
@@ -734,12 +752,12 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
         softmax_tile(st, sv, pk, g);
         r2o_u4 ap;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) ap[u] = r2o_pack_bf2(pk[2 * u], pk[2 * u + 1]);
-        pv_bf16(st, ap, R);
+        for (int u = 0; u < 4; ++u) ap[u] = pack_row2<RF>(pk[2 * u], pk[2 * u + 1]);
+        pv_rows<RF>(st, ap, R);
     }
 }
 
-template <int KF>
+template <int KF, int RF>
 __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
     __shared__ __align__(16) unsigned char smem[KernelCfg<KF>::kSmem];
     const r2o_work_item it = p.items[blockIdx.x];
@@ -754,13 +772,13 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP, KF, false>(p, it, smem, st); break;
-        case kI4: run_segment<kI4, KF, false>(p, it, smem, st); break;
+        case kFP: run_segment<kFP, KF, false, RF>(p, it, smem, st); break;
+        case kI4: run_segment<kI4, KF, false, RF>(p, it, smem, st); break;
         case kI2:  // INT2 values: one scale and zero point per token when a group spans all 128 dims
-            if (p.int2_group == 128) run_segment<kI2, KF, true>(p, it, smem, st);
-            else run_segment<kI2, KF, false>(p, it, smem, st);
+            if (p.int2_group == 128) run_segment<kI2, KF, true, RF>(p, it, smem, st);
+            else run_segment<kI2, KF, false, RF>(p, it, smem, st);
             break;
-        default: run_recent(p, it, st); break;
+        default: run_recent<RF>(p, it, st); break;
     }
 
     // ---- per-wave epilogue: reduce l (and u) over the 4 lane groups of each head
@@ -970,6 +988,7 @@ int validate(const r2o_decode_params* p) {
     if (p->q_dtype != 0 && p->q_dtype != 1) return R2O_EINVAL;
     if (p->page_size <= 0) return R2O_EINVAL;
     if (p->k_format != kKInt4 && p->k_format != kKBf16 && p->k_format != kKInt2) return R2O_EINVAL;
+    if (p->row_dtype != kRowBf16 && p->row_dtype != kRowF16) return R2O_EINVAL;
     if (p->do_append && (!p->append_k || !p->append_v)) return R2O_EINVAL;
     // the fused append moves the new rows in 16-byte pieces, 4 per thread of a 512-thread block
     if (p->do_append && (p->hkv > 128 || reinterpret_cast<uintptr_t>(p->append_k) % 16 ||
@@ -1011,10 +1030,20 @@ float* scratch_address() {
 
 int launch_decode(const r2o_decode_params& p, hipStream_t stream) {
     const dim3 grid((unsigned)p.n_items), block(256);
+    const bool f16 = p.row_dtype == kRowF16;
     switch (p.k_format) {
-        case kKInt4: hipLaunchKernelGGL(decode_partial_kernel<kKInt4>, grid, block, 0, stream, p); break;
-        case kKBf16: hipLaunchKernelGGL(decode_partial_kernel<kKBf16>, grid, block, 0, stream, p); break;
-        default: hipLaunchKernelGGL(decode_partial_kernel<kKInt2>, grid, block, 0, stream, p); break;
+        case kKInt4:
+            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKInt4, kRowF16>), grid, block, 0, stream, p);
+            else hipLaunchKernelGGL((decode_partial_kernel<kKInt4, kRowBf16>), grid, block, 0, stream, p);
+            break;
+        case kKBf16:
+            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowF16>), grid, block, 0, stream, p);
+            else hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowBf16>), grid, block, 0, stream, p);
+            break;
+        default:
+            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKInt2, kRowF16>), grid, block, 0, stream, p);
+            else hipLaunchKernelGGL((decode_partial_kernel<kKInt2, kRowBf16>), grid, block, 0, stream, p);
+            break;
     }
     R2O_CHECK_LAUNCH();
     return R2O_OK;

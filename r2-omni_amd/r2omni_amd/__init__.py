@@ -7,6 +7,7 @@ Import names mirror the reference modules the Qwen/MiniCPM SSPA manager imports
 from .batch import BatchedDecoder, DecodeStepGraph
 from .cache import (
     BF16KeyArena,
+    CacheVariant,
     CompactInt2KeyArena,
     CompactInt2ValueArena,
     CompactInt4KeyArena,
@@ -36,6 +37,7 @@ from .policy import (
     plan_from_pages,
     project_token_bits_to_pages,
 )
+from .reference import normalized_fwht, triton_mixed_reference
 from .rope import qwen3_qk_norm_rope, qwen_qk_mrope
 from .splitk import (
     SplitKExecutor,

@@ -52,6 +52,7 @@ class DecodeParams(ctypes.Structure):
         ("recent_len", ctypes.c_int32 * MAX_BATCH),
         ("append_global", c_i64 * MAX_BATCH),
         ("append_logical", c_i64 * MAX_BATCH),
+        ("row_dtype", c_i64),
     ]
 
 

@@ -62,8 +62,9 @@ class BatchedDecoder:
         # the planner's item count is bounded whatever the cache sizes: one workspace serves every flush
         self.workspace = allocate_splitk_workspace(self.caches[0], num_query_heads=self.hq, batch_size=b,
                                                    total_blocks=max_work_items(b, self.hkv, _num_cus(self.device)))
-        self.query_buffer = torch.zeros((b, self.hq, 128), device=self.device, dtype=torch.bfloat16)
-        self.key_buffer = torch.zeros((b, self.hkv, 128), device=self.device, dtype=torch.bfloat16)
+        rows = first.fp_k.dtype  # the step's query and appended rows in the cache's row dtype
+        self.query_buffer = torch.zeros((b, self.hq, 128), device=self.device, dtype=rows)
+        self.key_buffer = torch.zeros((b, self.hkv, 128), device=self.device, dtype=rows)
         self.value_buffer = torch.zeros_like(self.key_buffer)
         self.step_positions = torch.zeros((b, 2), device=self.device, dtype=torch.int64)
         self._next_positions: list[tuple[int, int]] | None = None  # what the device holds for the next step

@@ -95,13 +95,14 @@ class CompactMetadataArena:
 # ------------------------------------------------------------------------ BF16 K rows
 @dataclass
 class BF16KeyArena:
-    """Key rows kept in bf16 in physical pool order (FP, INT4, INT2) with append capacity.
+    """Key rows kept in the model dtype (bf16 or fp16) in physical pool order (FP, INT4, INT2) with
+    append capacity.
 
     Backs the matched-FP cache and the v_fourq_k_bf16 variant: the pools' ``fp_k`` are views of
     ``rows`` (precision_pool.py:834-906 keeps one bf16 K tensor per pool; one arena serves the
     decode kernel, which reads K rows by physical position).
     """
-    rows: torch.Tensor              # bf16 [H, capacity, D]
+    rows: torch.Tensor              # bf16 / fp16 [H, capacity, D]
     active_length: int
     capacity: int
     segment_offsets: tuple[int, int, int]
@@ -977,9 +978,7 @@ def build_three_precision_cache(
         raise ValueError("the SSPA decode path requires head_dim 128")
     _lib.require_device(key, "key")
     _lib.dtype_code(key.dtype)
-    bf16_keys = matched_fp or cache_variant == "v_fourq_k_bf16"
-    if bf16_keys and key.dtype != torch.bfloat16:
-        raise ValueError("the BF16-K decode path requires bfloat16 K/V")
+    bf16_keys = matched_fp or cache_variant == "v_fourq_k_bf16"  # key rows in the model dtype (bf16 or fp16)
     key = key.contiguous()
     value = value.contiguous()
     dev = key.device

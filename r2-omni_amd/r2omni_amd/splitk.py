@@ -237,8 +237,13 @@ def _request_words(cache: ThreePrecisionCache, ring=None) -> dict[str, int]:
     ck, cv = cache.compact_key, cache.compact_value
     fp, i4 = cache.fp_pool, cache.int4_pool
     rec = cache.recent_fp_pool if ring is None else ring
-    if rec.fp_k.dtype != torch.bfloat16:
-        raise ValueError("the gfx950 decode path requires bfloat16 FP-V / Recent-FP rows")
+    row = rec.fp_k.dtype
+    if row not in (torch.bfloat16, torch.float16):
+        raise ValueError("the gfx950 decode path requires bfloat16 or float16 FP-V / Recent-FP rows")
+    rows = [t for t in (rec.fp_v, fp.fp_v if fp.token_count else None,
+                        cache.bf16_key.rows if cache.bf16_key is not None else None) if t is not None]
+    if any(t.dtype != row for t in rows):
+        raise ValueError("FP-V, Recent-FP and BF16-K rows of one cache must share one dtype")
     i4_packed = i4.packed_v.packed if i4.token_count else None
     i4_scale = i4.packed_v.scale if i4.token_count else None
     if ck is not None:
@@ -342,6 +347,7 @@ class SplitKExecutor:
         p.batch, p.hq, p.hkv = len(self.caches), self.num_query_heads, self.num_key_value_heads
         p.superblock, p.int2_group, p.page_size = self.superblock, self.int2_group, self.page_size
         p.q_dtype = _lib.dtype_code(query.dtype)
+        p.row_dtype = _lib.dtype_code(self.caches[0].recent_fp_pool.fp_k.dtype)
         p.output_hadamard = int(self.output_hadamard)
         p.k_format = _k_format(self.caches[0])
         p.sm_scale = float(self.head_dim ** -0.5)
@@ -403,8 +409,9 @@ class SplitKExecutor:
             if ak.numel() != n or av.numel() != n or ak.device != query.device or av.device != query.device \
                     or not ak.is_contiguous() or not av.is_contiguous():
                 raise ValueError("append K/V must be contiguous [B,Hkv,1,D] or [B,Hkv,D]")
-            if ak.dtype != torch.bfloat16 or av.dtype != torch.bfloat16:
-                raise ValueError("append K/V must be bfloat16 like the Recent-FP ring")
+            ring_dtype = self.caches[0].recent_fp_pool.fp_k.dtype
+            if ak.dtype != ring_dtype or av.dtype != ring_dtype:
+                raise ValueError(f"append K/V must be {ring_dtype} like the Recent-FP ring")
             if ak.data_ptr() % 16 or av.data_ptr() % 16:  # the kernel moves the rows in 16-byte pieces
                 ak, av = ak.clone(), av.clone()
             capacity = self.caches[0].recent_fp_pool.capacity
@@ -474,7 +481,8 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
     sb = 32 if bf16k else first.compact_key.superblock_size
     group = 32 if first.compact_value is None else first.compact_value.group_size
     for r, c in enumerate(caches):
-        if _k_format(c) != kf or (not bf16k and c.compact_key.superblock_size != sb) \
+        if _k_format(c) != kf or c.recent_fp_pool.fp_k.dtype != rec.fp_k.dtype \
+                or (not bf16k and c.compact_key.superblock_size != sb) \
                 or (c.compact_value is not None and c.compact_value.group_size != group) \
                 or int(c.recent_fp_pool.fp_k.shape[0]) != hkv or c.page_size != first.page_size:
             raise ValueError(f"batched split-K geometry differs for request {r}")

@@ -31,6 +31,8 @@ class DecodeConfig:
     group: int = 32
     variant: str = "int4k"     # "int4k" (v_fourq_k_int4_compact), "int2k" (v_fourq_k_int2_compact),
                                # "bf16k" (v_fourq_k_bf16) or "matched" (matched-FP)
+    dtype: str = "bfloat16"    # model dtype of Q/K/V: "bfloat16" or "float16" (values drawn in bf16
+                               # and converted, exactly, so both dtypes hold the same numbers)
 
 
 CONFIGS = {
@@ -79,6 +81,10 @@ def make_request(cfg: DecodeConfig, total: int, seed: int, device) -> RequestDat
     classes = torch.tensor(TIER_CLASS, dtype=torch.long)[tiers]
     offsets = torch.arange(pages, dtype=torch.long) * cfg.page
     lengths = torch.full((pages,), cfg.page, dtype=torch.long)
+    if cfg.dtype == "float16":
+        query, key, value, rk, rv = (t.to(torch.float16) for t in (query, key, value, rk, rv))
+    elif cfg.dtype != "bfloat16":
+        raise ValueError("DecodeConfig.dtype must be bfloat16 or float16")
     return RequestData(query, key, value, rk, rv, offsets, lengths, classes, outliers)
 
 
