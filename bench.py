@@ -23,6 +23,7 @@ import dataclasses
 import json
 import os
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -323,11 +324,14 @@ class E2EQwenDecoder:
         hid, nkv, hd, inter = self.HID, self.NKV, self.HD, self.INTER
         self.layers = []
         for _ in range(n_layers):
-            self.layers.append({"wq": weight(hid, hid), "bq": weight(hid), "wk": weight(nkv * hd, hid),
-                                "bk": weight(nkv * hd), "wv": weight(nkv * hd, hid), "bv": weight(nkv * hd),
-                                "wo": weight(hid, hid), "wg": weight(inter, hid), "wu": weight(inter, hid),
-                                "wd": weight(hid, inter), "n1": torch.ones(hid, device=dev, dtype=bf),
-                                "n2": torch.ones(hid, device=dev, dtype=bf)})
+            wq, bq, wk, bk = weight(hid, hid), weight(hid), weight(nkv * hd, hid), weight(nkv * hd)
+            wv, bv, wo, wg, wu = weight(nkv * hd, hid), weight(nkv * hd), weight(hid, hid), weight(inter, hid), \
+                weight(inter, hid)
+            # q/k/v and gate/up projections as one GEMM each (the weights stacked along the output dim)
+            self.layers.append({"w_qkv": torch.cat((wq, wk, wv)), "b_qkv": torch.cat((bq, bk, bv)), "wo": wo,
+                                "w_gu": torch.cat((wg, wu)), "wd": weight(hid, inter),
+                                "n1": torch.ones(hid, device=dev, dtype=bf), "n2": torch.ones(hid, device=dev, dtype=bf)})
+            del wq, wk, wv, wg, wu
         self.embed, self.lm_head = weight(self.VOCAB, hid), weight(self.VOCAB, hid)
         self.n_final = torch.ones(hid, device=dev, dtype=bf)
         self.inv_freq = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
@@ -356,7 +360,8 @@ class E2EQwenDecoder:
         import torch.nn.functional as F
 
         h = self.rms(x, lw["n2"])
-        return x + F.linear(F.silu(F.linear(h, lw["wg"])) * F.linear(h, lw["wu"]), lw["wd"])
+        gate, up = F.linear(h, lw["w_gu"]).split(self.INTER, dim=-1)
+        return x + F.linear(F.silu(gate) * up, lw["wd"])
 
     # ------------------------------------------------------------------------- prefill
     def prefill(self) -> None:
@@ -379,9 +384,10 @@ class E2EQwenDecoder:
                 cos, sin = self.tables(torch.arange(context, device=dev)[None])
                 for li, lw in enumerate(self.layers):
                     h = self.rms(x, lw["n1"])
-                    q = F.linear(h, lw["wq"], lw["bq"]).view(context, nh, hd).transpose(0, 1)[None]
-                    k = F.linear(h, lw["wk"], lw["bk"]).view(context, nkv, hd).transpose(0, 1)[None]
-                    v = F.linear(h, lw["wv"], lw["bv"]).view(context, nkv, hd).transpose(0, 1)[None].contiguous()
+                    q, k, v = F.linear(h, lw["w_qkv"], lw["b_qkv"]).split((nh * hd, nkv * hd, nkv * hd), dim=-1)
+                    q = q.reshape(context, nh, hd).transpose(0, 1)[None]
+                    k = k.reshape(context, nkv, hd).transpose(0, 1)[None]
+                    v = v.reshape(context, nkv, hd).transpose(0, 1)[None].contiguous()
                     q, k = ro.qwen_qk_mrope(q, k, cos, sin, self.SECTIONS)
                     with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
                         a = F.scaled_dot_product_attention(q, k.repeat_interleave(nh // nkv, dim=1),
@@ -454,9 +460,10 @@ class E2EQwenDecoder:
             cos, sin = self.tables(pos_dev.expand(batch, 1))
             for lw, d in zip(self.layers, decs):
                 h = self.rms(x, lw["n1"])
-                q = F.linear(h, lw["wq"], lw["bq"]).view(batch, nh, 1, hd)
-                k = F.linear(h, lw["wk"], lw["bk"]).view(batch, nkv, 1, hd)
-                v = F.linear(h, lw["wv"], lw["bv"]).view(batch, nkv, hd)
+                q, k, v = F.linear(h, lw["w_qkv"], lw["b_qkv"]).split((nh * hd, nkv * hd, nkv * hd), dim=-1)
+                q = q.reshape(batch, nh, 1, hd)
+                k = k.reshape(batch, nkv, 1, hd)
+                v = v.reshape(batch, nkv, hd)
                 # Q/K rotation + FWHT and the V FWHT in one launch
                 ro.qwen_qk_mrope(q, k, cos, sin, self.SECTIONS, apply_hadamard=True, value=v.view(batch, nkv, 1, hd),
                                  output=(d.query_buffer.view(batch, nh, 1, hd), d.key_buffer.view(batch, nkv, 1, hd),
@@ -531,6 +538,19 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
 
     model = E2EQwenDecoder(dev, batch=batch, context=context, n_layers=n_layers)
     model.prefill()
+    # PyTorch-ROCm's own GEMM selection for the decode shapes (M = batch): TunableOp times the
+    # hipBLASLt / rocBLAS candidates once in a short untimed decode, then the choice is frozen so that
+    # the eager and graph runs use the same kernels
+    tunable = torch.cuda.tunable
+    tunable.enable(True)
+    tunable.set_filename(os.path.join(tempfile.gettempdir(), "r2o_tunableop_results.csv"))  # not into the repo
+    tunable.set_max_tuning_duration(30)
+    tunable.tuning_enable(True)
+    t_tune = time.perf_counter()
+    model.decode(2, False)
+    tunable.tuning_enable(False)
+    tune_s = time.perf_counter() - t_tune
+    _log(f"e2e GEMM tuning (TunableOp) {tune_s:.1f} s")
     eager_ms, eager_tokens, eager_finite = model.decode(steps, False)
     _log(f"e2e eager decode: {eager_ms:.1f} ms for {steps} steps")
     graph_ms, graph_tokens, graph_finite = model.decode(steps, True)
@@ -549,8 +569,11 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
                          "prefill_tokens": context, "decode_steps": steps, "value_tiers": "15/45/40 per 64-token page",
                          "keys": "compact INT4", "hadamard": True},
               "prefill_s": round(model.prefill_s, 1),
+              "gemm_selection": f"PyTorch TunableOp over hipBLASLt / rocBLAS, tuned in an untimed 2-step decode "
+                                f"({tune_s:.1f} s) and frozen; q/k/v and gate/up weights stacked into one GEMM each",
               "note": "HIP events around the decode steps (first step eager with the flush of every ring; graph "
                       "capture outside the timed span); greedy argmax in eager launches"}
+    tunable.enable(False)
     del model
     torch.cuda.empty_cache()
     return result
