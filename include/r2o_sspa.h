@@ -134,6 +134,11 @@ typedef struct r2o_decode_params {
     int64_t row_dtype;              /* 0 = bf16, 1 = fp16: element type of every 16-bit row (FP-V pool,
                                        Recent-FP ring, BF16-K arena, append_k / append_v); the output
                                        stays bf16, as the reference's (triton_fourq_splitk.py:1653-1655) */
+    const int32_t* group_begin_host; /* host [batch*hkv + 1] copy of group_begin, or NULL.  When given
+                                       and batch*hkv <= 32, r2o_decode_combine passes the slot ranges
+                                       in its launch arguments instead of reading group_begin on the
+                                       device (one dependent memory round trip less); it must equal
+                                       the device array.  Read on the host during the call only. */
 } r2o_decode_params;
 
 /* Split-K partial pass.  Replaces _fourq_page_partial_kernel / _full_head_page_partial_kernel

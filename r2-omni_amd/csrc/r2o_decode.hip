@@ -598,13 +598,26 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
     }
 }
 
+// Slot ranges of up to kInlineGroups groups travel in the combine launch's own arguments, next
+// to r2o_decode_params: a merge block's partial loads then wait on nothing but the launch
+// arguments (reading group_begin from device memory first cost one more dependent round trip).
+constexpr int kInlineGroups = 32;
+struct CombineArgs {
+    int32_t n_groups;                  // groups whose range is below; 0: read p.group_begin
+    int32_t gqa;                       // query heads per KV head
+    int32_t begin[kInlineGroups + 1];  // slots of group g: [begin[g], begin[g + 1])
+};
+
 // The first read of each 64-byte line of the launch arguments waits on memory.  The combine kernel
-// reads a word of each of its three lines (group_begin, hq, output_hadamard) at entry, so that
-// those misses overlap instead of each one queueing behind the loads that first use its line.
-// (The partial kernel reads lines 0x00 and 0x40 at entry by itself; forcing line 0x80 there as
-// well measured slower.)
-__device__ __forceinline__ void touch_combine_kernarg(const r2o_decode_params& p) {
-    asm volatile("" ::"s"(p.group_begin), "s"(p.hq), "s"(p.output_hadamard));
+// reads every argument word its merge path uses at entry (partial pointers and n_items, output
+// pointer, output_hadamard, the head count and the block's inline slot range, which may sit on a
+// line of its own), so that those misses overlap instead of each one queueing behind the loads
+// that first use its line.  (The partial kernel reads lines 0x00 and 0x40 at entry by itself;
+// forcing line 0x80 there as well measured slower.)
+__device__ __forceinline__ void touch_combine_kernarg(const r2o_decode_params& p, const CombineArgs& ca,
+                                                      int range_begin, int range_end) {
+    asm volatile("" ::"s"(p.partial_out), "s"(p.partial_max), "s"(p.partial_sum), "s"(p.n_items), "s"(p.out),
+                 "s"(p.output_hadamard), "s"(ca.gqa), "s"(ca.n_groups), "s"(range_begin), "s"(range_end));
 }
 
 template <int KIND, int KF, bool TS, int RF>
@@ -889,35 +902,58 @@ __device__ __forceinline__ void fused_append(const r2o_decode_params& p, int64_t
     }
 }
 
-// One 512-thread block per (request, query head): 16 slices of 32 lanes, lane l owning dims
-// 4l..4l+3.  Slice s merges partials beg+s, beg+s+16, ... kCombineUnroll at a time with every
-// load of a round issued before any is used, so a group of up to 128 partials costs one memory
-// round trip;
-// the 16 slice states then merge through LDS in wave 0, which also runs the output FWHT with
-// DPP and permlane butterflies.  Every merge is the exact fp32 softmax-state merge
-// (triton_fourq_attention.py:58-69; triton_fourq_splitk.py:977-999).
+// One 512-thread block per (group, query head of the group), a group being one (request, KV
+// head): 16 slices of 32 lanes, lane l owning dims 4l..4l+3.  Slice s merges partials beg+s,
+// beg+s+16, ... kCombineUnroll at a time with every load of a round issued before any is used, so
+// a group of up to 128 partials costs one memory round trip.  The two slices of each wave then
+// fold through a cross-half lane swap, the 8 wave states merge through LDS in wave 0, which also
+// runs the output FWHT with DPP and permlane butterflies.  Every merge is the exact fp32
+// softmax-state merge (triton_fourq_attention.py:58-69; triton_fourq_splitk.py:977-999).
 constexpr int kCombineSlices = 16;
+constexpr int kCombineWaves = kCombineSlices / 2;
 #ifndef R2O_COMBINE_UNROLL
 #define R2O_COMBINE_UNROLL 8
 #endif
 constexpr int kCombineUnroll = R2O_COMBINE_UNROLL;  // partials per slice per round: 16 x 8 = 128 per round trip
 
-__global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p) {
-    __shared__ float sl_m[kCombineSlices], sl_l[kCombineSlices];
-    __shared__ __align__(16) float sl_a[kCombineSlices][128];
-    const int64_t b = blockIdx.y;
-    const int hqi = blockIdx.x;
+// Exact merge of softmax state (m2, l2, a2) into (m, l, a), both in the log2 domain.
+__device__ __forceinline__ void merge_state(float& m, float& l, r2o_f4& a, float m2, float l2, r2o_f4 a2) {
+    const float mn = fmaxf(m, m2);
+    const float w1 = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+    const float w2 = (m2 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m2 - mn);
+    l = l * w1 + l2 * w2;
+    a = a * w1 + a2 * w2;
+    m = mn;
+}
+
+__global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p, CombineArgs ca) {
+    __shared__ float sl_m[kCombineWaves], sl_l[kCombineWaves];
+    __shared__ __align__(16) float sl_a[kCombineWaves][128];
+    const int g = blockIdx.y;   // group: request g / hkv, KV head g % hkv
+    const int h = blockIdx.x;   // query head within the group
     const int tid = threadIdx.x, lane = tid & 31, slice = tid >> 5;
-    touch_combine_kernarg(p);
-    if (hqi == p.hq) {  // the extra block of a fused append: runs beside the merges of request b
-        fused_append(p, b, tid);
+    // the inline range of this group (a clamped index keeps the read inside the arguments for any
+    // group; it is used only when g < ca.n_groups)
+    const int gi = min(g, kInlineGroups - 1);
+    const int inline_beg = ca.begin[gi], inline_end = ca.begin[gi + 1];
+    touch_combine_kernarg(p, ca, inline_beg, inline_end);
+    if (h == ca.gqa) {  // the extra block of a fused append: request g / hkv, on its KV head 0 group
+        const int hkv = (int)p.hkv;
+        const int b = __builtin_amdgcn_readfirstlane(r2o_div_small(g, hkv));
+        if (g == b * hkv) fused_append(p, b, tid);
         return;
     }
-    const int gqa = __builtin_amdgcn_readfirstlane(r2o_div_small((int)p.hq, (int)p.hkv));
-    const int kvh = __builtin_amdgcn_readfirstlane(r2o_div_small(hqi, gqa)), h = hqi - kvh * gqa;
     // slot range of the group, clamped to the slots a launch of n_items items writes
-    const int beg = max(r2o_ldg(p.group_begin + b * p.hkv + kvh), 0);
-    const int end = min(r2o_ldg(p.group_begin + b * p.hkv + kvh + 1), (int)p.n_items);
+    int beg, end;
+    if (g < ca.n_groups) {
+        beg = inline_beg;
+        end = inline_end;
+    } else {
+        beg = r2o_ldg(p.group_begin + g);
+        end = r2o_ldg(p.group_begin + g + 1);
+    }
+    beg = max(beg, 0);
+    end = min(end, (int)p.n_items);
     float m = -INFINITY, l = 0.f;
     r2o_f4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int base = beg + slice; base < end; base += kCombineUnroll * kCombineSlices) {
@@ -948,30 +984,53 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
         }
         m = mn;
     }
-    reinterpret_cast<r2o_f4*>(sl_a[slice])[lane] = acc;
-    if (lane == 0) {
-        sl_m[slice] = m;
-        sl_l[slice] = l;
+    // ---- fold the wave's two slices (lanes l and l + 32 own the same dims): both halves merge
+    // (slice 2w, slice 2w + 1) in that order
+    {
+        float m0, m1, l0, l1;
+        r2o_f4 a0, a1;
+        r2o_row_swap<32>(m, m0, m1);
+        r2o_row_swap<32>(l, l0, l1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float x0, x1;
+            r2o_row_swap<32>(acc[j], x0, x1);
+            a0[j] = x0;
+            a1[j] = x1;
+        }
+        merge_state(m0, l0, a0, m1, l1, a1);
+        m = m0;
+        l = l0;
+        acc = a0;
+    }
+    const int wave = tid >> 6;
+    if ((tid & 32) == 0) {  // lanes 0..31 of each wave
+        reinterpret_cast<r2o_f4*>(sl_a[wave])[lane] = acc;
+        if (lane == 0) {
+            sl_m[wave] = m;
+            sl_l[wave] = l;
+        }
     }
     __syncthreads();
     if (tid >= 64) return;
     // ---- wave 0: lane t owns dims t and t + 64
     float M = -INFINITY;
 #pragma unroll
-    for (int s2 = 0; s2 < kCombineSlices; ++s2) M = fmaxf(M, sl_m[s2]);
-    float L = 0.f, a0 = 0.f, a1 = 0.f;
+    for (int w = 0; w < kCombineWaves; ++w) M = fmaxf(M, sl_m[w]);
+    float L = 0.f, y0 = 0.f, y1 = 0.f;
 #pragma unroll
-    for (int s2 = 0; s2 < kCombineSlices; ++s2) {
-        const float ms = sl_m[s2];
-        const float w = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-        L += sl_l[s2] * w;
-        a0 += sl_a[s2][tid] * w;
-        a1 += sl_a[s2][tid + 64] * w;
+    for (int w = 0; w < kCombineWaves; ++w) {
+        const float ms = sl_m[w];
+        const float sc = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+        L += sl_l[w] * sc;
+        y0 += sl_a[w][tid] * sc;
+        y1 += sl_a[w][tid + 64] * sc;
     }
-    float y0 = r2o_bf16_to_f32(r2o_f32_to_bf16(a0 / L));
-    float y1 = r2o_bf16_to_f32(r2o_f32_to_bf16(a1 / L));
+    y0 = r2o_bf16_to_f32(r2o_f32_to_bf16(y0 / L));
+    y1 = r2o_bf16_to_f32(r2o_f32_to_bf16(y1 / L));
     if (p.output_hadamard) r2o_fwht128_pair(y0, y1, tid);  // of the bf16-rounded row (triton_fourq_splitk.py:1000-1006)
-    uint16_t* orow = p.out + (b * p.hq + hqi) * 128;
+    // output row of (request b, query head kvh * gqa + h) = g * gqa + h
+    uint16_t* orow = p.out + ((int64_t)g * ca.gqa + h) * 128;
     orow[tid] = (uint16_t)r2o_f32_to_bf16(y0);
     orow[tid + 64] = (uint16_t)r2o_f32_to_bf16(y1);
 }
@@ -1050,8 +1109,15 @@ int launch_decode(const r2o_decode_params& p, hipStream_t stream) {
 }
 
 int launch_combine(const r2o_decode_params& p, hipStream_t stream) {
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(p.hq + (p.do_append ? 1 : 0)), (unsigned)p.batch),
-                       dim3(512), 0, stream, p);
+    CombineArgs ca{};
+    const int64_t groups = p.batch * p.hkv;
+    ca.gqa = (int32_t)(p.hq / p.hkv);
+    if (p.group_begin_host && groups <= kInlineGroups) {
+        ca.n_groups = (int32_t)groups;
+        for (int64_t i = 0; i <= groups; ++i) ca.begin[i] = p.group_begin_host[i];
+    }
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(ca.gqa + (p.do_append ? 1 : 0)), (unsigned)groups),
+                       dim3(512), 0, stream, p, ca);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
 }

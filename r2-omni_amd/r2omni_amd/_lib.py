@@ -53,6 +53,7 @@ class DecodeParams(ctypes.Structure):
         ("append_global", c_i64 * MAX_BATCH),
         ("append_logical", c_i64 * MAX_BATCH),
         ("row_dtype", c_i64),
+        ("group_begin_host", ctypes.c_void_p),
     ]
 
 

@@ -315,6 +315,7 @@ class SplitKExecutor:
     block_n: int = 128
     batched: bool = False
     host_items: torch.Tensor | None = None
+    host_group_begin: torch.Tensor | None = None  # host int32 copy of group_begin (inline slot ranges)
     # Stacked executors (stack_homogeneous_splitk_executors) own a copy of each request's Recent-FP
     # ring and track its length here, as the reference's batched_recent / batched_recent_lengths
     # (triton_fourq_splitk.py:1232-1241, 1543-1546): the source caches are never written.
@@ -340,6 +341,8 @@ class SplitKExecutor:
             p.step_positions = step_positions.data_ptr()
         ws = self.workspace
         p.reqs, p.items, p.group_begin = self.reqs.data_ptr(), self.items.data_ptr(), self.group_begin.data_ptr()
+        if self.host_group_begin is not None:
+            p.group_begin_host = self.host_group_begin.data_ptr()
         p.n_items = self.n_items
         p.partial_max, p.partial_sum = ws.partial_max.data_ptr(), ws.partial_sum.data_ptr()
         p.partial_out = ws.partial_output.data_ptr()
@@ -500,7 +503,7 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
         caches=list(caches), workspace=workspace, reqs=reqs, items=host_items.to(dev), group_begin=begins.to(dev),
         n_items=n, num_query_heads=hq, num_key_value_heads=hkv, head_dim=head_dim, superblock=sb, int2_group=group,
         page_size=first.page_size, output_hadamard=bool(output_hadamard), block_n=block_n, batched=batched,
-        host_items=host_items,
+        host_items=host_items, host_group_begin=begins.contiguous(),
         batched_recent=None if rings is None else list(rings),
         batched_recent_lengths=None if rings is None else [int(r.active_length) for r in rings],
     )

@@ -214,3 +214,40 @@ def test_config4_e2e_decode_properties():
     assert eager_finite and graph_finite
     assert torch.equal(eager_tokens, graph_tokens)
     print(f"[cfg4] tokens of {steps} greedy steps equal in both modes", flush=True)
+
+
+TIER_CASES = {
+    # (key variant, V tier probabilities BF16/INT4/INT2, superblock = group)
+    "bf16v": ("int4k", (1.0, 0.0, 0.0), 32),
+    "int4v": ("int4k", (0.0, 1.0, 0.0), 32),
+    "int2v": ("int4k", (0.0, 0.0, 1.0), 32),
+    "int2v_int2k_sb128": ("int2k", (0.0, 0.0, 1.0), 128),
+}
+
+
+@pytest.mark.parametrize("case", sorted(TIER_CASES))
+def test_value_tier_error_at_full_size(case):
+    """The attention error of each value tier alone over a 65,536-token request at the cfg2 head
+    geometry (Hq 28 / Hkv 4): BF16-V and Recent-FP tiles feed P to the MFMA in bf16, INT4-V and INT2-V
+    tiles feed P' = p * scale in f16, where the reference's B=1 kernel keeps P in fp32
+    (triton_fourq_splitk.py:456-931).  Every case stays inside the parity bar."""
+    import dataclasses
+
+    import r2omni_amd as ro
+    from oracle.attention import mixed_reference, output_transform
+    from r2omni_amd.workloads import CONFIGS, build_request_cache, make_request
+
+    dev = _cuda()
+    variant, probs, sb = TIER_CASES[case]
+    cfg = dataclasses.replace(CONFIGS[2], name=case, lengths=(65536,), tier_probs=probs, variant=variant,
+                              superblock=sb, group=sb)
+    data = make_request(cfg, 65536, seed=7, device=dev)
+    cache = build_request_cache(cfg, data)
+    oc = _oracle(data, cfg)
+    _check_arenas(cache, oc, case)
+    ex = ro.prepare_splitk_executor(cache, ro.allocate_splitk_workspace(cache, num_query_heads=cfg.hq),
+                                    output_hadamard=False)
+    out = ex(data.query)
+    torch.cuda.synchronize()
+    mx, mn = _errors(out, output_transform(mixed_reference(_f32(data.query), oc), False), case)
+    print(f"[tier {case}] 65536 tokens, {ex.n_items} work items: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)

@@ -81,3 +81,36 @@ def test_batch_above_the_launch_maximum_is_refused():
     exs = [ro.prepare_splitk_executor(c, ro.allocate_splitk_workspace(c, num_query_heads=16)) for c in caches]
     with pytest.raises(ValueError, match="at most 32 requests"):
         ro.stack_homogeneous_splitk_executors(exs)
+
+
+def test_inline_slot_ranges_equal_device_ranges():
+    """r2o_decode_combine with the host copy of group_begin (the slot ranges travel in the launch
+    arguments) and without it (the ranges are read from the device array): the same output bits,
+    for a ragged batch of 4 (16 groups)."""
+    import ctypes
+
+    import r2omni_amd as ro
+    from r2omni_amd import _lib
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+
+    dev = _cuda()
+    cfg = DecodeConfig("inline", 28, 4, (740, 1252, 2276, 3300), (0.15, 0.45, 0.4), recent=100)
+    datas = [make_request(cfg, n, seed=1400 + r, device=dev) for r, n in enumerate(cfg.lengths)]
+    caches = [build_request_cache(cfg, d) for d in datas]
+    exs = [ro.prepare_splitk_executor(c, ro.allocate_splitk_workspace(c, num_query_heads=28), output_hadamard=True)
+           for c in caches]
+    ex = ro.stack_homogeneous_splitk_executors(exs)
+    q = torch.cat([d.query for d in datas]).contiguous()
+    lib, stream = _lib.load(), ctypes.c_void_p(_lib.stream_of(dev))
+    outs = []
+    for host_ranges in (True, False):
+        out = torch.empty_like(ex.workspace.output)
+        p = ex._params(q, out, None)
+        assert bool(p.group_begin_host) == (ex.host_group_begin is not None)
+        if not host_ranges:
+            p.group_begin_host = None
+        _lib.check(lib.r2o_decode_partial(ctypes.byref(p), stream), "r2o_decode_partial")
+        _lib.check(lib.r2o_decode_combine(ctypes.byref(p), stream), "r2o_decode_combine")
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
