@@ -76,7 +76,7 @@ struct KernelCfg {
     static constexpr int kWaveLds = kDmaStages * kStage;
     static constexpr int kSmem = (kWaves * kMergeFloats * 4 > kWaves * kWaveLds) ? kWaves * kMergeFloats * 4
                                                                                  : kWaves * kWaveLds;
-    static constexpr int kBlocksPerCU = KF == kKBf16 ? 2 : 3;     // resident partial workgroups per CU
+    static constexpr int kBlocksPerCU = 2;  // resident partial workgroups per CU (the planner launches 2 per CU)
 };
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
@@ -209,18 +209,16 @@ __device__ __forceinline__ VConst make_vconst() {
 template <int KF>
 struct KRegs;
 template <>
-struct KRegs<kKInt4> {  // INT4-K: codes of tokens 16 mg + l16 (channels 32g ..) and the operand vectors
+struct KRegs<kKInt4> {  // INT4-K: codes of tokens 16 mg + l16 (channels 32g ..)
     r2o_u4 kx[2];
-    r2o_u4 ops[8];
 };
 template <>
 struct KRegs<kKBf16> {  // BF16-K: channels 32g + 8j .. 32g + 8j + 7 of tokens 16 mg + l16
     r2o_u4 kb[2][4];
 };
 template <>
-struct KRegs<kKInt2> {  // INT2-K: codes of tokens 16 mg + l16 (channels 32g .., 8 bytes) and the operands
+struct KRegs<kKInt2> {  // INT2-K: codes of tokens 16 mg + l16 (channels 32g .., 8 bytes)
     uint32_t kx[2][2];
-    r2o_u4 ops[8];
 };
 template <int KIND>
 struct VRegs;
@@ -254,62 +252,82 @@ struct SegState {
                          // sum_k P'_k (1024 + z_k) (code offsets removed at the end)
 };
 
-// QK^T of one INT4-K tile: per MFMA j, Q'_j = q * s (superblock scale pairs), the codes of the
-// dword read in place (1024 + c for the low nibble of each byte, 1024 + 16 c for the high one,
-// whose operand pairs carry s / 16), and the correction -sum Q'_j (1024 + z) by one more MFMA.
-// The correction is the same for every token of a head, so it is returned as the lane scalar
-// `corr` and added to the logits by the softmax.  ko = the 4 scale-pair and the 4 zero-pair
+// QK operands of one K superblock for the lane's channel group: Q'_j per MFMA j and the logit
+// correction, which is the same for every token of a head and so a lane scalar added by the
+// softmax.  They change only when a tile starts a new superblock (every tile at SB 32, every fourth
+// at SB 128), so the tile loop keeps them across the tiles of a superblock.
+struct QkOps {
+    r2o_u4 q[4];
+    float corr;
+};
+
+// INT4-K: Q'_j = q * s (superblock scale pairs; the pairs of high-nibble channels carry s / 16)
+// and corr = -sum Q'_j (1024 + z) by one MFMA per j.  ko = the 4 scale-pair and the 4 zero-pair
 // operand vectors of the lane's channel group.
-__device__ __forceinline__ void qk_int4k(const uint32_t (&qp)[4][4], const VConst& vc, const r2o_u4 (&ko)[8],
-                                         const r2o_u4 (&kx)[2], r2o_f4 (&s)[2], float& corr) {
-    s[0] = r2o_f4{0, 0, 0, 0};
-    s[1] = r2o_f4{0, 0, 0, 0};
+__device__ __forceinline__ void qk_ops_int4k(const uint32_t (&qp)[4][4], const r2o_u4 (&ko)[8], QkOps& o) {
     r2o_f4 cz = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const r2o_u4 sj = ko[j], zj = ko[4 + j];
-        const r2o_u4 qj = {r2o_h2_mul(qp[j][0], sj[0]), r2o_h2_mul(qp[j][1], sj[1]), r2o_h2_mul(qp[j][2], sj[2]),
-                           r2o_h2_mul(qp[j][3], sj[3])};
-        cz = r2o_mfma_f16(zj, qj, cz);
+        const r2o_u4 sj = ko[j];
+        o.q[j] = r2o_u4{r2o_h2_mul(qp[j][0], sj[0]), r2o_h2_mul(qp[j][1], sj[1]), r2o_h2_mul(qp[j][2], sj[2]),
+                        r2o_h2_mul(qp[j][3], sj[3])};
+        cz = r2o_mfma_f16(ko[4 + j], o.q[j], cz);
+    }
+    o.corr = cz[0];  // every row of the correction product is the same
+}
+
+// QK^T of one INT4-K tile: the codes of the dword read in place (1024 + c for the low nibble of
+// each byte, 1024 + 16 c for the high one) against Q'_j.
+__device__ __forceinline__ void qk_int4k(const QkOps& o, const VConst& vc, const r2o_u4 (&kx)[2], r2o_f4 (&s)[2]) {
+    s[0] = r2o_f4{0, 0, 0, 0};
+    s[1] = r2o_f4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
         for (int mg = 0; mg < 2; ++mg) {
             const uint32_t w = kx[mg][j], w8 = w >> 8;
             const r2o_u4 a = {(w & vc.nib) | vc.magic, (w & vc.nib_hi) | vc.magic, (w8 & vc.nib) | vc.magic,
                               (w8 & vc.nib_hi) | vc.magic};
-            s[mg] = r2o_mfma_f16(a, qj, s[mg]);
+            s[mg] = r2o_mfma_f16(a, o.q[j], s[mg]);
         }
     }
-    corr = cz[0];  // every row of the correction product is the same
 }
 
-// QK^T of one INT2-K tile (k = code * s + o per channel and superblock): per MFMA j the codes of
-// half a dword enter in place as 1024 + 4^u c (crumb u of bytes 0/2 or 1/3), against
-// Q'_j = q * s / 4^u; the correction sum_c q_c o_c - 1024 sum_c Q'_c takes two more MFMAs (the
-// offset pairs against q, and -1024 against Q'_j, the very f16 values the code MFMAs used), and is
-// returned as the lane scalar `corr`.  ko = the 4 scale-pair and the 4 offset-pair vectors.
-__device__ __forceinline__ void qk_int2k(const uint32_t (&qp)[4][4], const VConst& vc, const r2o_u4 (&ko)[8],
-                                         const uint32_t (&kx)[2][2], r2o_f4 (&s)[2], float& corr) {
-    s[0] = r2o_f4{0, 0, 0, 0};
-    s[1] = r2o_f4{0, 0, 0, 0};
+// INT2-K (k = code * s + o per channel and superblock): Q'_j = q * s / 4^u for the crumb u each
+// lane of MFMA j carries, and corr = sum_c q_c o_c - 1024 sum_c Q'_c by two MFMAs per j (the offset
+// pairs against q, and -1024 against Q'_j, the very f16 values the code MFMAs use).  ko = the 4
+// scale-pair and the 4 offset-pair vectors.
+__device__ __forceinline__ void qk_ops_int2k(const uint32_t (&qp)[4][4], const r2o_u4 (&ko)[8], QkOps& o) {
     r2o_f4 cz = {0, 0, 0, 0};
     const r2o_u4 neg1024 = {0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const r2o_u4 sj = ko[j], oj = ko[4 + j];
+        const r2o_u4 sj = ko[j];
         const r2o_u4 qraw = {qp[j][0], qp[j][1], qp[j][2], qp[j][3]};
-        const r2o_u4 qj = {r2o_h2_mul(qp[j][0], sj[0]), r2o_h2_mul(qp[j][1], sj[1]), r2o_h2_mul(qp[j][2], sj[2]),
-                           r2o_h2_mul(qp[j][3], sj[3])};
-        cz = r2o_mfma_f16(oj, qraw, cz);
-        cz = r2o_mfma_f16(neg1024, qj, cz);
+        o.q[j] = r2o_u4{r2o_h2_mul(qp[j][0], sj[0]), r2o_h2_mul(qp[j][1], sj[1]), r2o_h2_mul(qp[j][2], sj[2]),
+                        r2o_h2_mul(qp[j][3], sj[3])};
+        cz = r2o_mfma_f16(ko[4 + j], qraw, cz);
+        cz = r2o_mfma_f16(neg1024, o.q[j], cz);
+    }
+    o.corr = cz[0];
+}
+
+// QK^T of one INT2-K tile: per MFMA j the codes of half a dword enter in place as 1024 + 4^u c
+// (crumb u of bytes 0/2 or 1/3) against Q'_j.
+__device__ __forceinline__ void qk_int2k(const QkOps& o, const VConst& vc, const uint32_t (&kx)[2][2],
+                                         r2o_f4 (&s)[2]) {
+    s[0] = r2o_f4{0, 0, 0, 0};
+    s[1] = r2o_f4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
         for (int mg = 0; mg < 2; ++mg) {
             const uint32_t w = (j & 1) ? (kx[mg][j >> 1] >> 8) : kx[mg][j >> 1];
             const r2o_u4 a = {(w & vc.crumb) | vc.magic, (w & (vc.crumb << 2)) | vc.magic,
                               (w & (vc.crumb << 4)) | vc.magic, (w & (vc.crumb << 6)) | vc.magic};
-            s[mg] = r2o_mfma_f16(a, qj, s[mg]);
+            s[mg] = r2o_mfma_f16(a, o.q[j], s[mg]);
         }
     }
-    corr = cz[0];  // every row of the correction product is the same
 }
 
 // Logits of a tile in the lane's token order (masks only on partial tiles; padded heads have
@@ -425,12 +443,14 @@ __device__ __forceinline__ void qk_bf16k(const uint32_t (&qp)[4][4], float qscal
 // One tile: QK, masks, online softmax, PV.
 template <int KIND, int KF, bool TS, int RF>
 __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegState<KIND>& ss, const VConst& vc,
-                                            int a0, int g, float qscale, const TileRegs<KIND, KF>& cur) {
+                                            int a0, int g, float qscale, const QkOps& qo,
+                                            const TileRegs<KIND, KF>& cur) {
     r2o_f4 s[2];
     float corr = 0.f;
     if constexpr (KF == kKBf16) qk_bf16k<RF>(ss.qp, qscale, cur.kb, s);
-    else if constexpr (KF == kKInt4) qk_int4k(ss.qp, vc, cur.ops, cur.kx, s, corr);
-    else qk_int2k(ss.qp, vc, cur.ops, cur.kx, s, corr);
+    else if constexpr (KF == kKInt4) qk_int4k(qo, vc, cur.kx, s);
+    else qk_int2k(qo, vc, cur.kx, s);
+    if constexpr (KF != kKBf16) corr = qo.corr;
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
     softmax_tile(st, sv, pk, g, corr, (KIND == kI4 || TS) ? &ss.bias : nullptr);
@@ -514,7 +534,7 @@ struct DmaCtx {
 };
 
 template <int KIND, int KF>
-__device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char* stage, int lane) {
+__device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char* stage, int lane, bool ops = true) {
     using Lay = StageLayout<KIND, KF>;
     if constexpr (KF == kKBf16) {  // 8 x 1 KB of bf16 rows: slot s = 64 j + lane holds chunk c of token t
 #pragma unroll
@@ -540,8 +560,8 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
     } else {
         dma<16>(c.vrows + row(c.vt0) * 32 + c.vc0 * 16, stage + Lay::kV);
     }
-    if constexpr (KF != kKBf16)
-        if (lane < 32) dma<16>(c.kops + (a0 >> c.sb_shift) * 128 + lane * 4, stage + Lay::kOps);
+    if constexpr (KF != kKBf16)  // the tile's superblock operands, when the tile loop needs them
+        if (ops && lane < 32) dma<16>(c.kops + (a0 >> c.sb_shift) * 128 + lane * 4, stage + Lay::kOps);
     if constexpr (KIND == kI4) {
         if (lane < 32) dma<4>(c.vscale + row(lane) * 4, stage + Lay::kScale);
     } else if constexpr (KIND == kI2) {
@@ -556,6 +576,14 @@ __device__ __forceinline__ void dma_tile(const DmaCtx& c, int a0, unsigned char*
             if (lane < 32) dma<1>(c.vzero + row(lane), stage + Lay::kZero);
         }
     }
+}
+
+// The K superblock operand vectors of lane group g (INT4-K and INT2-K stages).
+template <int KIND, int KF>
+__device__ __forceinline__ void read_ops(const unsigned char* stage, int g, r2o_u4 (&ko)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        ko[j] = *reinterpret_cast<const r2o_u4*>(stage + StageLayout<KIND, KF>::kOps + g * 128 + 16 * j);
 }
 
 template <int KIND, int KF>
@@ -579,8 +607,6 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
                 tr.kx[mg][1] = w.y;
             }
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tr.ops[j] = *reinterpret_cast<const r2o_u4*>(stage + Lay::kOps + g * 128 + 16 * j);
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -671,9 +697,14 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     }
     const int n = t_end - t_begin;
     const int a_first = (int)it.tile0 + 32 * t_begin;
+    // With one stage per wave the superblock operands are moved and read only for the first tile of
+    // the wave and of each superblock (a ring of more stages moves them with every tile, so that
+    // its wait counts stay fixed).
+    const int sb_mask = (1 << c.sb_shift) - 1;
+    auto needs_ops = [&](int i) { return kDmaStages > 1 || i == 0 || ((a_first + 32 * i) & sb_mask) == 0; };
 #pragma unroll
     for (int j = 0; j < kDmaStages; ++j)
-        if (j < n) dma_tile<KIND, KF>(c, a_first + 32 * j, ring + j * Cfg::kStage, lane);
+        if (j < n) dma_tile<KIND, KF>(c, a_first + 32 * j, ring + j * Cfg::kStage, lane, true);
 
     const VConst vc = make_vconst();
     const float qscale = p.sm_scale * kLog2e;
@@ -681,18 +712,28 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     load_query<KF, RF>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: row-type pairs, scaled after the MFMA
     ss.bias = r2o_f4{0, 0, 0, 0};
     const SegCtx sc = {c.lo, c.hi};
+    QkOps qo;  // operands of the current K superblock (INT4-K / INT2-K)
     for (int i = 0; i < n; ++i) {
         wait_tiles<StageLayout<KIND, KF>::kDma>(min(kDmaStages, n - i) - 1);  // tile i has landed
         __builtin_amdgcn_wave_barrier();
         unsigned char* stage = ring + (i % kDmaStages) * Cfg::kStage;
         TileRegs<KIND, KF> cur;
         read_tile<KIND, KF>(stage, l16, g, gamma, c.groups, cur);
+        const bool fresh = __builtin_amdgcn_readfirstlane(needs_ops(i));  // wave-uniform
+        r2o_u4 ko[8];
+        if constexpr (KF != kKBf16)
+            if (fresh) read_ops<KIND, KF>(stage, g, ko);
         if (i + kDmaStages < n) {
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the whole stage is in registers
             __builtin_amdgcn_wave_barrier();
-            dma_tile<KIND, KF>(c, a_first + 32 * (i + kDmaStages), stage, lane);
+            dma_tile<KIND, KF>(c, a_first + 32 * (i + kDmaStages), stage, lane, needs_ops(i + kDmaStages));
         }
-        seg_compute<KIND, KF, TS, RF>(sc, st, ss, vc, a_first + 32 * i, g, qscale, cur);
+        if constexpr (KF == kKInt4) {
+            if (fresh) qk_ops_int4k(ss.qp, ko, qo);
+        } else if constexpr (KF == kKInt2) {
+            if (fresh) qk_ops_int2k(ss.qp, ko, qo);
+        }
+        seg_compute<KIND, KF, TS, RF>(sc, st, ss, vc, a_first + 32 * i, g, qscale, qo, cur);
     }
     if constexpr (TS) {  // remove the code offsets of the per-token-scale form
 #pragma unroll
