@@ -582,7 +582,8 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
 def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed_base: int = 0) -> dict:
     """Build ``n_layers`` distinct layer caches of ``cfg`` (seeds 1000 * layer + request) and time one
     decode-attention layer call (partial + combine, no append) rotating over them with HIP events on
-    the launch stream; then the partial kernel alone the same way."""
+    the launch stream; then the partial kernel alone the same way (back-to-back partial launches: an
+    event pair around each partial inside the call sequence would add ~2 us of its own)."""
     import torch
 
     import r2omni_amd as ro
@@ -781,7 +782,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "decode_partial_kernel", "avg_us": round(ms_partial * 1e3, 3)},
+                     "kernel": "decode_partial_kernel", "avg_us": round(ms_partial * 1e3, 3),
+                     "avg_us_source": "HIP events over back-to-back partial launches on the launch stream"},
         "cpu_baseline": cpu,
         "hbm_copy": copy,
         "e2e": e2e,

@@ -877,13 +877,15 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
                 A += *reinterpret_cast<const r2o_f4*>(base + w * kMergeFloats + 32 + h * 128 + d4) * sc;
             }
         }
-        // streaming stores: the partials are read once, by the combine launch, so they are not left
-        // dirty in this XCD's L2 for the end-of-kernel writeback
+        // plain (write-back) stores: the end-of-kernel writeback leaves the partials in the Infinity
+        // Cache, where the combine launch reads them.  Streaming (non-temporal) stores shorten this
+        // kernel by ~0.6 us but send them to DRAM, and the combine's reads then cost more than that
+        // (cfg2 layer call 24.3 vs 23.7 us); write-through stores are slower still.
         const int64_t slot = it.slot * 16 + h;
-        __builtin_nontemporal_store(A, reinterpret_cast<r2o_f4*>(p.partial_out + slot * 128 + d4));
+        *reinterpret_cast<r2o_f4*>(p.partial_out + slot * 128 + d4) = A;
         if (d4 == 0) {
-            __builtin_nontemporal_store(M, p.partial_max + slot);
-            __builtin_nontemporal_store(L, p.partial_sum + slot);
+            p.partial_max[slot] = M;
+            p.partial_sum[slot] = L;
         }
     }
 }
