@@ -173,6 +173,38 @@ def summarize_pmc(directory: str) -> dict:
     return out
 
 
+def summarize_trace(directory: str) -> dict:
+    """Per-dispatch durations of the decode kernels in a rocprofv3 --kernel-trace CSV run, in launch
+    order: partial dispatches followed by a combine (layer calls) apart from back-to-back partial-only
+    ones, the combine, and the gap from a partial's end to its combine's start."""
+    import csv
+    import glob
+
+    rows = []
+    for path in glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True):
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                name = row["Kernel_Name"]
+                kind = ("partial" if "decode_partial_kernel" in name else
+                        "combine" if "decode_combine_kernel" in name else None)
+                if kind:
+                    rows.append((int(row["Start_Timestamp"]), int(row["End_Timestamp"]), kind))
+    rows.sort()
+    acc: dict = {"partial_in_call": [], "partial_only": [], "combine": [], "partial_end_to_combine_start": []}
+    for k, (t0, t1, kind) in enumerate(rows):
+        if kind == "combine":
+            acc["combine"].append(t1 - t0)
+            continue
+        nxt = rows[k + 1] if k + 1 < len(rows) else None
+        if nxt is not None and nxt[2] == "combine":
+            acc["partial_in_call"].append(t1 - t0)
+            acc["partial_end_to_combine_start"].append(nxt[0] - t1)
+        else:
+            acc["partial_only"].append(t1 - t0)
+    return {key: {"dispatches": len(v), "avg_us": round(sum(v) / len(v) / 1e3, 3) if v else None}
+            for key, v in acc.items()}
+
+
 def traffic_from_profile() -> tuple[int | None, str | None]:
     """HBM bytes per partial-kernel launch recorded in the committed PMC summary, if any."""
     path = os.path.join(ROOT, "profiles", "decode_partial_cfg2_hbm_traffic.md")
@@ -693,7 +725,13 @@ def main() -> int:
     ap.add_argument("--summarize-pmc", metavar="DIR",
                     help="only print the mean per-dispatch value of every counter in a rocprofv3 --pmc CSV "
                          "output directory, per decode kernel (and the calibration copy kernel)")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="only print the decode kernels' average durations in a rocprofv3 --kernel-trace CSV "
+                         "output directory: partials inside layer calls and partial-only launches apart")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(json.dumps(summarize_trace(args.summarize_trace)))
+        return 0
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(args.summarize_pmc)))
         return 0
