@@ -44,15 +44,21 @@ __device__ __forceinline__ float r2o_f16_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
-// Round-to-nearest-even float -> bfloat16 bits (finite inputs; NaN stays NaN).
+// The float -> 16-bit roundings below round x itself, as the reference's float32 torch ops followed
+// by a cast do: the empty asm makes x opaque, so the compiler cannot fold the operation that produced
+// it into the conversion (it turns fp16(a * b) into one v_fma_mixlo_f16, a single rounding, even
+// with contraction off).  r2o_pack_h2 / r2o_pack_bf2 (MFMA operands, no bit-exact contract) keep
+// that freedom.
+
+// Round-to-nearest-even float -> bfloat16 bits: gfx950's v_cvt_pk_bf16_f32 (NaN stays NaN).
 __device__ __forceinline__ uint32_t r2o_f32_to_bf16(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7f800000u) == 0x7f800000u) return (u >> 16) | ((u & 0xffffu) ? 0x40u : 0u);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    asm("" : "+v"(x));
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
 }
 
 // Round-to-nearest-even float -> fp16 bits.
 __device__ __forceinline__ uint32_t r2o_f32_to_f16(float x) {
+    asm("" : "+v"(x));
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
@@ -107,9 +113,11 @@ __device__ __forceinline__ uint32_t r2o_pack_h2(float lo, float hi) {
     r2o_h2 r = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, r);
 }
-// Two floats -> packed bf16 pair (round to nearest even).
+// Two floats -> packed bf16 pair (round to nearest even), one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t r2o_pack_bf2(float lo, float hi) {
-    return r2o_f32_to_bf16(lo) | (r2o_f32_to_bf16(hi) << 16);
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
 }
 
 // Cross-lane exchanges through the VALU, in place of the LDS-unit permute behind __shfl_xor:
