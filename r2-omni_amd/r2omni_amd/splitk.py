@@ -81,7 +81,7 @@ def _tiles(lo: int, hi: int) -> tuple[int, int]:
 
 # Relative cost of one 32-token tile per kind (partial kernel, measured on MI355X): the
 # planner sizes items so that every workgroup slot gets about the same amount of work.
-_TILE_COST = {_lib.KIND_FP: 1.6, _lib.KIND_INT4: 1.0, _lib.KIND_INT2: 1.4, _lib.KIND_RECENT: 2.0}
+_TILE_COST = {_lib.KIND_FP: 1.45, _lib.KIND_INT4: 1.0, _lib.KIND_INT2: 1.4, _lib.KIND_RECENT: 1.6}
 
 
 def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_int2: int = 0):
