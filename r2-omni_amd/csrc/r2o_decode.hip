@@ -130,13 +130,13 @@ __device__ __forceinline__ float head_max(float x) {
 
 // Online-softmax update for one tile: sv are the lane's 8 logits (log2 domain, -inf = masked).
 // Returns the probabilities in pk.  The running max is raised lazily: only when a tile's max
-// exceeds it by more than kRescaleSlack (log2 units) are the state and `extra` (a 4-row
-// accumulator in the PV output layout) rescaled, so p = exp2(s - m) stays below
+// exceeds it by more than kRescaleSlack (log2 units) are the state and the NE accumulators at `extra`
+// (4-row accumulators in the PV output layout) rescaled, so p = exp2(s - m) stays below
 // 2^kRescaleSlack while the rescale branch is taken only a few times per work item.  (m, l, acc)
 // always refer to the same m, so the state and its later merges are exact.
 constexpr float kRescaleSlack = 4.f;
 
-template <int N>
+template <int N, int NE>
 __device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N], float (&pk)[N], int g, float add,
                                              r2o_f4* extra) {
     float tmax = sv[0];
@@ -153,7 +153,8 @@ __device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N]
             const float ai = __shfl(alpha, 4 * g + i, R2O_WAVE);
 #pragma unroll
             for (int q = 0; q < 8; ++q) st.acc[q][i] *= ai;
-            if (extra) (*extra)[i] *= ai;
+#pragma unroll
+            for (int e = 0; e < NE; ++e) extra[e][i] *= ai;
         }
         st.m = m_new;
     }
@@ -166,9 +167,10 @@ __device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N]
 }
 
 // Online-softmax update for one tile whose logits are sv + add (log2 domain, -inf = masked).
+template <int NE = 0>
 __device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8], float (&pk)[8], int g,
                                              float add = 0.f, r2o_f4* extra = nullptr) {
-    softmax_step<8>(st, sv, pk, g, add, extra);
+    softmax_step<8, NE>(st, sv, pk, g, add, extra);
 }
 
 // PV for 16-bit V rows held as R[k] = 8 dims (8*l16 ..) of token tile_token(g, k).
@@ -248,8 +250,9 @@ struct SegCtx {
 template <int KIND>
 struct SegState {
     uint32_t qp[4][4];   // q (scaled), f16 pairs in the K-unpack channel order
-    r2o_f4 bias;         // INT4-V: sum_k P'_k per head row; INT2-V with one group per token:
-                         // sum_k P'_k (1024 + z_k) (code offsets removed at the end)
+    r2o_f4 bias[2];      // INT4-V: [0] = sum_k P'_k per head row; INT2-V with one group per token:
+                         // [0] = sum_k P'_k (1024 + z_k), [1] = sum_k P'_k (code offsets and the
+                         // in-place crumb factors removed at the end)
 };
 
 // QK operands of one K superblock for the lane's channel group: Q'_j per MFMA j and the logit
@@ -362,7 +365,7 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             ap[u] = r2o_pack_h2(pk[2 * u] * __uint_as_float(cur.vm[2 * u]), pk[2 * u + 1] * __uint_as_float(cur.vm[2 * u + 1]));
-        ss.bias = r2o_mfma_f16(ap, r2o_u4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}, ss.bias);
+        ss.bias[0] = r2o_mfma_f16(ap, r2o_u4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}, ss.bias[0]);
         uint32_t X[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) X[k] = cur.v[k] ^ 0x88888888u;
@@ -380,26 +383,31 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
             st.acc[2 * bb + 1] = r2o_mfma_f16(ap, hi, st.acc[2 * bb + 1]);
         }
     } else if constexpr (TS) {
-        // one scale and zero point per token (a group of all 128 dims): P' = p * s_t, the crumbs
-        // enter exactly as f16 1024 + c, and sum_k P'_k (1024 + z_k) is accumulated by one more
-        // MFMA on the same A operand (removed after the last tile), as for INT4 values
+        // one scale and zero point per token (a group of all 128 dims): P' = p * s_t.  The crumbs
+        // of dims q < 4 (bits 2q of each token's word) and q >= 4 (bits 8 + 2(q - 4)) enter in place,
+        // from the token words and from them shifted by 8, as f16 1024 + 4^u c with u = q % 4, so
+        // column q of the product carries 4^u sum P' c.  sum_k P'_k (1024 + z_k) and sum_k P'_k
+        // accumulate by two more MFMAs on the same A operand; the offsets and the 4^u factors are
+        // removed after the last tile.
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             ap[u] = r2o_pack_h2(pk[2 * u] * r2o_f16_to_f32(cur.vm[2 * u]), pk[2 * u + 1] * r2o_f16_to_f32(cur.vm[2 * u + 1]));
-        uint32_t yp[4];
+        uint32_t yp[4], y8[4];
         r2o_u4 zb;
 #pragma unroll
         for (int pr = 0; pr < 4; ++pr) {
             yp[pr] = cur.v[2 * pr] | (cur.v[2 * pr + 1] << 16);
+            y8[pr] = yp[pr] >> 8;
             zb[pr] = (cur.vz[2 * pr] | (cur.vz[2 * pr + 1] << 16)) | vc.magic;
         }
-        ss.bias = r2o_mfma_f16(ap, zb, ss.bias);
+        ss.bias[0] = r2o_mfma_f16(ap, zb, ss.bias[0]);
+        ss.bias[1] = r2o_mfma_f16(ap, r2o_u4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}, ss.bias[1]);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const int shift = (q < 4) ? 2 * q : 8 + 2 * (q - 4);
+            const uint32_t mask = 0x00030003u << (2 * (q & 3));
             r2o_u4 bop;
 #pragma unroll
-            for (int pr = 0; pr < 4; ++pr) bop[pr] = ((yp[pr] >> shift) & vc.crumb) | vc.magic;
+            for (int pr = 0; pr < 4; ++pr) bop[pr] = ((q < 4 ? yp[pr] : y8[pr]) & mask) | vc.magic;
             st.acc[q] = r2o_mfma_f16(ap, bop, st.acc[q]);
         }
     } else {
@@ -453,7 +461,7 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
     if constexpr (KF != kKBf16) corr = qo.corr;
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
-    softmax_tile(st, sv, pk, g, corr, (KIND == kI4 || TS) ? &ss.bias : nullptr);
+    softmax_tile<TS ? 2 : (KIND == kI4 ? 1 : 0)>(st, sv, pk, g, corr, ss.bias);
     pv_tile<KIND, TS, RF>(st, ss, vc, pk, cur);
 }
 
@@ -710,7 +718,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const float qscale = p.sm_scale * kLog2e;
     SegState<KIND> ss;
     load_query<KF, RF>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: row-type pairs, scaled after the MFMA
-    ss.bias = r2o_f4{0, 0, 0, 0};
+    ss.bias[0] = ss.bias[1] = r2o_f4{0, 0, 0, 0};
     const SegCtx sc = {c.lo, c.hi};
     QkOps qo;  // operands of the current K superblock (INT4-K / INT2-K)
     for (int i = 0; i < n; ++i) {
@@ -735,15 +743,18 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
         }
         seg_compute<KIND, KF, TS, RF>(sc, st, ss, vc, a_first + 32 * i, g, qscale, qo, cur);
     }
-    if constexpr (TS) {  // remove the code offsets of the per-token-scale form
+    if constexpr (TS) {  // column q = 4^-u (sum P' (1024 + 4^u c)) - sum P' (1024 + z) + 1024 (1 - 4^-u) sum P'
 #pragma unroll
-        for (int q = 0; q < 8; ++q) st.acc[q] -= ss.bias;
+        for (int q = 0; q < 8; ++q) {
+            const float f = 1.f / (float)(1 << (2 * (q & 3)));
+            st.acc[q] = st.acc[q] * f - ss.bias[0] + ss.bias[1] * (1024.f * (1.f - f));
+        }
     }
     if constexpr (KIND == kI4) {  // remove the code offsets: lo dims 1032 * sum P', hi dims (1152 * sum P') / 16
 #pragma unroll
         for (int q = 0; q < 8; q += 2) {
-            st.acc[q] -= 1032.f * ss.bias;
-            st.acc[q + 1] = (st.acc[q + 1] - 1152.f * ss.bias) * 0.0625f;
+            st.acc[q] -= 1032.f * ss.bias[0];
+            st.acc[q + 1] = (st.acc[q + 1] - 1152.f * ss.bias[0]) * 0.0625f;
         }
     }
 }
