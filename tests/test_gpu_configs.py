@@ -24,6 +24,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _f32(t):
+    """bf16 or fp16 values as float32 (exact for both)."""
+    if t.dtype == torch.float16:
+        return t.detach().float().cpu().numpy()
     from oracle.quant import bf16_bits_to_f32
 
     return bf16_bits_to_f32(_bf16_np(t))
@@ -43,7 +46,7 @@ def _oracle(data, cfg):
     from oracle.cache import append_token, build_cache
 
     oc = build_cache(_f32(data.key), _f32(data.value), data.page_offsets.numpy(), data.page_lengths.numpy(),
-                     data.page_classes.numpy(), dtype="bfloat16", page_size=cfg.page, superblock=cfg.superblock,
+                     data.page_classes.numpy(), dtype=cfg.dtype, page_size=cfg.page, superblock=cfg.superblock,
                      group=cfg.group, recent_capacity=128, append_capacity=260, variant=cfg.variant)
     hist = int(data.key.shape[1])
     rk, rv = _f32(data.recent_k), _f32(data.recent_v)
@@ -251,3 +254,36 @@ def test_value_tier_error_at_full_size(case):
     torch.cuda.synchronize()
     mx, mn = _errors(out, output_transform(mixed_reference(_f32(data.query), oc), False), case)
     print(f"[tier {case}] 65536 tokens, {ex.n_items} work items: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+
+
+def test_config2_fp16_model_full_size_matches_oracle():
+    """Configuration 2 for an fp16 model (the reference runner's --model_dtype float16,
+    benchmark_mixed_active.py:1255-1263) at full size: arenas and fp16 rows bit-exact against the
+    oracle, the decode of every request (the fp16-row kernel instances) within the bar."""
+    import dataclasses
+
+    import r2omni_amd as ro
+    from oracle.attention import mixed_reference, output_transform
+    from r2omni_amd.workloads import CONFIGS, build_request_cache, make_request
+
+    dev = _cuda()
+    cfg = dataclasses.replace(CONFIGS[2], dtype="float16")
+    datas = [make_request(cfg, total, seed=r, device=dev) for r, total in enumerate(cfg.lengths)]
+    caches = [build_request_cache(cfg, d) for d in datas]
+    torch.cuda.synchronize()
+    assert caches[0].recent_fp_pool.fp_k.dtype == torch.float16
+    ocs = []
+    for r, (d, c) in enumerate(zip(datas, caches)):
+        oc = _oracle(d, cfg)
+        _check_arenas(c, oc, f"cfg2 fp16 request {r}")
+        ocs.append(oc)
+    exs = [ro.prepare_splitk_executor(c, ro.allocate_splitk_workspace(c, num_query_heads=cfg.hq),
+                                      output_hadamard=True) for c in caches]
+    ex = ro.stack_homogeneous_splitk_executors(exs)
+    q = torch.cat([d.query for d in datas]).contiguous()
+    out = ex(q)
+    torch.cuda.synchronize()
+    for r, (d, oc) in enumerate(zip(datas, ocs)):
+        mx, mn = _errors(out[r : r + 1], output_transform(mixed_reference(_f32(d.query), oc), True),
+                         f"cfg2 fp16 request {r}")
+        print(f"[cfg2 fp16] request {r} ({cfg.lengths[r]} tokens): max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
