@@ -97,6 +97,37 @@ typedef struct r2o_work_item {
     int64_t reserved;            /* 0                                                             */
 } r2o_work_item;
 
+/* One run of the planner's input: the 32-token tiles of one pool segment of one (request, kv head)
+ * (or its Recent-FP ring, kind 3), runs of one (request, kv head) adjacent, groups in order. */
+typedef struct r2o_plan_run {
+    int64_t req, kvh, kind, tile0, ntiles, lo, hi, v_delta;
+} r2o_plan_run;
+
+/* Planner settings (the Python side owns the tuned values). */
+typedef struct r2o_plan_config {
+    int64_t num_cus;             /* compute units of the GPU                                        */
+    int64_t blocks_per_cu;       /* at most this many items per CU                                  */
+    int64_t tiles_per_item;      /* small caches: about this many tiles per item, >= num_cus items  */
+    int64_t waves_per_item;      /* item sizes are multiples of this many tiles (one share a wave)  */
+    int64_t min_tiles_per_item;  /* a run is not split into items smaller than this                 */
+    double tile_cost[4];         /* weight of one tile of kind FP-V, INT4-V, INT2-V, Recent-FP      */
+    double late_share;           /* single-kind plans over more than num_cus items: the work of the
+                                    later-launched half of each run's items, relative to the first */
+} r2o_plan_config;
+
+/* Work-item plan of one decode launch (host code, no GPU work).  Splits every run into items of
+ * about equal weighted cost (water-filling up to min(blocks_per_cu * num_cus, max(num_cus,
+ * tiles / tiles_per_item)) items), numbers their partial slots in (request, kv head) order into
+ * group_begin [n_groups + 1], and writes the items to items[0 .. *n_items) largest first.  With
+ * reqs (host copies of the request descriptors) each item's base pointers are filled in, else they
+ * are 0.  Returns R2O_EINVAL for an inconsistent input or when more than max_items would result.
+ * No counterpart in the reference's launch plan (one program per BLOCK_N tile, counted while
+ * preparing the executor, triton_fourq_splitk.py:1772-1817); it replaces that preparation step. */
+int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, const r2o_plan_config* cfg,
+                        const r2o_request_desc* reqs, int64_t n_reqs, int64_t k_format, int64_t int2_group,
+                        r2o_work_item* items, int64_t max_items, int32_t* group_begin, int64_t n_groups,
+                        int64_t* n_items);
+
 typedef struct r2o_decode_params {
     const r2o_request_desc* reqs;   /* device [batch]                                  */
     const r2o_work_item* items;     /* device [n_items] in launch order                */

@@ -74,7 +74,25 @@ KIND_FP, KIND_INT4, KIND_INT2, KIND_RECENT = 0, 1, 2, 3
 # r2o_decode_params.k_format: how the request descriptors' k_* fields hold the history keys
 K_INT4, K_BF16, K_INT2 = 0, 1, 2
 
+class PlanRun(ctypes.Structure):  # r2o_plan_run
+    _fields_ = [(f, c_i64) for f in ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta")]
+
+
+class PlanConfig(ctypes.Structure):  # r2o_plan_config
+    _fields_ = [
+        ("num_cus", c_i64),
+        ("blocks_per_cu", c_i64),
+        ("tiles_per_item", c_i64),
+        ("waves_per_item", c_i64),
+        ("min_tiles_per_item", c_i64),
+        ("tile_cost", ctypes.c_double * 4),
+        ("late_share", ctypes.c_double),
+    ]
+
+
 _SIGNATURES = {
+    "r2o_plan_work_items": (ctypes.POINTER(PlanRun), c_i64, ctypes.POINTER(PlanConfig), c_vp, c_i64, c_i64, c_i64,
+                            c_vp, c_i64, c_vp, c_i64, ctypes.POINTER(c_i64)),
     "r2o_decode_partial": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_combine": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_noalloc": (ctypes.POINTER(DecodeParams), c_vp),

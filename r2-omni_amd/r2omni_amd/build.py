@@ -19,7 +19,7 @@ CSRC = os.path.join(ROOT_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libr2o_sspa.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ("r2o_decode.hip", "r2o_pack.hip", "r2o_rope.hip")
+SOURCES = ("r2o_decode.hip", "r2o_pack.hip", "r2o_rope.hip", "r2o_plan.cpp")  # r2o_plan.cpp: host code only
 ARCH = "gfx950"
 
 
@@ -51,7 +51,7 @@ def build_library(verbose: bool = False) -> str:
     os.makedirs(build_dir, exist_ok=True)
     objects = []
     for src in SOURCES:
-        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+        obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
         cmd = [hipcc, *common_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
         _run(cmd, verbose)
         objects.append(obj)

@@ -15,7 +15,6 @@ workspace is one split-K work item (a run of 32-token tiles handled by one workg
 from __future__ import annotations
 
 import ctypes
-import heapq
 from dataclasses import dataclass, field
 from typing import Sequence
 
@@ -84,6 +83,50 @@ def _tiles(lo: int, hi: int) -> tuple[int, int]:
 _TILE_COST = {_lib.KIND_FP: 1.45, _lib.KIND_INT4: 1.0, _lib.KIND_INT2: 1.4, _lib.KIND_RECENT: 1.6}
 
 
+def _plan_runs(caches: Sequence[ThreePrecisionCache], hkv: int, extra_int2: int = 0) -> list[tuple]:
+    """(req, kv head, kind, first tile position, tiles, lo, hi, v_delta) of every pool segment and
+    Recent-FP ring, grouped by (request, kv head) in order."""
+    runs = []
+    for r, c in enumerate(caches):
+        ss = _segments(c, extra_int2)
+        rcap = c.recent_fp_pool.capacity
+        if rcap % TILE:
+            raise ValueError("Recent-FP capacity must be a multiple of 32 for the gfx950 decode path")
+        for h in range(hkv):
+            for kind, lo, hi, vd in ss:
+                t0, nt = _tiles(lo, hi)
+                runs.append((r, h, kind, t0, nt, lo, hi, vd))
+            runs.append((r, h, _lib.KIND_RECENT, 0, rcap // TILE, 0, rcap, 0))
+    return runs
+
+
+def _plan(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_int2: int = 0,
+          reqs: torch.Tensor | None = None, k_format: int = _lib.K_INT4, int2_group: int = 32):
+    """r2o_plan_work_items over the caches' runs: (work items int64 [n, 16] in launch order, with their
+    base pointers when ``reqs`` (host int64 [B, 22] request descriptors) is given, group_begin int32
+    [B*hkv + 1]) on the host."""
+    runs = _plan_runs(caches, hkv, extra_int2)
+    n_runs, n_groups = len(runs), len(caches) * hkv
+    cus = max(1, int(num_cus))
+    cap = max(_BLOCKS_PER_CU * cus, n_runs)
+    cfg = _lib.PlanConfig(num_cus=cus, blocks_per_cu=_BLOCKS_PER_CU, tiles_per_item=_TILES_PER_ITEM_TARGET,
+                          waves_per_item=_WAVES_PER_ITEM, min_tiles_per_item=_MIN_TILES_PER_ITEM,
+                          late_share=_LATE_SHARE)
+    for k in (_lib.KIND_FP, _lib.KIND_INT4, _lib.KIND_INT2, _lib.KIND_RECENT):
+        cfg.tile_cost[k] = _TILE_COST[k]
+    run_arr = (_lib.PlanRun * n_runs)(*[_lib.PlanRun(*r) for r in runs])
+    items = torch.zeros(cap, 16, dtype=torch.int64)
+    begins = torch.empty(n_groups + 1, dtype=torch.int32)
+    n = ctypes.c_int64(0)
+    if reqs is not None:
+        reqs = reqs.contiguous()
+    _lib.check(_lib.load().r2o_plan_work_items(run_arr, n_runs, ctypes.byref(cfg),
+                                               None if reqs is None else reqs.data_ptr(), len(caches), k_format,
+                                               int2_group, items.data_ptr(), cap, begins.data_ptr(), n_groups,
+                                               ctypes.byref(n)), "r2o_plan_work_items")
+    return items[: n.value], begins
+
+
 def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_int2: int = 0):
     """Split every (request, kv head, pool segment) into runs of 32-token tiles.
 
@@ -93,85 +136,11 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
     puts two items on each CU splits its runs unevenly, see _LATE_SHARE).  A small cache aims at
     about _TILES_PER_ITEM_TARGET tiles per item instead, but at no fewer than CUs items.  Items keep a partial
     slot in (request, kv head) order, so the combine reads one contiguous slot range per group,
-    and are launched largest first.
+    and are launched largest first.  The planning runs in native code (r2o_plan_work_items).
     Returns (items [n, 9] int64 in launch order, group_begin [B*hkv + 1] int32) on the host.
     """
-    segs = [_segments(c, extra_int2) for c in caches]
-    runs = []  # (req, head, kind, first tile position, tiles, lo, hi, v_delta)
-    for r, (c, ss) in enumerate(zip(caches, segs)):
-        rcap = c.recent_fp_pool.capacity
-        if rcap % TILE:
-            raise ValueError("Recent-FP capacity must be a multiple of 32 for the gfx950 decode path")
-        for h in range(hkv):
-            for kind, lo, hi, vd in ss:
-                t0, nt = _tiles(lo, hi)
-                runs.append((r, h, kind, t0, nt, lo, hi, vd))
-            runs.append((r, h, _lib.KIND_RECENT, 0, rcap // TILE, 0, rcap, 0))
-    # Water-filling: give one more item to the run whose items are currently the most
-    # expensive until the workgroup slots are used up (or no run can be split further).
-    cus = max(1, num_cus)
-    total_tiles = sum(r[4] for r in runs)
-    target = min(_BLOCKS_PER_CU * cus, max(cus, total_tiles // _TILES_PER_ITEM_TARGET))
-    counts = [1] * len(runs)
-
-    def item_cost(i: int) -> float:
-        nt = runs[i][4]
-        per = -(-nt // counts[i])
-        return (-(-per // _WAVES_PER_ITEM) * _WAVES_PER_ITEM) * _TILE_COST[runs[i][2]]
-
-    heap = [(-item_cost(i), i) for i in range(len(runs))]
-    heapq.heapify(heap)
-    total = sum(counts)
-    while total < target and heap:
-        _, i = heapq.heappop(heap)
-        if -(-runs[i][4] // (counts[i] + 1)) < _MIN_TILES_PER_ITEM:
-            continue  # already at the smallest useful item size
-        counts[i] += 1
-        total += 1
-        heapq.heappush(heap, (-item_cost(i), i))
-    uniform = len({r[2] for r in runs if r[2] != _lib.KIND_RECENT}) == 1
-    late_share = _LATE_SHARE if uniform and total > cus else 1.0
-    items = []
-    begins = [0]
-    group = (0, 0)
-    for (r, h, kind, t0, nt, lo, hi, vd), n_items in zip(runs, counts):
-        if (r, h) != group:
-            begins.append(len(items))
-            group = (r, h)
-        for first, size in _split_run(nt, n_items, late_share):
-            items.append([r, h, kind, t0 + TILE * first, size, lo, hi, vd, len(items)])
-    begins.append(len(items))
-    items.sort(key=lambda it: -it[4] * _TILE_COST[it[2]])  # stable: largest first, ties keep slot order
-    return torch.tensor(items, dtype=torch.int64), torch.tensor(begins, dtype=torch.int32)
-
-
-def _split_run(nt: int, n_items: int, late_share: float = 1.0):
-    """(first tile, tiles) of the items of one run: multiples of a wave share each, all but the
-    last; with late_share < 1 the second half of the items gets that share of the first half's."""
-    w = _WAVES_PER_ITEM
-    if late_share >= 1.0 or n_items < 2:
-        n = -(-(-(-nt // n_items)) // w) * w  # even split, a share per wave
-        return [(f, min(n, nt - f)) for f in range(0, nt, n)]
-    big = -(-n_items // 2)
-    small = n_items - big
-    x = nt / (big + late_share * small)
-    bsize = -(-int(round(x)) // w) * w
-    out, f = [], 0
-    for k in range(n_items):
-        if f >= nt:
-            break
-        if k < big:
-            size = bsize
-        else:
-            left = n_items - k
-            size = -(-(-(-(nt - f) // left)) // w) * w
-        size = min(size, nt - f)
-        out.append((f, size))
-        f += size
-    if f < nt:  # rounding left a remainder: extend the last item
-        last_f, last_s = out[-1]
-        out[-1] = (last_f, last_s + nt - f)
-    return out
+    items, begins = _plan(caches, hkv, num_cus, extra_int2)
+    return items[:, :9].contiguous(), begins
 
 
 def max_work_items(num_requests: int, hkv: int, num_cus: int) -> int:
@@ -274,27 +243,6 @@ def _request_words(cache: ThreePrecisionCache, ring=None) -> dict[str, int]:
 def _request_desc(cache: ThreePrecisionCache) -> list[int]:
     words = _request_words(cache)
     return [words[f] for f in _lib.REQUEST_FIELDS]
-
-
-_K_ROW_BYTES = {_lib.K_INT4: 64, _lib.K_INT2: 32, _lib.K_BF16: 256}
-
-
-def _item_pointers(words: dict[str, int], k_format: int, kind: int, h: int, groups: int) -> list[int]:
-    """Base pointers (k_base, k_ops, v_base, v_scale, v_zero, ring_length) of KV head ``h`` for
-    an item of ``kind``: the pointer arithmetic the kernel would otherwise do per item."""
-    if kind == _lib.KIND_RECENT:
-        row = h * words["recent_capacity"] * 256
-        return [words["recent_k"] + row, 0, words["recent_v"] + row, 0, 0, words["recent_length"]]
-    k_base = words["k_packed"] + h * words["k_capacity"] * _K_ROW_BYTES[k_format]
-    k_ops = words["k_operands"] + h * words["k_superblocks"] * 128 * 4 if words["k_operands"] else 0
-    if kind == _lib.KIND_FP:
-        return [k_base, k_ops, words["fp_v"] + h * words["fp_stride"] * 256, 0, 0, 0]
-    if kind == _lib.KIND_INT4:
-        st = words["i4_stride"]
-        return [k_base, k_ops, words["i4_v"] + h * st * 64, words["i4_scale"] + h * st * 4, 0, 0]
-    st = words["i2_stride"]
-    return [k_base, k_ops, words["i2_v"] + h * st * 32, words["i2_scale"] + h * st * groups * 2,
-            words["i2_zero"] + h * st * groups, 0]
 
 
 @dataclass
@@ -459,6 +407,14 @@ def _per_request(value, b: int) -> list[int]:
     return [int(v) for v in vals]
 
 
+def _to_device_async(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    """Host -> device copy that does not wait for the work already queued on the stream: from pinned
+    memory, non-blocking (torch's pinned-memory allocator keeps the block until the copy has run).  A
+    copy from pageable memory blocks the host until the stream drains, which serialised every re-plan
+    after a flush with the launches queued before it."""
+    return t.pin_memory().to(dev, non_blocking=True)
+
+
 def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWorkspace, *, output_hadamard: bool,
                     block_n: int, batched: bool, rings: Sequence | None = None) -> SplitKExecutor:
     """Plan the work items and resolve the pool pointers of ``caches``.  ``rings`` (one Recent-FP
@@ -490,17 +446,16 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
                 or int(c.recent_fp_pool.fp_k.shape[0]) != hkv or c.page_size != first.page_size:
             raise ValueError(f"batched split-K geometry differs for request {r}")
     dev = workspace.output.device
-    host_items, begins = plan_work_items(caches, hkv, _num_cus(dev))
+    words = [_request_words(c, None if rings is None else rings[r]) for r, c in enumerate(caches)]
+    host_reqs = torch.tensor([[w[f] for f in _lib.REQUEST_FIELDS] for w in words], dtype=torch.int64)
+    host_items, begins = _plan(caches, hkv, _num_cus(dev), reqs=host_reqs, k_format=kf, int2_group=group)
     n = int(host_items.shape[0])
     if n > workspace.total_blocks:
         raise ValueError("workspace block capacity is smaller than the active cache")
-    words = [_request_words(c, None if rings is None else rings[r]) for r, c in enumerate(caches)]
-    reqs = torch.tensor([[w[f] for f in _lib.REQUEST_FIELDS] for w in words], dtype=torch.int64).to(dev)
-    groups = 128 // group
-    rows = [it + _item_pointers(words[it[0]], kf, it[2], it[1], groups) + [0] for it in host_items.tolist()]
-    host_items = torch.tensor(rows, dtype=torch.int64)
+    reqs = _to_device_async(host_reqs, dev)
     return SplitKExecutor(
-        caches=list(caches), workspace=workspace, reqs=reqs, items=host_items.to(dev), group_begin=begins.to(dev),
+        caches=list(caches), workspace=workspace, reqs=reqs, items=_to_device_async(host_items, dev),
+        group_begin=_to_device_async(begins, dev),
         n_items=n, num_query_heads=hq, num_key_value_heads=hkv, head_dim=head_dim, superblock=sb, int2_group=group,
         page_size=first.page_size, output_hadamard=bool(output_hadamard), block_n=block_n, batched=batched,
         host_items=host_items, host_group_begin=begins.contiguous(),

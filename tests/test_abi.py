@@ -54,6 +54,14 @@ def test_params_struct_layout_matches_header(tmp_path):
     assert ctypes.sizeof(p) == size
 
 
+def test_planner_struct_layouts_match_header(tmp_path):
+    for struct, cls in (("r2o_plan_run", _lib.PlanRun), ("r2o_plan_config", _lib.PlanConfig)):
+        names = [f[0] for f in cls._fields_]
+        offsets, size = _c_layout(struct, names, tmp_path)
+        assert [getattr(cls, n).offset for n in names] == offsets, struct
+        assert ctypes.sizeof(cls) == size, struct
+
+
 def test_descriptor_word_layouts_match_header(tmp_path):
     # the request descriptor and work item are rows of int64 words written by the host planner
     for struct, fields in (("r2o_request_desc", _lib.REQUEST_FIELDS), ("r2o_work_item", _lib.ITEM_FIELDS)):
@@ -71,3 +79,14 @@ def test_host_side_validation_rejects_bad_arguments_without_a_gpu():
     params = _lib.DecodeParams()
     assert lib.r2o_decode_partial(ctypes.byref(params), None) == 1
     assert lib.r2o_build_target() == b"gfx950"
+    # the planner refuses runs whose groups do not match the group count, without a GPU
+    run = _lib.PlanRun(0, 0, _lib.KIND_RECENT, 0, 4, 0, 128, 0)
+    cfg = _lib.PlanConfig(num_cus=8, blocks_per_cu=2, tiles_per_item=8, waves_per_item=4, min_tiles_per_item=4,
+                          late_share=1.0)
+    n = ctypes.c_int64(0)
+    items = (ctypes.c_int64 * (16 * 16))()
+    begins = (ctypes.c_int32 * 4)()
+    assert lib.r2o_plan_work_items(ctypes.byref(run), 1, ctypes.byref(cfg), None, 1, 0, 32, items, 16, begins, 3,
+                                   ctypes.byref(n)) == 1
+    assert lib.r2o_plan_work_items(ctypes.byref(run), 1, ctypes.byref(cfg), None, 1, 0, 32, items, 16, begins, 1,
+                                   ctypes.byref(n)) == 0 and n.value >= 1

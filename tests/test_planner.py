@@ -1,4 +1,6 @@
-"""CPU checks of the split-K work-item planner (host logic only, fake cache geometry)."""
+"""CPU checks of the split-K work-item planner (host logic only, fake cache geometry).  The planner runs
+in native code (r2o_plan_work_items, callable without a GPU); tests/planner_reference.py restates it in
+Python, and the native plans must equal that restatement item for item."""
 import random
 from types import SimpleNamespace
 
@@ -57,8 +59,9 @@ def test_items_cover_every_tile_once_and_respect_the_bound(seed):
 @pytest.mark.parametrize("nt,n_items,share", [(4096, 64, 0.7), (4097, 63, 0.7), (100, 3, 0.7), (37, 2, 0.7),
                                               (8, 2, 0.7), (5, 2, 0.7), (4096, 64, 1.0), (130, 7, 0.5)])
 def test_split_run_covers_the_run_with_wave_shares(nt, n_items, share):
-    from r2omni_amd.splitk import _WAVES_PER_ITEM, _split_run
-    items = _split_run(nt, n_items, share)
+    from planner_reference import split_run
+    from r2omni_amd.splitk import _WAVES_PER_ITEM
+    items = split_run(nt, n_items, share)
     assert 1 <= len(items) <= n_items
     assert items[0][0] == 0 and sum(s for _, s in items) == nt
     assert all(f2 == f1 + s1 for (f1, s1), (f2, _) in zip(items, items[1:]))
@@ -95,3 +98,49 @@ def test_single_kind_plans_give_the_later_launched_half_less_work():
     assert len(small) <= cus
     sizes = sorted(it[4] for it in small if it[2] == _lib.KIND_INT2)
     assert sizes[-1] - sizes[1] <= 4  # even (one wave share of rounding), the remainder aside
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_native_plan_equals_the_python_restatement(seed):
+    from planner_reference import python_plan_work_items
+
+    import torch
+
+    rnd = random.Random(1000 + seed)
+    b = rnd.randint(1, 8)
+    hkv = rnd.choice([1, 2, 4, 8])
+    cus = rnd.choice([8, 64, 80, 256])
+    caches = [_fake_cache(rnd.choice([0, rnd.randint(1, 20000)]), rnd.choice([0, rnd.randint(1, 40000)]),
+                          rnd.choice([0, rnd.randint(1, 131072)]), rnd.choice([32, 128, 256])) for _ in range(b)]
+    extra = rnd.choice([0, 128, 256])
+    got = plan_work_items(caches, hkv, cus, extra_int2=extra)
+    want = python_plan_work_items(caches, hkv, cus, extra_int2=extra)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
+@pytest.mark.parametrize("k_format,group", [(_lib.K_INT4, 32), (_lib.K_INT2, 128), (_lib.K_BF16, 64)])
+def test_native_plan_fills_each_items_base_pointers(k_format, group):
+    """With the host request descriptors the planner writes each item's base pointers: the per-head
+    offsets into the request's K arena, K operand blocks, V pool, V scales and zeros, or its ring."""
+    from planner_reference import item_pointers
+
+    import torch
+
+    from r2omni_amd.splitk import _plan
+
+    rnd = random.Random(7)
+    caches = [_fake_cache(4096, 8192, 16384), _fake_cache(0, 3072, 640)]
+    hkv = 4
+    words = []
+    for r in range(len(caches)):
+        w = {f: (r + 1) * (1 << 40) + (i + 1) * (1 << 32) for i, f in enumerate(_lib.REQUEST_FIELDS)}
+        for f in ("k_capacity", "k_superblocks", "fp_stride", "i4_stride", "i2_stride", "recent_capacity"):
+            w[f] = rnd.randint(1, 1 << 16)
+        if k_format == _lib.K_BF16:
+            w["k_operands"] = 0
+        words.append(w)
+    reqs = torch.tensor([[w[f] for f in _lib.REQUEST_FIELDS] for w in words], dtype=torch.int64)
+    items, _ = _plan(caches, hkv, 64, reqs=reqs, k_format=k_format, int2_group=group)
+    for it in items.tolist():
+        assert it[9:15] == item_pointers(words[it[0]], k_format, it[2], it[1], 128 // group)
+        assert it[15] == 0
