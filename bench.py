@@ -18,8 +18,10 @@ print their own line instead.
 from __future__ import annotations
 
 import argparse
+import contextlib
 import ctypes
 import dataclasses
+import gc
 import json
 import os
 import sys
@@ -37,17 +39,33 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+@contextlib.contextmanager
+def _gc_paused():
+    """Run a timed region with Python's garbage collector paused after a collection, as ``timeit``
+    does: a full collection of this process takes tens of milliseconds, a pause of the Python host
+    that would otherwise land in a timed window now and then."""
+    gc.collect()
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was_enabled:
+            gc.enable()
+
+
 def _time_events(fn, steps: int, stream) -> float:
     import torch
 
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    start.record(stream)
-    for i in range(steps):
-        fn(i)
-    stop.record(stream)
-    torch.cuda.synchronize()
+    with _gc_paused():
+        start.record(stream)
+        for i in range(steps):
+            fn(i)
+        stop.record(stream)
+        torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps  # ms
 
 
@@ -299,17 +317,19 @@ def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dic
             one_step()
         torch.cuda.synchronize()
         steady = 100
-        t0 = time.perf_counter()
-        for _ in range(steady):
-            one_step()
-        torch.cuda.synchronize()
-        t_steady = (time.perf_counter() - t0) / steady
+        with _gc_paused():
+            t0 = time.perf_counter()
+            for _ in range(steady):
+                one_step()
+            torch.cuda.synchronize()
+            t_steady = (time.perf_counter() - t0) / steady
         flushes0 = sum(st.flushed_superblocks for d in decs for st in d.stats)
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            one_step()
-        torch.cuda.synchronize()
-        t_all = (time.perf_counter() - t0) / steps
+        with _gc_paused():
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                one_step()
+            torch.cuda.synchronize()
+            t_all = (time.perf_counter() - t0) / steps
         out[mode] = {"us_per_step_steady": round(t_steady * 1e6, 2),
                      "us_per_layer_call_steady": round(t_steady * 1e6 / layers, 2),
                      "us_per_step_with_flushes": round(t_all * 1e6, 2),
@@ -320,7 +340,7 @@ def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dic
         torch.cuda.empty_cache()
     out["note"] = ("host wall clock per decode step (all layers) over back-to-back steps, no per-step sync: "
                    "launch overhead, flush packing, re-plans and graph re-captures included; 'steady' = 100 "
-                   "steps without a flush")
+                   "steps without a flush; Python's garbage collector paused in the timed loops")
     return out
 
 
@@ -523,7 +543,7 @@ class E2EQwenDecoder:
         stream = torch.cuda.current_stream(dev)
         e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         graph = None
-        with torch.no_grad():
+        with torch.no_grad(), _gc_paused():
             torch.cuda.synchronize()
             e[0].record(stream)
             body(eager_attend)  # step 1: every ring is full and flushes inside the batch

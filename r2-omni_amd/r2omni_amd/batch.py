@@ -28,6 +28,24 @@ from .splitk import (
 )
 
 
+def _capture_launches(device: torch.device, side: torch.cuda.Stream, launch) -> torch.cuda.CUDAGraph:
+    """Capture ``launch()`` into a HIP graph on ``side``, a stream kept for the captures of one
+    decoder (a fresh pool stream would set up a hardware queue at its first use, milliseconds per
+    re-capture), after making it wait for the current stream.  The capture is begun and ended
+    directly: ``torch.cuda.graph`` would also synchronise the device, run the Python garbage
+    collector and empty the allocator cache on every re-capture."""
+    graph = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        try:
+            launch()
+        finally:
+            graph.capture_end()
+    torch.cuda.current_stream(device).wait_stream(side)
+    return graph
+
+
 class BatchedDecoder:
     """Decode steps over ``caches`` (one per request, same head geometry and K format).
 
@@ -70,6 +88,7 @@ class BatchedDecoder:
         self._next_positions: list[tuple[int, int]] | None = None  # what the device holds for the next step
         self.executor: SplitKExecutor | None = None
         self._graph: torch.cuda.CUDAGraph | None = None
+        self._capture_stream: torch.cuda.Stream | None = None
         self._params = None
         self.replans = 0
         self.graph_captures = 0
@@ -90,13 +109,10 @@ class BatchedDecoder:
         # one eager launch first (no append, host-provided lengths: it only rewrites the output) so
         # that nothing is loaded or initialised for the first time while the stream is capturing
         self.executor._launch(self.executor._params(self.query_buffer, self.workspace.output, None), self.device)
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(device=self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.graph(graph, stream=side):
-            self.executor._launch(self._params, self.device)
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        self._graph = graph
+        if self._capture_stream is None:
+            self._capture_stream = torch.cuda.Stream(device=self.device)
+        self._graph = _capture_launches(self.device, self._capture_stream,
+                                        lambda: self.executor._launch(self._params, self.device))
         self.graph_captures += 1
 
     # ------------------------------------------------------------------------------ steps
@@ -168,19 +184,18 @@ class DecodeStepGraph:
             raise ValueError("a decode step needs at least one layer")
         self.device = self.layers[0].device
         self._graph: torch.cuda.CUDAGraph | None = None
+        self._capture_stream = torch.cuda.Stream(device=self.device)
         self.graph_captures = 0
 
     def _capture(self) -> None:
         for d in self.layers:  # eager warm-up without append (rewrites the outputs only)
             d.executor._launch(d.executor._params(d.query_buffer, d.workspace.output, None), self.device)
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(device=self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.graph(graph, stream=side):
+
+        def launches():
             for d in self.layers:
                 d.executor._launch(d._params, self.device)
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        self._graph = graph
+
+        self._graph = _capture_launches(self.device, self._capture_stream, launches)
         self.graph_captures += 1
 
     def step_in_place(self, *, global_token_index, logical_position) -> list[torch.Tensor]:

@@ -407,12 +407,43 @@ def _per_request(value, b: int) -> list[int]:
     return [int(v) for v in vals]
 
 
-def _to_device_async(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
-    """Host -> device copy that does not wait for the work already queued on the stream: from pinned
-    memory, non-blocking (torch's pinned-memory allocator keeps the block until the copy has run).  A
-    copy from pageable memory blocks the host until the stream drains, which serialised every re-plan
-    after a flush with the launches queued before it."""
-    return t.pin_memory().to(dev, non_blocking=True)
+_UPLOAD_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _upload_stream(dev: torch.device) -> torch.cuda.Stream:
+    """The device's stream for plan uploads (created once, default priority)."""
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = _UPLOAD_STREAMS.get(index)
+    if stream is None:
+        stream = _UPLOAD_STREAMS[index] = torch.cuda.Stream(device=index)
+    return stream
+
+
+def _upload_plan(dev: torch.device, *host: torch.Tensor) -> list[torch.Tensor]:
+    """Device copies of the host tensors of a plan, uploaded as one pinned block on a stream of their
+    own.  A host-to-device copy queued behind the launches already on the compute stream could make
+    the host wait until they had drained (milliseconds at a flush step, after which the GPU idled
+    while the host re-planned); on its own stream the copy runs at once.  The device block is
+    allocated on the upload stream and marked as used by the compute stream, so the allocator reuses
+    it only after the compute stream's later work has run, and the compute stream waits for the copy
+    before its next launch."""
+    align = 256
+    offsets, total = [], 0
+    for t in host:
+        offsets.append(total)
+        total += -(-t.numel() * t.element_size() // align) * align
+    staging = torch.empty(total, dtype=torch.uint8, pin_memory=True)
+    for t, o in zip(host, offsets):
+        raw = t.contiguous().reshape(-1).view(torch.uint8)
+        staging[o : o + raw.numel()].copy_(raw)
+    compute = torch.cuda.current_stream(dev)
+    side = _upload_stream(dev)
+    with torch.cuda.stream(side):
+        block = torch.empty(total, dtype=torch.uint8, device=dev)
+        block.copy_(staging, non_blocking=True)
+    block.record_stream(compute)
+    compute.wait_stream(side)
+    return [block[o : o + t.numel() * t.element_size()].view(t.dtype).view(t.shape) for t, o in zip(host, offsets)]
 
 
 def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWorkspace, *, output_hadamard: bool,
@@ -452,10 +483,9 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
     n = int(host_items.shape[0])
     if n > workspace.total_blocks:
         raise ValueError("workspace block capacity is smaller than the active cache")
-    reqs = _to_device_async(host_reqs, dev)
+    reqs, items, group_begin = _upload_plan(dev, host_reqs, host_items, begins)
     return SplitKExecutor(
-        caches=list(caches), workspace=workspace, reqs=reqs, items=_to_device_async(host_items, dev),
-        group_begin=_to_device_async(begins, dev),
+        caches=list(caches), workspace=workspace, reqs=reqs, items=items, group_begin=group_begin,
         n_items=n, num_query_heads=hq, num_key_value_heads=hkv, head_dim=head_dim, superblock=sb, int2_group=group,
         page_size=first.page_size, output_hadamard=bool(output_hadamard), block_n=block_n, batched=batched,
         host_items=host_items, host_group_begin=begins.contiguous(),

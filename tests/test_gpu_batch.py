@@ -137,3 +137,49 @@ def test_decode_step_graph_over_layers_matches_oracle():
                 _compare(outs[layer][r : r + 1], want, f"step graph step {step} layer {layer} request {r}")
         pos = [p + 1 for p in pos]
     assert step_graph.graph_captures == 2  # the first step and the flush step
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_steps_queued_behind_a_busy_stream_across_re_plans(use_graph):
+    """Steps issued without any host synchronisation while the stream is held busy, across the three
+    re-plans of a ragged batch: each re-plan uploads its work items on the upload stream while the
+    launches of the previous plan are still queued, and every step must still match the oracle
+    (outputs copied out on the stream, compared after one synchronisation at the end)."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference
+    from oracle.cache import append_token
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    hq, hkv = 16, 2
+    shapes = [(1024, 125), (2048, 121), (640, 116)]
+    caches, oracles = [], []
+    for r, (hist, recent) in enumerate(shapes):
+        cfg = DecodeConfig("q", hq, hkv, (0,), (0.15, 0.45, 0.4), recent=recent)
+        data = make_request(cfg, hist + recent, seed=800 + r, device=dev)
+        caches.append(build_request_cache(cfg, data))
+        oracles.append(_oracle_for(data, cfg))
+    dec = ro.BatchedDecoder(caches, num_query_heads=hq, use_graph=use_graph)
+    gen = torch.Generator(device=dev).manual_seed(13)
+    steps = 16
+    q = torch.randn(steps, 3, hq, 128, generator=gen, device=dev).to(torch.bfloat16)
+    k = torch.randn(steps, 3, hkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(steps, 3, hkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+    pos0 = [hist + recent for hist, recent in shapes]
+    torch.cuda.synchronize()
+    print(f"[queued steps graph={use_graph}] issuing {steps} steps behind a busy stream", flush=True)
+    torch.cuda._sleep(50_000_000)  # a bounded spin: the steps below queue up behind it
+    outs = []
+    for step in range(steps):
+        pos = [p + step for p in pos0]
+        outs.append(dec.step(q[step], k[step], v[step], global_token_index=pos, logical_position=pos).clone())
+    torch.cuda.synchronize()
+    assert dec.replans == 1 + 3
+    for step in range(steps):
+        for r in range(3):
+            p = pos0[r] + step
+            append_token(oracles[r], bf16_bits_to_f32(_bf16_np(k[step, r])), bf16_bits_to_f32(_bf16_np(v[step, r])),
+                         global_index=p, logical_position=p)
+            want = mixed_reference(bf16_bits_to_f32(_bf16_np(q[step, r : r + 1])), oracles[r])
+            _compare(outs[step][r : r + 1], want, f"queued graph={use_graph} step {step} request {r}")
