@@ -90,3 +90,12 @@ def test_host_side_validation_rejects_bad_arguments_without_a_gpu():
                                    ctypes.byref(n)) == 1
     assert lib.r2o_plan_work_items(ctypes.byref(run), 1, ctypes.byref(cfg), None, 1, 0, 32, items, 16, begins, 1,
                                    ctypes.byref(n)) == 0 and n.value >= 1
+
+
+def test_stream_lookup_refuses_a_cpu_device():
+    """Launches take their stream from the tensor's device; a CPU tensor is refused before any
+    launch instead of being handed to a kernel."""
+    import torch
+
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        _lib.stream_of(torch.device("cpu"))
