@@ -26,7 +26,7 @@ from .cache import ThreePrecisionCache
 TILE = 32
 _WAVES_PER_ITEM = 4          # waves of the partial kernel's workgroup (each takes a contiguous share)
 _MIN_TILES_PER_ITEM = 4      # one tile per wave
-_BLOCKS_PER_CU = 2           # work items planned per CU (the kernel holds up to 3 resident; 2 keeps the combine short)
+_BLOCKS_PER_CU = 2           # work items planned per CU: the kernel holds 2 resident, and more queue behind them
 # Small caches: fewer, longer items (about two tiles per wave) while every CU still gets one; more
 # items would only add partial states for the combine (measured on MI355X: a 3B layer at 32k
 # tokens takes 13.0 us per call at 256 items against 14.9 at 512).
