@@ -136,7 +136,7 @@ __device__ __forceinline__ float head_max(float x) {
 // always refer to the same m, so the state and its later merges are exact.
 constexpr float kRescaleSlack = 4.f;
 
-template <int N, int NE>
+template <int N, int NE, bool ACC_L = true>
 __device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N], float (&pk)[N], int g, float add,
                                              r2o_f4* extra) {
     float tmax = sv[0];
@@ -162,15 +162,16 @@ __device__ __forceinline__ void softmax_step(WaveState& st, const float (&sv)[N]
 #pragma unroll
     for (int k = 0; k < N; ++k) {
         pk[k] = __builtin_amdgcn_exp2f(sv[k] - d);  // exp2(-inf) = 0 for masked tokens
-        st.l += pk[k];
+        if constexpr (ACC_L) st.l += pk[k];
     }
 }
 
-// Online-softmax update for one tile whose logits are sv + add (log2 domain, -inf = masked).
-template <int NE = 0>
+// Online-softmax update for one tile whose logits are sv + add (log2 domain, -inf = masked).  With
+// ACC_L false the caller accumulates the sum of p itself (in one of the `extra` accumulators).
+template <int NE = 0, bool ACC_L = true>
 __device__ __forceinline__ void softmax_tile(WaveState& st, const float (&sv)[8], float (&pk)[8], int g,
                                              float add = 0.f, r2o_f4* extra = nullptr) {
-    softmax_step<8, NE>(st, sv, pk, g, add, extra);
+    softmax_step<8, NE, ACC_L>(st, sv, pk, g, add, extra);
 }
 
 // PV for 16-bit V rows held as R[k] = 8 dims (8*l16 ..) of token tile_token(g, k).
@@ -236,8 +237,8 @@ struct VRegs<kI4> {
 template <>
 struct VRegs<kI2> {
     uint32_t v[8];
-    uint32_t vm[8];  // fp16 scale bits (group of dims 8*l16)
-    uint32_t vz[8];  // u8 zero point
+    uint32_t vm[8];  // fp16 scale bits (group of dims 8*l16); one token per group: [pr] = pair (2pr, 2pr + 1)
+    uint32_t vz[8];  // u8 zero point; one token per group: [pr] = z(2pr) | z(2pr + 1) << 16
 };
 template <int KIND, int KF>
 struct TileRegs : KRegs<KF>, VRegs<KIND> {};
@@ -250,9 +251,10 @@ struct SegCtx {
 template <int KIND>
 struct SegState {
     uint32_t qp[4][4];   // q (scaled), f16 pairs in the K-unpack channel order
-    r2o_f4 bias[2];      // INT4-V: [0] = sum_k P'_k per head row; INT2-V with one group per token:
-                         // [0] = sum_k P'_k (1024 + z_k), [1] = sum_k P'_k (code offsets and the
-                         // in-place crumb factors removed at the end)
+    r2o_f4 bias[KIND == kI2 ? 3 : 2];  // INT4-V: [0] = sum_k P'_k per head row; INT2-V with one group
+                         // per token: [0] = sum_k P'_k (1024 + z_k), [1] = sum_k P'_k (code offsets and
+                         // the in-place crumb factors removed at the end), [2] = sum_k p_k (the softmax
+                         // denominator, from the same f16 p the P' are formed of)
 };
 
 // QK operands of one K superblock for the lane's channel group: Q'_j per MFMA j and the logit
@@ -389,19 +391,26 @@ __device__ __forceinline__ void pv_tile(WaveState& st, SegState<KIND>& ss, const
         // column q of the product carries 4^u sum P' c.  sum_k P'_k (1024 + z_k) and sum_k P'_k
         // accumulate by two more MFMAs on the same A operand; the offsets and the 4^u factors are
         // removed after the last tile.
+        // p in f16 pairs, P' = p * s in packed f16 against the tokens' scale pairs; sum_k p_k accumulates
+        // by one more MFMA (the softmax leaves l to it)
+        r2o_u4 p2;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            ap[u] = r2o_pack_h2(pk[2 * u] * r2o_f16_to_f32(cur.vm[2 * u]), pk[2 * u + 1] * r2o_f16_to_f32(cur.vm[2 * u + 1]));
+        for (int u = 0; u < 4; ++u) {
+            p2[u] = r2o_pack_h2(pk[2 * u], pk[2 * u + 1]);
+            ap[u] = r2o_h2_mul(p2[u], cur.vm[u]);
+        }
+        const r2o_u4 ones = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+        ss.bias[2] = r2o_mfma_f16(p2, ones, ss.bias[2]);
         uint32_t yp[4], y8[4];
         r2o_u4 zb;
 #pragma unroll
         for (int pr = 0; pr < 4; ++pr) {
             yp[pr] = cur.v[2 * pr] | (cur.v[2 * pr + 1] << 16);
             y8[pr] = yp[pr] >> 8;
-            zb[pr] = (cur.vz[2 * pr] | (cur.vz[2 * pr + 1] << 16)) | vc.magic;
+            zb[pr] = cur.vz[pr] | vc.magic;
         }
         ss.bias[0] = r2o_mfma_f16(ap, zb, ss.bias[0]);
-        ss.bias[1] = r2o_mfma_f16(ap, r2o_u4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}, ss.bias[1]);
+        ss.bias[1] = r2o_mfma_f16(ap, ones, ss.bias[1]);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const uint32_t mask = 0x00030003u << (2 * (q & 3));
@@ -461,7 +470,7 @@ __device__ __forceinline__ void seg_compute(const SegCtx& c, WaveState& st, SegS
     if constexpr (KF != kKBf16) corr = qo.corr;
     float sv[8], pk[8];
     tile_logits(c, a0, g, s, sv);
-    softmax_tile<TS ? 2 : (KIND == kI4 ? 1 : 0)>(st, sv, pk, g, corr, ss.bias);
+    softmax_tile<TS ? 3 : (KIND == kI4 ? 1 : 0), !TS>(st, sv, pk, g, corr, ss.bias);
     pv_tile<KIND, TS, RF>(st, ss, vc, pk, cur);
 }
 
@@ -594,7 +603,7 @@ __device__ __forceinline__ void read_ops(const unsigned char* stage, int g, r2o_
         ko[j] = *reinterpret_cast<const r2o_u4*>(stage + StageLayout<KIND, KF>::kOps + g * 128 + 16 * j);
 }
 
-template <int KIND, int KF>
+template <int KIND, int KF, bool TS = false>
 __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, int g, int gamma, int groups,
                                           TileRegs<KIND, KF>& tr) {
     using Lay = StageLayout<KIND, KF>;
@@ -624,6 +633,14 @@ __device__ __forceinline__ void read_tile(const unsigned char* stage, int l16, i
         } else if constexpr (KIND == kI4) {
             tr.v[k] = *reinterpret_cast<const uint32_t*>(stage + Lay::kV + 16 * v4_slot(t, l16 >> 2) + 4 * (l16 & 3));
             tr.vm[k] = *reinterpret_cast<const uint32_t*>(stage + Lay::kScale + 4 * t);
+        } else if constexpr (TS) {  // one group per token: scales and zeros of tokens t, t + 1 (t even) together
+            tr.v[k] = *reinterpret_cast<const uint16_t*>(stage + Lay::kV + 16 * v2_slot(t, l16 >> 3) + 2 * (l16 & 7));
+            if ((k & 1) == 0) {  // one dword slot per token: the 8 bytes at 4t hold both tokens' slots
+                const uint2 sc = *reinterpret_cast<const uint2*>(stage + Lay::kScale + 4 * t);
+                const uint2 zr = *reinterpret_cast<const uint2*>(stage + Lay::kZero + 4 * t);
+                tr.vm[k >> 1] = r2o_perm(sc.y, sc.x, 0x05040100u);  // (s_t, s_t+1) as an f16 pair
+                tr.vz[k >> 1] = r2o_perm(zr.y, zr.x, 0x0C040C00u);  // z_t | z_t+1 << 16
+            }
         } else {  // scale rows: 8 bytes (G = 32) or one dword slot; zero rows: one dword slot
             tr.v[k] = *reinterpret_cast<const uint16_t*>(stage + Lay::kV + 16 * v2_slot(t, l16 >> 3) + 2 * (l16 & 7));
             tr.vm[k] = *reinterpret_cast<const uint16_t*>(stage + Lay::kScale + t * (groups == 4 ? 8 : 4) + 2 * gamma);
@@ -718,7 +735,8 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const float qscale = p.sm_scale * kLog2e;
     SegState<KIND> ss;
     load_query<KF, RF>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: row-type pairs, scaled after the MFMA
-    ss.bias[0] = ss.bias[1] = r2o_f4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < (KIND == kI2 ? 3 : 2); ++e) ss.bias[e] = r2o_f4{0, 0, 0, 0};
     const SegCtx sc = {c.lo, c.hi};
     QkOps qo;  // operands of the current K superblock (INT4-K / INT2-K)
     for (int i = 0; i < n; ++i) {
@@ -726,7 +744,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
         __builtin_amdgcn_wave_barrier();
         unsigned char* stage = ring + (i % kDmaStages) * Cfg::kStage;
         TileRegs<KIND, KF> cur;
-        read_tile<KIND, KF>(stage, l16, g, gamma, c.groups, cur);
+        read_tile<KIND, KF, TS>(stage, l16, g, gamma, c.groups, cur);
         const bool fresh = __builtin_amdgcn_readfirstlane(needs_ops(i));  // wave-uniform
         r2o_u4 ko[8];
         if constexpr (KF != kKBf16)
@@ -749,6 +767,12 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
             const float f = 1.f / (float)(1 << (2 * (q & 3)));
             st.acc[q] = st.acc[q] * f - ss.bias[0] + ss.bias[1] * (1024.f * (1.f - f));
         }
+        // sum p of head 4g' + i sits in row i of every lane of group g'; the epilogue expects head l16's
+        // share in lanes l16 + 16 g, summed over g: lane 16 (l16 >> 2) + l16 holds it as row l16 & 3
+        const int r = l16 & 3;
+        const float mine = r == 0 ? ss.bias[2][0] : (r == 1 ? ss.bias[2][1] : (r == 2 ? ss.bias[2][2] : ss.bias[2][3]));
+        const float head_l = __shfl(mine, 16 * (l16 >> 2) + l16, R2O_WAVE);
+        st.l = g == 0 ? head_l : 0.f;
     }
     if constexpr (KIND == kI4) {  // remove the code offsets: lo dims 1032 * sum P', hi dims (1152 * sum P') / 16
 #pragma unroll
