@@ -522,10 +522,11 @@ template <int SIZE>
 __device__ __forceinline__ void dma(const void* gsrc, unsigned char* lds) {
     const auto g = (const __attribute__((address_space(1))) void*)gsrc;
     const auto l = (__attribute__((address_space(3))) void*)lds;
-    if constexpr (SIZE == 16) __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
-    else if constexpr (SIZE == 4) __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
-    else if constexpr (SIZE == 2) __builtin_amdgcn_global_load_lds(g, l, 2, 0, 0);
-    else __builtin_amdgcn_global_load_lds(g, l, 1, 0, 0);
+    constexpr int kNT = 2;  // cache policy: nontemporal (each KV byte is read once per call)
+    if constexpr (SIZE == 16) __builtin_amdgcn_global_load_lds(g, l, 16, 0, kNT);
+    else if constexpr (SIZE == 4) __builtin_amdgcn_global_load_lds(g, l, 4, 0, kNT);
+    else if constexpr (SIZE == 2) __builtin_amdgcn_global_load_lds(g, l, 2, 0, kNT);
+    else __builtin_amdgcn_global_load_lds(g, l, 1, 0, kNT);
 }
 
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
