@@ -10,9 +10,9 @@ To make the bytes come from HBM rather than the 256 MB Infinity Cache, the steps
 Reported: ``value`` = algorithmic GB/s of a layer call, ``ms_per_step`` = time per layer call,
 ``roofline`` for the dominant partial kernel (its average duration from HIP events on its
 stream), ``cpu_baseline`` = the reference's CPU dequantise+attention path (restated in torch) on
-the same packed data, ``hbm_copy`` = the box's measured device copy rate, and ``e2e`` = the rest
-of the metric: configuration 4's decode tok/s (a random-init 28-layer Qwen2.5-Omni-7B decoder, batch
-8 x 32k, 128 greedy steps on this path).  Other modes (--prefill, --decode-steps, --sweep, --e2e)
+the same packed data, ``hbm_copy`` / ``hbm_read`` = the box's measured device copy and streaming-read
+rates, and ``e2e`` = the rest of the metric: configuration 4's decode tok/s (a random-init 28-layer
+Qwen2.5-Omni-7B decoder, batch 8 x 32k, 128 greedy steps on this path).  Other modes (--prefill, --decode-steps, --sweep, --e2e)
 print their own line instead.
 """
 from __future__ import annotations
@@ -39,12 +39,28 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _clock_warmup(dev, ms: float = 50.0) -> None:
+    """Keep the GPU busy for ``ms`` milliseconds right before a timed window (a loop of bf16 matrix
+    products): after the host-side setup the clocks are low and take ~20 ms of load to come up."""
+    import torch
+
+    a = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            torch.mm(a, a, out=b)
+        torch.cuda.synchronize()
+    del a, b
+
+
 @contextlib.contextmanager
 def _gc_paused():
-    """Run a timed region with Python's garbage collector paused after a collection, as ``timeit``
-    does: a full collection of this process takes tens of milliseconds, a pause of the Python host
-    that would otherwise land in a timed window now and then."""
-    gc.collect()
+    """Run a timed region with Python's garbage collector paused, as ``timeit`` does: a full
+    collection of this process takes tens of milliseconds, a pause of the Python host that would
+    otherwise land in a timed window now and then.  No collection is run on entry: that many idle
+    milliseconds just before the window let the GPU clocks fall, and the timed launches then paid
+    for the ramp back up (~2 us per cfg2 layer call over 200 calls)."""
     was_enabled = gc.isenabled()
     gc.disable()
     try:
@@ -139,6 +155,47 @@ def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
                       f"{reps} after 1 warm-up: {med * 1e6:.0f} us/call on {threads} threads (torch CPU restatement "
                       "of triton_mixed_reference: every pool dequantised with torch ops per call, fp32 softmax "
                       "states per pool, exact merge)"}
+
+
+def read_bandwidth(dev, mib: int = 2048, reps: int = 20, blocks: int = 8192) -> dict:
+    """The box's read-only HBM rate: one pass of ``r2o_bench_stream_read`` (16-byte nontemporal loads,
+    nothing written) over ``mib`` MiB, bytes / time, median of ``reps`` HIP-event timings.  The
+    practical ceiling of a read-dominated kernel such as the partial kernel."""
+    import torch
+
+    from r2omni_amd.build import BENCH_LIB_PATH
+
+    lib = ctypes.CDLL(BENCH_LIB_PATH)
+    lib.r2o_bench_stream_read.restype = ctypes.c_int
+    lib.r2o_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.c_int, ctypes.c_void_p]
+    nbytes = mib * (1 << 20)
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(blocks, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def one():
+        rc = lib.r2o_bench_stream_read(src.data_ptr(), nbytes, sink.data_ptr(), blocks, 1, stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"r2o_bench_stream_read failed ({rc})")
+
+    for _ in range(3):
+        one()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        one()
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    ms = sorted(times)[reps // 2]
+    del src, sink
+    torch.cuda.empty_cache()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"GBs": round(gbs, 1), "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_read": nbytes,
+            "method": f"one streaming read of {mib} MiB (16-byte nontemporal loads, {blocks} workgroups, nothing "
+                      f"written), bytes / time, median of {reps} HIP-event timings"}
 
 
 def copy_bandwidth(dev, mib: int = 1024, reps: int = 20) -> dict:
@@ -316,6 +373,7 @@ def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dic
         for _ in range(4):  # the rings start full: the first step flushes every request of every layer
             one_step()
         torch.cuda.synchronize()
+        _clock_warmup(dev)
         steady = 100
         with _gc_paused():
             t0 = time.perf_counter()
@@ -716,7 +774,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed calls before the timed ones (default 2000, ~50 ms on cfg2: the GPU clocks take "
+                         "~20 ms of load to come up after the idle cache build)")
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--variant", choices=("int4k", "int2k", "bf16k", "matched"), default="int4k",
@@ -809,9 +869,11 @@ def main() -> int:
         cpu = cpu_baseline(caches0, [q0[i : i + 1] for i in range(len(cfg.lengths))], cfg.hq)
     del r
     torch.cuda.empty_cache()
-    _log("copy bandwidth ...")
+    _log("copy and read bandwidth ...")
     copy = copy_bandwidth(dev)
     copy["partial_kernel_pct_of_copy"] = round(100 * part_gbs / copy["GBs"], 1)
+    read = read_bandwidth(dev)
+    read["partial_kernel_pct_of_read"] = round(100 * part_gbs / read["GBs"], 1)
     e2e = None
     if not args.no_e2e:
         _log("e2e (configuration 4) ...")
@@ -844,6 +906,7 @@ def main() -> int:
                      "avg_us_source": "HIP events over back-to-back partial launches on the launch stream"},
         "cpu_baseline": cpu,
         "hbm_copy": copy,
+        "hbm_read": read,
         "e2e": e2e,
     }
     print(json.dumps(line), flush=True)

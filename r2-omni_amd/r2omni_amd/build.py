@@ -20,6 +20,9 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libr2o_sspa.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ("r2o_decode.hip", "r2o_pack.hip", "r2o_rope.hip", "r2o_plan.cpp")  # r2o_plan.cpp: host code only
+# bench.py's streaming-read probe, a library of its own (not part of the decode C-ABI)
+BENCH_LIB_PATH = os.path.join(PKG_DIR, "libr2o_bench.so")
+BENCH_SOURCES = ("bench_read.hip",)
 ARCH = "gfx950"
 
 
@@ -45,20 +48,26 @@ def common_flags() -> list[str]:
 
 
 def build_library(verbose: bool = False) -> str:
-    """Compile every source and link ``libr2o_sspa.so`` next to this file; returns its path."""
+    """Compile every source and link ``libr2o_sspa.so`` (and bench.py's ``libr2o_bench.so``) next to
+    this file; returns the decode library's path."""
+    _link(SOURCES, LIB_PATH, verbose)
+    _link(BENCH_SOURCES, BENCH_LIB_PATH, verbose)
+    return LIB_PATH
+
+
+def _link(sources, path: str, verbose: bool) -> None:
     hipcc = _hipcc()
     build_dir = os.path.join(ROOT_DIR, "_build")
     os.makedirs(build_dir, exist_ok=True)
     objects = []
-    for src in SOURCES:
+    for src in sources:
         obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
         cmd = [hipcc, *common_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
         _run(cmd, verbose)
         objects.append(obj)
-    tmp = LIB_PATH + ".tmp"
+    tmp = path + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", tmp], verbose)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, path)
 
 
 def _run(cmd: list[str], verbose: bool) -> None:

@@ -99,3 +99,17 @@ def test_stream_lookup_refuses_a_cpu_device():
 
     with pytest.raises(RuntimeError, match="GPU tensor"):
         _lib.stream_of(torch.device("cpu"))
+
+
+def test_bench_read_probe_library_rejects_bad_arguments_without_a_gpu():
+    """bench.py's streaming-read probe library checks its arguments on the host before any launch."""
+    from r2omni_amd.build import BENCH_LIB_PATH
+
+    lib = ctypes.CDLL(BENCH_LIB_PATH)
+    fn = lib.r2o_bench_stream_read
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    assert fn(None, 1024, 64, 8, 1, None) == 1          # no source
+    assert fn(4096, 1000, 64, 8, 1, None) == 1          # not a multiple of 16 bytes
+    assert fn(4096 + 8, 1024, 64, 8, 1, None) == 1      # source not 16-byte aligned
+    assert fn(4096, 1024, 64, 0, 1, None) == 1          # no workgroups
