@@ -248,10 +248,12 @@ def summarize_pmc(directory: str) -> dict:
     return out
 
 
-def summarize_trace(directory: str) -> dict:
+def summarize_trace(directory: str, tail: int = 200) -> dict:
     """Per-dispatch durations of the decode kernels in a rocprofv3 --kernel-trace CSV run, in launch
     order: partial dispatches followed by a combine (layer calls) apart from back-to-back partial-only
-    ones, the combine, and the gap from a partial's end to its combine's start."""
+    ones, the combine, and the gap from a partial's end to its combine's start.  Besides the average
+    over every dispatch, ``tail_avg_us`` averages the last ``tail`` of each kind: the timed calls,
+    after the warm-up calls during which the clocks come up."""
     import csv
     import glob
 
@@ -276,7 +278,8 @@ def summarize_trace(directory: str) -> dict:
             acc["partial_end_to_combine_start"].append(nxt[0] - t1)
         else:
             acc["partial_only"].append(t1 - t0)
-    return {key: {"dispatches": len(v), "avg_us": round(sum(v) / len(v) / 1e3, 3) if v else None}
+    return {key: {"dispatches": len(v), "avg_us": round(sum(v) / len(v) / 1e3, 3) if v else None,
+                  "tail_avg_us": round(sum(v[-tail:]) / len(v[-tail:]) / 1e3, 3) if v else None}
             for key, v in acc.items()}
 
 
