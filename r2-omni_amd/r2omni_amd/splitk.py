@@ -38,6 +38,9 @@ _TILES_PER_ITEM_TARGET = 8
 # this share of the work of the earlier half.  Plans that mix kinds already launch their larger
 # items first and keep an even split (an uneven one measured 1 us slower on the mixed-tier layer).
 _LATE_SHARE = 0.7
+# The share that measured best per key format (single-kind cfg3 plans, nontemporal tile loads): INT4-K
+# 0.8 (layer call 0.55 us shorter than at 0.7), INT2-K 0.7 (0.8 was 0.3-0.5 us longer); BF16-K keeps 0.7.
+_LATE_SHARE_BY_K = {_lib.K_INT4: 0.8}
 
 
 @dataclass
@@ -111,7 +114,7 @@ def _plan(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: int, extra_i
     cap = max(_BLOCKS_PER_CU * cus, n_runs)
     cfg = _lib.PlanConfig(num_cus=cus, blocks_per_cu=_BLOCKS_PER_CU, tiles_per_item=_TILES_PER_ITEM_TARGET,
                           waves_per_item=_WAVES_PER_ITEM, min_tiles_per_item=_MIN_TILES_PER_ITEM,
-                          late_share=_LATE_SHARE)
+                          late_share=_LATE_SHARE_BY_K.get(k_format, _LATE_SHARE))
     for k in (_lib.KIND_FP, _lib.KIND_INT4, _lib.KIND_INT2, _lib.KIND_RECENT):
         cfg.tile_cost[k] = _TILE_COST[k]
     run_arr = (_lib.PlanRun * n_runs)(*[_lib.PlanRun(*r) for r in runs])

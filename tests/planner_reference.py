@@ -11,7 +11,7 @@ import heapq
 import torch
 
 from r2omni_amd import _lib
-from r2omni_amd.splitk import (TILE, _BLOCKS_PER_CU, _LATE_SHARE, _MIN_TILES_PER_ITEM, _TILE_COST,
+from r2omni_amd.splitk import (TILE, _BLOCKS_PER_CU, _LATE_SHARE, _LATE_SHARE_BY_K, _MIN_TILES_PER_ITEM, _TILE_COST,
                                _TILES_PER_ITEM_TARGET, _WAVES_PER_ITEM, _plan_runs)
 
 
@@ -44,7 +44,7 @@ def split_run(nt: int, n_items: int, late_share: float = 1.0):
     return out
 
 
-def python_plan_work_items(caches, hkv: int, num_cus: int, extra_int2: int = 0):
+def python_plan_work_items(caches, hkv: int, num_cus: int, extra_int2: int = 0, k_format: int = _lib.K_INT4):
     """Water-filling of the runs (the most expensive run's items split once more, ties to the earlier
     run, until 2 x CUs items, or about _TILES_PER_ITEM_TARGET tiles per item but at least CUs items),
     partial slots in (request, kv head) order, launch order largest first.  Returns
@@ -71,7 +71,7 @@ def python_plan_work_items(caches, hkv: int, num_cus: int, extra_int2: int = 0):
         total += 1
         heapq.heappush(heap, (-item_cost(i), i))
     uniform = len({r[2] for r in runs if r[2] != _lib.KIND_RECENT}) == 1
-    late_share = _LATE_SHARE if uniform and total > cus else 1.0
+    late_share = _LATE_SHARE_BY_K.get(k_format, _LATE_SHARE) if uniform and total > cus else 1.0
     items = []
     begins = [0]
     group = (0, 0)

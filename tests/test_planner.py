@@ -75,9 +75,10 @@ def test_split_run_covers_the_run_with_wave_shares(nt, n_items, share):
 
 def test_single_kind_plans_give_the_later_launched_half_less_work():
     """Two workgroups share a CU (launch slots j and j + CUs) and the earlier one runs ahead: an
-    all-INT2 plan that fills both slots gives the later-launched half about _LATE_SHARE of the
+    all-INT2 plan that fills both slots gives the later-launched half about the late share of the
     work, a mixed plan keeps equal items per run, and a plan within one slot per CU is even."""
-    from r2omni_amd.splitk import _LATE_SHARE
+    from r2omni_amd.splitk import _LATE_SHARE, _LATE_SHARE_BY_K
+    share = _LATE_SHARE_BY_K.get(_lib.K_INT4, _LATE_SHARE)  # plan_work_items plans INT4-K caches
     cus = 256
     uniform = [_fake_cache(0, 0, 131072)]
     items = plan_work_items(uniform, 8, cus)[0].tolist()
@@ -86,7 +87,7 @@ def test_single_kind_plans_give_the_later_launched_half_less_work():
     early = [it[4] for it in seg if items.index(it) < cus]
     late = [it[4] for it in seg if items.index(it) >= cus]
     ratio = (sum(late) / len(late)) / (sum(early) / len(early))
-    assert abs(ratio - _LATE_SHARE) < 0.06
+    assert abs(ratio - share) < 0.06
     mixed = [_fake_cache(8192, 24576, 32768), _fake_cache(2048, 6144, 8192)]
     items = plan_work_items(mixed, 4, cus)[0].tolist()
     for r in range(2):
