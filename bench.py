@@ -11,7 +11,8 @@ Reported: ``value`` = algorithmic GB/s of a layer call, ``ms_per_step`` = time p
 ``roofline`` for the dominant partial kernel (its average duration from HIP events on its
 stream), ``cpu_baseline`` = the reference's CPU dequantise+attention path (restated in torch) on
 the same packed data, ``hbm_copy`` / ``hbm_read`` = the box's measured device copy and streaming-read
-rates, and ``e2e`` = the rest of the metric: configuration 4's decode tok/s (a random-init 28-layer
+rates, ``dma_floor`` = the time a compute-free kernel of the partial kernel's launch shape and DMA pattern
+takes to move the call's bytes, and ``e2e`` = the rest of the metric: configuration 4's decode tok/s (a random-init 28-layer
 Qwen2.5-Omni-7B decoder, batch 8 x 32k, 128 greedy steps on this path).  Other modes (--prefill, --decode-steps, --sweep, --e2e)
 print their own line instead.
 """
@@ -196,6 +197,43 @@ def read_bandwidth(dev, mib: int = 2048, reps: int = 20, blocks: int = 8192) -> 
     return {"GBs": round(gbs, 1), "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes_per_read": nbytes,
             "method": f"one streaming read of {mib} MiB (16-byte nontemporal loads, {blocks} workgroups, nothing "
                       f"written), bytes / time, median of {reps} HIP-event timings"}
+
+
+def dma_floor(dev, nbytes: int, *, steps: int = 200, warmup: int = 300, blocks: int = 512, tile_kb: int = 4) -> dict:
+    """What moving ``nbytes`` costs at the partial kernel's launch shape with no compute:
+    ``r2o_bench_dma_read`` (512 blocks of 4 waves, two per CU, each wave streaming its own contiguous
+    run of ``tile_kb`` KiB tiles by nontemporal global->LDS DMA, one tile in flight), back-to-back
+    launches rotating over 8 buffers (so the bytes come from HBM), timed like the layer calls."""
+    import torch
+
+    from r2omni_amd.build import BENCH_LIB_PATH
+
+    lib = ctypes.CDLL(BENCH_LIB_PATH)
+    lib.r2o_bench_dma_read.restype = ctypes.c_int
+    lib.r2o_bench_dma_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                       ctypes.c_void_p]
+    nb = nbytes // (tile_kb * 1024) * (tile_kb * 1024)
+    bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(8)]
+    sink = torch.zeros(blocks, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def one(i):
+        rc = lib.r2o_bench_dma_read(bufs[i % 8].data_ptr(), nb, sink.data_ptr(), blocks, tile_kb, stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"r2o_bench_dma_read failed ({rc})")
+
+    _clock_warmup(dev)
+    for i in range(warmup):
+        one(i)
+    ms = _time_events(one, steps, stream)
+    del bufs, sink
+    torch.cuda.empty_cache()
+    gbs = nb / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 3), "GBs": round(gbs, 1), "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+            "bytes": nb, "method": f"the partial kernel's launch shape without compute: {blocks} blocks x 4 waves "
+                                   f"(2 per CU), each wave streaming its own run of {tile_kb} KiB tiles by "
+                                   f"nontemporal global->LDS DMA, one tile in flight; {steps} back-to-back launches "
+                                   f"over 8 rotated buffers, HIP events"}
 
 
 def copy_bandwidth(dev, mib: int = 1024, reps: int = 20) -> dict:
@@ -741,6 +779,104 @@ def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed
             "n_items": layers[0][2].n_items}
 
 
+def timeline_bench(cfg, dev, *, n_layers: int, warmup: int, trials: int = 3) -> dict:
+    """Phase breakdown of the layer call from the measurement build (libr2o_timeline.so, the decode
+    library compiled with -DR2O_TIMELINE: every wave keeps real-time counter stamps in registers and
+    stores them at its end).  After the warm-up, ``trials`` times: 200 back-to-back layer calls, then
+    the stamps of the last call are read.  Times in microseconds; each entry lists the 0/10/50/90/100th
+    percentiles over work items (partial kernel) or blocks (combine), median over the trials."""
+    import numpy as np
+    import torch
+
+    from r2omni_amd import _lib
+
+    lib = _lib.load()
+    if not hasattr(lib, "r2o_timeline_read"):
+        raise RuntimeError(f"{_lib.LIB_PATH} has no phase stamps: run bench.py --timeline (it loads libr2o_timeline.so)")
+    lib.r2o_timeline_read.restype = ctypes.c_int
+    lib.r2o_timeline_read.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+    r = time_decode_layers(cfg, dev, n_layers=n_layers, steps=200, warmup=warmup)
+    layers, n = r["layers"], r["n_items"]
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    params = [ex._params(q, ex.workspace.output, None) for _, q, ex in layers]
+    n_comb = len(cfg.lengths) * cfg.hq  # combine blocks: one per (request, query head) without an append
+    pct = (0, 10, 50, 90, 100)
+
+    def q(v):
+        v = np.asarray(v, dtype=np.float64)
+        v = v[np.isfinite(v)]
+        return [round(float(x), 2) for x in np.percentile(v, pct)] if v.size else None
+
+    runs = []
+    for _ in range(trials):
+        with _gc_paused():
+            for i in range(200):
+                pp = ctypes.byref(params[i % len(params)])
+                lib.r2o_decode_partial(pp, sp)
+                lib.r2o_decode_combine(pp, sp)
+        torch.cuda.synchronize()
+        a = np.zeros(4096 * 4 * 12, dtype=np.uint64)
+        c = np.zeros(4096 * 8 * 12, dtype=np.uint64)
+        _lib.check(lib.r2o_timeline_read(0, a.ctypes.data, a.nbytes), "r2o_timeline_read")
+        _lib.check(lib.r2o_timeline_read(1, c.ctypes.data, c.nbytes), "r2o_timeline_read")
+        a = a.reshape(4096, 4, 12)[:n].astype(np.int64)
+        c = c.reshape(4096, 8, 12)[:n_comb].astype(np.int64)
+        t0 = a[:, :, 0].min()
+        kind = a[:, 0, 8] >> 32
+        tiles = a[:, 0, 8] & 0xFFFFFFFF
+
+        def at(x, j):  # stamp j in us from the first entry; NaN where a wave took no such step
+            return np.where(x[..., j] > 0, (x[..., j] - t0) / 100.0, np.nan)
+
+        seg = kind != 3
+        loop_end = np.nanmax(at(a, 5), 1)
+        block_end = at(a[:, 0], 6)
+        last = float(np.nanmax(block_end))
+        res = {
+            "work_item_arrival": q(at(a[:, 0], 1)),
+            "first_dma_after_item": q(np.nanmin(at(a[seg], 2), 1) - at(a[seg, 0], 1)),
+            "first_tile_after_dma": q(np.nanmin(at(a[seg], 3), 1) - np.nanmin(at(a[seg], 2), 1)),
+            "first_tile": q(np.nanmin(at(a[seg], 3), 1)),
+            "wave_loop_end_spread": q(np.nanmax(at(a, 5), 1) - np.nanmin(at(a, 5), 1)),
+            "epilogue": q(block_end - loop_end),
+            "block_end": q(block_end),
+            "xcc_blocks": np.bincount(a[:, 0, 7] & 0xF, minlength=8).tolist(),
+        }
+        for k, name in ((0, "bf16_v"), (1, "int4_v"), (2, "int2_v"), (3, "recent")):
+            m = kind == k
+            if not m.any():
+                continue
+            d = {"items": int(m.sum()), "block_end": q(block_end[m])}
+            if k != 3:
+                per_wave = np.ceil(tiles[m] / 4.0)
+                d["us_per_tile"] = q((np.nanmax(at(a[m], 4), 1) - np.nanmin(at(a[m], 3), 1)) / np.maximum(per_wave - 1, 1))
+            res[f"kind_{name}"] = d
+        res["combine"] = {
+            "blocks": n_comb,
+            "start_after_partial_end": q(np.nanmin(at(c, 0), 1) - last),
+            "arguments": q(np.nanmax(at(c, 1) - at(c, 0), 1)),
+            "first_partials": q(np.nanmax(at(c, 2) - at(c, 1), 1)),
+            "merge": q(np.nanmax(at(c, 3) - at(c, 2), 1)),
+            "tail": q(at(c[:, 0], 4) - np.nanmax(at(c, 3), 1)),
+            "end_after_partial_end": q(at(c[:, 0], 4) - last),
+        }
+        res["partial_last_block_end"] = round(last, 2)
+        runs.append(res)
+
+    def med(objs):
+        if isinstance(objs[0], dict):
+            return {k: med([o[k] for o in objs]) for k in objs[0]}
+        if isinstance(objs[0], list):
+            return [round(float(np.median([o[i] for o in objs])), 2) for i in range(len(objs[0]))]
+        return objs[len(objs) // 2]
+
+    return {"metric": "layer-call phase timeline (us; 0/10/50/90/100th percentiles, median of trials)",
+            "config": cfg.name, "work_items": n, "us_call": round(r["ms_step"] * 1e3, 3),
+            "us_partial": round(r["ms_partial"] * 1e3, 3), "trials": trials, "timeline": med(runs),
+            "note": "measurement build (-DR2O_TIMELINE): the product kernels with real-time stamps kept in registers"}
+
+
 def context_sweep(cfg, dev, *, factors, n_layers: int, steps: int, warmup: int) -> dict:
     """The layer call of ``cfg`` at context lengths scaled by ``factors`` (the recent window kept at
     128, the history rounded to whole pages), and a least-squares fit time = fixed + bytes / rate of
@@ -805,6 +941,10 @@ def main() -> int:
     ap.add_argument("--e2e-context", type=int, default=32768)
     ap.add_argument("--e2e-steps", type=int, default=128)
     ap.add_argument("--e2e-layers", type=int, default=28)
+    ap.add_argument("--timeline", action="store_true",
+                    help="only print the phase breakdown of the layer call of --config (work-item start-up, "
+                         "first tile, per-kind tile times, epilogue, combine phases) from libr2o_timeline.so, "
+                         "the decode library built with per-wave real-time stamps")
     ap.add_argument("--summarize-pmc", metavar="DIR",
                     help="only print the mean per-dispatch value of every counter in a rocprofv3 --pmc CSV "
                          "output directory, per decode kernel (and the calibration copy kernel)")
@@ -823,6 +963,9 @@ def main() -> int:
                                    "shards by (request, kv head) or token range across GPUs by design, "
                                    "but no multi-GPU run is implemented)"}))
         return 2
+
+    if args.timeline:  # before the package is imported: it binds the library named here
+        os.environ["R2O_SSPA_LIB"] = os.path.join(ROOT, "r2-omni_amd", "r2omni_amd", "libr2o_timeline.so")
 
     import torch
 
@@ -851,6 +994,9 @@ def main() -> int:
     if args.decode_steps:
         print(json.dumps(decode_steps_bench(cfg, args.config, dev, args.decode_steps, args.layers)), flush=True)
         return 0
+    if args.timeline:
+        print(json.dumps(timeline_bench(cfg, dev, n_layers=args.layers, warmup=args.warmup)), flush=True)
+        return 0
     if args.sweep:
         factors = [float(f) for f in args.sweep.split(",")]
         print(json.dumps(context_sweep(cfg, dev, factors=factors, n_layers=args.layers, steps=args.steps,
@@ -877,6 +1023,9 @@ def main() -> int:
     copy["partial_kernel_pct_of_copy"] = round(100 * part_gbs / copy["GBs"], 1)
     read = read_bandwidth(dev)
     read["partial_kernel_pct_of_read"] = round(100 * part_gbs / read["GBs"], 1)
+    _log("dma floor at the call's bytes ...")
+    floor = dma_floor(dev, nbytes)
+    floor["partial_kernel_pct_of_floor"] = round(100 * floor["us"] / (ms_partial * 1e3), 1)
     e2e = None
     if not args.no_e2e:
         _log("e2e (configuration 4) ...")
@@ -910,6 +1059,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "hbm_copy": copy,
         "hbm_read": read,
+        "dma_floor": floor,
         "e2e": e2e,
     }
     print(json.dumps(line), flush=True)

@@ -81,6 +81,34 @@ struct KernelCfg {
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
 
+// Phase stamps of the measurement build (-DR2O_TIMELINE, libr2o_timeline.so, bench.py --timeline): each
+// wave keeps real-time counter reads (100 MHz, one clock for the whole GPU) in registers and stores
+// them once at its end.  In the product build the struct is empty and every stamp compiles to nothing.
+struct Stamps {
+#ifdef R2O_TIMELINE
+    unsigned long long t[12];
+#endif
+};
+__device__ __forceinline__ void stamp(Stamps& s, int i) {
+#ifdef R2O_TIMELINE
+    s.t[i] = __builtin_amdgcn_s_memrealtime();
+#endif
+}
+#ifdef R2O_TIMELINE
+// partial kernel: per (block, wave) 12 slots: 0 entry, 1 work item arrived, 2 first DMA issued, 3 first
+// tile landed, 4 last tile landed, 5 tile loop done, 6 block done (partial stores issued), 7 XCC id |
+// HW_ID << 32, 8 tiles | kind << 32.  combine: per (block, wave) 12 slots: 0 entry, 1 arguments
+// arrived, 2 first round of partials landed, 3 merged, 4 (wave 0) output stored.
+constexpr int kTimelineBlocks = 4096;
+__device__ unsigned long long g_timeline_partial[kTimelineBlocks * 4 * 12];
+__device__ unsigned long long g_timeline_combine[kTimelineBlocks * 8 * 12];
+__device__ __forceinline__ void stamps_store(unsigned long long* dst, int block, int wave, int waves, const Stamps& s) {
+    if ((threadIdx.x & 63) == 0 && block < kTimelineBlocks)
+#pragma unroll
+        for (int k = 0; k < 12; ++k) dst[((int64_t)block * waves + wave) * 12 + k] = s.t[k];
+}
+#endif
+
 // Lane's 8 tokens of a 32-token tile, in MFMA K order: tokens 4g..4g+3 then 16+4g..16+4g+3.
 __device__ __forceinline__ int tile_token(int g, int k) { return (k < 4) ? 4 * g + k : 16 + 4 * g + (k - 4); }
 
@@ -674,7 +702,7 @@ __device__ __forceinline__ void touch_combine_kernarg(const r2o_decode_params& p
 
 template <int KIND, int KF, bool TS, int RF>
 __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
-                            unsigned char* smem, WaveState& st) {
+                            unsigned char* smem, WaveState& st, Stamps& ts) {
     using Cfg = KernelCfg<KF>;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
@@ -731,6 +759,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
 #pragma unroll
     for (int j = 0; j < kDmaStages; ++j)
         if (j < n) dma_tile<KIND, KF>(c, a_first + 32 * j, ring + j * Cfg::kStage, lane, true);
+    stamp(ts, 2);
 
     const VConst vc = make_vconst();
     const float qscale = p.sm_scale * kLog2e;
@@ -743,6 +772,8 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     for (int i = 0; i < n; ++i) {
         wait_tiles<StageLayout<KIND, KF>::kDma>(min(kDmaStages, n - i) - 1);  // tile i has landed
         __builtin_amdgcn_wave_barrier();
+        if (i == 0) stamp(ts, 3);
+        if (i == n - 1) stamp(ts, 4);
         unsigned char* stage = ring + (i % kDmaStages) * Cfg::kStage;
         TileRegs<KIND, KF> cur;
         read_tile<KIND, KF, TS>(stage, l16, g, gamma, c.groups, cur);
@@ -850,7 +881,19 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
 template <int KF, int RF>
 __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
     __shared__ __align__(16) unsigned char smem[KernelCfg<KF>::kSmem];
+    Stamps ts{};
+    stamp(ts, 0);
     const r2o_work_item it = p.items[blockIdx.x];
+#ifdef R2O_TIMELINE
+    {
+        const int64_t kind0 = it.kind;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::"s"(kind0) : "memory");
+        stamp(ts, 1);
+        ts.t[7] = (unsigned long long)__builtin_amdgcn_s_getreg((3 << 11) | 20) |          // XCC_ID
+                  ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4) << 32);   // HW_ID
+        ts.t[8] = (unsigned long long)(uint32_t)it.ntiles | ((unsigned long long)(uint32_t)it.kind << 32);
+    }
+#endif
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = __builtin_amdgcn_readfirstlane(r2o_div_small((int)p.hq, (int)p.hkv));
@@ -862,11 +905,11 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP, KF, false, RF>(p, it, smem, st); break;
-        case kI4: run_segment<kI4, KF, false, RF>(p, it, smem, st); break;
+        case kFP: run_segment<kFP, KF, false, RF>(p, it, smem, st, ts); break;
+        case kI4: run_segment<kI4, KF, false, RF>(p, it, smem, st, ts); break;
         case kI2:  // INT2 values: one scale and zero point per token when a group spans all 128 dims
-            if (p.int2_group == 128) run_segment<kI2, KF, true, RF>(p, it, smem, st);
-            else run_segment<kI2, KF, false, RF>(p, it, smem, st);
+            if (p.int2_group == 128) run_segment<kI2, KF, true, RF>(p, it, smem, st, ts);
+            else run_segment<kI2, KF, false, RF>(p, it, smem, st, ts);
             break;
         default: run_recent<RF>(p, it, st); break;
     }
@@ -875,6 +918,7 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     float l_h = st.l;
     l_h = r2o_sum_lane_pair<16>(l_h);
     l_h = r2o_sum_lane_pair<32>(l_h);
+    stamp(ts, 5);
     __syncthreads();  // every wave is done with its staging area
     float* mrg = reinterpret_cast<float*>(smem) + wave * kMergeFloats;
     if (g == 0) {
@@ -924,6 +968,10 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
             p.partial_sum[slot] = L;
         }
     }
+    stamp(ts, 6);
+#ifdef R2O_TIMELINE
+    stamps_store(g_timeline_partial, blockIdx.x, wave, 4, ts);
+#endif
 }
 
 // Fused Recent-FP append (triton_fourq_splitk.py:1007-1020) of every KV head of request b, by one
@@ -1011,11 +1059,17 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
     const int g = blockIdx.y;   // group: request g / hkv, KV head g % hkv
     const int h = blockIdx.x;   // query head within the group
     const int tid = threadIdx.x, lane = tid & 31, slice = tid >> 5;
+    Stamps ts{};
+    stamp(ts, 0);
     // the inline range of this group (a clamped index keeps the read inside the arguments for any
     // group; it is used only when g < ca.n_groups)
     const int gi = min(g, kInlineGroups - 1);
     const int inline_beg = ca.begin[gi], inline_end = ca.begin[gi + 1];
     touch_combine_kernarg(p, ca, inline_beg, inline_end);
+#ifdef R2O_TIMELINE
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+    stamp(ts, 1);
     if (h == ca.gqa) {  // the extra block of a fused append: request g / hkv, on its KV head 0 group
         const int hkv = (int)p.hkv;
         const int b = __builtin_amdgcn_readfirstlane(r2o_div_small(g, hkv));
@@ -1047,6 +1101,10 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
             aa[k] = r2o_ldg(reinterpret_cast<const r2o_f4*>(p.partial_out + slot * 128) + lane);
         }
         float mn = m;
+#ifdef R2O_TIMELINE
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (base == beg + slice) stamp(ts, 2);
+#endif
 #pragma unroll
         for (int k = 0; k < kCombineUnroll; ++k) {
             if (base + k * kCombineSlices >= end) mm[k] = -INFINITY;
@@ -1083,6 +1141,10 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
         acc = a0;
     }
     const int wave = tid >> 6;
+    stamp(ts, 3);
+#ifdef R2O_TIMELINE
+    if (wave != 0) stamps_store(g_timeline_combine, g * gridDim.x + h, wave, 8, ts);
+#endif
     if ((tid & 32) == 0) {  // lanes 0..31 of each wave
         reinterpret_cast<r2o_f4*>(sl_a[wave])[lane] = acc;
         if (lane == 0) {
@@ -1112,6 +1174,10 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(r2o_decode_params p
     uint16_t* orow = p.out + ((int64_t)g * ca.gqa + h) * 128;
     orow[tid] = (uint16_t)r2o_f32_to_bf16(y0);
     orow[tid + 64] = (uint16_t)r2o_f32_to_bf16(y1);
+    stamp(ts, 4);
+#ifdef R2O_TIMELINE
+    stamps_store(g_timeline_combine, g * gridDim.x + h, 0, 8, ts);
+#endif
 }
 
 int validate(const r2o_decode_params* p) {
@@ -1232,5 +1298,18 @@ int r2o_decode_noalloc(const r2o_decode_params* params, void* stream) {
     if (lrc) return lrc;
     return launch_combine(p, (hipStream_t)stream);
 }
+
+#ifdef R2O_TIMELINE
+// Measurement build only: copies the last launch's phase stamps to the host (which 0: partial kernel,
+// [4096 blocks][4 waves][12]; 1: combine, [4096 blocks][8 waves][12]; u64 each).
+int r2o_timeline_read(int which, void* dst, size_t bytes) {
+    if (!dst || (which != 0 && which != 1)) return R2O_EINVAL;
+    const size_t cap = which == 0 ? sizeof(g_timeline_partial) : sizeof(g_timeline_combine);
+    if (bytes > cap) return R2O_EINVAL;
+    const hipError_t e = which == 0 ? hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_timeline_partial), bytes, 0, hipMemcpyDeviceToHost)
+                                    : hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_timeline_combine), bytes, 0, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? R2O_OK : R2O_ELAUNCH;
+}
+#endif
 
 }  // extern "C"

@@ -23,6 +23,8 @@ SOURCES = ("r2o_decode.hip", "r2o_pack.hip", "r2o_rope.hip", "r2o_plan.cpp")  # 
 # bench.py's streaming-read probe, a library of its own (not part of the decode C-ABI)
 BENCH_LIB_PATH = os.path.join(PKG_DIR, "libr2o_bench.so")
 BENCH_SOURCES = ("bench_read.hip",)
+# the same decode library built with per-wave phase stamps (-DR2O_TIMELINE), for bench.py --timeline only
+TIMELINE_LIB_PATH = os.path.join(PKG_DIR, "libr2o_timeline.so")
 ARCH = "gfx950"
 
 
@@ -48,21 +50,29 @@ def common_flags() -> list[str]:
 
 
 def build_library(verbose: bool = False) -> str:
-    """Compile every source and link ``libr2o_sspa.so`` (and bench.py's ``libr2o_bench.so``) next to
-    this file; returns the decode library's path."""
+    """Compile every source and link ``libr2o_sspa.so`` (and bench.py's ``libr2o_bench.so`` and
+    ``libr2o_timeline.so``) next to this file; returns the decode library's path."""
     _link(SOURCES, LIB_PATH, verbose)
     _link(BENCH_SOURCES, BENCH_LIB_PATH, verbose)
+    _link(SOURCES, TIMELINE_LIB_PATH, verbose, defines=("R2O_TIMELINE",), rebuild=("r2o_decode.hip",))
     return LIB_PATH
 
 
-def _link(sources, path: str, verbose: bool) -> None:
+def _link(sources, path: str, verbose: bool, defines=(), rebuild=None) -> None:
+    """Compile ``sources`` (only those in ``rebuild`` when given, reusing the other objects of the
+    plain build) with ``defines`` and link them into ``path``."""
     hipcc = _hipcc()
     build_dir = os.path.join(ROOT_DIR, "_build")
     os.makedirs(build_dir, exist_ok=True)
+    suffix = "".join("_" + d.lower() for d in defines)
     objects = []
     for src in sources:
-        obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
-        cmd = [hipcc, *common_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+        stem = os.path.splitext(src)[0]
+        if rebuild is not None and src not in rebuild:
+            objects.append(os.path.join(build_dir, stem + ".o"))
+            continue
+        obj = os.path.join(build_dir, stem + suffix + ".o")
+        cmd = [hipcc, *common_flags(), *[f"-D{d}" for d in defines], "-c", os.path.join(CSRC, src), "-o", obj]
         _run(cmd, verbose)
         objects.append(obj)
     tmp = path + ".tmp"

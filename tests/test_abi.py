@@ -113,3 +113,19 @@ def test_bench_read_probe_library_rejects_bad_arguments_without_a_gpu():
     assert fn(4096, 1000, 64, 8, 1, None) == 1          # not a multiple of 16 bytes
     assert fn(4096 + 8, 1024, 64, 8, 1, None) == 1      # source not 16-byte aligned
     assert fn(4096, 1024, 64, 0, 1, None) == 1          # no workgroups
+
+
+def test_bench_dma_read_probe_rejects_bad_arguments_without_a_gpu():
+    """bench.py's DMA read-floor probe checks its arguments on the host before any launch."""
+    from r2omni_amd.build import BENCH_LIB_PATH
+
+    lib = ctypes.CDLL(BENCH_LIB_PATH)
+    fn = lib.r2o_bench_dma_read
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    assert fn(None, 8192, 64, 8, 4, None) == 1          # no source
+    assert fn(4096 + 8, 8192, 64, 8, 4, None) == 1      # source not 16-byte aligned
+    assert fn(4096, 8192, 64, 0, 4, None) == 1          # no workgroups
+    assert fn(4096, 8192, 64, 8, 2, None) == 1          # tile size other than 4 or 8 KiB
+    assert fn(4096, 2048, 64, 8, 4, None) == 1          # less than one tile
+    assert fn(4096, 8192, None, 8, 4, None) == 1        # no sink
