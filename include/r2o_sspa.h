@@ -94,7 +94,9 @@ typedef struct r2o_work_item {
     const void* v_scale;         /* INT4-V f32 / INT2-V fp16 scales of the head, or NULL          */
     const uint8_t* v_zero;       /* INT2-V zero points of the head, or NULL                       */
     const int32_t* ring_length;  /* Recent-FP items: the request's device ring length, or NULL    */
-    int64_t reserved;            /* 0                                                             */
+    int64_t v_group;             /* INT2-V items: the V group size (32, 64 or 128), so the kernel's */
+                                 /* start-up needs no launch argument beyond the first two lines;  */
+                                 /* 0 for the other kinds (the planner fills it)                   */
 } r2o_work_item;
 
 /* One run of the planner's input: the 32-token tiles of one pool segment of one (request, kv head)

@@ -721,7 +721,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     c.hi = (int)it.hi;
     c.vdelta = (int)it.v_delta;
     c.sb_shift = p.superblock == 32 ? 5 : (p.superblock == 64 ? 6 : 7);
-    const int g_shift = p.int2_group == 32 ? 5 : (p.int2_group == 64 ? 6 : 7);
+    const int g_shift = it.v_group == 32 ? 5 : (it.v_group == 64 ? 6 : 7);  // INT2-V only
     c.groups = 128 >> g_shift;
     const int gamma = (8 * l16) >> g_shift;
     c.vrows = reinterpret_cast<const uint8_t*>(it.v_base);
@@ -908,7 +908,7 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
         case kFP: run_segment<kFP, KF, false, RF>(p, it, smem, st, ts); break;
         case kI4: run_segment<kI4, KF, false, RF>(p, it, smem, st, ts); break;
         case kI2:  // INT2 values: one scale and zero point per token when a group spans all 128 dims
-            if (p.int2_group == 128) run_segment<kI2, KF, true, RF>(p, it, smem, st, ts);
+            if (it.v_group == 128) run_segment<kI2, KF, true, RF>(p, it, smem, st, ts);
             else run_segment<kI2, KF, false, RF>(p, it, smem, st, ts);
             break;
         default: run_recent<RF>(p, it, st); break;

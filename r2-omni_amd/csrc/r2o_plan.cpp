@@ -155,6 +155,7 @@ extern "C" int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, con
             it.v_base = d.i4_v + h * d.i4_stride * 64;
             it.v_scale = d.i4_scale + h * d.i4_stride;
         } else {
+            it.v_group = int2_group;
             it.v_base = d.i2_v + h * d.i2_stride * 32;
             it.v_scale = d.i2_scale + h * d.i2_stride * groups;
             it.v_zero = d.i2_zero + h * d.i2_stride * groups;

@@ -68,7 +68,7 @@ REQUEST_FIELDS = (
 )
 # r2o_work_item: 16 eight-byte words.
 ITEM_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta", "slot",
-               "k_base", "k_ops", "v_base", "v_scale", "v_zero", "ring_length", "reserved")
+               "k_base", "k_ops", "v_base", "v_scale", "v_zero", "ring_length", "v_group")
 WORK_FIELDS = ("req", "kvh", "kind", "tile0", "ntiles", "lo", "hi", "v_delta", "slot")
 KIND_FP, KIND_INT4, KIND_INT2, KIND_RECENT = 0, 1, 2, 3
 # r2o_decode_params.k_format: how the request descriptors' k_* fields hold the history keys

@@ -122,7 +122,8 @@ def test_native_plan_equals_the_python_restatement(seed):
 @pytest.mark.parametrize("k_format,group", [(_lib.K_INT4, 32), (_lib.K_INT2, 128), (_lib.K_BF16, 64)])
 def test_native_plan_fills_each_items_base_pointers(k_format, group):
     """With the host request descriptors the planner writes each item's base pointers: the per-head
-    offsets into the request's K arena, K operand blocks, V pool, V scales and zeros, or its ring."""
+    offsets into the request's K arena, K operand blocks, V pool, V scales and zeros, or its ring; and
+    INT2-V items carry the V group size."""
     from planner_reference import item_pointers
 
     import torch
@@ -144,4 +145,4 @@ def test_native_plan_fills_each_items_base_pointers(k_format, group):
     items, _ = _plan(caches, hkv, 64, reqs=reqs, k_format=k_format, int2_group=group)
     for it in items.tolist():
         assert it[9:15] == item_pointers(words[it[0]], k_format, it[2], it[1], 128 // group)
-        assert it[15] == 0
+        assert it[15] == (group if it[2] == _lib.KIND_INT2 else 0)  # v_group: INT2-V items carry the group size
