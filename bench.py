@@ -11,7 +11,8 @@ Reported: ``value`` = algorithmic GB/s of a layer call, ``ms_per_step`` = time p
 ``roofline`` for the dominant partial kernel (its average duration from HIP events on its
 stream), ``cpu_baseline`` = the reference's CPU dequantise+attention path (restated in torch) on
 the same packed data, ``hbm_copy`` / ``hbm_read`` = the box's measured device copy and streaming-read
-rates, ``dma_floor`` = the time a compute-free kernel of the partial kernel's launch shape and DMA pattern
+rates, ``drop_in_call`` = the same call through the Python drop-in ``SplitKExecutor.__call__``,
+``dma_floor`` = the time a compute-free kernel of the partial kernel's launch shape and DMA pattern
 takes to move the call's bytes, and ``e2e`` = the rest of the metric: configuration 4's decode tok/s (a random-init 28-layer
 Qwen2.5-Omni-7B decoder, batch 8 x 32k, 128 greedy steps on this path).  Other modes (--prefill, --decode-steps, --sweep, --e2e)
 print their own line instead.
@@ -770,13 +771,18 @@ def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed
     def partial_only(i):
         lib.r2o_decode_partial(ctypes.byref(params[i % n_rot]), sp)
 
+    def drop_in(i):  # the manager's entry: SplitKExecutor.__call__ (checks, arguments, two launches)
+        _, q, ex = layers[i % n_rot]
+        ex(q)
+
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     ms_step = _time_events(step, steps, stream)
     ms_partial = _time_events(partial_only, steps, stream)
+    ms_drop_in = _time_events(drop_in, steps, stream)
     return {"layers": layers, "bytes": nbytes, "ms_step": ms_step, "ms_partial": ms_partial,
-            "n_items": layers[0][2].n_items}
+            "ms_drop_in": ms_drop_in, "n_items": layers[0][2].n_items}
 
 
 def timeline_bench(cfg, dev, *, n_layers: int, warmup: int, trials: int = 3) -> dict:
@@ -1006,7 +1012,7 @@ def main() -> int:
     t0 = time.perf_counter()
     r = time_decode_layers(cfg, dev, n_layers=args.layers, steps=args.steps, warmup=args.warmup)
     wall = time.perf_counter() - t0
-    nbytes, ms_step, ms_partial = r["bytes"], r["ms_step"], r["ms_partial"]
+    nbytes, ms_step, ms_partial, ms_drop_in = r["bytes"], r["ms_step"], r["ms_partial"], r["ms_drop_in"]
     gbs = nbytes / (ms_step * 1e-3) / 1e9
     part_gbs = nbytes / (ms_partial * 1e-3) / 1e9
     _log(f"step {ms_step * 1e3:.2f} us ({gbs:.0f} GB/s), partial {ms_partial * 1e3:.2f} us ({part_gbs:.0f} GB/s), "
@@ -1056,6 +1062,9 @@ def main() -> int:
                      "traffic_source": traffic_src,
                      "kernel": "decode_partial_kernel", "avg_us": round(ms_partial * 1e3, 3),
                      "avg_us_source": "HIP events over back-to-back partial launches on the launch stream"},
+        "drop_in_call": {"us": round(ms_drop_in * 1e3, 3), "GBs": round(nbytes / (ms_drop_in * 1e-3) / 1e9, 1),
+                         "method": "the same layer calls through SplitKExecutor.__call__ (the Python drop-in the "
+                                   "manager calls: checks, launch arguments, the two launches), HIP events"},
         "cpu_baseline": cpu,
         "hbm_copy": copy,
         "hbm_read": read,
