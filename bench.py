@@ -12,6 +12,7 @@ Reported: ``value`` = algorithmic GB/s of a layer call, ``ms_per_step`` = time p
 stream), ``cpu_baseline`` = the reference's CPU dequantise+attention path (restated in torch) on
 the same packed data, ``hbm_copy`` / ``hbm_read`` = the box's measured device copy and streaming-read
 rates, ``drop_in_call`` = the same call through the Python drop-in ``SplitKExecutor.__call__``,
+``graph_call`` = the same calls replayed from a HIP graph (no host launch cost),
 ``dma_floor`` = the time a compute-free kernel of the partial kernel's launch shape and DMA pattern
 takes to move the call's bytes, and ``e2e`` = the rest of the metric: configuration 4's decode tok/s (a random-init 28-layer
 Qwen2.5-Omni-7B decoder, batch 8 x 32k, 128 greedy steps on this path).  Other modes (--prefill, --decode-steps, --sweep, --e2e)
@@ -375,6 +376,53 @@ def prefill_bench(cfg, config_id: int, dev) -> dict:
             "tokens": hist, "hkv": cfg.hkv, "us_per_build": round(ms * 1e3, 1),
             "GBs": round((read + written) / (ms * 1e-3) / 1e9, 1), "bytes_read": read, "bytes_written": written,
             "note": "one call of build_three_precision_cache on resident bf16 K/V, host launch gaps included"}
+
+
+def flush_bench(cfg, config_id: int, dev, flushes: int = 8) -> dict:
+    """The flush of a full Recent-FP ring (its oldest 128 tokens quantised and packed into the compact
+    K arena and the INT2-V arena, metadata appended, the ring shifted: ``flush_full_recent_pool``) on the
+    longest request of the configuration, one layer.  Between timed flushes 128 single-token appends
+    refill the ring (untimed).  GPU time from HIP events around the flush's launches; host time from the
+    wall clock of the call."""
+    import torch
+
+    from r2omni_amd.cache import DynamicCacheStats, append_generated_token, flush_full_recent_pool
+    from r2omni_amd.workloads import build_request_cache, make_request
+
+    total = max(cfg.lengths)
+    data = make_request(cfg, total, seed=11, device=dev)
+    cache = build_request_cache(cfg, data, append_capacity=(flushes + 2) * 128 + 128)
+    hist = int(data.key.shape[1]) + cfg.recent
+    stats = DynamicCacheStats()
+    gen = torch.Generator(device=dev).manual_seed(3)
+    h = cfg.hkv
+    stream = torch.cuda.current_stream(dev)
+    gpu, host = [], []
+    pos = hist
+    for k in range(flushes + 1):
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        t0 = time.perf_counter()
+        if not flush_full_recent_pool(cache, stats):
+            raise RuntimeError("the Recent-FP ring was not full")
+        t1 = time.perf_counter()
+        b.record(stream)
+        b.synchronize()
+        if k:  # the first flush warms the allocator and the code paths
+            gpu.append(a.elapsed_time(b) * 1e3)
+            host.append((t1 - t0) * 1e6)
+        for _ in range(int(cache.recent_fp_pool.capacity)):  # refill the ring (untimed)
+            nk = torch.randn((h, 1, 128), generator=gen, device=dev).to(data.key.dtype)
+            nv = torch.randn((h, 1, 128), generator=gen, device=dev).to(data.key.dtype)
+            append_generated_token(cache, nk, nv, global_token_index=pos, logical_position=pos, stats=stats)
+            pos += 1
+    med = lambda v: round(sorted(v)[len(v) // 2], 2)  # noqa: E731
+    return {"metric": "Recent-FP flush (128 tokens -> compact K + INT2-V, ring shift), one layer",
+            "config": f"cfg{config_id} {cfg.name}", "k_format": cfg.variant, "hkv": h, "flush_tokens": 128,
+            "flushes": flushes, "us_gpu_median": med(gpu), "us_host_median": med(host),
+            "note": "GPU: HIP events around the flush's launches on the compute stream; host: wall clock of "
+                    "flush_full_recent_pool (the launches are asynchronous); median over the timed flushes"}
 
 
 def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dict:
@@ -761,15 +809,17 @@ def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
     params = [ex._params(q, ex.workspace.output, None) for _, q, ex in layers]
+    refs = [ctypes.byref(p) for p in params]
     n_rot = len(layers)
+    f_partial, f_combine = lib.r2o_decode_partial, lib.r2o_decode_combine
 
     def step(i):
-        p = ctypes.byref(params[i % n_rot])
-        lib.r2o_decode_partial(p, sp)
-        lib.r2o_decode_combine(p, sp)
+        r = refs[i % n_rot]
+        f_partial(r, sp)
+        f_combine(r, sp)
 
     def partial_only(i):
-        lib.r2o_decode_partial(ctypes.byref(params[i % n_rot]), sp)
+        f_partial(refs[i % n_rot], sp)
 
     def drop_in(i):  # the manager's entry: SplitKExecutor.__call__ (checks, arguments, two launches)
         _, q, ex = layers[i % n_rot]
@@ -781,8 +831,27 @@ def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed
     ms_step = _time_events(step, steps, stream)
     ms_partial = _time_events(partial_only, steps, stream)
     ms_drop_in = _time_events(drop_in, steps, stream)
+
+    # the same calls replayed from one HIP graph holding a layer call per rotated cache: no host
+    # launch cost, so on small caches this is the GPU's own time per call
+    from r2omni_amd.batch import _capture_launches
+
+    side = torch.cuda.Stream(device=dev)
+
+    def rotation():
+        cs = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for r in refs:
+            f_partial(r, cs)
+            f_combine(r, cs)
+
+    graph = _capture_launches(dev, side, rotation)
+    for _ in range(20):
+        graph.replay()
+    replays = max(1, steps // n_rot)
+    ms_graph = _time_events(lambda i: graph.replay(), replays, stream) / n_rot
+    del graph
     return {"layers": layers, "bytes": nbytes, "ms_step": ms_step, "ms_partial": ms_partial,
-            "ms_drop_in": ms_drop_in, "n_items": layers[0][2].n_items}
+            "ms_drop_in": ms_drop_in, "ms_graph": ms_graph, "n_items": layers[0][2].n_items}
 
 
 def timeline_bench(cfg, dev, *, n_layers: int, warmup: int, trials: int = 3) -> dict:
@@ -937,6 +1006,9 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=0, metavar="N",
                     help="only time N decode steps of --layers BatchedDecoder layers of --config (eager launches "
                          "and one HIP graph per step, flushes inside the batch) and print one JSON line")
+    ap.add_argument("--flush", action="store_true",
+                    help="only time the flush of a full Recent-FP ring (128 tokens quantised and packed, ring "
+                         "shifted) on the longest request of --config and print one JSON line")
     ap.add_argument("--sweep", type=str, default="", metavar="F1,F2,...",
                     help="only time the layer call of --config with its history scaled by each factor and print "
                          "the points and the fit time = fixed + bytes / rate as one JSON line")
@@ -997,6 +1069,9 @@ def main() -> int:
     if args.prefill:
         print(json.dumps(prefill_bench(cfg, args.config, dev)), flush=True)
         return 0
+    if args.flush:
+        print(json.dumps(flush_bench(cfg, args.config, dev)), flush=True)
+        return 0
     if args.decode_steps:
         print(json.dumps(decode_steps_bench(cfg, args.config, dev, args.decode_steps, args.layers)), flush=True)
         return 0
@@ -1013,6 +1088,7 @@ def main() -> int:
     r = time_decode_layers(cfg, dev, n_layers=args.layers, steps=args.steps, warmup=args.warmup)
     wall = time.perf_counter() - t0
     nbytes, ms_step, ms_partial, ms_drop_in = r["bytes"], r["ms_step"], r["ms_partial"], r["ms_drop_in"]
+    ms_graph = r["ms_graph"]
     gbs = nbytes / (ms_step * 1e-3) / 1e9
     part_gbs = nbytes / (ms_partial * 1e-3) / 1e9
     _log(f"step {ms_step * 1e3:.2f} us ({gbs:.0f} GB/s), partial {ms_partial * 1e3:.2f} us ({part_gbs:.0f} GB/s), "
@@ -1062,6 +1138,9 @@ def main() -> int:
                      "traffic_source": traffic_src,
                      "kernel": "decode_partial_kernel", "avg_us": round(ms_partial * 1e3, 3),
                      "avg_us_source": "HIP events over back-to-back partial launches on the launch stream"},
+        "graph_call": {"us": round(ms_graph * 1e3, 3), "GBs": round(nbytes / (ms_graph * 1e-3) / 1e9, 1),
+                       "method": "the same layer calls replayed from one HIP graph per rotation of the layer caches "
+                                 "(no host launch cost), HIP events over the replays"},
         "drop_in_call": {"us": round(ms_drop_in * 1e3, 3), "GBs": round(nbytes / (ms_drop_in * 1e-3) / 1e9, 1),
                          "method": "the same layer calls through SplitKExecutor.__call__ (the Python drop-in the "
                                    "manager calls: checks, launch arguments, the two launches), HIP events"},
