@@ -871,7 +871,10 @@ def timeline_bench(cfg, dev, *, n_layers: int, warmup: int, trials: int = 3) -> 
     lib.r2o_timeline_read.restype = ctypes.c_int
     lib.r2o_timeline_read.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
     r = time_decode_layers(cfg, dev, n_layers=n_layers, steps=200, warmup=warmup)
-    layers, n = r["layers"], r["n_items"]
+    layers = r["layers"]
+    n = layers[(200 - 1) % len(layers)][2].n_items  # the stamps read are the last call's, on this layer
+    if n > 4096:
+        raise RuntimeError("the stamp arrays hold 4096 work items")
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
     params = [ex._params(q, ex.workspace.output, None) for _, q, ex in layers]
@@ -943,6 +946,8 @@ def timeline_bench(cfg, dev, *, n_layers: int, warmup: int, trials: int = 3) -> 
         if isinstance(objs[0], dict):
             return {k: med([o[k] for o in objs]) for k in objs[0]}
         if isinstance(objs[0], list):
+            if any(o is None for o in objs):
+                return None
             return [round(float(np.median([o[i] for o in objs])), 2) for i in range(len(objs[0]))]
         return objs[len(objs) // 2]
 

@@ -129,3 +129,18 @@ def test_bench_dma_read_probe_rejects_bad_arguments_without_a_gpu():
     assert fn(4096, 8192, 64, 8, 2, None) == 1          # tile size other than 4 or 8 KiB
     assert fn(4096, 2048, 64, 8, 4, None) == 1          # less than one tile
     assert fn(4096, 8192, None, 8, 4, None) == 1        # no sink
+
+
+def test_phase_stamps_live_only_in_the_measurement_library():
+    """libr2o_timeline.so (bench.py --timeline) is the decode library with -DR2O_TIMELINE: it exports the
+    stamp reader and every product symbol; the product library has no stamp code at all."""
+    from r2omni_amd.build import TIMELINE_LIB_PATH
+
+    def defined(path):
+        return subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True).stdout
+
+    product, timeline = defined(_lib.LIB_PATH), defined(TIMELINE_LIB_PATH)
+    assert "r2o_timeline_read" not in product
+    assert re.search(r"\bT r2o_timeline_read\b", timeline)
+    for name in _declared():
+        assert re.search(rf"\bT {name}\b", timeline), name
