@@ -226,14 +226,17 @@ int r2o_pack_int2_k(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src
                     uint8_t* packed, uint16_t* scale, uint16_t* offset, uint32_t* operands,
                     int64_t capacity, int64_t superblocks, int64_t superblock, void* stream);
 
-/* Per-token symmetric INT4-V: packed[h, dst+i] / scale[h, dst+i] from src[h, index[i]].
- * Replaces _gather_pack_int4_value_kernel (fused_value_pack.py:28-70). */
+/* Per-token symmetric INT4-V: packed[h, dst+i] / scale[h, dst+i] from src[h, index[i]] (index
+ * NULL: src[h, i], n <= src_tokens).  Replaces _gather_pack_int4_value_kernel
+ * (fused_value_pack.py:28-70), in the static gather and in CompactInt4ValueArena.append_block
+ * (fused_value_pack.py:263-299), the flush of generated INT4 values. */
 int r2o_pack_int4_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
                     const int64_t* index, int64_t n, int64_t dst_start,
                     uint8_t* packed, float* scale, int64_t capacity, void* stream);
 
-/* Per-token-group affine INT2-V (group 32/64/128).  Replaces _gather_pack_int2_value_kernel
- * (fused_value_pack.py:75-149), both the gathered prefill and the contiguous flush forms. */
+/* Per-token-group affine INT2-V (group 32/64/128) from src[h, index[i]] (index NULL: src[h, i],
+ * n <= src_tokens).  Replaces _gather_pack_int2_value_kernel (fused_value_pack.py:75-149), both
+ * the gathered prefill and the contiguous flush forms. */
 int r2o_pack_int2_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src_tokens,
                     const int64_t* index, int64_t n, int64_t dst_start, int64_t group,
                     uint8_t* packed, uint16_t* scale, uint8_t* zero, int64_t capacity,

@@ -102,6 +102,12 @@ class OracleCache:
     # BF16-K variants: K rows in physical order [H, cap, D] float32 (values of the input dtype)
     variant: str = "int4k"
     k_rows: np.ndarray | None = None
+    # generated values: "int2" (released) or "int4" (the INT4 pool's V rows are an arena of
+    # capacity v4_capacity, static tokens first; generated keys start at gen_k_offset)
+    gen_values: str = "int2"
+    v4_capacity: int = 0
+    static_i4: int = 0
+    gen_k_offset: int = 0
 
     @property
     def recent_capacity(self) -> int:
@@ -119,9 +125,11 @@ def survivor_layout(page_offsets, page_lengths, page_classes):
 def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: str,
                 page_size: int = 32, superblock: int = 32, group: int = 32,
                 recent_capacity: int = 128, append_capacity: int = 260,
-                flush_size: int = 128, variant: str = "int4k") -> OracleCache:
+                flush_size: int = 128, variant: str = "int4k", gen_values: str = "int2") -> OracleCache:
     """Restatement of ``build_three_precision_cache``: ``variant`` "int4k" (``v_fourq_k_int4_compact``),
-    "int2k" (``v_fourq_k_int2_compact``), "bf16k" (``v_fourq_k_bf16``) or "matched" (``matched_fp=True``).
+    "int2k" (``v_fourq_k_int2_compact``), "bf16k" (``v_fourq_k_bf16``) or "matched" (``matched_fp=True``);
+    ``gen_values`` the ``generated_value_precision`` ("int4": the INT4 pool's V rows get
+    ``append_capacity`` tokens of room, the INT2-V arena none, precision_pool.py:935-956).
 
     ``key``/``value`` are float32 arrays holding values of ``dtype`` ([Hkv, S, 128]).
     """
@@ -164,8 +172,15 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
         k_rows[:, :active] = key[:, ordered]
     # value pools
     fp_v = value[:, fp_t].copy()
+    if gen_values not in ("int2", "int4"):
+        raise ValueError("gen_values must be int2 or int4")
+    int4_gen = gen_values == "int4" and variant != "matched"
     v4_packed, v4_scale = quantize_int4_value(value[:, i4_t])
-    v2_cap = max(128, _round_up(len(i2_t) + append_capacity, 128))
+    v4_cap = max(1, len(i4_t) + append_capacity) if int4_gen else len(i4_t)  # fused_value_pack.py:302-330
+    if int4_gen:
+        v4_packed = np.concatenate((v4_packed, np.zeros((h, v4_cap - len(i4_t), d // 2), np.uint8)), axis=1)
+        v4_scale = np.concatenate((v4_scale, np.zeros((h, v4_cap - len(i4_t), 1), np.float32)), axis=1)
+    v2_cap = max(128, _round_up(len(i2_t) + (0 if int4_gen else append_capacity), 128))
     groups = d // group
     v2_packed = np.zeros((h, v2_cap, d // 4), np.uint8)
     v2_scale = np.zeros((h, v2_cap, groups, 1), np.float16)
@@ -193,6 +208,7 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
         pool_tokens=[len(fp_t), len(i4_t), len(i2_t)],
         int2_global=list(i2_t), int2_logical=list(i2_t),
         variant=variant, k_rows=k_rows,
+        gen_values=gen_values, v4_capacity=v4_cap, static_i4=len(i4_t), gen_k_offset=active,
     )
 
 
@@ -249,8 +265,19 @@ def _flush_value_int2(c: OracleCache, value_block: np.ndarray) -> None:
     c.v2_active += n
 
 
+def _flush_value_int4(c: OracleCache, value_block: np.ndarray) -> None:
+    """``CompactInt4ValueArena.append_block`` (fused_value_pack.py:263-299)."""
+    n = value_block.shape[1]
+    dst = c.pool_tokens[1]
+    if dst + n > c.v4_capacity:
+        raise RuntimeError(f"compact INT4 V capacity exhausted: need {dst + n}, have {c.v4_capacity}")
+    p, s = quantize_int4_value(value_block)
+    c.v4_packed[:, dst : dst + n] = p
+    c.v4_scale[:, dst : dst + n] = s
+
+
 def append_token(c: OracleCache, new_k, new_v, *, global_index: int, logical_position: int) -> bool:
-    """``append_generated_token`` with the compact INT4-K / INT2-V flush.
+    """``append_generated_token`` with the compact INT4-K / INT2-V (or INT4-V) flush.
 
     ``new_k``/``new_v`` are [Hkv, D] float32 holding values of the cache dtype.
     """
@@ -276,10 +303,14 @@ def append_token(c: OracleCache, new_k, new_v, *, global_index: int, logical_pos
                                "covering the requested generation horizon")
         else:
             c.tail_dequant_tokens += _flush_key_superblock(c, key_block)
-            _flush_value_int2(c, value_block)
-            c.int2_global.extend(g_block.tolist())
-            c.int2_logical.extend(l_block.tolist())
-            c.pool_tokens[2] += f
+            if c.gen_values == "int4":  # dynamic_fourq_cache.py:212-219
+                _flush_value_int4(c, value_block)
+                c.pool_tokens[1] += f
+            else:
+                _flush_value_int2(c, value_block)
+                c.int2_global.extend(g_block.tolist())
+                c.int2_logical.extend(l_block.tolist())
+                c.pool_tokens[2] += f
         rem = c.recent_active - f
         c.recent_k[:, :rem] = c.recent_k[:, f : c.recent_active].copy()
         c.recent_v[:, :rem] = c.recent_v[:, f : c.recent_active].copy()
@@ -316,7 +347,15 @@ def pool_kv(c: OracleCache):
 
     if s_fp:
         out.append((keys(segs[0], s_fp), c.fp_v))
-    if s_i4:
+    if s_i4 and c.gen_values == "int4" and c.variant != "matched":
+        # static keys at their segment, generated ones at gen_k_offset (triton_fourq_attention.py:95-111);
+        # CompactInt4ValueArena.dequantize_range stays fp32 (fused_value_pack.py:241-256)
+        static = min(c.static_i4, s_i4)
+        k4 = keys(segs[1], static)
+        if s_i4 > static:
+            k4 = np.concatenate((k4, keys(c.gen_k_offset, s_i4 - static)), axis=1)
+        out.append((k4, dequantize_int4_value(c.v4_packed[:, :s_i4], c.v4_scale[:, :s_i4])))
+    elif s_i4:
         # PackedTensor.dequantize rounds the fp32 product back to the input dtype
         # (packed_kv_layout.py:30-32); the compact INT4-K / INT2-V arenas stay fp32.
         out.append((keys(segs[1], s_i4), round_to_dtype(dequantize_int4_value(c.v4_packed, c.v4_scale), c.dtype)))

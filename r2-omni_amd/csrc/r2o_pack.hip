@@ -555,7 +555,7 @@ int r2o_pack_int4_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src
                     int64_t n, int64_t dst_start, uint8_t* packed, float* scale, int64_t capacity, void* stream) {
     if ((dtype != 0 && dtype != 1) || hkv <= 0 || n < 0 || dst_start < 0 || dst_start + n > capacity) return R2O_EINVAL;
     if (n == 0) return R2O_OK;
-    if (!src || src_tokens <= 0 || n > 0x7fffffff) return R2O_EINVAL;
+    if (!src || src_tokens <= 0 || n > 0x7fffffff || (!index && n > src_tokens)) return R2O_EINVAL;
     hipLaunchKernelGGL(pack_int4_v_kernel, dim3((unsigned)((n + 4 * kVRows - 1) / (4 * kVRows)), (unsigned)hkv), dim3(256),
                        0, (hipStream_t)stream, src, (int)dtype, src_tokens, index, n, dst_start, packed, scale, capacity);
     R2O_CHECK_LAUNCH();
@@ -568,7 +568,7 @@ int r2o_pack_int2_v(const uint16_t* src, int64_t dtype, int64_t hkv, int64_t src
     if ((dtype != 0 && dtype != 1) || !(group == 32 || group == 64 || group == 128)) return R2O_EINVAL;
     if (hkv <= 0 || n < 0 || dst_start < 0 || dst_start + n > capacity) return R2O_EINVAL;
     if (n == 0) return R2O_OK;
-    if (!src || src_tokens <= 0 || n > 0x7fffffff) return R2O_EINVAL;
+    if (!src || src_tokens <= 0 || n > 0x7fffffff || (!index && n > src_tokens)) return R2O_EINVAL;
     hipLaunchKernelGGL(pack_int2_v_kernel, dim3((unsigned)((n + 4 * kVRows - 1) / (4 * kVRows)), (unsigned)hkv), dim3(256),
                        0, (hipStream_t)stream, src, (int)dtype, src_tokens, index, n, dst_start, (int)group, packed, scale,
                        zero, capacity);

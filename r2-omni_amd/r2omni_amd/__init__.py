@@ -11,6 +11,7 @@ from .cache import (
     CompactInt2KeyArena,
     CompactInt2ValueArena,
     CompactInt4KeyArena,
+    CompactInt4ValueArena,
     CompactMetadataArena,
     DynamicCacheStats,
     PackedTensor,
@@ -21,6 +22,7 @@ from .cache import (
     build_compact_int2_key_arena,
     build_compact_int2_value_arena,
     build_compact_int4_key_arena,
+    build_compact_int4_value_arena,
     build_three_precision_cache,
     flush_full_recent_pool,
     fused_gather_pack_int4_value,

@@ -4,14 +4,16 @@ Drop-in for the reference runtime (same names, fields, layouts and error message
   CompactInt4KeyArena        r2omni/sspa/runtime/compact_int4_key.py:113-220
   build (INT4-K gather-pack) compact_int4_key.py:223-281
   PackedTensor (INT4-V pool) packed_kv_layout.py:11-32, fused_value_pack.py:152-193
+  CompactInt4ValueArena      fused_value_pack.py:196-299, build :302-330 (generated INT4 values)
   CompactInt2ValueArena      fused_value_pack.py:401-516, build :519-575
   PrecisionPool, ThreePrecisionCache, build_three_precision_cache  precision_pool.py:152-274, 787-984
   CompactMetadataArena       precision_pool.py:45-145, 400-585
   append_generated_token, DynamicCacheStats  dynamic_fourq_cache.py:16-24, 172-267
 All payload bytes are produced by the gfx950 kernels of libr2o_sspa.so (r2o_pack_int4_k,
 r2o_pack_int4_v, r2o_pack_int2_v, r2o_gather_rows, r2o_recent_append, r2o_recent_shift);
-torch only allocates the tensors and keeps small index vectors.  Supported variant: the
-released ``v_fourq_k_int4_compact`` cache with INT2 generated values.
+torch only allocates the tensors and keeps small index vectors.  Variants: the released
+``v_fourq_k_int4_compact`` cache, ``v_fourq_k_int2_compact``, ``v_fourq_k_bf16`` and the matched-FP
+cache; generated (flushed) values INT2 (released) or INT4 (``generated_value_precision="int4"``).
 """
 from __future__ import annotations
 
@@ -50,11 +52,11 @@ class CompactMetadataArena:
     """Every page and token index of a compact cache in one int64 allocation
     (precision_pool.py:45-145, 400-585).
 
-    The INT2 pool's five fields are reserved up to the packed arenas' append capacity, and the page
-    fields of the reserved pages (id -1, offsets continuing the pool, full length) are written at
-    build time, so a flush copies its token indices in place and allocates nothing.  The INT2 pool's
-    ``page_index`` is re-pointed at longer views of the same buffers.  Generated INT4 values are not
-    supported here, so no INT4 reserve exists.
+    The INT4 and INT2 pools' five fields are each reserved up to what their packed V arena and the
+    compact K arena can still take (INT4 only when generated values are INT4), and the page fields
+    of the reserved pages (id -1, offsets continuing the pool, full length) are written at build
+    time, so a flush copies its token indices in place and allocates nothing.  The flushed pool's
+    ``page_index`` is re-pointed at longer views of the same buffers.
     """
 
     storage: torch.Tensor
@@ -65,31 +67,47 @@ class CompactMetadataArena:
     int2_logical_position_buffer: torch.Tensor
     int2_page_count: int
     int2_token_count: int
+    int4_original_page_ids_buffer: torch.Tensor
+    int4_physical_offsets_buffer: torch.Tensor
+    int4_lengths_buffer: torch.Tensor
+    int4_global_index_buffer: torch.Tensor
+    int4_logical_position_buffer: torch.Tensor
+    int4_page_count: int
+    int4_token_count: int
+
+    def _append_pages(self, pool: "PrecisionPool", global_indices: torch.Tensor, logical_positions: torch.Tensor,
+                      page_size: int, tier: str) -> None:
+        n = int(global_indices.numel())
+        if n <= 0 or n != int(logical_positions.numel()) or n % int(page_size):
+            raise ValueError(f"compact {tier.upper()} metadata append requires matching complete pages")
+        if global_indices.dtype != torch.long or logical_positions.dtype != torch.long \
+                or global_indices.device != self.storage.device or logical_positions.device != self.storage.device:
+            raise ValueError(f"compact {tier.upper()} metadata append requires same-device int64 indices")
+        ids, offs, lens, g, l = (getattr(self, f"{tier}_{name}_buffer") for name in
+                                 ("original_page_ids", "physical_offsets", "lengths", "global_index",
+                                  "logical_position"))
+        pages, tokens = getattr(self, f"{tier}_page_count"), getattr(self, f"{tier}_token_count")
+        page_end = pages + n // int(page_size)
+        token_end = tokens + n
+        if page_end > lens.numel():
+            raise RuntimeError(f"compact {tier.upper()} page metadata capacity exhausted")
+        if token_end > g.numel():
+            raise RuntimeError(f"compact {tier.upper()} token metadata capacity exhausted")
+        g[tokens:token_end].copy_(global_indices)
+        l[tokens:token_end].copy_(logical_positions)
+        setattr(self, f"{tier}_page_count", page_end)
+        setattr(self, f"{tier}_token_count", token_end)
+        pool.page_index = PhysicalPageIndex(original_page_ids=ids[:page_end], physical_offsets=offs[:page_end],
+                                            lengths=lens[:page_end], global_token_indices=g[:token_end],
+                                            logical_positions=l[:token_end])
 
     def append_int2_pages(self, pool: "PrecisionPool", global_indices: torch.Tensor,
                           logical_positions: torch.Tensor, page_size: int) -> None:
-        n = int(global_indices.numel())
-        if n <= 0 or n != int(logical_positions.numel()) or n % int(page_size):
-            raise ValueError("compact INT2 metadata append requires matching complete pages")
-        if global_indices.dtype != torch.long or logical_positions.dtype != torch.long \
-                or global_indices.device != self.storage.device or logical_positions.device != self.storage.device:
-            raise ValueError("compact INT2 metadata append requires same-device int64 indices")
-        page_end = self.int2_page_count + n // int(page_size)
-        token_end = self.int2_token_count + n
-        if page_end > self.int2_lengths_buffer.numel():
-            raise RuntimeError("compact INT2 page metadata capacity exhausted")
-        if token_end > self.int2_global_index_buffer.numel():
-            raise RuntimeError("compact INT2 token metadata capacity exhausted")
-        self.int2_global_index_buffer[self.int2_token_count:token_end].copy_(global_indices)
-        self.int2_logical_position_buffer[self.int2_token_count:token_end].copy_(logical_positions)
-        self.int2_page_count, self.int2_token_count = page_end, token_end
-        pool.page_index = PhysicalPageIndex(
-            original_page_ids=self.int2_original_page_ids_buffer[:page_end],
-            physical_offsets=self.int2_physical_offsets_buffer[:page_end],
-            lengths=self.int2_lengths_buffer[:page_end],
-            global_token_indices=self.int2_global_index_buffer[:token_end],
-            logical_positions=self.int2_logical_position_buffer[:token_end],
-        )
+        self._append_pages(pool, global_indices, logical_positions, page_size, "int2")
+
+    def append_int4_pages(self, pool: "PrecisionPool", global_indices: torch.Tensor,
+                          logical_positions: torch.Tensor, page_size: int) -> None:
+        self._append_pages(pool, global_indices, logical_positions, page_size, "int4")
 
 
 # ------------------------------------------------------------------------ BF16 K rows
@@ -444,6 +462,105 @@ def fused_gather_pack_int4_value(value: torch.Tensor, token_indices: torch.Tenso
                         quant_metadata={"dim": 2, "fused_gather": True})
 
 
+# ------------------------------------------------------------------------ compact INT4 V
+@dataclass
+class CompactInt4ValueArena:
+    """Per-token symmetric INT4 V with room for generated flushes (fused_value_pack.py:196-299): the
+    static INT4 pool's tokens first, then each flushed block, packed in place by r2o_pack_int4_v."""
+
+    packed: torch.Tensor          # u8  [H, capacity, D/2]
+    scale: torch.Tensor           # f32 [H, capacity, 1]
+    active_length: int
+    capacity: int
+    original_dtype: torch.dtype
+    num_bits: int = 4
+    quant_scheme: str = "per_token"
+    zero_point: None = None
+
+    def __post_init__(self) -> None:
+        if self.packed.ndim != 3 or self.packed.dtype != torch.uint8:
+            raise ValueError("compact INT4 V packed storage must be uint8 [H,capacity,D/2]")
+        h, capacity, _ = map(int, self.packed.shape)
+        if capacity != self.capacity or not 0 <= self.active_length <= capacity:
+            raise ValueError("compact INT4 V active length/capacity is invalid")
+        if tuple(self.scale.shape) != (h, capacity, 1) or self.scale.dtype != torch.float32:
+            raise ValueError("compact INT4 V scale storage must be float32 [H,capacity,1]")
+
+    @property
+    def original_shape(self) -> tuple[int, int, int]:
+        return int(self.packed.shape[0]), int(self.active_length), int(self.packed.shape[2]) * 2
+
+    @property
+    def nbytes(self) -> int:
+        return sum(_nbytes(t) for t in self.allocation_tensors())
+
+    @property
+    def active_nbytes(self) -> int:
+        h, _, d2 = map(int, self.packed.shape)
+        return int(h * self.active_length * (d2 + self.scale.element_size()))
+
+    def allocation_tensors(self):
+        return self.packed, self.scale
+
+    def dequantize_range(self, start: int, length: int) -> torch.Tensor:
+        """fp32 code * scale (not rounded to the input dtype, unlike ``PackedTensor.dequantize``)."""
+        start, length = int(start), int(length)
+        if start < 0 or length < 0 or start + length > self.active_length:
+            raise ValueError("compact INT4 V dequantization range is outside active storage")
+        h, _, d2 = map(int, self.packed.shape)
+        p = self.packed[:, start:start + length]
+        lo = (p & 15).to(torch.int16)
+        hi = (p >> 4).to(torch.int16)
+        codes = torch.stack((torch.where(lo >= 8, lo - 16, lo), torch.where(hi >= 8, hi - 16, hi)), -1)
+        return codes.reshape(h, length, d2 * 2).float() * self.scale[:, start:start + length]
+
+    def dequantize(self) -> torch.Tensor:
+        return self.dequantize_range(0, self.active_length)
+
+    def append_block(self, value_block: torch.Tensor, *, source_tokens: int | None = None) -> None:
+        """Pack ``value_block`` [H, n, D] (rows of ``source_tokens`` per head, default n) after the
+        active tokens."""
+        h, _, d = self.original_shape
+        if value_block.ndim != 3 or int(value_block.shape[0]) != h or int(value_block.shape[2]) != d \
+                or int(value_block.shape[1]) <= 0:
+            raise ValueError("compact INT4 V append must contain matching tokens")
+        n = int(value_block.shape[1])
+        dst = self.active_length
+        if dst + n > self.capacity:
+            raise RuntimeError(f"compact INT4 V capacity exhausted: need {dst + n}, have {self.capacity}")
+        _lib.require_device(value_block, "compact INT4 V append block")
+        rows = int(source_tokens) if source_tokens is not None else n
+        if value_block.stride() != (rows * d, d, 1):
+            raise ValueError("compact INT4 V append block must have contiguous rows")
+        _lib.call("r2o_pack_int4_v", _lib.ptr(value_block), _lib.dtype_code(value_block.dtype), h, rows, None, n, dst,
+                  _lib.ptr(self.packed), _lib.ptr(self.scale), self.capacity, _lib.stream_of(value_block.device))
+        self.active_length += n
+
+
+def build_compact_int4_value_arena(value: torch.Tensor, token_indices: torch.Tensor, *,
+                                   append_capacity: int = 0) -> CompactInt4ValueArena:
+    """INT4 V of ``value[:, token_indices]`` with ``append_capacity`` more tokens of room
+    (fused_value_pack.py:302-330: capacity = max(1, tokens + append_capacity))."""
+    if value.ndim != 3 or int(value.shape[2]) != 128:
+        raise ValueError("compact INT4 V source must be [Hkv,S,128]")
+    if append_capacity < 0:
+        raise ValueError("append_capacity must be non-negative")
+    _lib.require_device(value, "value")
+    n = int(token_indices.numel())
+    capacity = max(1, n + int(append_capacity))
+    h, s, d = map(int, value.shape)
+    dev = value.device
+    arena = CompactInt4ValueArena(packed=torch.zeros((h, capacity, d // 2), device=dev, dtype=torch.uint8),
+                                  scale=torch.zeros((h, capacity, 1), device=dev, dtype=torch.float32),
+                                  active_length=n, capacity=capacity, original_dtype=value.dtype)
+    if n:
+        value = value.contiguous()
+        idx = token_indices.to(device=dev, dtype=torch.long).contiguous()
+        _lib.call("r2o_pack_int4_v", _lib.ptr(value), _lib.dtype_code(value.dtype), h, s, _lib.ptr(idx), n, 0,
+                  _lib.ptr(arena.packed), _lib.ptr(arena.scale), capacity, _lib.stream_of(dev))
+    return arena
+
+
 # ------------------------------------------------------------------------ compact INT2 V
 @dataclass
 class CompactInt2ValueArena:
@@ -611,7 +728,7 @@ class ThreePrecisionCache:
     cache_variant: str
     compact_key: CompactInt4KeyArena | CompactInt2KeyArena | None = None
     compact_value: CompactInt2ValueArena | None = None
-    compact_int4_value: Any = None
+    compact_int4_value: CompactInt4ValueArena | None = None  # INT4 pool's V when generated values are INT4
     metadata_arena: CompactMetadataArena | None = None
     recent_flush_size: int = 128
     generated_value_precision: str = "int2"
@@ -782,41 +899,41 @@ def _expand_tier_tokens(tab: _TierTable, device) -> torch.Tensor:
 
 
 def _build_metadata_arena(tab: _TierTable, tokens: torch.Tensor, gi: torch.Tensor, lp: torch.Tensor, *,
-                          page_size: int, recent_capacity: int, int2_reserve: int):
+                          page_size: int, recent_capacity: int, int2_reserve: int, int4_reserve: int = 0):
     """One int64 allocation holding the page index of every pool, the evicted global indices, the
     Recent-FP ring's index buffers and its device length (precision_pool.py:400-585).
 
     ``tokens`` are the tier-ordered token indices of ``_expand_tier_tokens``; ``gi`` / ``lp`` the
-    plan's global / logical token indices on the same device.  ``int2_reserve`` tokens (whole pages)
-    are reserved after the INT2 pool's fields.  Layout: the page fields of every pool and the length
-    slot (built on the host, one copy), then the token fields: global [FP INT4 INT2 reserve], logical
-    [FP INT4 INT2 reserve], evicted, ring global, ring logical.  Returns the arena, the four pools'
-    page indexes, the evicted indices and the ring's (global, logical, length) buffers.
+    plan's global / logical token indices on the same device.  ``int4_reserve`` / ``int2_reserve``
+    tokens (whole pages) are reserved after the INT4 / INT2 pool's fields.  Layout: the page fields
+    of every pool and the length slot (built on the host, one copy), then the token fields: global
+    [FP INT4 INT4-reserve INT2 INT2-reserve], logical [the same], evicted, ring global, ring logical.
+    Returns the arena, the four pools' page indexes, the evicted indices and the ring's (global,
+    logical, length) buffers.
     """
     ps = int(page_size)
     cap = int(recent_capacity)
-    if int2_reserve % ps or cap % ps:
+    if int2_reserve % ps or int4_reserve % ps or cap % ps:
         raise ValueError("metadata reserves must be whole pages")
     dev = tokens.device
-    fp_, i4_, i2_, ev_ = (slice(int(tab.first_page[t]), int(tab.first_page[t + 1])) for t in range(4))
-    reserve_pages = int2_reserve // ps
-    n_i2 = int(tab.tier_tokens[2])
+    tiers = [slice(int(tab.first_page[t]), int(tab.first_page[t + 1])) for t in range(3)]
+    reserve_pages = (0, int(int4_reserve) // ps, int(int2_reserve) // ps)
     ring_pages = cap // ps
 
-    def fields(ids, offs, lens):
-        return np.concatenate((ids, offs, lens))
-
-    page_parts = [fields(tab.pages[t], tab.offsets[t], tab.lengths[t]) for t in (fp_, i4_)]
-    page_parts.append(fields(np.concatenate((tab.pages[i2_], np.full(reserve_pages, -1))),
-                             np.concatenate((tab.offsets[i2_], n_i2 + ps * np.arange(reserve_pages))),
-                             np.concatenate((tab.lengths[i2_], np.full(reserve_pages, ps)))))
-    page_parts.append(fields(np.full(ring_pages, -1), ps * np.arange(ring_pages), np.zeros(ring_pages, np.int64)))
+    page_parts = []
+    for t, extra in zip(tiers, reserve_pages):
+        n_tok = int(tab.tier_tokens[len(page_parts)])
+        page_parts.append(np.concatenate((tab.pages[t], np.full(extra, -1), tab.offsets[t],
+                                          n_tok + ps * np.arange(extra), tab.lengths[t], np.full(extra, ps))))
+    page_parts.append(np.concatenate((np.full(ring_pages, -1), ps * np.arange(ring_pages),
+                                      np.zeros(ring_pages, np.int64))))
     page_parts.append(np.zeros(1, np.int64))  # the ring's device length (int32 in the low half)
     page_block = torch.from_numpy(np.concatenate(page_parts).astype(np.int64))
     n_pages_total = int(page_block.numel())
     n_surv = int(tab.tier_tokens[:3].sum())
     n_ev = int(tab.tier_tokens[3])
-    surv_span = n_surv + int(int2_reserve)
+    n_head = int(tab.tier_tokens[:2].sum())  # FP + INT4 tokens, before the INT4 reserve
+    surv_span = n_surv + int(int4_reserve) + int(int2_reserve)
     storage = torch.empty(n_pages_total + 2 * surv_span + n_ev + 2 * cap, device=dev, dtype=torch.long)
     if dev.type != "cpu":
         page_block = page_block.pin_memory()
@@ -827,9 +944,11 @@ def _build_metadata_arena(tab: _TierTable, tokens: torch.Tensor, gi: torch.Tenso
     evicted = tok[2 * surv_span:2 * surv_span + n_ev]
     ring_g = tok[2 * surv_span + n_ev:2 * surv_span + n_ev + cap]
     ring_l = tok[2 * surv_span + n_ev + cap:]
-    if n_surv:
-        torch.index_select(gi, 0, tokens[:n_surv], out=g_all[:n_surv])
-        torch.index_select(lp, 0, tokens[:n_surv], out=l_all[:n_surv])
+    i2_at = n_head + int(int4_reserve)
+    for dst, lo, hi in ((0, 0, n_head), (i2_at, n_head, n_surv)):
+        if hi > lo:
+            torch.index_select(gi, 0, tokens[lo:hi], out=g_all[dst:dst + hi - lo])
+            torch.index_select(lp, 0, tokens[lo:hi], out=l_all[dst:dst + hi - lo])
     if n_ev:
         torch.index_select(gi, 0, tokens[n_surv:], out=evicted)
 
@@ -843,7 +962,7 @@ def _build_metadata_arena(tab: _TierTable, tokens: torch.Tensor, gi: torch.Tenso
 
     indexes = []
     tok_start = 0
-    for t, extra in ((fp_, 0), (i4_, 0), (i2_, reserve_pages)):
+    for t, extra in zip(tiers, reserve_pages):
         npg = t.stop - t.start + extra
         ids, offs, lens = take(npg), take(npg), take(npg)
         nt = int(tab.tier_tokens[len(indexes)])
@@ -858,11 +977,13 @@ def _build_metadata_arena(tab: _TierTable, tokens: torch.Tensor, gi: torch.Tenso
              for ids, offs, lens, g, l, np_, nt in indexes]
     pools.append(PhysicalPageIndex(original_page_ids=ring_ids, physical_offsets=ring_offs, lengths=ring_lens,
                                    global_token_indices=ring_g, logical_positions=ring_l))
-    ids, offs, lens, g, l, np_, nt = indexes[2]
-    arena = CompactMetadataArena(storage=storage, int2_original_page_ids_buffer=ids,
-                                 int2_physical_offsets_buffer=offs, int2_lengths_buffer=lens,
-                                 int2_global_index_buffer=g, int2_logical_position_buffer=l,
-                                 int2_page_count=np_, int2_token_count=nt)
+    tier_fields = {}
+    for name, (ids, offs, lens, g, l, np_, nt) in (("int4", indexes[1]), ("int2", indexes[2])):
+        tier_fields.update({f"{name}_original_page_ids_buffer": ids, f"{name}_physical_offsets_buffer": offs,
+                            f"{name}_lengths_buffer": lens, f"{name}_global_index_buffer": g,
+                            f"{name}_logical_position_buffer": l, f"{name}_page_count": np_,
+                            f"{name}_token_count": nt})
+    arena = CompactMetadataArena(storage=storage, **tier_fields)
     return arena, pools, evicted, (ring_g, ring_l, length)
 
 
@@ -971,9 +1092,8 @@ def build_three_precision_cache(
         raise ValueError(f"unsupported cache_variant: {cache_variant}")
     if generated_value_precision not in ("int2", "int4"):
         raise ValueError("generated_value_precision must be int2 or int4")
-    if generated_value_precision != "int2" or not preallocate_recent:
-        raise NotImplementedError(
-            "the gfx950 path implements the caches with INT2 generated values and a preallocated Recent-FP ring")
+    if not preallocate_recent:
+        raise NotImplementedError("the gfx950 path implements the caches with a preallocated Recent-FP ring")
     if int(key.shape[2]) != 128:
         raise ValueError("the SSPA decode path requires head_dim 128")
     _lib.require_device(key, "key")
@@ -998,7 +1118,7 @@ def build_three_precision_cache(
     n_surv = s_fp + s_i4 + s_i2
     common = dict(page_size=int(page_size), quantization_superblock=int(quantization_superblock),
                   cache_variant=cache_variant, recent_flush_size=int(recent_flush_size),
-                  generated_value_precision="int2")
+                  generated_value_precision=str(generated_value_precision))
     if matched_fp:  # every surviving page, K and V in bf16, in one FP pool (precision_pool.py:834-876)
         surv = _survivor_layout(plan, dev)
         n = int(surv[0].numel())
@@ -1017,28 +1137,34 @@ def build_three_precision_cache(
             evicted_global_indices=gi[tokens[n_surv:]], **common)
     fp_tokens, i4_tokens, i2_tokens = tokens[:s_fp], tokens[s_fp:s_fp + s_i4], tokens[s_fp + s_i4:n_surv]
 
-    fp_v = int4_v = None
+    fp_v = int4_v = compact_int4_value = None
     if s_fp:
         fp_v = torch.empty((h, s_fp, 128), device=dev, dtype=value.dtype)
         _lib.call("r2o_gather_rows", _lib.ptr(value), h, int(value.shape[1]), _lib.ptr(fp_tokens), s_fp,
                   _lib.ptr(fp_v), s_fp, stream)
-    if s_i4:
+    int4_generated = generated_value_precision == "int4"
+    if int4_generated:  # the INT4 pool's V is an arena with room for generated flushes (precision_pool.py:935-942)
+        compact_int4_value = int4_v = build_compact_int4_value_arena(value, i4_tokens, append_capacity=append_capacity)
+    elif s_i4:
         int4_v = fused_gather_pack_int4_value(value, i4_tokens)
-    compact_value = build_compact_int2_value_arena(value, i2_tokens, append_capacity=append_capacity,
-                                                   group_size=int2_group_size)
+    compact_value = build_compact_int2_value_arena(value, i2_tokens, group_size=int2_group_size,
+                                                   append_capacity=0 if int4_generated else append_capacity)
     compact_key = bf16_arena = None
     if bf16_keys:  # v_fourq_k_bf16: every pool keeps bf16 K rows (precision_pool.py:878-906)
         bf16_arena = _gather_key_rows(key, tokens[:n_surv], append_capacity, (0, s_fp, s_fp + s_i4))
-        reserve = 0  # no compact K arena to flush into (precision_pool.py:404-408)
+        reserve = reserve4 = 0  # no compact K arena to flush into (precision_pool.py:404-408)
     else:
         build_key = build_compact_int2_key_arena if cache_variant == "v_fourq_k_int2_compact" \
             else build_compact_int4_key_arena
         compact_key = build_key(key, (fp_tokens, i4_tokens, i2_tokens), append_capacity=append_capacity,
                                 superblock_size=key_quantization_superblock)
-        reserve = min(compact_value.capacity - compact_value.active_length,
-                      compact_key.capacity - compact_key.active_length) // page_size * page_size
+        key_room = compact_key.capacity - compact_key.active_length
+        reserve = min(compact_value.capacity - compact_value.active_length, key_room) // page_size * page_size
+        reserve4 = 0 if compact_int4_value is None else \
+            min(compact_int4_value.capacity - compact_int4_value.active_length, key_room) // page_size * page_size
     meta, (fp_pi, i4_pi, i2_pi, ring_pi), evicted, (ring_g, ring_l, ring_len) = _build_metadata_arena(
-        tab, tokens, gi, lp, page_size=page_size, recent_capacity=plan.recent_fp_capacity, int2_reserve=reserve)
+        tab, tokens, gi, lp, page_size=page_size, recent_capacity=plan.recent_fp_capacity, int2_reserve=reserve,
+        int4_reserve=reserve4)
     fp_pool = PrecisionPool(name="fp", page_index=fp_pi, fp_v=fp_v)
     int4_pool = PrecisionPool(name="int4", page_index=i4_pi, packed_v=int4_v)
     int2_pool = PrecisionPool(name="int2", page_index=i2_pi, packed_v=compact_value)
@@ -1049,12 +1175,13 @@ def build_three_precision_cache(
         int2_pool.fp_k = bf16_arena.view(s_fp + s_i4, s_i2)
         return ThreePrecisionCache(
             fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
-            compact_value=compact_value, static_int4_tokens=s_i4, bf16_key=bf16_arena, metadata_arena=meta,
-            evicted_global_indices=evicted, **common)
+            compact_value=compact_value, compact_int4_value=compact_int4_value, static_int4_tokens=s_i4,
+            bf16_key=bf16_arena, metadata_arena=meta, evicted_global_indices=evicted, **common)
     return ThreePrecisionCache(
         fp_pool=fp_pool, int4_pool=int4_pool, int2_pool=int2_pool, recent_fp_pool=recent, matched_fp=False,
-        compact_key=compact_key, compact_value=compact_value, static_int4_tokens=s_i4,
-        generated_k_offset=compact_key.active_length, metadata_arena=meta, evicted_global_indices=evicted,
+        compact_key=compact_key, compact_value=compact_value, compact_int4_value=compact_int4_value,
+        static_int4_tokens=s_i4, generated_k_offset=compact_key.active_length, metadata_arena=meta,
+        evicted_global_indices=evicted,
         **common)
 
 
@@ -1070,8 +1197,8 @@ class DynamicCacheStats:
     full_dequant_tensor_count: int = 0
 
 
-def _append_int2_page_metadata(pool: PrecisionPool, global_block: torch.Tensor, logical_block: torch.Tensor,
-                               page_size: int) -> None:
+def _append_lowbit_page_metadata(pool: PrecisionPool, global_block: torch.Tensor, logical_block: torch.Tensor,
+                                 page_size: int) -> None:
     n = int(global_block.numel())
     if n <= 0 or n % page_size:
         raise ValueError("low-bit metadata append must contain complete pages")
@@ -1091,7 +1218,8 @@ def _append_int2_page_metadata(pool: PrecisionPool, global_block: torch.Tensor, 
 
 def flush_full_recent_pool(cache: ThreePrecisionCache, stats: DynamicCacheStats) -> bool:
     """If the Recent-FP ring is full, move its oldest ``recent_flush_size`` tokens into the cache
-    (compact INT4/INT2-K + INT2-V arenas, or the matched-FP pool) and shift the ring: the flush half of
+    (compact INT4/INT2-K + INT2-V or, with INT4 generated values, INT4-V arenas, or the matched-FP
+    pool) and shift the ring: the flush half of
     ``append_generated_token`` (dynamic_fourq_cache.py:185-253).  Returns whether it flushed.  The
     caller re-prepares its executors afterwards."""
     pool = cache.recent_fp_pool
@@ -1109,7 +1237,7 @@ def flush_full_recent_pool(cache: ThreePrecisionCache, stats: DynamicCacheStats)
     global_block = pool.global_index_buffer[:flush]
     logical_block = pool.logical_position_buffer[:flush]
     if cache.matched_fp:  # _append_matched_fp_block (dynamic_fourq_cache.py:145-170)
-        _append_int2_page_metadata(cache.fp_pool, global_block, logical_block, cache.page_size)
+        _append_lowbit_page_metadata(cache.fp_pool, global_block, logical_block, cache.page_size)
         cache.bf16_key.append_block(key_block)
         n = cache.bf16_key.active_length
         cache.bf16_key.segment_offsets = (0, n, n)
@@ -1120,15 +1248,27 @@ def flush_full_recent_pool(cache: ThreePrecisionCache, stats: DynamicCacheStats)
         raise RuntimeError("K-BF16/V-FourQ requires an append_fp_only Recent-FP capacity covering the "
                            "requested generation horizon")
     else:
-        if cache.compact_key is None or cache.compact_value is None:
+        if cache.compact_key is None:
+            raise RuntimeError("compact K cache is missing its compact K arena")
+        int4_values = cache.generated_value_precision == "int4"
+        if int4_values and cache.compact_int4_value is None:
+            raise RuntimeError("generated INT4 V policy is missing its compact arena")
+        if not int4_values and cache.compact_value is None:
             raise RuntimeError("compact INT2 K cache is missing its compact INT2 V arena")
         stats.local_tail_dequant_tokens += cache.compact_key.append_superblock(key_block, source_tokens=cap) \
             if flush == 128 else _flush_size_error(flush)
-        cache.compact_value.append_superblock(value_block, source_tokens=cap)
-        if cache.metadata_arena is not None:  # in place (dynamic_fourq_cache.py:236-239)
-            cache.metadata_arena.append_int2_pages(cache.int2_pool, global_block, logical_block, cache.page_size)
+        if int4_values:  # dynamic_fourq_cache.py:212-219
+            cache.compact_int4_value.append_block(value_block, source_tokens=cap)
+            stats.flushed_int4_value_tokens += flush
+            target = cache.int4_pool
         else:
-            _append_int2_page_metadata(cache.int2_pool, global_block, logical_block, cache.page_size)
+            cache.compact_value.append_superblock(value_block, source_tokens=cap)
+            target = cache.int2_pool
+        if cache.metadata_arena is not None:  # in place (dynamic_fourq_cache.py:236-243)
+            append = cache.metadata_arena.append_int4_pages if int4_values else cache.metadata_arena.append_int2_pages
+            append(target, global_block, logical_block, cache.page_size)
+        else:
+            _append_lowbit_page_metadata(target, global_block, logical_block, cache.page_size)
     _lib.call("r2o_recent_shift", _lib.ptr(pool.fp_k), _lib.ptr(pool.fp_v), h, cap, flush, pool.active_length,
               _lib.ptr(pool.global_index_buffer), _lib.ptr(pool.logical_position_buffer),
               _lib.ptr(pool.length_device), _lib.ptr(pool.page_index.lengths), cache.page_size, stream)

@@ -40,7 +40,14 @@ def _pool_payload(cache: ThreePrecisionCache, index: int, pool):
     n = pool.token_count
     if n == 0:
         return None
-    if cache.compact_key is not None and index < 3:
+    if cache.compact_key is not None and index == 1 and cache.generated_value_precision == "int4":
+        # static INT4 keys at their segment, generated ones after the static INT2 segment
+        # (triton_fourq_attention.py:95-111)
+        static = min(cache.static_int4_tokens, n)
+        key = cache.compact_key.dequantize_range(cache.compact_key.segment_offsets[1], static)
+        if n > static:
+            key = torch.cat((key, cache.compact_key.dequantize_range(cache.generated_k_offset, n - static)), dim=1)
+    elif cache.compact_key is not None and index < 3:
         key = cache.compact_key.dequantize_range(cache.compact_key.segment_offsets[index], n)
     elif pool.fp_k is not None:
         key = pool.fp_k[:, :n].float()
@@ -84,8 +91,6 @@ def triton_mixed_reference(query: torch.Tensor, cache: ThreePrecisionCache, *,
         query = query[:, :, 0]
     if query.ndim != 3 or int(query.shape[0]) != 1:
         raise ValueError("query must be [1,Hq,D]")
-    if cache.generated_value_precision != "int2":
-        raise NotImplementedError("generated INT4 values are not supported by this cache")
     scale = float(sm_scale) if sm_scale is not None else int(query.shape[-1]) ** -0.5
     q = query.float()
     state = None

@@ -60,19 +60,36 @@ def _num_cus(device: torch.device) -> int:
 
 
 def _segments(cache: ThreePrecisionCache, extra_int2: int = 0):
-    """(kind, lo, hi, v_delta) arena ranges of the FP, INT4 and INT2(+generated) pools."""
+    """(kind, lo, hi, v_delta) K-arena ranges of the FP, INT4 and INT2 pools and of the generated
+    tokens: a V row is K position - v_delta.  ``extra_int2`` adds tokens to the tier that generated
+    tokens flush into (the INT2 pool, the INT4 pool with INT4 generated values, the FP pool of a
+    matched-FP cache).
+
+    With INT4 generated values the INT4 pool is two runs, as the reference's mixed reference
+    reassembles it (triton_fourq_attention.py:95-111): its static tokens at the INT4 segment of the
+    K arena, and its generated tokens at ``generated_k_offset`` (after the static INT2 segment),
+    whose values follow the static ones in the INT4-V arena."""
     ck = cache.compact_key if cache.compact_key is not None else cache.bf16_key
     if ck is None:
         raise NotImplementedError("the gfx950 decode path requires a compact INT4/INT2-K or a bf16 K arena")
     k_fp, k_i4, k_i2 = ck.segment_offsets
-    s_fp = cache.fp_pool.token_count + (int(extra_int2) if cache.matched_fp else 0)
+    extra = int(extra_int2)
+    int4_values = cache.compact_int4_value is not None and not cache.matched_fp
+    s_fp = cache.fp_pool.token_count + (extra if cache.matched_fp else 0)
     s_i4 = cache.int4_pool.token_count
+    gen_i4 = 0
+    if int4_values:
+        static = min(cache.static_int4_tokens, s_i4)
+        s_i4, gen_i4 = static, s_i4 - static + extra
     s_i2 = (0 if cache.compact_value is None else cache.compact_value.active_length) \
-        + (0 if cache.matched_fp else int(extra_int2))
+        + (0 if cache.matched_fp or int4_values else extra)
     out = []
     for kind, lo, n in ((_lib.KIND_FP, k_fp, s_fp), (_lib.KIND_INT4, k_i4, s_i4), (_lib.KIND_INT2, k_i2, s_i2)):
         if n > 0:
             out.append((kind, lo, lo + n, lo))
+    if gen_i4 > 0:
+        g = int(cache.generated_k_offset)
+        out.append((_lib.KIND_INT4, g, g + gen_i4, g - s_i4))
     return out
 
 
@@ -149,8 +166,8 @@ def plan_work_items(caches: Sequence[ThreePrecisionCache], hkv: int, num_cus: in
 def max_work_items(num_requests: int, hkv: int, num_cus: int) -> int:
     """Upper bound of ``plan_work_items`` for any cache sizes: the water-filling stops at
     _BLOCKS_PER_CU x CUs items unless the runs alone (one per request, KV head and pool segment,
-    at most 4 per head) are more."""
-    return max(_BLOCKS_PER_CU * max(1, num_cus), 4 * int(num_requests) * int(hkv))
+    at most 5 per head: FP, static INT4, INT2, generated INT4 and the Recent-FP ring) are more."""
+    return max(_BLOCKS_PER_CU * max(1, num_cus), 5 * int(num_requests) * int(hkv))
 
 
 def required_splitk_blocks(cache: ThreePrecisionCache, *, block_n: int = 128, reserve_tokens: int = 0) -> int:
@@ -216,8 +233,10 @@ def _request_words(cache: ThreePrecisionCache, ring=None) -> dict[str, int]:
                         cache.bf16_key.rows if cache.bf16_key is not None else None) if t is not None]
     if any(t.dtype != row for t in rows):
         raise ValueError("FP-V, Recent-FP and BF16-K rows of one cache must share one dtype")
-    i4_packed = i4.packed_v.packed if i4.token_count else None
-    i4_scale = i4.packed_v.scale if i4.token_count else None
+    i4_packed = i4.packed_v.packed if i4.token_count or cache.compact_int4_value is not None else None
+    i4_scale = i4.packed_v.scale if i4.token_count or cache.compact_int4_value is not None else None
+    # per-head stride of the INT4-V rows: the arena's capacity when generated values are INT4
+    i4_stride = cache.compact_int4_value.capacity if cache.compact_int4_value is not None else i4.token_count
     if ck is not None:
         kw = {"k_packed": ck.packed.data_ptr(), "k_scale": ck.scale.data_ptr(), "k_zero": ck.zero_point.data_ptr(),
               "k_capacity": ck.capacity, "k_superblocks": ck.superblock_count,
@@ -230,7 +249,7 @@ def _request_words(cache: ThreePrecisionCache, ring=None) -> dict[str, int]:
         **kw,
         "fp_v": fp.fp_v.data_ptr() if fp.token_count else 0, "fp_stride": fp.token_count,
         "i4_v": i4_packed.data_ptr() if i4_packed is not None else 0,
-        "i4_scale": i4_scale.data_ptr() if i4_scale is not None else 0, "i4_stride": i4.token_count,
+        "i4_scale": i4_scale.data_ptr() if i4_scale is not None else 0, "i4_stride": i4_stride,
         "i2_v": cv.packed.data_ptr() if cv is not None else 0,
         "i2_scale": cv.scale.data_ptr() if cv is not None else 0,
         "i2_zero": cv.zero_point.data_ptr() if cv is not None else 0,

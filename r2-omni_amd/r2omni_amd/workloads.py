@@ -33,6 +33,7 @@ class DecodeConfig:
                                # "bf16k" (v_fourq_k_bf16) or "matched" (matched-FP)
     dtype: str = "bfloat16"    # model dtype of Q/K/V: "bfloat16" or "float16" (values drawn in bf16
                                # and converted, exactly, so both dtypes hold the same numbers)
+    gen_values: str = "int2"   # generated_value_precision: flushed values INT2 (released) or INT4
 
 
 CONFIGS = {
@@ -100,7 +101,7 @@ def build_request_cache(cfg: DecodeConfig, data: RequestData, *, append_capacity
         data.key, data.value, plan, page_size=cfg.page if cfg.page in (16, 32, 64) else 32,
         key_quantization_superblock=cfg.superblock, int2_group_size=cfg.group,
         compact_key_append_capacity=append_capacity, recent_flush_size=128,
-        matched_fp=cfg.variant == "matched",
+        matched_fp=cfg.variant == "matched", generated_value_precision=cfg.gen_values,
         cache_variant={"bf16k": "v_fourq_k_bf16", "int2k": "v_fourq_k_int2_compact"}.get(
             cfg.variant, "v_fourq_k_int4_compact"))
     for i in range(int(data.recent_k.shape[0])):

@@ -113,7 +113,8 @@ def _oracle_for(data, cfg):
     f32 = lambda t: bf16_bits_to_f32(_bf16_np(t))  # noqa: E731
     c = build_cache(f32(data.key), f32(data.value), data.page_offsets.numpy(), data.page_lengths.numpy(),
                     data.page_classes.numpy(), dtype="bfloat16", page_size=cfg.page, superblock=cfg.superblock,
-                    group=cfg.group, recent_capacity=128, append_capacity=260, variant=cfg.variant)
+                    group=cfg.group, recent_capacity=128, append_capacity=260, variant=cfg.variant,
+                    gen_values=cfg.gen_values)
     hist = int(data.key.shape[1])
     rk, rv = f32(data.recent_k), f32(data.recent_v)
     for i in range(rk.shape[0]):
@@ -328,6 +329,75 @@ def test_k_format_variants_decode_matches_oracle(variant, case, hadamard):
     q = bf16_bits_to_f32(_bf16_np(data.query))
     want = output_transform(mixed_reference(q, oc), hadamard)
     _compare(out, want, f"{variant} case {case} hadamard {hadamard}")
+
+
+# ------------------------------------------------------------- INT4 generated values
+@pytest.mark.parametrize("variant", ["int4k", "int2k"])
+def test_generated_int4_values_flush_matches_oracle(variant):
+    """``generated_value_precision="int4"``: the INT4 pool's values live in a compact INT4-V arena
+    with append room; a flush packs the ring's oldest 128 values into it (bit-exact against the
+    oracle), appends their page metadata to the INT4 pool in place, and the decode over the
+    two-run INT4 pool (static keys at their segment, generated keys after the INT2 segment) and
+    the torch mixed reference both match the oracle."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+    from oracle.attention import mixed_reference, output_transform
+    from oracle.cache import append_token
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    cfg = DecodeConfig("t", 16, 2, (0,), (0.2, 0.5, 0.3), recent=120, variant=variant, gen_values="int4")
+    data = make_request(cfg, 1280 + 120, seed=9, device=dev)
+    cache = build_request_cache(cfg, data)
+    oc = _oracle_for(data, cfg)
+    a4 = cache.compact_int4_value
+    assert a4 is not None and cache.int4_pool.packed_v is a4 and cache.generated_value_precision == "int4"
+    static = cache.static_int4_tokens
+    assert static == oc.static_i4 == a4.active_length and a4.capacity == oc.v4_capacity
+    assert cache.compact_value.capacity == oc.v2_capacity
+    np.testing.assert_array_equal(a4.packed[:, :static].cpu().numpy(), oc.v4_packed[:, :static])
+    np.testing.assert_array_equal(a4.scale[:, :static].cpu().numpy(), oc.v4_scale[:, :static])
+    ws = ro.allocate_splitk_workspace(cache, num_query_heads=16, reserve_tokens=260)
+    ex = ro.prepare_splitk_executor(cache, ws)
+    gen = torch.Generator(device=dev).manual_seed(10)
+    stats = ro.DynamicCacheStats()
+    s_hist = int(data.key.shape[1])
+    pos0 = s_hist + 120
+    for step in range(20):
+        q = torch.randn(1, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn(1, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+        pos = pos0 + step
+        kf, vf = bf16_bits_to_f32(_bf16_np(k[0])), bf16_bits_to_f32(_bf16_np(v[0]))
+        qf = bf16_bits_to_f32(_bf16_np(q))
+        rec = cache.recent_fp_pool
+        if rec.active_length < rec.capacity:
+            out = ex(q, append=(k, v, pos, pos))
+            rec.active_length += 1
+            want = mixed_reference(qf, oc, append=(kf, vf))
+            append_token(oc, kf, vf, global_index=pos, logical_position=pos)
+        else:
+            assert ro.append_generated_token(cache, k[0][:, None], v[0][:, None], global_token_index=pos,
+                                             logical_position=pos, stats=stats)
+            ex = ro.prepare_splitk_executor(cache, ws)
+            append_token(oc, kf, vf, global_index=pos, logical_position=pos)
+            out = ex(q)
+            want = mixed_reference(qf, oc)
+            ref = ro.triton_mixed_reference(q, cache)
+            _compare(ref, output_transform(want, False), "torch mixed reference after the flush")
+        torch.cuda.synchronize()
+        _compare(out, output_transform(want, False), f"step {step}")
+    assert stats.flushed_tokens == stats.flushed_int4_value_tokens == 128
+    n4 = cache.int4_pool.token_count
+    assert n4 == oc.pool_tokens[1] == static + 128 == a4.active_length
+    assert cache.int2_pool.token_count == oc.pool_tokens[2] == cache.compact_value.active_length
+    np.testing.assert_array_equal(a4.packed[:, :n4].cpu().numpy(), oc.v4_packed[:, :n4])
+    np.testing.assert_array_equal(a4.scale[:, :n4].cpu().numpy(), oc.v4_scale[:, :n4])
+    pi = cache.int4_pool.page_index
+    assert pi.global_token_indices[static:].tolist() == list(range(s_hist, s_hist + 128))
+    assert pi.logical_positions[static:].tolist() == list(range(s_hist, s_hist + 128))
+    assert pi.global_token_indices.data_ptr() == cache.metadata_arena.int4_global_index_buffer.data_ptr()
+    _check_k_arena(cache, oc)
 
 
 def test_matched_fp_fused_append_then_flush_matches_oracle():

@@ -187,3 +187,66 @@ def test_ring_invariants_match_reference_cache_test():
         append_token(c, tok, tok, global_index=128 + i, logical_position=128 + i)
     assert c.flushed_tokens == 128 and c.recent_active == 1
     assert c.pool_tokens[2] == 32 + 128 and c.k_active == 96 + 128
+
+
+def _bf16_values(rng, shape):
+    return bf16_bits_to_f32(f32_to_bf16_bits(rng.standard_normal(shape).astype(np.float32)))
+
+
+def test_generated_int4_values_reassemble_the_int4_pool():
+    """``generated_value_precision="int4"``: the same appends as the released INT2 mode leave the K
+    arena byte-identical (only the V tier differs, dynamic_fourq_cache.py:207-224); the INT4 pool
+    grows by the flushed tokens, whose keys are the K arena rows after the static INT2 segment (the
+    rows the INT2 mode adds to its INT2 pool) and whose values are the per-token INT4 round trip of
+    the flushed rows, fp32 (fused_value_pack.py:241-256); the static INT4 values stay those of the
+    build, unrounded; the INT2 pool keeps its static tokens."""
+    rng = np.random.default_rng(11)
+    h, s = 2, 256
+    key, value = _bf16_values(rng, (h, s, 128)), _bf16_values(rng, (h, s, 128))
+    offsets, lengths = np.arange(8) * 32, np.full(8, 32)
+    classes = np.array([1, 2, 5, 2, 0, 5, 2, 4])  # FP 64, INT4 96, INT2 64, evicted 32
+    rows_k, rows_v = _bf16_values(rng, (130, h, 128)), _bf16_values(rng, (130, h, 128))
+    caches = {}
+    for mode in ("int2", "int4"):
+        c = build_cache(key, value, offsets, lengths, classes, dtype="bfloat16", append_capacity=260,
+                        gen_values=mode)
+        for i in range(130):
+            append_token(c, rows_k[i], rows_v[i], global_index=s + i, logical_position=s + i)
+        caches[mode] = c
+    c2, c4 = caches["int2"], caches["int4"]
+    for f in ("k_packed", "k_scale", "k_zero"):
+        np.testing.assert_array_equal(getattr(c2, f), getattr(c4, f))
+    assert c2.k_active == c4.k_active == 224 + 128
+    assert c2.pool_tokens == [64, 96, 64 + 128] and c4.pool_tokens == [64, 96 + 128, 64]
+    assert c4.static_i4 == 96 and c4.gen_k_offset == 224 and c4.v4_capacity == 96 + 260
+    assert c2.v2_capacity == 384 and c4.v2_capacity == 128  # the INT2-V arena gets no append room
+    p2, p4 = pool_kv_by_tier(c2), pool_kv_by_tier(c4)
+    np.testing.assert_array_equal(p4["int4"][0][:, :96], p2["int4"][0])
+    np.testing.assert_array_equal(p4["int4"][0][:, 96:], p2["int2"][0][:, 64:])
+    np.testing.assert_array_equal(p4["int2"][0], p2["int2"][0][:, :64])
+    np.testing.assert_array_equal(p4["int2"][1], p2["int2"][1][:, :64])
+    flushed = np.transpose(rows_v[:128], (1, 0, 2))
+    np.testing.assert_array_equal(p4["int4"][1][:, 96:], dequantize_int4_value(*quantize_int4_value(flushed)))
+    static_v = dequantize_int4_value(*quantize_int4_value(value[:, np.r_[32:64, 96:128, 192:224]]))  # INT4 pages
+    np.testing.assert_array_equal(p4["int4"][1][:, :96], static_v)
+    assert not np.array_equal(p2["int4"][1], static_v)  # the released INT4 pool rounds to bf16
+    np.testing.assert_array_equal(bf16_bits_to_f32(f32_to_bf16_bits(static_v)), p2["int4"][1])
+    # both modes attend over the same tokens
+    for c in caches.values():
+        assert sum(k.shape[1] for k, _ in pool_kv_by_tier(c).values()) == 64 + 96 + 64 + 130
+    # capacity: the INT4-V arena refuses a flush past its room
+    c = build_cache(key, value, offsets, lengths, classes, dtype="bfloat16", append_capacity=100, gen_values="int4")
+    try:
+        for i in range(129):
+            append_token(c, rows_k[i], rows_v[i], global_index=s + i, logical_position=s + i)
+    except RuntimeError as e:
+        assert "capacity exhausted" in str(e)
+    else:
+        raise AssertionError("a flush past the INT4-V arena's room must raise")
+
+
+def pool_kv_by_tier(c):
+    from oracle.cache import pool_kv
+
+    names = [n for n, k in zip(("fp", "int4", "int2"), c.pool_tokens) if k] + (["recent"] if c.recent_active else [])
+    return dict(zip(names, pool_kv(c)))

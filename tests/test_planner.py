@@ -10,11 +10,22 @@ from r2omni_amd import _lib
 from r2omni_amd.splitk import _TILE_COST, TILE, _segments, max_work_items, plan_work_items
 
 
-def _fake_cache(s_fp, s_i4, s_i2, recent_cap=128):
+def _fake_cache(s_fp, s_i4, s_i2, recent_cap=128, gen_i4=None):
+    """Pool geometry of a cache; ``gen_i4`` (not None) makes its generated values INT4, with that
+    many tokens flushed into the INT4 pool after the static ones."""
     n = SimpleNamespace
+    i4_arena = None if gen_i4 is None else n(capacity=s_i4 + gen_i4 + 256)
     return n(compact_key=n(segment_offsets=(0, s_fp, s_fp + s_i4)), bf16_key=None, matched_fp=False,
-             fp_pool=n(token_count=s_fp), int4_pool=n(token_count=s_i4), compact_value=n(active_length=s_i2),
-             recent_fp_pool=n(capacity=recent_cap))
+             fp_pool=n(token_count=s_fp), int4_pool=n(token_count=s_i4 + (gen_i4 or 0)),
+             compact_value=n(active_length=s_i2), recent_fp_pool=n(capacity=recent_cap),
+             compact_int4_value=i4_arena, static_int4_tokens=s_i4, generated_k_offset=s_fp + s_i4 + s_i2)
+
+
+def _random_cache(rnd, max_i2=60000, recent_caps=(128,)):
+    sizes = (rnd.choice([0, rnd.randint(1, 20000)]), rnd.choice([0, rnd.randint(1, 40000)]),
+             rnd.choice([0, rnd.randint(1, max_i2)]))
+    gen = rnd.choice([None, None, 0, 128 * rnd.randint(1, 40)])
+    return _fake_cache(*sizes, rnd.choice(recent_caps), gen_i4=gen)
 
 
 @pytest.mark.parametrize("seed", range(40))
@@ -23,8 +34,7 @@ def test_items_cover_every_tile_once_and_respect_the_bound(seed):
     b = rnd.randint(1, 6)
     hkv = rnd.choice([1, 2, 4, 8])
     cus = rnd.choice([8, 64, 256])
-    caches = [_fake_cache(rnd.choice([0, rnd.randint(1, 20000)]), rnd.choice([0, rnd.randint(1, 40000)]),
-                          rnd.choice([0, rnd.randint(1, 60000)])) for _ in range(b)]
+    caches = [_random_cache(rnd) for _ in range(b)]
     extra = rnd.choice([0, 128, 256])
     items, begins = plan_work_items(caches, hkv, cus, extra_int2=extra)
     items = items.tolist()
@@ -42,15 +52,16 @@ def test_items_cover_every_tile_once_and_respect_the_bound(seed):
         segs = _segments(c, extra) + [(_lib.KIND_RECENT, 0, c.recent_fp_pool.capacity, 0)]
         for h in range(hkv):
             for kind, lo, hi, vd in segs:
-                mine = sorted((it[3], it[4]) for it in items if it[0] == r and it[1] == h and it[2] == kind)
+                mine = sorted((it[3], it[4]) for it in items
+                              if it[0] == r and it[1] == h and it[2] == kind and it[5] == lo)
                 t0 = lo // TILE * TILE
                 pos = t0
                 for tile0, ntiles in mine:
                     assert tile0 == pos and ntiles >= 1
                     pos += TILE * ntiles
                 assert pos >= hi and pos - TILE < hi
-                assert all(it[5] == lo and it[6] == hi and it[7] == vd
-                           for it in items if it[0] == r and it[1] == h and it[2] == kind)
+                assert all(it[6] == hi and it[7] == vd
+                           for it in items if it[0] == r and it[1] == h and it[2] == kind and it[5] == lo)
     # launch order: largest (cost-weighted) first
     costs = [it[4] * _TILE_COST[it[2]] for it in items]
     assert all(a >= b for a, b in zip(costs, costs[1:]))
@@ -111,8 +122,7 @@ def test_native_plan_equals_the_python_restatement(seed):
     b = rnd.randint(1, 8)
     hkv = rnd.choice([1, 2, 4, 8])
     cus = rnd.choice([8, 64, 80, 256])
-    caches = [_fake_cache(rnd.choice([0, rnd.randint(1, 20000)]), rnd.choice([0, rnd.randint(1, 40000)]),
-                          rnd.choice([0, rnd.randint(1, 131072)]), rnd.choice([32, 128, 256])) for _ in range(b)]
+    caches = [_random_cache(rnd, 131072, (32, 128, 256)) for _ in range(b)]
     extra = rnd.choice([0, 128, 256])
     got = plan_work_items(caches, hkv, cus, extra_int2=extra)
     want = python_plan_work_items(caches, hkv, cus, extra_int2=extra)
@@ -146,3 +156,24 @@ def test_native_plan_fills_each_items_base_pointers(k_format, group):
     for it in items.tolist():
         assert it[9:15] == item_pointers(words[it[0]], k_format, it[2], it[1], 128 // group)
         assert it[15] == (group if it[2] == _lib.KIND_INT2 else 0)  # v_group: INT2-V items carry the group size
+
+
+@pytest.mark.parametrize("s_fp,s_i4,s_i2,gen,extra", [(640, 1000, 3000, 0, 0), (0, 0, 500, 256, 0),
+                                                      (64, 4096, 0, 384, 128), (100, 37, 2000, 128, 256),
+                                                      (0, 96, 64, 0, 128)])
+def test_generated_int4_runs_map_every_int4_row_once(s_fp, s_i4, s_i2, gen, extra):
+    """With INT4 generated values the INT4 pool is two K runs: its static segment, and the generated
+    keys after the static INT2 segment.  Together their V rows (K position - v_delta) are the INT4-V
+    arena's rows 0..n-1, each once, in that order; no run's K range overlaps another's; ``extra``
+    tokens go to the generated run."""
+    c = _fake_cache(s_fp, s_i4, s_i2, gen_i4=gen)
+    segs = _segments(c, extra)
+    runs4 = [(lo, hi, vd) for kind, lo, hi, vd in segs if kind == _lib.KIND_INT4]
+    rows = [k - vd for lo, hi, vd in runs4 for k in range(lo, hi)]
+    assert rows == list(range(s_i4 + gen + extra))
+    spans = sorted((lo, hi) for _, lo, hi, _ in segs)
+    assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+    i2 = [(lo, hi) for kind, lo, hi, _ in segs if kind == _lib.KIND_INT2]
+    assert i2 == ([(s_fp + s_i4, s_fp + s_i4 + s_i2)] if s_i2 else [])
+    if gen + extra:
+        assert runs4[-1][:2] == (s_fp + s_i4 + s_i2, s_fp + s_i4 + s_i2 + gen + extra)
