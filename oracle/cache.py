@@ -1,7 +1,8 @@
 """numpy restatement of the three-pool SSPA cache and its append/flush (test infrastructure only).
 
-Follows, for the released ``v_fourq_k_int4_compact`` cache with INT2 generated values (and the
-other K formats: ``v_fourq_k_int2_compact`` keeps K in a per-channel affine INT2 arena,
+Follows, for the released ``v_fourq_k_int4_compact`` cache with INT2 generated values (INT4 ones with
+``gen_values="int4"``: precision_pool.py:935-971, dynamic_fourq_cache.py:212-219,
+triton_fourq_attention.py:95-111; and the other K formats: ``v_fourq_k_int2_compact`` keeps K in a per-channel affine INT2 arena,
 compact_int2_key.py:14-153; ``v_fourq_k_bf16`` keeps the pools' K rows in the input dtype; the
 matched-FP cache keeps every surviving page, K and V, in one FP pool in page order,
 precision_pool.py:834-876, with flushes appended to it, dynamic_fourq_cache.py:145-170, 200-204):
