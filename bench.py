@@ -124,16 +124,20 @@ def cpu_baseline(caches, queries, hq: int, budget_s: float = 12.0) -> dict:
         else:
             v2 = dict(v2_packed=np.zeros((h, 0, 32), np.uint8), v2_scale=np.zeros((h, 0, 4, 1), np.float16),
                       v2_zero=np.zeros((h, 0, 4, 1), np.uint8), v2_active=0, v2_capacity=0, group=32)
+        a4 = c.compact_int4_value  # INT4 generated values: the INT4 pool's rows are an arena
+        gen4 = {} if a4 is None else dict(gen_values="int4", v4_capacity=a4.capacity,
+                                          static_i4=c.static_int4_tokens, gen_k_offset=c.generated_k_offset)
         oc = OracleCache(
             dtype="bfloat16", hkv=h, page_size=c.page_size, flush_size=128, fp_v=fp,
-            v4_packed=i4.packed_v.packed.cpu().numpy().reshape(h, i4.token_count, 64) if i4.token_count
+            v4_packed=i4.packed_v.packed.cpu().numpy().reshape(h, -1, 64)[:, :i4.token_count] if i4.token_count
             else np.zeros((h, 0, 64), np.uint8),
-            v4_scale=i4.packed_v.scale.cpu().numpy() if i4.token_count else np.zeros((h, 0, 1), np.float32),
+            v4_scale=i4.packed_v.scale.cpu().numpy()[:, :i4.token_count] if i4.token_count
+            else np.zeros((h, 0, 1), np.float32),
             recent_k=rec.fp_k.float().cpu().numpy(), recent_v=rec.fp_v.float().cpu().numpy(),
             recent_active=rec.active_length, recent_global=rec.global_index_buffer.cpu().numpy(),
             recent_logical=rec.logical_position_buffer.cpu().numpy(),
             recent_page_lengths=rec.page_index.lengths.cpu().numpy(),
-            pool_tokens=[c.fp_pool.token_count, i4.token_count, v2["v2_active"]], **kw, **v2,
+            pool_tokens=[c.fp_pool.token_count, i4.token_count, v2["v2_active"]], **kw, **v2, **gen4,
         )
         oc_list.append(torch_path.from_oracle(oc))  # the packed cache as torch tensors, as the reference holds it
     qs = [q.float().cpu().numpy() for q in queries]
@@ -418,8 +422,9 @@ def flush_bench(cfg, config_id: int, dev, flushes: int = 8) -> dict:
             append_generated_token(cache, nk, nv, global_token_index=pos, logical_position=pos, stats=stats)
             pos += 1
     med = lambda v: round(sorted(v)[len(v) // 2], 2)  # noqa: E731
-    return {"metric": "Recent-FP flush (128 tokens -> compact K + INT2-V, ring shift), one layer",
-            "config": f"cfg{config_id} {cfg.name}", "k_format": cfg.variant, "hkv": h, "flush_tokens": 128,
+    return {"metric": f"Recent-FP flush (128 tokens -> compact K + {cfg.gen_values.upper()}-V, ring shift), one layer",
+            "config": f"cfg{config_id} {cfg.name}", "k_format": cfg.variant, "gen_values": cfg.gen_values,
+            "hkv": h, "flush_tokens": 128,
             "flushes": flushes, "us_gpu_median": med(gpu), "us_host_median": med(host),
             "note": "GPU: HIP events around the flush's launches on the compute stream; host: wall clock of "
                     "flush_full_recent_pool (the launches are asynchronous); median over the timed flushes"}
@@ -434,7 +439,8 @@ def decode_steps_bench(cfg, config_id: int, dev, steps: int, layers: int) -> dic
     from r2omni_amd.workloads import build_request_cache, make_request
 
     out = {"metric": "batched decode step (flush inside the batch)", "config": f"cfg{config_id} {cfg.name}",
-           "steps": steps, "layers": layers, "requests": len(cfg.lengths)}
+           "k_format": cfg.variant, "gen_values": cfg.gen_values, "steps": steps, "layers": layers,
+           "requests": len(cfg.lengths)}
     for mode in ("eager", "step_graph"):
         decs, positions = [], None
         for layer in range(layers):
@@ -1001,6 +1007,9 @@ def main() -> int:
     ap.add_argument("--variant", choices=("int4k", "int2k", "bf16k", "matched"), default="int4k",
                     help="K format of the layer caches: compact INT4-K (default), compact INT2-K, "
                          "v_fourq_k_bf16 or matched-FP")
+    ap.add_argument("--gen-values", choices=("int2", "int4"), default="int2",
+                    help="generated_value_precision of the layer caches: flushed values INT2 (released, default) "
+                         "or INT4 (the INT4 pool's values in a compact arena with append room)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="leave configuration 4 (decode tok/s) out of the line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -1071,6 +1080,8 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     if args.variant != "int4k":
         cfg = dataclasses.replace(cfg, variant=args.variant)
+    if args.gen_values != "int2":
+        cfg = dataclasses.replace(cfg, gen_values=args.gen_values)
     if args.prefill:
         print(json.dumps(prefill_bench(cfg, args.config, dev)), flush=True)
         return 0
@@ -1117,7 +1128,8 @@ def main() -> int:
     if not args.no_e2e:
         _log("e2e (configuration 4) ...")
         e2e = e2e_decode_bench(dev, **e2e_kw)
-    traffic, traffic_src = traffic_from_profile() if args.config == 2 and args.variant == "int4k" else (None, None)
+    traffic, traffic_src = traffic_from_profile() if args.config == 2 and args.variant == "int4k" \
+        and args.gen_values == "int2" else (None, None)
     line = {
         "metric": "packed-KV decode attn: HBM GB/s (% peak), us/layer @32k ctx; decode tok/s",
         "value": round(gbs, 2),
@@ -1133,8 +1145,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int4-k/bf16|int4|int2-v, f16/bf16 mfma, f32 accumulate",
         "data": "synthetic (seeded N(0,1) bf16, 4 key outlier channels x8, seeded per-page V tiers)",
-        "config": {"workload": f"cfg{args.config} {cfg.name}" + ("" if args.variant == "int4k" else f" {args.variant}"),
-                   "k_format": args.variant, "hq": cfg.hq, "hkv": cfg.hkv,
+        "config": {"workload": f"cfg{args.config} {cfg.name}" + ("" if args.variant == "int4k" else f" {args.variant}")
+                               + ("" if args.gen_values == "int2" else " int4-generated"),
+                   "k_format": args.variant, "gen_values": args.gen_values, "hq": cfg.hq, "hkv": cfg.hkv,
                    "context_lengths": list(cfg.lengths), "v_tiers_bf16_int4_int2": list(cfg.tier_probs),
                    "recent_window": cfg.recent, "k_superblock": cfg.superblock, "int2_group": cfg.group,
                    "rotated_layer_caches": args.layers, "algorithmic_bytes_per_call": nbytes, "output_hadamard": True},

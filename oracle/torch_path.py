@@ -51,6 +51,9 @@ class TorchCache:
     v2_zero: torch.Tensor
     recent_k: torch.Tensor
     recent_v: torch.Tensor
+    int4_generated: bool = False  # INT4 generated values: the INT4 pool's keys in two runs, fp32 values
+    static_i4: int = 0
+    gen_k_offset: int = 0
 
 
 def from_oracle(c: OracleCache) -> TorchCache:
@@ -58,14 +61,16 @@ def from_oracle(c: OracleCache) -> TorchCache:
     dt = torch.bfloat16 if c.dtype == "bfloat16" else torch.float16
     rows = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dt)  # noqa: E731
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
-    s_i2 = c.pool_tokens[2]
+    s_i4, s_i2 = c.pool_tokens[1], c.pool_tokens[2]
     return TorchCache(
         variant=c.variant, dtype=dt, superblock=c.superblock, group=c.group, pool_tokens=tuple(c.pool_tokens),
         k_segments=tuple(c.k_segments), k_packed=t(c.k_packed), k_scale=t(c.k_scale), k_zero=t(c.k_zero),
         k_rows=None if c.k_rows is None else rows(c.k_rows),
-        fp_v=rows(c.fp_v), v4_packed=t(c.v4_packed), v4_scale=t(c.v4_scale),
+        fp_v=rows(c.fp_v), v4_packed=t(c.v4_packed[:, :s_i4]), v4_scale=t(c.v4_scale[:, :s_i4]),
         v2_packed=t(c.v2_packed[:, :s_i2]), v2_scale=t(c.v2_scale[:, :s_i2]), v2_zero=t(c.v2_zero[:, :s_i2]),
         recent_k=rows(c.recent_k[:, : c.recent_active]), recent_v=rows(c.recent_v[:, : c.recent_active]),
+        int4_generated=c.gen_values == "int4" and c.variant != "matched", static_i4=c.static_i4,
+        gen_k_offset=c.gen_k_offset,
     )
 
 
@@ -94,7 +99,15 @@ def pool_kv(c: TorchCache):
     if s_i4:
         nib = torch.stack((c.v4_packed & 15, (c.v4_packed >> 4) & 15), dim=-1).to(torch.int16)
         signed = torch.where(nib >= 8, nib - 16, nib).reshape(c.v4_packed.shape[0], s_i4, 128)
-        out.append((_keys(c, seg[1], s_i4), (signed.float() * c.v4_scale.float()).to(c.dtype).float()))
+        v = signed.float() * c.v4_scale.float()
+        if c.int4_generated:  # triton_fourq_attention.py:95-111; the compact INT4-V arena stays fp32
+            static = min(c.static_i4, s_i4)
+            k = _keys(c, seg[1], static)
+            if s_i4 > static:
+                k = torch.cat((k, _keys(c, c.gen_k_offset, s_i4 - static)), dim=1)
+            out.append((k, v))
+        else:  # PackedTensor.dequantize rounds to the input dtype (packed_kv_layout.py:30-32)
+            out.append((_keys(c, seg[1], s_i4), v.to(c.dtype).float()))
     if s_i2:
         h = c.v2_packed.shape[0]
         codes = torch.stack([(c.v2_packed >> (2 * k)) & 3 for k in range(4)], dim=-1).reshape(h, s_i2, 128)

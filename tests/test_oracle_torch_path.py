@@ -16,9 +16,11 @@ def _bf16(x):
     return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(x, np.float32)))
 
 
-@pytest.mark.parametrize("variant,sb,group", [("int4k", 32, 32), ("int4k", 128, 128), ("int2k", 32, 64),
-                                              ("bf16k", 32, 32), ("matched", 32, 32)])
-def test_torch_path_equals_numpy_oracle(variant, sb, group):
+@pytest.mark.parametrize("variant,sb,group,gen", [("int4k", 32, 32, "int2"), ("int4k", 128, 128, "int2"),
+                                                  ("int2k", 32, 64, "int2"), ("bf16k", 32, 32, "int2"),
+                                                  ("matched", 32, 32, "int2"), ("int4k", 32, 32, "int4"),
+                                                  ("int2k", 128, 128, "int4")])
+def test_torch_path_equals_numpy_oracle(variant, sb, group, gen):
     rng = np.random.default_rng(5)
     h, pages = 2, 23
     hist = pages * 32 + 16  # a partial last page: the K arena ends inside a superblock
@@ -28,7 +30,7 @@ def test_torch_path_equals_numpy_oracle(variant, sb, group):
     lengths = np.array([32] * pages + [16])
     classes = rng.choice([1, 2, 5], size=pages + 1, p=(0.2, 0.5, 0.3))
     oc = build_cache(key, value, offsets, lengths, classes, dtype="bfloat16", page_size=32, superblock=sb,
-                     group=group, variant=variant)
+                     group=group, variant=variant, gen_values=gen)
     q = _bf16(rng.standard_normal((1, 8, 128)))
     steps = 60 if variant == "bf16k" else 140  # v_fourq_k_bf16 refuses a flush
     for step in range(steps):
