@@ -32,11 +32,13 @@ def _f32(t):
     return bf16_bits_to_f32(_bf16_np(t))
 
 
-def _layer0(cfg_id, dev):
+def _layer0(cfg_id, dev, gen_values="int2"):
     """The bench's layer-0 requests of configuration ``cfg_id`` (seed 1000 * layer + request)."""
+    import dataclasses
+
     from r2omni_amd.workloads import CONFIGS, build_request_cache, make_request
 
-    cfg = CONFIGS[cfg_id]
+    cfg = dataclasses.replace(CONFIGS[cfg_id], gen_values=gen_values)
     datas = [make_request(cfg, total, seed=r, device=dev) for r, total in enumerate(cfg.lengths)]
     caches = [build_request_cache(cfg, d) for d in datas]
     return cfg, datas, caches
@@ -47,7 +49,8 @@ def _oracle(data, cfg):
 
     oc = build_cache(_f32(data.key), _f32(data.value), data.page_offsets.numpy(), data.page_lengths.numpy(),
                      data.page_classes.numpy(), dtype=cfg.dtype, page_size=cfg.page, superblock=cfg.superblock,
-                     group=cfg.group, recent_capacity=128, append_capacity=260, variant=cfg.variant)
+                     group=cfg.group, recent_capacity=128, append_capacity=260, variant=cfg.variant,
+                     gen_values=cfg.gen_values)
     hist = int(data.key.shape[1])
     rk, rv = _f32(data.recent_k), _f32(data.recent_v)
     for i in range(rk.shape[0]):
@@ -64,10 +67,11 @@ def _check_arenas(cache, oc, what):
     if cache.fp_pool.token_count:
         np.testing.assert_array_equal(_f32(cache.fp_pool.fp_v[:, : cache.fp_pool.token_count]), oc.fp_v)
     i4 = cache.int4_pool
-    if i4.token_count:
-        np.testing.assert_array_equal(i4.packed_v.packed.cpu().numpy().reshape(h, i4.token_count, 64), oc.v4_packed)
-        np.testing.assert_array_equal(i4.packed_v.scale.cpu().numpy().reshape(h, i4.token_count, 1).view(np.uint32),
-                                      oc.v4_scale.view(np.uint32))
+    if i4.token_count:  # the PackedTensor of the released mode, or the INT4-V arena (rows up to its capacity)
+        n = i4.token_count
+        np.testing.assert_array_equal(i4.packed_v.packed.cpu().numpy().reshape(h, -1, 64)[:, :n], oc.v4_packed[:, :n])
+        np.testing.assert_array_equal(i4.packed_v.scale.cpu().numpy().reshape(h, -1, 1)[:, :n].view(np.uint32),
+                                      oc.v4_scale[:, :n].view(np.uint32))
     cv = cache.compact_value
     if cv is not None and cv.active_length:
         a = cv.active_length
@@ -124,18 +128,19 @@ def test_config_full_size_arenas_and_decode_match_oracle(cfg_id):
                   flush=True)
 
 
-def test_config1_sixty_four_steps_with_flush_match_oracle():
+@pytest.mark.parametrize("gen_values", ["int2", "int4"])
+def test_config1_sixty_four_steps_with_flush_match_oracle(gen_values):
     """Configuration 1's decode loop as the manager runs it (qwen_sspa_attention.py:1794-1826): the
     first token finds the ring full and goes through append_generated_token (flush of 128 tokens
-    into INT4-K and INT2-V, then the ring append) and a re-prepared executor; the next 63 are fused
-    into the split-K call."""
+    into INT4-K and INT2-V, or INT4-V with INT4 generated values, then the ring append) and a
+    re-prepared executor; the next 63 are fused into the split-K call."""
     import r2omni_amd as ro
     from oracle.attention import mixed_reference, output_transform
     from oracle.cache import append_token
 
     dev = _cuda()
-    print("[cfg1] building the layer-0 cache at full size", flush=True)
-    cfg, (data,), (cache,) = _layer0(1, dev)
+    print(f"[cfg1] building the layer-0 cache at full size, generated values {gen_values}", flush=True)
+    cfg, (data,), (cache,) = _layer0(1, dev, gen_values)
     oc = _oracle(data, cfg)
     _check_arenas(cache, oc, "cfg1 build")
     ws = ro.allocate_splitk_workspace(cache, num_query_heads=cfg.hq)
@@ -169,6 +174,7 @@ def test_config1_sixty_four_steps_with_flush_match_oracle():
             print(f"[cfg1] step {step}: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
         pos += 1
     assert stats.flushed_tokens == 128 and cache.recent_fp_pool.active_length == 64
+    assert stats.flushed_int4_value_tokens == (128 if gen_values == "int4" else 0)
     _check_arenas(cache, oc, "cfg1 after 64 steps")
     print(f"[cfg1] 64 steps: worst max-abs {worst[0]:.2e}, worst mean-abs {worst[1]:.2e}", flush=True)
 
