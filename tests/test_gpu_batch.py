@@ -13,8 +13,9 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("use_graph", [True, False])
-@pytest.mark.parametrize("variant", ["int4k", "int2k", "matched"])
-def test_batched_decoder_flushes_inside_the_batch(variant, use_graph):
+@pytest.mark.parametrize("variant,gen_values", [("int4k", "int2"), ("int2k", "int2"), ("matched", "int2"),
+                                                ("int4k", "int4")])
+def test_batched_decoder_flushes_inside_the_batch(variant, gen_values, use_graph):
     import r2omni_amd as ro
     from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
     from oracle.attention import mixed_reference
@@ -27,7 +28,8 @@ def test_batched_decoder_flushes_inside_the_batch(variant, use_graph):
     shapes = [(1024, 125), (2048, 121), (640, 116)]
     cfgs, datas, caches, oracles = [], [], [], []
     for r, (hist, recent) in enumerate(shapes):
-        cfg = DecodeConfig("b", hq, hkv, (0,), (0.15, 0.45, 0.4), recent=recent, variant=variant)
+        cfg = DecodeConfig("b", hq, hkv, (0,), (0.15, 0.45, 0.4), recent=recent, variant=variant,
+                           gen_values=gen_values)
         data = make_request(cfg, hist + recent, seed=500 + r, device=dev)
         cfgs.append(cfg)
         datas.append(data)
@@ -42,7 +44,7 @@ def test_batched_decoder_flushes_inside_the_batch(variant, use_graph):
         q = torch.randn(3, hq, 128, generator=gen, device=dev).to(torch.bfloat16)
         k = torch.randn(3, hkv, 128, generator=gen, device=dev).to(torch.bfloat16)
         v = torch.randn(3, hkv, 128, generator=gen, device=dev).to(torch.bfloat16)
-        print(f"[batch {variant} graph={use_graph}] step {step}", flush=True)
+        print(f"[batch {variant} gen={gen_values} graph={use_graph}] step {step}", flush=True)
         out = dec.step(q, k, v, global_token_index=pos, logical_position=pos)
         torch.cuda.synchronize()
         for r in range(3):
@@ -64,6 +66,11 @@ def test_batched_decoder_flushes_inside_the_batch(variant, use_graph):
         np.testing.assert_array_equal(bf16_bits_to_f32(_bf16_np(rec.fp_k[:, :r_act])), oc.recent_k[:, :r_act])
         np.testing.assert_array_equal(bf16_bits_to_f32(_bf16_np(rec.fp_v[:, :r_act])), oc.recent_v[:, :r_act])
         _check_k_arena(c, oc)
+        if gen_values == "int4":  # the flushed values went to the INT4-V arena, bit for bit
+            a4, n4 = c.compact_int4_value, c.int4_pool.token_count
+            assert st.flushed_int4_value_tokens == 128 and n4 == oc.pool_tokens[1] == a4.active_length
+            np.testing.assert_array_equal(a4.packed[:, :n4].cpu().numpy(), oc.v4_packed[:, :n4])
+            np.testing.assert_array_equal(a4.scale[:, :n4].cpu().numpy(), oc.v4_scale[:, :n4])
     assert dec.replans == 1 + 3  # the initial plan and one per flushing step
     if use_graph:
         assert dec.graph_captures == dec.replans
