@@ -122,7 +122,13 @@ typedef struct r2o_plan_config {
  * tiles / tiles_per_item)) items), numbers their partial slots in (request, kv head) order into
  * group_begin [n_groups + 1], and writes the items to items[0 .. *n_items) largest first.  With
  * reqs (host copies of the request descriptors) each item's base pointers are filled in, else they
- * are 0.  Returns R2O_EINVAL for an inconsistent input or when more than max_items would result.
+ * are 0; INT2-V items get v_group = int2_group either way (int2_group must be 32, 64 or 128 whenever
+ * a run has kind 2).  Every run needs tile0 >= 0, tile0 % 32 == 0, tile0 <= lo <= hi <=
+ * tile0 + 32 * ntiles; with reqs also 0 <= kvh < n_groups / n_reqs, its tiles inside the K arena
+ * (k_capacity) or the ring (recent_capacity), and its V rows [lo - v_delta, hi - v_delta) inside the
+ * pool (fp_stride / i4_stride / i2_stride), since the partial kernel reads whole K tiles at the
+ * items' base pointers.  Returns R2O_EINVAL for an inconsistent input or when more than max_items
+ * would result.
  * No counterpart in the reference's launch plan (one program per BLOCK_N tile, counted while
  * preparing the executor, triton_fourq_splitk.py:1772-1817); it replaces that preparation step. */
 int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, const r2o_plan_config* cfg,
@@ -172,6 +178,12 @@ typedef struct r2o_decode_params {
                                        in its launch arguments instead of reading group_begin on the
                                        device (one dependent memory round trip less); it must equal
                                        the device array.  Read on the host during the call only. */
+    int64_t partial_capacity;       /* partial-state slots the workspace holds (rows of partial_max /
+                                       partial_sum / partial_out): every entry point returns R2O_EINVAL
+                                       before any launch when n_items exceeds it, as the reference sizes
+                                       and checks its workspace first (triton_fourq_splitk.py:1607-1692,
+                                       qwen_sspa_attention.py:1157-1160).  r2o_decode_noalloc sets it
+                                       itself. */
 } r2o_decode_params;
 
 /* Split-K partial pass.  Replaces _fourq_page_partial_kernel / _full_head_page_partial_kernel
@@ -185,7 +197,9 @@ int r2o_decode_combine(const r2o_decode_params* params, void* stream);
 
 /* Workspace-free decode: r2o_decode_partial then r2o_decode_combine on `stream`, with the split-K
  * partial states held in a library-owned device array (one per GPU, kept until the process ends)
- * instead of params->partial_max / partial_sum / partial_out, which are ignored and may be NULL.
+ * instead of params->partial_max / partial_sum / partial_out / partial_capacity, which are ignored
+ * and may be NULL / 0.  The array of the stream's device is used (hipStreamGetDevice); its address
+ * is looked up once per device, by r2o_decode_noalloc_init or else by the first call on that device.
  * No counterpart in the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops).  Allocates nothing (no hipMalloc / hipFree).
  * Limit: params->n_items <= 1024 work items (8.1 MiB of partial states), else R2O_EINVAL before any
@@ -193,6 +207,14 @@ int r2o_decode_combine(const r2o_decode_params* params, void* stream);
  * slot a launch reads is written first by that launch): calls that overlap on one GPU (different
  * streams, or threads without ordering) race on it. */
 int r2o_decode_noalloc(const r2o_decode_params* params, void* stream);
+
+/* Set-up of r2o_decode_noalloc on `device`: looks up the device address of that GPU's partial-state
+ * array (with the device current for the lookup; the caller's current device is restored).  No
+ * counterpart in the reference; for the same callers as r2o_decode_noalloc.  Call it once per device
+ * before capturing r2o_decode_noalloc into a HIP graph, so that no runtime lookup falls inside the
+ * capture.  Allocates nothing.  R2O_EINVAL for a device index out of range, R2O_ELAUNCH if the
+ * lookup fails. */
+int r2o_decode_noalloc_init(int device);
 
 /* ----------------------------------------------------------------- pack / append --------- */
 

@@ -830,7 +830,7 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
     const int t_end = min((int)it.ntiles, t_begin + per);
     // device-state mode: the ring length lives in device memory (advanced by the previous step's
     // combine), so a captured launch stays valid from step to step
-    const int recent_len = p.step_positions ? min(*it.ring_length, (int)it.hi) : p.recent_len[b];
+    const int recent_len = min(p.step_positions ? *it.ring_length : p.recent_len[b], (int)it.hi);
     const bool app = p.do_append != 0;
     const int valid_end = recent_len + (app ? 1 : 0);
     if (t_begin >= t_end || valid_end == 0) return;
@@ -1185,6 +1185,7 @@ int validate(const r2o_decode_params* p) {
         !p->query || !p->out)
         return R2O_EINVAL;
     if (p->n_items <= 0 || p->n_items > 0x7fffffff || p->batch <= 0 || p->batch > R2O_MAX_BATCH) return R2O_EINVAL;
+    if (p->n_items > p->partial_capacity) return R2O_EINVAL;  // every item writes one partial-state slot
     if (p->hkv <= 0 || p->hq <= 0 || p->hq > R2O_MAX_HEADS || p->hq % p->hkv || p->hq / p->hkv > R2O_MAX_GQA)
         return R2O_EINVAL;
     if (!(p->superblock == 32 || p->superblock == 64 || p->superblock == 128)) return R2O_EINVAL;
@@ -1216,19 +1217,23 @@ static __device__ __align__(256) float scratch[kScratchFloats];
 
 namespace {
 
-// Device address of this GPU's `scratch` (the host-side name is only a stand-in): looked up once
-// per device, with that device current, on its first r2o_decode_noalloc call.  Returns nullptr if
+// Device address of `scratch` on `dev` (the host-side name is only a stand-in): looked up once per
+// device, with that device current for the lookup (the caller's current device is restored), by
+// r2o_decode_noalloc_init or by the first r2o_decode_noalloc call on that device.  Returns nullptr if
 // the lookup fails.
-float* scratch_address() {
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+float* scratch_address(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
     float* ptr = g_scratch[dev].load(std::memory_order_acquire);
-    if (ptr == nullptr) {
-        void* addr = nullptr;
-        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) return nullptr;
-        ptr = static_cast<float*>(addr);
-        g_scratch[dev].store(ptr, std::memory_order_release);
-    }
+    if (ptr != nullptr) return ptr;
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return nullptr;
+    if (e != hipSuccess || addr == nullptr) return nullptr;
+    ptr = static_cast<float*>(addr);
+    g_scratch[dev].store(ptr, std::memory_order_release);
     return ptr;
 }
 
@@ -1283,15 +1288,25 @@ int r2o_decode_combine(const r2o_decode_params* params, void* stream) {
     return launch_combine(*params, (hipStream_t)stream);
 }
 
+int r2o_decode_noalloc_init(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return R2O_ELAUNCH;
+    if (device < 0 || device >= n || device >= kMaxDevices) return R2O_EINVAL;
+    return scratch_address(device) ? R2O_OK : R2O_ELAUNCH;
+}
+
 int r2o_decode_noalloc(const r2o_decode_params* params, void* stream) {
     if (!params) return R2O_EINVAL;
     if (params->n_items > kScratchSlots) return R2O_EINVAL;  // more partial states than `scratch` holds
-    float* base = scratch_address();
+    int dev = -1;  // the array of the GPU the stream runs on, whatever device is current
+    if (hipStreamGetDevice((hipStream_t)stream, &dev) != hipSuccess) return R2O_EINVAL;
+    float* base = scratch_address(dev);
     if (base == nullptr) return R2O_ELAUNCH;
     r2o_decode_params p = *params;  // the caller's partial pointers are ignored
     p.partial_out = base;
     p.partial_max = base + kScratchSlots * 16 * 128;
     p.partial_sum = p.partial_max + kScratchSlots * 16;
+    p.partial_capacity = kScratchSlots;
     const int rc = validate(&p);
     if (rc) return rc;
     const int lrc = launch_decode(p, (hipStream_t)stream);

@@ -46,6 +46,21 @@ void split_run(int64_t nt, int64_t n_items, double late_share, int64_t w, std::v
     if (f < nt) out.back().size += nt - f;  // rounding left a remainder: the last item takes it
 }
 
+// A run's tiles and valid range: tile0 >= 0, aligned to a tile, tile0 <= lo < hi <= tile0 + 32 * ntiles.
+// With the request descriptors, the tiles must lie inside the request's K arena (or ring) and the
+// V rows [lo - v_delta, hi - v_delta) inside the run's V pool: the partial kernel reads whole K tiles
+// and clamps V rows to the valid range, at the base pointers the planner computes from these.
+bool run_in_bounds(const r2o_plan_run& r, const r2o_request_desc* reqs, int64_t k_format) {
+    const int64_t end = r.tile0 + kTile * r.ntiles;
+    if (r.tile0 < 0 || r.tile0 % kTile || r.lo < r.tile0 || r.hi <= r.lo || r.hi > end) return false;
+    if (!reqs) return true;
+    const r2o_request_desc& d = reqs[r.req];
+    if (r.kind == kKindRecent) return r.v_delta == 0 && end <= d.recent_capacity;
+    if (end > d.k_capacity || (k_format != R2O_K_BF16 && (!d.k_operands || d.k_superblocks <= 0))) return false;
+    const int64_t stride = r.kind == 0 ? d.fp_stride : (r.kind == 1 ? d.i4_stride : d.i2_stride);
+    return r.lo - r.v_delta >= 0 && r.hi - r.v_delta <= stride;
+}
+
 }  // namespace
 
 extern "C" int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, const r2o_plan_config* cfg,
@@ -56,12 +71,17 @@ extern "C" int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, con
     if (cfg->waves_per_item <= 0 || cfg->min_tiles_per_item <= 0 || cfg->tiles_per_item <= 0 ||
         cfg->blocks_per_cu <= 0)
         return R2O_EINVAL;
+    if (n_reqs <= 0 || n_groups % n_reqs) return R2O_EINVAL;
+    const int64_t hkv = n_groups / n_reqs;
     if (reqs && !(k_format == R2O_K_INT4 || k_format == R2O_K_BF16 || k_format == R2O_K_INT2)) return R2O_EINVAL;
-    if (reqs && !(int2_group == 32 || int2_group == 64 || int2_group == 128)) return R2O_EINVAL;
+    const bool group_ok = int2_group == 32 || int2_group == 64 || int2_group == 128;
     int64_t total_tiles = 0;
     for (int64_t i = 0; i < n_runs; ++i) {
         const r2o_plan_run& r = runs[i];
-        if (r.kind < 0 || r.kind > kKindRecent || r.ntiles < 1 || r.req < 0 || (reqs && r.req >= n_reqs)) return R2O_EINVAL;
+        if (r.kind < 0 || r.kind > kKindRecent || r.ntiles < 1 || r.req < 0 || r.req >= n_reqs) return R2O_EINVAL;
+        if (r.kvh < 0 || r.kvh >= hkv) return R2O_EINVAL;
+        if (r.kind == 2 && !group_ok) return R2O_EINVAL;  // every INT2-V item carries its group size
+        if (!run_in_bounds(r, reqs, k_format)) return R2O_EINVAL;
         total_tiles += r.ntiles;
     }
     // Water-filling: one more item for the run whose items are the most expensive (ties: the
@@ -99,17 +119,17 @@ extern "C" int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, con
     // Items in (request, KV head) order, which numbers their partial slots; then launched largest first.
     std::vector<r2o_work_item> planned;
     planned.reserve(total);
+    // Group g = request g / hkv, KV head g % hkv: the runs come in group order, every group has one.
     int64_t group = 0;
-    int64_t group_req = 0, group_kvh = 0;
     group_begin[0] = 0;
     std::vector<Split> parts;
     for (int64_t i = 0; i < n_runs; ++i) {
         const r2o_plan_run& r = runs[i];
-        if (r.req != group_req || r.kvh != group_kvh) {
-            if (++group >= n_groups) return R2O_EINVAL;
+        const int64_t gid = r.req * hkv + r.kvh;
+        if (gid != group) {
+            if (gid != group + 1 || i == 0) return R2O_EINVAL;
+            group = gid;
             group_begin[group] = (int32_t)planned.size();
-            group_req = r.req;
-            group_kvh = r.kvh;
         }
         split_run(r.ntiles, counts[i], late_share, cfg->waves_per_item, parts);
         for (const Split& s : parts) {
@@ -135,8 +155,9 @@ extern "C" int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, con
 
     // Base pointers of each item's head (the pointer arithmetic the kernel would otherwise do).
     const int64_t k_row = k_format == R2O_K_INT4 ? 64 : (k_format == R2O_K_INT2 ? 32 : 256);
-    const int64_t groups = 128 / (reqs ? int2_group : 128);
+    const int64_t groups = group_ok ? 128 / int2_group : 1;  // INT2-V scale / zero columns per token
     for (r2o_work_item& it : planned) {
+        if (it.kind == 2) it.v_group = int2_group;
         if (!reqs) continue;
         const r2o_request_desc& d = reqs[it.req];
         const int64_t h = it.kvh;
@@ -155,7 +176,6 @@ extern "C" int r2o_plan_work_items(const r2o_plan_run* runs, int64_t n_runs, con
             it.v_base = d.i4_v + h * d.i4_stride * 64;
             it.v_scale = d.i4_scale + h * d.i4_stride;
         } else {
-            it.v_group = int2_group;
             it.v_base = d.i2_v + h * d.i2_stride * 32;
             it.v_scale = d.i2_scale + h * d.i2_stride * groups;
             it.v_zero = d.i2_zero + h * d.i2_stride * groups;

@@ -54,6 +54,7 @@ class DecodeParams(ctypes.Structure):
         ("append_logical", c_i64 * MAX_BATCH),
         ("row_dtype", c_i64),
         ("group_begin_host", ctypes.c_void_p),
+        ("partial_capacity", c_i64),
     ]
 
 
@@ -96,6 +97,7 @@ _SIGNATURES = {
     "r2o_decode_partial": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_combine": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_noalloc": (ctypes.POINTER(DecodeParams), c_vp),
+    "r2o_decode_noalloc_init": (ctypes.c_int,),
     "r2o_pack_int4_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                         c_vp),
     "r2o_pack_int2_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,

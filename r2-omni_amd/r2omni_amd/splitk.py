@@ -317,6 +317,8 @@ class SplitKExecutor:
         p.n_items = self.n_items
         p.partial_max, p.partial_sum = ws.partial_max.data_ptr(), ws.partial_sum.data_ptr()
         p.partial_out = ws.partial_output.data_ptr()
+        p.partial_capacity = min(int(ws.partial_max.shape[0]), int(ws.partial_sum.shape[0]),
+                                 int(ws.partial_output.shape[0]))
         p.batch, p.hq, p.hkv = len(self.caches), self.num_query_heads, self.num_key_value_heads
         p.superblock, p.int2_group, p.page_size = self.superblock, self.int2_group, self.page_size
         p.row_dtype = _lib.dtype_code(self.caches[0].recent_fp_pool.fp_k.dtype)
@@ -370,6 +372,8 @@ class SplitKExecutor:
             raise ValueError(f"workspace-free decode holds at most {_lib.NOALLOC_MAX_ITEMS} work items")
         p, query, fused = self._prepare_call(query, append, out)
         p.partial_max = p.partial_sum = p.partial_out = None
+        p.partial_capacity = 0
+        _noalloc_init(query.device)
         _lib.check(_lib.load().r2o_decode_noalloc(ctypes.byref(p), ctypes.c_void_p(_lib.stream_of(query.device))),
                    "r2o_decode_noalloc")
         self._finish_call(fused)
@@ -428,6 +432,18 @@ class SplitKExecutor:
         lib = _lib.load()
         _lib.check(lib.r2o_decode_partial(ctypes.byref(p), stream), "r2o_decode_partial")
         _lib.check(lib.r2o_decode_combine(ctypes.byref(p), stream), "r2o_decode_combine")
+
+
+_NOALLOC_READY: set[int] = set()
+
+
+def _noalloc_init(device: torch.device) -> None:
+    """Look up the device's partial-state array once (r2o_decode_noalloc_init), so that a later
+    call under HIP graph capture makes no runtime lookup."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _NOALLOC_READY:
+        _lib.call("r2o_decode_noalloc_init", index)
+        _NOALLOC_READY.add(index)
 
 
 def _per_request(value, b: int) -> list[int]:

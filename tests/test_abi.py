@@ -78,6 +78,16 @@ def test_host_side_validation_rejects_bad_arguments_without_a_gpu():
     assert rc == 1
     params = _lib.DecodeParams()
     assert lib.r2o_decode_partial(ctypes.byref(params), None) == 1
+    # a workspace with fewer partial-state slots than work items is refused before any launch (the
+    # pointers are never dereferenced on the host, so placeholders do)
+    params = _lib.DecodeParams(reqs=0x1000, items=0x2000, group_begin=0x3000, n_items=40, partial_max=0x4000,
+                               partial_sum=0x5000, partial_out=0x6000, query=0x7000, out=0x8000, batch=1, hq=28,
+                               hkv=4, superblock=32, int2_group=32, page_size=64, k_format=_lib.K_INT4,
+                               partial_capacity=39)
+    assert lib.r2o_decode_partial(ctypes.byref(params), None) == 1
+    assert lib.r2o_decode_combine(ctypes.byref(params), None) == 1
+    params.partial_capacity = 0
+    assert lib.r2o_decode_partial(ctypes.byref(params), None) == 1
     assert lib.r2o_build_target() == b"gfx950"
     # the planner refuses runs whose groups do not match the group count, without a GPU
     run = _lib.PlanRun(0, 0, _lib.KIND_RECENT, 0, 4, 0, 128, 0)

@@ -141,13 +141,17 @@ def test_native_plan_fills_each_items_base_pointers(k_format, group):
     from r2omni_amd.splitk import _plan
 
     rnd = random.Random(7)
-    caches = [_fake_cache(4096, 8192, 16384), _fake_cache(0, 3072, 640)]
+    sizes = [(4096, 8192, 16384), (0, 3072, 640)]
+    caches = [_fake_cache(*s) for s in sizes]
     hkv = 4
     words = []
-    for r in range(len(caches)):
+    for r, (s_fp, s_i4, s_i2) in enumerate(sizes):
         w = {f: (r + 1) * (1 << 40) + (i + 1) * (1 << 32) for i, f in enumerate(_lib.REQUEST_FIELDS)}
-        for f in ("k_capacity", "k_superblocks", "fp_stride", "i4_stride", "i2_stride", "recent_capacity"):
-            w[f] = rnd.randint(1, 1 << 16)
+        # random sizes that still hold every run (the planner rejects runs outside them)
+        need = {"k_capacity": -(-(s_fp + s_i4 + s_i2) // 128) * 128, "k_superblocks": 1, "fp_stride": s_fp,
+                "i4_stride": s_i4, "i2_stride": s_i2, "recent_capacity": 128}
+        for f, lo in need.items():
+            w[f] = rnd.randint(lo, lo + (1 << 14))
         if k_format == _lib.K_BF16:
             w["k_operands"] = 0
         words.append(w)
@@ -177,3 +181,74 @@ def test_generated_int4_runs_map_every_int4_row_once(s_fp, s_i4, s_i2, gen, extr
     assert i2 == ([(s_fp + s_i4, s_fp + s_i4 + s_i2)] if s_i2 else [])
     if gen + extra:
         assert runs4[-1][:2] == (s_fp + s_i4 + s_i2, s_fp + s_i4 + s_i2 + gen + extra)
+
+
+def _plan_raw(runs, reqs=None, n_reqs=1, n_groups=1, k_format=_lib.K_INT4, int2_group=32):
+    """r2o_plan_work_items on explicit runs: (status, items as int64 rows)."""
+    import ctypes
+
+    import torch
+
+    arr = (_lib.PlanRun * len(runs))(*[_lib.PlanRun(*r) for r in runs])
+    cfg = _lib.PlanConfig(num_cus=8, blocks_per_cu=2, tiles_per_item=8, waves_per_item=4, min_tiles_per_item=4,
+                          late_share=1.0)
+    items = torch.zeros(64, 16, dtype=torch.int64)
+    begins = torch.zeros(n_groups + 1, dtype=torch.int32)
+    n = ctypes.c_int64(0)
+    rc = _lib.load().r2o_plan_work_items(arr, len(runs), ctypes.byref(cfg), None if reqs is None else reqs.data_ptr(),
+                                         n_reqs, k_format, int2_group, items.data_ptr(), 64, begins.data_ptr(),
+                                         n_groups, ctypes.byref(n))
+    return rc, items[: n.value].tolist()
+
+
+def _reqs(k_capacity=1024, strides=(256, 256, 256), recent=128):
+    import torch
+
+    w = {f: (i + 1) << 32 for i, f in enumerate(_lib.REQUEST_FIELDS)}
+    w.update(k_capacity=k_capacity, k_superblocks=k_capacity // 32, fp_stride=strides[0], i4_stride=strides[1],
+             i2_stride=strides[2], recent_capacity=recent)
+    return torch.tensor([[w[f] for f in _lib.REQUEST_FIELDS]], dtype=torch.int64)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_int2_items_carry_their_group_without_descriptors(group):
+    """The partial kernel takes the INT2-V group size from the item alone, so the planner writes it
+    whether or not the request descriptors are given."""
+    runs = [(0, 0, _lib.KIND_INT2, 0, 8, 0, 256, 0), (0, 0, _lib.KIND_RECENT, 0, 4, 0, 128, 0)]
+    rc, items = _plan_raw(runs, int2_group=group)
+    assert rc == 0 and items
+    assert all(it[15] == (group if it[2] == _lib.KIND_INT2 else 0) for it in items)
+    assert _plan_raw(runs, int2_group=48)[0] == 1            # an INT2 run needs a valid group
+    assert _plan_raw(runs[1:], int2_group=0)[0] == 0         # a plan without INT2 runs does not
+
+
+def test_planner_rejects_runs_outside_their_arena():
+    """Runs whose tiles, valid range, KV head or V rows would make the partial kernel read outside the
+    request's arenas are refused before any item is written."""
+    ok = (0, 1, _lib.KIND_INT4, 64, 4, 70, 180, 0)
+    reqs = _reqs()
+    good = [ok[:1] + (0,) + ok[2:], ok]
+    assert _plan_raw(good, reqs, n_groups=2)[0] == 0
+    # every group (request g / hkv, KV head g % hkv) has runs, in group order
+    assert _plan_raw([ok], reqs, n_groups=2)[0] == 1
+    assert _plan_raw(good[::-1], reqs, n_groups=2)[0] == 1
+    assert _plan_raw(good, reqs, n_groups=3)[0] == 1
+    bad = {
+        "kvh past the request's heads": (0, 2, _lib.KIND_INT4, 64, 4, 70, 180, 0),
+        "request past the batch": (1, 1, _lib.KIND_INT4, 64, 4, 70, 180, 0),
+        "negative kvh": (0, -1, _lib.KIND_INT4, 64, 4, 70, 180, 0),
+        "lo > hi": (0, 1, _lib.KIND_INT4, 64, 4, 180, 70, 0),
+        "empty range": (0, 1, _lib.KIND_INT4, 64, 4, 100, 100, 0),
+        "tile0 > lo": (0, 1, _lib.KIND_INT4, 96, 4, 70, 180, 0),
+        "unaligned tile0": (0, 1, _lib.KIND_INT4, 48, 4, 70, 180, 0),
+        "hi past the tiles": (0, 1, _lib.KIND_INT4, 64, 2, 70, 180, 0),
+        "tiles past the K arena": (0, 1, _lib.KIND_INT4, 960, 4, 960, 1000, 0),
+        "V rows past the pool": (0, 1, _lib.KIND_INT2, 64, 8, 70, 300, 0),
+        "V rows before the pool": (0, 1, _lib.KIND_FP, 64, 4, 70, 180, 100),
+        "ring tiles past the ring": (0, 1, _lib.KIND_RECENT, 0, 8, 0, 256, 0),
+    }
+    for what, run in bad.items():
+        assert _plan_raw([good[0], run], reqs, n_groups=2)[0] == 1, what
+        if what in ("kvh past the request's heads", "negative kvh", "request past the batch", "lo > hi",
+                    "empty range", "tile0 > lo", "unaligned tile0", "hi past the tiles"):
+            assert _plan_raw([good[0], run], None, n_groups=2)[0] == 1, what  # checked without descriptors too

@@ -97,3 +97,46 @@ def test_noalloc_rejects_more_work_items_than_it_holds():
     ex.n_items = _lib.NOALLOC_MAX_ITEMS + 1
     with pytest.raises(ValueError, match="at most"):
         ex.call_noalloc(q)
+
+
+def test_noalloc_init_checks_the_device_index():
+    from r2omni_amd import _lib
+
+    _cuda()
+    lib = _lib.load()
+    assert lib.r2o_decode_noalloc_init(-1) == 1
+    assert lib.r2o_decode_noalloc_init(torch.cuda.device_count()) == 1
+    assert lib.r2o_decode_noalloc_init(0) == 0
+    assert lib.r2o_decode_noalloc_init(0) == 0  # looked up once; later calls return at once
+
+
+def test_noalloc_call_captured_in_a_graph_replays_the_eager_result():
+    """The callers r2o_decode_noalloc is for capture it: after the set-up call (made by the first
+    call_noalloc, outside the capture) the captured launch pair replays bit-identical outputs, also
+    when an eager workspace-free call of another cache overwrote the partial-state array between
+    the replays."""
+    from r2omni_amd.batch import _capture_launches
+    from r2omni_amd.workloads import DecodeConfig
+
+    dev = _cuda()
+    cfg = DecodeConfig("graph", 28, 4, (0,), (0.15, 0.45, 0.4), recent=128)
+    ex, q, _ = _executor(cfg, (4096 + 128, 2048 + 128), 440, dev, True)
+    small_cfg = DecodeConfig("small", 16, 2, (0,), (0.2, 0.5, 0.3), recent=64)
+    small, qs, _ = _executor(small_cfg, (1024 + 64,), 450, dev, False)
+    want_small = small(qs).clone()
+    want = ex(q).clone()
+    out = torch.full_like(want, 3.0)
+    ex.call_noalloc(q, out=out)  # set-up outside the capture
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    out.fill_(5.0)
+    side = torch.cuda.Stream(device=dev)
+    graph = _capture_launches(dev, side, lambda: ex.call_noalloc(q, out=out))
+    for replay in range(3):
+        print(f"[noalloc] graph replay {replay}", flush=True)
+        out.fill_(float(replay + 11))
+        other = small.call_noalloc(qs, out=torch.empty_like(want_small))  # the same array, other contents
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(other.view(torch.int16), want_small.view(torch.int16)), replay
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), replay
