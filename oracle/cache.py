@@ -98,6 +98,8 @@ class OracleCache:
     pool_tokens: list = field(default_factory=list)   # [fp, int4, int2(incl. generated)]
     int2_global: list = field(default_factory=list)
     int2_logical: list = field(default_factory=list)
+    int4_global: list = field(default_factory=list)    # INT4 pool's token indices (static, then flushed
+    int4_logical: list = field(default_factory=list)   # with INT4 generated values)
     flushed_tokens: int = 0
     tail_dequant_tokens: int = 0
     # BF16-K variants: K rows in physical order [H, cap, D] float32 (values of the input dtype)
@@ -207,7 +209,7 @@ def build_cache(key, value, page_offsets, page_lengths, page_classes, *, dtype: 
         recent_logical=np.full(recent_capacity, -1, np.int64),
         recent_page_lengths=np.zeros(pages, np.int64),
         pool_tokens=[len(fp_t), len(i4_t), len(i2_t)],
-        int2_global=list(i2_t), int2_logical=list(i2_t),
+        int2_global=list(i2_t), int2_logical=list(i2_t), int4_global=list(i4_t), int4_logical=list(i4_t),
         variant=variant, k_rows=k_rows,
         gen_values=gen_values, v4_capacity=v4_cap, static_i4=len(i4_t), gen_k_offset=active,
     )
@@ -304,8 +306,10 @@ def append_token(c: OracleCache, new_k, new_v, *, global_index: int, logical_pos
                                "covering the requested generation horizon")
         else:
             c.tail_dequant_tokens += _flush_key_superblock(c, key_block)
-            if c.gen_values == "int4":  # dynamic_fourq_cache.py:212-219
+            if c.gen_values == "int4":  # dynamic_fourq_cache.py:212-219, metadata :240-243
                 _flush_value_int4(c, value_block)
+                c.int4_global.extend(g_block.tolist())
+                c.int4_logical.extend(l_block.tolist())
                 c.pool_tokens[1] += f
             else:
                 _flush_value_int2(c, value_block)

@@ -16,9 +16,13 @@ against closed forms and invariants in tests/test_oracle_*.py):
 * the Recent-FP ring state after ``append_generated_token`` (dynamic_fourq_cache.py:172-267);
 * ``triton_mixed_reference`` attention outputs on those caches (triton_fourq_attention.py:72-125);
 * the matched-FP and K-BF16 caches (precision_pool.py:834-980): survivor order, pool K rows,
-  the matched flush append (dynamic_fourq_cache.py:145-170) and the K-BF16 flush refusal (:226-230).
+  the matched flush append (dynamic_fourq_cache.py:145-170) and the K-BF16 flush refusal (:226-230);
+* generated INT4 values (``generated_value_precision="int4"``, precision_pool.py:935-956): the
+  INT4-V arena with its static and flushed values (fused_value_pack.py:197-330), the INT4 pool's
+  metadata after a flush (dynamic_fourq_cache.py:212-219, 236-243) and the attention over the INT4
+  pool's two K runs (triton_fourq_attention.py:95-111).
 
-Usage:  python tests/golden/make_golden.py
+Usage:  python tests/golden/make_golden.py [fixture names from _VARIANTS]
 """
 from __future__ import annotations
 
@@ -267,6 +271,104 @@ def _variant_case(name, *, variant, seq, hkv, dtype, page_size, sb, group, tier_
     print(f"wrote {path}: flushes at {flushed_at}, refused at {refused_at}")
 
 
+def _gen_int4_case(name, *, seq, hkv, dtype, page_size, sb, group, tier_probs, appends, seed):
+    """``generated_value_precision="int4"`` (precision_pool.py:935-956): the INT4 pool's values are a
+    ``CompactInt4ValueArena`` with append room (fused_value_pack.py:197-330), a flush packs the 128
+    oldest ring values into it (dynamic_fourq_cache.py:212-219), and ``triton_mixed_reference``
+    reassembles the INT4 pool's keys from two K arena runs (triton_fourq_attention.py:95-111)."""
+    sys.path.insert(0, REFERENCE)
+    from r2omni.sspa.policy.page_assignment import build_page_table, project_token_bits_to_pages
+    from r2omni.sspa.runtime.cache_plan import build_layer_compression_plan
+    from r2omni.sspa.runtime.precision_pool import build_three_precision_cache
+    from r2omni.sspa.runtime.dynamic_fourq_cache import DynamicCacheStats, append_generated_token
+    from r2omni.sspa.kernels.triton_fourq_attention import triton_mixed_reference
+
+    gen = torch.Generator().manual_seed(seed)
+    d = 128
+    key = torch.randn(hkv, seq, d, generator=gen).to(dtype)
+    outlier = torch.randperm(d, generator=gen)[:4]
+    key[:, :, outlier] = (key[:, :, outlier].float() * 8.0).to(dtype)
+    value = torch.randn(hkv, seq, d, generator=gen).to(dtype)
+    modality = _modality(seq, gen)
+    table = build_page_table(modality, page_size=page_size, protected_mask=torch.zeros(seq, dtype=torch.bool),
+                             recent_mask=torch.zeros(seq, dtype=torch.bool))
+    probs = torch.tensor(tier_probs, dtype=torch.float)
+    page_tier = torch.multinomial(probs, table.num_pages, replacement=True, generator=gen)
+    bits_per_tier = torch.tensor([16, 4, 2], dtype=torch.int8)
+    bits = torch.empty(seq, dtype=torch.int8)
+    for page, (off, ln) in enumerate(zip(table.offsets.tolist(), table.lengths.tolist())):
+        bits[off : off + ln] = bits_per_tier[page_tier[page]]
+    assignment = project_token_bits_to_pages(table, bits)
+    plan = build_layer_compression_plan(0, assignment, recent_fp_capacity=128)
+    cache = build_three_precision_cache(key, value, plan, page_size=page_size, key_quantization_superblock=sb,
+                                        int2_group_size=group, compact_key_append_capacity=260,
+                                        recent_flush_size=128, generated_value_precision="int4")
+    query = torch.randn(1, hkv * 8, d, generator=gen)
+    record = {"key": _np(key), "value": _np(value), "dtype": np.array(str(dtype)),
+              "page_offsets": _np(plan.page_offsets), "page_lengths": _np(plan.page_lengths),
+              "page_classes": _np(plan.page_classes.to(torch.int64)), "page_size": np.array(page_size),
+              "superblock": np.array(sb), "group": np.array(group), "query": _np(query),
+              "gen_values": np.array("int4")}
+
+    def snapshot(prefix):
+        ck = cache.compact_key
+        blocks = -(-ck.active_length // ck.superblock_size)
+        record[prefix + "k_packed"] = _np(ck.packed[:, : ck.active_length])
+        record[prefix + "k_scale"] = _np(ck.scale[:, :blocks])
+        record[prefix + "k_zero"] = _np(ck.zero_point[:, :blocks])
+        record[prefix + "k_active"] = np.array(ck.active_length)
+        record[prefix + "k_capacity"] = np.array(ck.capacity)
+        record[prefix + "k_segments"] = np.array(ck.segment_offsets)
+        record[prefix + "generated_k_offset"] = np.array(cache.generated_k_offset)
+        record[prefix + "static_int4_tokens"] = np.array(cache.static_int4_tokens)
+        v4 = cache.compact_int4_value
+        record[prefix + "v4_packed"] = _np(v4.packed[:, : v4.active_length])
+        record[prefix + "v4_scale"] = _np(v4.scale[:, : v4.active_length])
+        record[prefix + "v4_active"] = np.array(v4.active_length)
+        record[prefix + "v4_capacity"] = np.array(v4.capacity)
+        cv = cache.compact_value
+        record[prefix + "v2_packed"] = _np(cv.packed[:, : cv.active_length])
+        record[prefix + "v2_scale"] = _np(cv.scale[:, : cv.active_length])
+        record[prefix + "v2_zero"] = _np(cv.zero_point[:, : cv.active_length])
+        record[prefix + "v2_active"] = np.array(cv.active_length)
+        record[prefix + "v2_capacity"] = np.array(cv.capacity)
+        fp = cache.fp_pool
+        record[prefix + "fp_v"] = (_np(fp.fp_v) if fp.token_count
+                                   else np.zeros((hkv, 0, d), np.uint16 if dtype == torch.bfloat16 else np.float16))
+        rec = cache.recent_fp_pool
+        record[prefix + "recent_k"] = _np(rec.fp_k[:, : rec.active_length])
+        record[prefix + "recent_v"] = _np(rec.fp_v[:, : rec.active_length])
+        record[prefix + "recent_active"] = np.array(rec.active_length)
+        record[prefix + "recent_global"] = _np(rec.global_index_buffer[: rec.active_length])
+        record[prefix + "pool_tokens"] = np.array([fp.token_count, cache.int4_pool.token_count,
+                                                   cache.int2_pool.token_count, rec.token_count])
+        i4, i2 = cache.int4_pool, cache.int2_pool
+        record[prefix + "int4_global"] = _np(i4.page_index.global_token_indices[: i4.token_count])
+        record[prefix + "int4_logical"] = _np(i4.page_index.logical_positions[: i4.token_count])
+        record[prefix + "int2_global"] = _np(i2.page_index.global_token_indices[: i2.token_count])
+        record[prefix + "attn"] = _np(triton_mixed_reference(query, cache).float())
+
+    snapshot("build_")
+    stats = DynamicCacheStats()
+    app_k = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
+    app_v = torch.randn(appends, hkv, 1, d, generator=gen).to(dtype)
+    record["append_k"] = _np(app_k)
+    record["append_v"] = _np(app_v)
+    flushed_at = []
+    for step in range(appends):
+        if append_generated_token(cache, app_k[step], app_v[step], global_token_index=seq + step,
+                                  logical_position=seq + step, stats=stats):
+            flushed_at.append(step)
+    record["flushed_at"] = np.array(flushed_at, dtype=np.int64)
+    record["tail_dequant_tokens"] = np.array(stats.local_tail_dequant_tokens)
+    record["flushed_int4_value_tokens"] = np.array(stats.flushed_int4_value_tokens)
+    snapshot("after_")
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, **record)
+    print(f"wrote {path}: flushes at {flushed_at}, tail tokens {stats.local_tail_dequant_tokens}, "
+          f"INT4 value tokens flushed {stats.flushed_int4_value_tokens}")
+
+
 def main() -> None:
     only = set(sys.argv[1:])
     if only:
@@ -292,12 +394,23 @@ def main() -> None:
     # compact INT2-K caches: Qwen-style 32-token K blocks, and MiniCPM-style 128-token blocks in fp16
     _VARIANTS["k_int2_tiered_bf16"]()
     _VARIANTS["k_int2_sb128_fp16"]()
+    # generated INT4 values (generated_value_precision="int4")
+    _VARIANTS["gen_int4_bf16"]()
+    _VARIANTS["gen_int4_sb128_fp16"]()
 
 
 _VARIANTS = {
     "k_int2_tiered_bf16": lambda: _variant_case("k_int2_tiered_bf16", variant="int2k", seq=333, hkv=2,
                                                 dtype=torch.bfloat16, page_size=32, sb=32, group=32,
                                                 tier_probs=(0.2, 0.4, 0.3, 0.1), appends=140, seed=16),
+    # generated INT4 values: Qwen-style geometry (K superblock 32, INT2 group 32), two flushes, the
+    # second after a ring that refilled across the first flush's K tail
+    "gen_int4_bf16": lambda: _gen_int4_case("gen_int4_bf16", seq=333, hkv=2, dtype=torch.bfloat16, page_size=32,
+                                            sb=32, group=32, tier_probs=(0.2, 0.5, 0.3), appends=260, seed=18),
+    # fp16 with 64-token pages, K superblock 128, INT2 group 64
+    "gen_int4_sb128_fp16": lambda: _gen_int4_case("gen_int4_sb128_fp16", seq=420, hkv=2, dtype=torch.float16,
+                                                  page_size=64, sb=128, group=64, tier_probs=(0.15, 0.45, 0.4),
+                                                  appends=131, seed=19),
     "k_int2_sb128_fp16": lambda: _variant_case("k_int2_sb128_fp16", variant="int2k", seq=300, hkv=2,
                                                dtype=torch.float16, page_size=64, sb=128, group=128,
                                                tier_probs=(0.1, 0.2, 0.7, 0.0), appends=131, seed=17),

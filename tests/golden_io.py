@@ -11,14 +11,23 @@ def _all_names():
     return sorted(os.path.splitext(os.path.basename(p))[0] for p in glob.glob(os.path.join(HERE, "*.npz")))
 
 
+def _keys(name):
+    return set(np.load(os.path.join(HERE, name + ".npz"), allow_pickle=False).files)
+
+
 def fixture_names():
-    """Fixtures of the compact INT4-K cache (v_fourq_k_int4_compact)."""
-    return [n for n in _all_names() if "variant" not in np.load(os.path.join(HERE, n + ".npz"), allow_pickle=False)]
+    """Fixtures of the compact INT4-K cache (v_fourq_k_int4_compact) with INT2 generated values."""
+    return [n for n in _all_names() if not {"variant", "gen_values"} & _keys(n)]
+
+
+def gen_int4_fixture_names():
+    """Fixtures of the compact INT4-K cache with INT4 generated values (generated_value_precision="int4")."""
+    return [n for n in _all_names() if "gen_values" in _keys(n)]
 
 
 def variant_fixture_names():
     """Fixtures of the BF16-K caches (matched-FP and v_fourq_k_bf16)."""
-    return [n for n in _all_names() if "variant" in np.load(os.path.join(HERE, n + ".npz"), allow_pickle=False)]
+    return [n for n in _all_names() if "variant" in _keys(n)]
 
 
 def load(name):

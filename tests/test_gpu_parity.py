@@ -559,3 +559,98 @@ def test_k_format_variant_build_and_appends_bit_exact_against_reference_fixtures
                      global_index=seq + step, logical_position=seq + step)
     assert flushed == list(g["flushed_at"]) and refused == int(g["refused_at"])
     check("after_")
+
+
+# ------------------------------------------------------------- generated INT4 values (fixtures)
+from golden_io import gen_int4_fixture_names  # noqa: E402
+
+
+@pytest.mark.parametrize("name", gen_int4_fixture_names())
+def test_generated_int4_values_bit_exact_against_reference_fixtures(name):
+    """generated_value_precision="int4" on the GPU against the reference's own cache states: the build
+    (the INT4-V arena with room, the INT2-V arena without), every append and flush (the oldest ring
+    values packed into the INT4-V arena, their indices into the INT4 pool), then the decode against
+    the reference's attention output and against the oracle on the same bf16 query."""
+    import r2omni_amd as ro
+    from oracle.attention import mixed_reference
+    from oracle.cache import append_token, build_cache
+    from oracle.quant import bf16_bits_to_f32
+
+    dev = _cuda()
+    g = load(name)
+    dt = str(g["dtype"])
+    key = _to_torch(g["key"], dt, dev)
+    value = _to_torch(g["value"], dt, dev)
+    plan = ro.plan_from_pages(g["page_offsets"], g["page_lengths"], g["page_classes"], recent_fp_capacity=128,
+                              device=dev)
+    cache = ro.build_three_precision_cache(
+        key, value, plan, page_size=int(g["page_size"]), key_quantization_superblock=int(g["superblock"]),
+        int2_group_size=int(g["group"]), compact_key_append_capacity=260, recent_flush_size=128,
+        generated_value_precision="int4")
+    oc = build_cache(as_f32(g["key"], dt), as_f32(g["value"], dt), g["page_offsets"], g["page_lengths"],
+                     g["page_classes"], dtype=dt.replace("torch.", ""), page_size=int(g["page_size"]),
+                     superblock=int(g["superblock"]), group=int(g["group"]), recent_capacity=128,
+                     append_capacity=260, gen_values="int4")
+    q = torch.from_numpy(g["query"]).to(dev).to(torch.bfloat16)
+    qf = bf16_bits_to_f32(_bf16_np(q))
+
+    def check(prefix):
+        torch.cuda.synchronize()
+        ck, cv, v4 = cache.compact_key, cache.compact_value, cache.compact_int4_value
+        k = ck.active_length
+        blocks = -(-k // ck.superblock_size)
+        assert k == int(g[prefix + "k_active"]) and ck.capacity == int(g[prefix + "k_capacity"])
+        assert cache.generated_k_offset == int(g[prefix + "generated_k_offset"])
+        assert cache.static_int4_tokens == int(g[prefix + "static_int4_tokens"])
+        np.testing.assert_array_equal(ck.packed[:, :k].cpu().numpy(), g[prefix + "k_packed"])
+        np.testing.assert_array_equal(_bits16(ck.scale[:, :blocks]), g[prefix + "k_scale"].view(np.uint16))
+        np.testing.assert_array_equal(ck.zero_point[:, :blocks].cpu().numpy(), g[prefix + "k_zero"])
+        n4 = v4.active_length
+        assert n4 == int(g[prefix + "v4_active"]) and v4.capacity == int(g[prefix + "v4_capacity"])
+        np.testing.assert_array_equal(v4.packed[:, :n4].cpu().numpy(), g[prefix + "v4_packed"])
+        np.testing.assert_array_equal(v4.scale[:, :n4].cpu().numpy().view(np.uint32),
+                                      g[prefix + "v4_scale"].view(np.uint32))
+        a = cv.active_length
+        assert a == int(g[prefix + "v2_active"]) and cv.capacity == int(g[prefix + "v2_capacity"])
+        np.testing.assert_array_equal(cv.packed[:, :a].cpu().numpy(), g[prefix + "v2_packed"])
+        np.testing.assert_array_equal(_bits16(cv.scale[:, :a]), g[prefix + "v2_scale"].view(np.uint16))
+        np.testing.assert_array_equal(cv.zero_point[:, :a].cpu().numpy(), g[prefix + "v2_zero"])
+        if cache.fp_pool.token_count:
+            np.testing.assert_array_equal(_bits16(cache.fp_pool.fp_v), g[prefix + "fp_v"].view(np.uint16))
+        rec = cache.recent_fp_pool
+        r = rec.active_length
+        assert r == int(g[prefix + "recent_active"]) == int(rec.length_device.item())
+        np.testing.assert_array_equal(_bits16(rec.fp_k[:, :r]), g[prefix + "recent_k"].view(np.uint16))
+        np.testing.assert_array_equal(_bits16(rec.fp_v[:, :r]), g[prefix + "recent_v"].view(np.uint16))
+        np.testing.assert_array_equal(rec.global_index_buffer[:r].cpu().numpy(), g[prefix + "recent_global"])
+        i4, i2 = cache.int4_pool, cache.int2_pool
+        pools = [cache.fp_pool.token_count, i4.token_count, i2.token_count, r]
+        assert pools == [int(v) for v in g[prefix + "pool_tokens"]]
+        np.testing.assert_array_equal(i4.page_index.global_token_indices[: i4.token_count].cpu().numpy(),
+                                      g[prefix + "int4_global"])
+        np.testing.assert_array_equal(i4.page_index.logical_positions[: i4.token_count].cpu().numpy(),
+                                      g[prefix + "int4_logical"])
+        np.testing.assert_array_equal(i2.page_index.global_token_indices[: i2.token_count].cpu().numpy(),
+                                      g[prefix + "int2_global"])
+        ws = ro.allocate_splitk_workspace(cache, num_query_heads=int(q.shape[1]))
+        out = ro.prepare_splitk_executor(cache, ws)(q)
+        torch.cuda.synchronize()
+        print(f"[gen-int4] {name} {prefix}decode", flush=True)
+        _compare(out, mixed_reference(qf, oc), f"{name} {prefix}decode vs oracle")
+        _compare(out, g[prefix + "attn"].reshape(out.shape), f"{name} {prefix}decode vs reference")
+
+    stats = ro.DynamicCacheStats()
+    check("build_")
+    ak = _to_torch(g["append_k"], dt, dev)
+    av = _to_torch(g["append_v"], dt, dev)
+    seq = int(g["key"].shape[1])
+    flushed = []
+    for step in range(int(ak.shape[0])):
+        if ro.append_generated_token(cache, ak[step], av[step], global_token_index=seq + step,
+                                     logical_position=seq + step, stats=stats):
+            flushed.append(step)
+        append_token(oc, as_f32(g["append_k"][step, :, 0], dt), as_f32(g["append_v"][step, :, 0], dt),
+                     global_index=seq + step, logical_position=seq + step)
+    assert flushed == list(g["flushed_at"])
+    assert stats.local_tail_dequant_tokens == int(g["tail_dequant_tokens"])
+    check("after_")
