@@ -43,16 +43,18 @@ def _log(msg: str) -> None:
 
 
 def _clock_warmup(dev, ms: float = 50.0) -> None:
-    """Keep the GPU busy for ``ms`` milliseconds right before a timed window (a loop of bf16 matrix
-    products): after the host-side setup the clocks are low and take ~20 ms of load to come up."""
+    """Keep the GPU busy for ``ms`` milliseconds right before a timed window, with memory-bound work
+    (device copies of 256 MiB) like the kernels measured here: after the host-side setup the clocks
+    are low and take ~20 ms of load to come up.  (Matrix products as the warm-up load measured ~2 %
+    slower decode calls afterwards than this build's own calls did; an idle gap of 50 ms, ~12 %.)"""
     import torch
 
-    a = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
+    a = torch.empty(1 << 28, device=dev, dtype=torch.uint8)
     b = torch.empty_like(a)
     t0 = time.perf_counter()
     while (time.perf_counter() - t0) * 1e3 < ms:
         for _ in range(8):
-            torch.mm(a, a, out=b)
+            b.copy_(a)
         torch.cuda.synchronize()
     del a, b
 
@@ -73,16 +75,32 @@ def _gc_paused():
             gc.enable()
 
 
-def _time_events(fn, steps: int, stream) -> float:
+def _time_events(fn, steps: int, stream, warm_ms: float = 30.0, lead: int = 16) -> float:
+    """Average milliseconds of ``fn(i)`` over ``steps`` calls, HIP events on ``stream``.
+
+    Steady state: ``fn`` itself runs untimed for ``warm_ms`` milliseconds first (synchronising every 64
+    calls, so the host never runs far ahead), which brings the GPU clocks up under the very load that
+    is timed, and then ``lead`` more untimed calls are queued right before the start event, with no
+    host synchronisation in between, so that the timed calls start on a busy GPU and none of them
+    waits on the host's first launch."""
     import torch
 
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     with _gc_paused():
-        start.record(stream)
-        for i in range(steps):
+        t0, i = time.perf_counter(), 0
+        while (time.perf_counter() - t0) * 1e3 < warm_ms:
+            for _ in range(64):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
+        for _ in range(lead):
             fn(i)
+            i += 1
+        start.record(stream)
+        for k in range(steps):
+            fn(i + k)
         stop.record(stream)
         torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps  # ms
@@ -228,7 +246,6 @@ def dma_floor(dev, nbytes: int, *, steps: int = 200, warmup: int = 300, blocks: 
         if rc != 0:
             raise RuntimeError(f"r2o_bench_dma_read failed ({rc})")
 
-    _clock_warmup(dev)
     for i in range(warmup):
         one(i)
     ms = _time_events(one, steps, stream)
@@ -786,10 +803,17 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
 
 
 def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed_base: int = 0) -> dict:
-    """Build ``n_layers`` distinct layer caches of ``cfg`` (seeds 1000 * layer + request) and time one
-    decode-attention layer call (partial + combine, no append) rotating over them with HIP events on
-    the launch stream; then the partial kernel alone the same way (back-to-back partial launches: an
-    event pair around each partial inside the call sequence would add ~2 us of its own)."""
+    """Build ``n_layers`` distinct layer caches of ``cfg`` (seeds 1000 * layer + request) and time the
+    decode-attention layer call rotating over them with HIP events on the launch stream.
+
+    The call is timed as the manager issues it at every decode step (qwen_sspa_attention.py:1794-1826):
+    partial + combine with the step's K/V row appended to each Recent-FP ring by the fused append.  Each
+    ring then holds min(its tokens, capacity - 1) tokens (host-mode ring lengths, so every call rewrites
+    the same slot) and the call attends over those plus the new token: at a full 128-token window the
+    same 128 ring tokens as the call without the append, which is timed too.  The partial kernel alone
+    is timed by back-to-back partial launches (an event pair around each partial inside the call
+    sequence would add ~2 us of its own).  Every timed window follows ~30 ms of its own untimed calls and
+    a queued lead of them (``_time_events``) and times exactly ``steps`` calls."""
     import torch
 
     import r2omni_amd as ro
@@ -816,27 +840,63 @@ def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed
     sp = ctypes.c_void_p(stream.cuda_stream)
     params = [ex._params(q, ex.workspace.output, None) for _, q, ex in layers]
     refs = [ctypes.byref(p) for p in params]
-    n_rot = len(layers)
-    f_partial, f_combine = lib.r2o_decode_partial, lib.r2o_decode_combine
 
-    def step(i):
-        r = refs[i % n_rot]
-        f_partial(r, sp)
-        f_combine(r, sp)
+    # the step's new K/V rows ([B, Hkv, 128], the model dtype) and the ring lengths they are appended at
+    b = len(cfg.lengths)
+    gen = torch.Generator(device=dev).manual_seed(97)
+    row_dtype = layers[0][0][0].recent_fp_pool.fp_k.dtype
+    app_k = torch.randn(b, cfg.hkv, 128, generator=gen, device=dev).to(row_dtype)
+    app_v = torch.randn(b, cfg.hkv, 128, generator=gen, device=dev).to(row_dtype)
+    ring_n = [min(int(c.recent_fp_pool.active_length), c.recent_fp_pool.capacity - 1) for c in layers[0][0]]
+    nbytes_app = nbytes + sum(cfg.hkv * 512 * (n + 1 - int(c.recent_fp_pool.active_length)) + cfg.hkv * 512
+                              for n, c in zip(ring_n, layers[0][0]))
+    params_app = []
+    for caches, q, ex in layers:
+        p = _lib.DecodeParams.from_buffer_copy(ex._params(q, ex.workspace.output, None))
+        p.do_append, p.append_k, p.append_v = 1, app_k.data_ptr(), app_v.data_ptr()
+        for r, c in enumerate(caches):
+            p.recent_len[r] = ring_n[r]
+            p.append_global[r] = p.append_logical[r] = int(c.compact_key.active_length if c.compact_key is not None
+                                                           else c.bf16_key.active_length) + ring_n[r]
+        params_app.append(p)
+    refs_app = [ctypes.byref(p) for p in params_app]
+    n_rot = len(layers)
+    f_call, f_partial = lib.r2o_decode, lib.r2o_decode_partial
+
+    def call(i):  # the manager's call (r2o_decode: partial + combine) with the fused append
+        f_call(refs_app[i % n_rot], sp)
+
+    def call_no_append(i):
+        f_call(refs[i % n_rot], sp)
 
     def partial_only(i):
         f_partial(refs[i % n_rot], sp)
 
-    def drop_in(i):  # the manager's entry: SplitKExecutor.__call__ (checks, arguments, two launches)
+    # the drop-in: SplitKExecutor.__call__ with the append (checks, arguments, the two launches); the
+    # host ring lengths are set back before each call, since a stacked executor advances them
+    k4, v4 = app_k[:, :, None], app_v[:, :, None]
+    gpos = [int(params_app[0].append_global[r]) for r in range(b)]
+    ring_full = [[int(c.recent_fp_pool.active_length) for c in caches] for caches, _, _ in layers]
+    for caches, _, ex in layers:
+        for r, c in enumerate(caches):
+            c.recent_fp_pool.active_length = ring_n[r]
+
+    def drop_in(i):
         _, q, ex = layers[i % n_rot]
-        ex(q)
+        if ex.batched_recent_lengths is not None:
+            ex.batched_recent_lengths[:] = ring_n
+        ex(q, append=(k4, v4, gpos, gpos))
 
     for i in range(warmup):
-        step(i)
+        call(i)
     torch.cuda.synchronize()
-    ms_step = _time_events(step, steps, stream)
+    ms_step = _time_events(call, steps, stream)
+    ms_no_append = _time_events(call_no_append, steps, stream)
     ms_partial = _time_events(partial_only, steps, stream)
     ms_drop_in = _time_events(drop_in, steps, stream)
+    for (caches, _, _), lengths in zip(layers, ring_full):
+        for c, n in zip(caches, lengths):
+            c.recent_fp_pool.active_length = n
 
     # the same calls replayed from one HIP graph holding a layer call per rotated cache: no host
     # launch cost, so on small caches this is the GPU's own time per call
@@ -846,18 +906,18 @@ def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed
 
     def rotation():
         cs = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        for r in refs:
-            f_partial(r, cs)
-            f_combine(r, cs)
+        for r in refs_app:
+            f_call(r, cs)
 
     graph = _capture_launches(dev, side, rotation)
     for _ in range(20):
         graph.replay()
-    replays = max(1, steps // n_rot)
-    ms_graph = _time_events(lambda i: graph.replay(), replays, stream) / n_rot
+    replays = max(1, -(-steps // n_rot))
+    ms_graph = _time_events(lambda i: graph.replay(), replays, stream, lead=2) / n_rot
     del graph
-    return {"layers": layers, "bytes": nbytes, "ms_step": ms_step, "ms_partial": ms_partial,
-            "ms_drop_in": ms_drop_in, "ms_graph": ms_graph, "n_items": layers[0][2].n_items}
+    return {"layers": layers, "bytes": nbytes_app, "bytes_no_append": nbytes, "ms_step": ms_step,
+            "ms_no_append": ms_no_append, "ms_partial": ms_partial, "ms_drop_in": ms_drop_in, "ms_graph": ms_graph,
+            "graph_calls": replays * n_rot, "n_items": layers[0][2].n_items, "ring_tokens": ring_n}
 
 
 def timeline_bench(cfg, dev, *, n_layers: int, warmup: int, trials: int = 3) -> dict:
@@ -976,10 +1036,12 @@ def context_sweep(cfg, dev, *, factors, n_layers: int, steps: int, warmup: int) 
         lengths = tuple(int(round((t - cfg.recent) * f / cfg.page)) * cfg.page + cfg.recent for t in cfg.lengths)
         c = dataclasses.replace(cfg, lengths=lengths)
         r = time_decode_layers(c, dev, n_layers=n_layers, steps=steps, warmup=warmup)
-        points.append({"factor": f, "context_lengths": list(lengths), "bytes": r["bytes"], "work_items": r["n_items"],
-                       "us_call": round(r["ms_step"] * 1e3, 3), "us_partial": round(r["ms_partial"] * 1e3, 3),
-                       "call_GBs": round(r["bytes"] / (r["ms_step"] * 1e-3) / 1e9, 1),
-                       "partial_GBs": round(r["bytes"] / (r["ms_partial"] * 1e-3) / 1e9, 1)})
+        points.append({"factor": f, "context_lengths": list(lengths), "bytes": r["bytes_no_append"],
+                       "work_items": r["n_items"], "us_call": round(r["ms_no_append"] * 1e3, 3),
+                       "us_call_with_append": round(r["ms_step"] * 1e3, 3),
+                       "us_partial": round(r["ms_partial"] * 1e3, 3),
+                       "call_GBs": round(r["bytes_no_append"] / (r["ms_no_append"] * 1e-3) / 1e9, 1),
+                       "partial_GBs": round(r["bytes_no_append"] / (r["ms_partial"] * 1e-3) / 1e9, 1)})
         _log(f"sweep x{f}: {points[-1]}")
         del r
         torch.cuda.empty_cache()
@@ -1104,11 +1166,12 @@ def main() -> int:
     r = time_decode_layers(cfg, dev, n_layers=args.layers, steps=args.steps, warmup=args.warmup)
     wall = time.perf_counter() - t0
     nbytes, ms_step, ms_partial, ms_drop_in = r["bytes"], r["ms_step"], r["ms_partial"], r["ms_drop_in"]
-    ms_graph = r["ms_graph"]
+    nbytes_na, ms_na, ms_graph = r["bytes_no_append"], r["ms_no_append"], r["ms_graph"]
+    ring_tokens, graph_calls = r["ring_tokens"], r["graph_calls"]
     gbs = nbytes / (ms_step * 1e-3) / 1e9
-    part_gbs = nbytes / (ms_partial * 1e-3) / 1e9
-    _log(f"step {ms_step * 1e3:.2f} us ({gbs:.0f} GB/s), partial {ms_partial * 1e3:.2f} us ({part_gbs:.0f} GB/s), "
-         f"wall {wall:.2f} s")
+    part_gbs = nbytes_na / (ms_partial * 1e-3) / 1e9
+    _log(f"call {ms_step * 1e3:.2f} us ({gbs:.0f} GB/s), without append {ms_na * 1e3:.2f} us, partial "
+         f"{ms_partial * 1e3:.2f} us ({part_gbs:.0f} GB/s), wall {wall:.2f} s")
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
@@ -1122,7 +1185,7 @@ def main() -> int:
     read = read_bandwidth(dev)
     read["partial_kernel_pct_of_read"] = round(100 * part_gbs / read["GBs"], 1)
     _log("dma floor at the call's bytes ...")
-    floor = dma_floor(dev, nbytes)
+    floor = dma_floor(dev, nbytes_na)
     floor["partial_kernel_pct_of_floor"] = round(100 * floor["us"] / (ms_partial * 1e3), 1)
     e2e = None
     if not args.no_e2e:
@@ -1150,18 +1213,26 @@ def main() -> int:
                    "k_format": args.variant, "gen_values": args.gen_values, "hq": cfg.hq, "hkv": cfg.hkv,
                    "context_lengths": list(cfg.lengths), "v_tiers_bf16_int4_int2": list(cfg.tier_probs),
                    "recent_window": cfg.recent, "k_superblock": cfg.superblock, "int2_group": cfg.group,
-                   "rotated_layer_caches": args.layers, "algorithmic_bytes_per_call": nbytes, "output_hadamard": True},
+                   "rotated_layer_caches": args.layers, "algorithmic_bytes_per_call": nbytes, "output_hadamard": True,
+                   "fused_append": True, "ring_tokens_before_append": ring_tokens},
         "roofline": {"bound": "hbm", "achieved": round(part_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
                      "kernel": "decode_partial_kernel", "avg_us": round(ms_partial * 1e3, 3),
-                     "avg_us_source": "HIP events over back-to-back partial launches on the launch stream"},
+                     "algorithmic_bytes": nbytes_na,
+                     "avg_us_source": "HIP events over back-to-back partial launches on the launch stream "
+                                      "(after 30 ms of the same launches untimed and a queued lead of them)"},
+        "call_without_append": {"us": round(ms_na * 1e3, 3), "GBs": round(nbytes_na / (ms_na * 1e-3) / 1e9, 1),
+                                "bytes": nbytes_na,
+                                "method": "the same rotated layer calls without the fused append, HIP events"},
         "graph_call": {"us": round(ms_graph * 1e3, 3), "GBs": round(nbytes / (ms_graph * 1e-3) / 1e9, 1),
-                       "method": "the same layer calls replayed from one HIP graph per rotation of the layer caches "
-                                 "(no host launch cost), HIP events over the replays"},
+                       "calls": graph_calls,
+                       "method": "the same layer calls (fused append) replayed from one HIP graph per rotation of "
+                                 "the layer caches (no host launch cost), HIP events over the replays"},
         "drop_in_call": {"us": round(ms_drop_in * 1e3, 3), "GBs": round(nbytes / (ms_drop_in * 1e-3) / 1e9, 1),
-                         "method": "the same layer calls through SplitKExecutor.__call__ (the Python drop-in the "
-                                   "manager calls: checks, launch arguments, the two launches), HIP events"},
+                         "method": "the same layer calls through SplitKExecutor.__call__(query, append=...) (the "
+                                   "Python drop-in the manager calls: checks, launch arguments, the two launches), "
+                                   "HIP events"},
         "cpu_baseline": cpu,
         "hbm_copy": copy,
         "hbm_read": read,

@@ -195,6 +195,11 @@ int r2o_decode_partial(const r2o_decode_params* params, void* stream);
  * (triton_fourq_splitk.py:1023-1155, :936-1020, launched at :1467-1541). */
 int r2o_decode_combine(const r2o_decode_params* params, void* stream);
 
+/* The whole decode call: r2o_decode_partial then r2o_decode_combine on `stream`, after one check of
+ * the arguments.  Replaces the launch sequence of SplitKExecutor.__call__ (triton_fourq_splitk.py:
+ * 1393-1541: the partial, group-reduce and final-reduce launches); one host call instead of two. */
+int r2o_decode(const r2o_decode_params* params, void* stream);
+
 /* Workspace-free decode: r2o_decode_partial then r2o_decode_combine on `stream`, with the split-K
  * partial states held in a library-owned device array (one per GPU, kept until the process ends)
  * instead of params->partial_max / partial_sum / partial_out / partial_capacity, which are ignored

@@ -40,14 +40,7 @@
 
 namespace {
 
-constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
-// Build-time tuning knob (the default is the measured best on MI355X).
-#ifndef R2O_DMA_STAGES
-#define R2O_DMA_STAGES 1          // LDS stages per wave: tiles in flight while one is computed
-#endif
-constexpr int kDmaStages = R2O_DMA_STAGES;
-static_assert(kDmaStages >= 1 && kDmaStages <= 3, "1 to 3 LDS stages per wave");
 constexpr int kMergeFloats = 16 + 16 + 16 * 128;    // per wave: m, l, acc
 
 // History-key formats (r2o_decode_params.k_format): the compact INT4 arena, bf16 rows
@@ -70,14 +63,26 @@ __device__ __forceinline__ r2o_f4 mfma_rows(r2o_u4 a, r2o_u4 b, r2o_f4 c) {
 }
 
 // Per-kernel LDS / occupancy configuration.
+// Build-time tuning knob (the default is the measured best on MI355X).
+#ifndef R2O_DMA_STAGES
+#define R2O_DMA_STAGES 1          // LDS stages per wave: tiles in flight while one is computed
+#endif
+constexpr int kDmaStages = R2O_DMA_STAGES;
+static_assert(kDmaStages >= 1 && kDmaStages <= 3, "1 to 3 LDS stages per wave");
+
 template <int KF>
 struct KernelCfg {
+    static constexpr int kWaves = 4;  // waves per workgroup
+    static constexpr int kThreads = 64 * kWaves;
     static constexpr int kStage = KF == kKBf16 ? 16384 : 10752;  // one tile stage (sized for BF16 V, see StageLayout)
     static constexpr int kWaveLds = kDmaStages * kStage;
     static constexpr int kSmem = (kWaves * kMergeFloats * 4 > kWaves * kWaveLds) ? kWaves * kMergeFloats * 4
                                                                                  : kWaves * kWaveLds;
     static constexpr int kBlocksPerCU = 2;  // resident partial workgroups per CU (the planner launches 2 per CU)
+    static constexpr int kWavesPerSimd = kBlocksPerCU * kWaves / 4;  // __launch_bounds__' second argument
 };
+static_assert(2 * KernelCfg<kKInt4>::kSmem <= 160 * 1024 && 2 * KernelCfg<kKBf16>::kSmem <= 160 * 1024,
+              "two partial workgroups fit one CU's LDS");
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
 
@@ -100,7 +105,8 @@ __device__ __forceinline__ void stamp(Stamps& s, int i) {
 // HW_ID << 32, 8 tiles | kind << 32.  combine: per (block, wave) 12 slots: 0 entry, 1 arguments
 // arrived, 2 first round of partials landed, 3 merged, 4 (wave 0) output stored.
 constexpr int kTimelineBlocks = 4096;
-__device__ unsigned long long g_timeline_partial[kTimelineBlocks * 4 * 12];
+constexpr int kTimelineWaves = 4;  // stamp slots per partial workgroup (one per wave)
+__device__ unsigned long long g_timeline_partial[kTimelineBlocks * kTimelineWaves * 12];
 __device__ unsigned long long g_timeline_combine[kTimelineBlocks * 8 * 12];
 __device__ __forceinline__ void stamps_store(unsigned long long* dst, int block, int wave, int waves, const Stamps& s) {
     if ((threadIdx.x & 63) == 0 && block < kTimelineBlocks)
@@ -539,7 +545,10 @@ __device__ __forceinline__ int v4_slot(int t, int c) { return 8 * ((t & 3) + 4 *
 // INT2 V: token t, chunk c (0..1) of its 32-byte row; tokens t, t+4, t+8, t+12 share 8 slots.
 __device__ __forceinline__ int v2_slot(int t, int c) { return 8 * (t & 3) + 32 * (t >> 4) + 2 * ((t >> 2) & 3) + c; }
 // INT2-K codes: token t, chunk c (0..1) of its 32-byte row.  Reads: 16 lanes take 8 bytes of one
-// chunk of 16 consecutive tokens, so tokens 8..15 of a group swap their two chunks.
+// chunk of 16 consecutive tokens, so tokens 8..15 of a group swap their two chunks.  (Their 16-lane
+// passes still meet 2-way bank conflicts, which a layout cannot remove while 16 lanes read the same
+// half of 16 chunks; reading each chunk once with 16 bytes a lane and two row swaps removes them, but
+// the swaps cost this VALU-bound loop more than the conflicts do.)
 __device__ __forceinline__ int k2_slot(int t, int c) { return 2 * t + (c ^ ((t >> 3) & 1)); }
 // BF16 V rows stay in natural order: 8 lanes read 8 consecutive chunks of one 256-byte row.
 // BF16 K: token t, chunk c (0..15) of its 256-byte row.  Reads: 8 lanes take one chunk of 8
@@ -708,7 +717,7 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = __builtin_amdgcn_readfirstlane(r2o_div_small((int)p.hq, (int)p.hkv));
     const int64_t kvh = it.kvh, b = it.req;
-    const int per = (int)((it.ntiles + kWaves - 1) / kWaves);
+    const int per = (int)((it.ntiles + Cfg::kWaves - 1) / Cfg::kWaves);
     const int t_begin = wave * per;
     const int t_end = min((int)it.ntiles, t_begin + per);
     if (t_begin >= t_end) return;
@@ -818,9 +827,10 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
 // Recent-FP ring tiles (bf16 K and V, plus the fused-append token).  Every load of a tile is
 // issued before any is used (rows past the valid end read the last valid row, whose
 // probability is 0); a tile with no valid token is skipped.
-template <int RF>
+template <int KF, int RF>
 __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
                            WaveState& st) {
+    constexpr int kWaves = KernelCfg<KF>::kWaves;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
     const int gqa = __builtin_amdgcn_readfirstlane(r2o_div_small((int)p.hq, (int)p.hkv));
@@ -879,7 +889,9 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
 }
 
 template <int KF, int RF>
-__global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_partial_kernel(r2o_decode_params p) {
+__global__ __launch_bounds__(KernelCfg<KF>::kThreads, KernelCfg<KF>::kWavesPerSimd) void decode_partial_kernel(
+        r2o_decode_params p) {
+    constexpr int kWaves = KernelCfg<KF>::kWaves;
     __shared__ __align__(16) unsigned char smem[KernelCfg<KF>::kSmem];
     Stamps ts{};
     stamp(ts, 0);
@@ -911,7 +923,7 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
             if (it.v_group == 128) run_segment<kI2, KF, true, RF>(p, it, smem, st, ts);
             else run_segment<kI2, KF, false, RF>(p, it, smem, st, ts);
             break;
-        default: run_recent<RF>(p, it, st); break;
+        default: run_recent<KF, RF>(p, it, st); break;
     }
 
     // ---- per-wave epilogue: reduce l (and u) over the 4 lane groups of each head
@@ -970,7 +982,7 @@ __global__ __launch_bounds__(256, KernelCfg<KF>::kBlocksPerCU) void decode_parti
     }
     stamp(ts, 6);
 #ifdef R2O_TIMELINE
-    stamps_store(g_timeline_partial, blockIdx.x, wave, 4, ts);
+    stamps_store(g_timeline_partial, blockIdx.x, wave, kTimelineWaves, ts);
 #endif
 }
 
@@ -1238,7 +1250,9 @@ float* scratch_address(int dev) {
 }
 
 int launch_decode(const r2o_decode_params& p, hipStream_t stream) {
-    const dim3 grid((unsigned)p.n_items), block(256);
+    const dim3 grid((unsigned)p.n_items);
+    const dim3 block(KernelCfg<kKInt4>::kThreads), block_bf16(KernelCfg<kKBf16>::kThreads);
+    static_assert(KernelCfg<kKInt4>::kThreads == KernelCfg<kKInt2>::kThreads, "one workgroup size for the low-bit K formats");
     const bool f16 = p.row_dtype == kRowF16;
     switch (p.k_format) {
         case kKInt4:
@@ -1246,8 +1260,8 @@ int launch_decode(const r2o_decode_params& p, hipStream_t stream) {
             else hipLaunchKernelGGL((decode_partial_kernel<kKInt4, kRowBf16>), grid, block, 0, stream, p);
             break;
         case kKBf16:
-            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowF16>), grid, block, 0, stream, p);
-            else hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowBf16>), grid, block, 0, stream, p);
+            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowF16>), grid, block_bf16, 0, stream, p);
+            else hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowBf16>), grid, block_bf16, 0, stream, p);
             break;
         default:
             if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKInt2, kRowF16>), grid, block, 0, stream, p);
@@ -1285,6 +1299,14 @@ int r2o_decode_partial(const r2o_decode_params* params, void* stream) {
 int r2o_decode_combine(const r2o_decode_params* params, void* stream) {
     const int rc = validate(params);
     if (rc) return rc;
+    return launch_combine(*params, (hipStream_t)stream);
+}
+
+int r2o_decode(const r2o_decode_params* params, void* stream) {
+    const int rc = validate(params);
+    if (rc) return rc;
+    const int lrc = launch_decode(*params, (hipStream_t)stream);
+    if (lrc) return lrc;
     return launch_combine(*params, (hipStream_t)stream);
 }
 

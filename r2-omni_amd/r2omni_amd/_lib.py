@@ -96,6 +96,7 @@ _SIGNATURES = {
                             c_vp, c_i64, c_vp, c_i64, ctypes.POINTER(c_i64)),
     "r2o_decode_partial": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_combine": (ctypes.POINTER(DecodeParams), c_vp),
+    "r2o_decode": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_noalloc": (ctypes.POINTER(DecodeParams), c_vp),
     "r2o_decode_noalloc_init": (ctypes.c_int,),
     "r2o_pack_int4_k": (c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,

@@ -428,10 +428,9 @@ class SplitKExecutor:
 
     @staticmethod
     def _launch(p: _lib.DecodeParams, device: torch.device) -> None:
-        stream = ctypes.c_void_p(_lib.stream_of(device))
-        lib = _lib.load()
-        _lib.check(lib.r2o_decode_partial(ctypes.byref(p), stream), "r2o_decode_partial")
-        _lib.check(lib.r2o_decode_combine(ctypes.byref(p), stream), "r2o_decode_combine")
+        # one host call for the partial and combine launches (r2o_decode): each ctypes crossing costs
+        # ~2 us of host time, which launch-bound small caches pay per call
+        _lib.check(_lib.load().r2o_decode(ctypes.byref(p), ctypes.c_void_p(_lib.stream_of(device))), "r2o_decode")
 
 
 _NOALLOC_READY: set[int] = set()

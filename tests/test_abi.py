@@ -86,6 +86,7 @@ def test_host_side_validation_rejects_bad_arguments_without_a_gpu():
                                partial_capacity=39)
     assert lib.r2o_decode_partial(ctypes.byref(params), None) == 1
     assert lib.r2o_decode_combine(ctypes.byref(params), None) == 1
+    assert lib.r2o_decode(ctypes.byref(params), None) == 1
     params.partial_capacity = 0
     assert lib.r2o_decode_partial(ctypes.byref(params), None) == 1
     assert lib.r2o_build_target() == b"gfx950"
