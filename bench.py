@@ -658,9 +658,12 @@ class E2EQwenDecoder:
         return out
 
     # -------------------------------------------------------------------------- decode
-    def decode(self, steps: int, use_graph: bool, inspect=None):
+    def decode(self, steps: int, use_graph: bool, inspect=None, fused_rotation: bool = True):
         """``steps`` greedy steps from fresh caches: eager launches, or (``use_graph``) the steps
         after the first replayed from one HIP graph per step (the argmax stays outside the graph).
+        ``fused_rotation``: each layer's QKV projection is written into one static buffer whose views
+        the layer's decoder reads, and the attention call applies the mRoPE / FWHT itself (two launches
+        per layer for the attention); otherwise a separate rotation launch writes the decoder's buffers.
         ``inspect(step, decoders)`` runs after each step's synchronisation (not for timing).
         Returns (decode ms from HIP events, tokens [steps, B], whether every step's logits were finite)."""
         import torch
@@ -670,7 +673,17 @@ class E2EQwenDecoder:
 
         dev, batch, nh, nkv, hd, hid = self.dev, self.batch, self.NH, self.NKV, self.HD, self.HID
         caches = self.build_caches(steps)
-        decs = [ro.BatchedDecoder(c, num_query_heads=nh, output_hadamard=True, use_graph=False) for c in caches]
+        cos_buf = torch.empty(3, batch, 1, hd, device=dev, dtype=torch.bfloat16)
+        sin_buf = torch.empty_like(cos_buf)
+        qkv_buf = torch.empty(batch, (nh + 2 * nkv) * hd, device=dev, dtype=torch.bfloat16)
+        rotary = ro.FusedRotary(cos_buf, sin_buf, self.SECTIONS, True, True) if fused_rotation else None
+        decs = [ro.BatchedDecoder(c, num_query_heads=nh, output_hadamard=True, use_graph=False, rotary=rotary)
+                for c in caches]
+        if fused_rotation:
+            for d in decs:  # every layer reads the one projection buffer, written right before its call
+                d.bind_inputs(qkv_buf[:, : nh * hd].view(batch, nh, hd),
+                              qkv_buf[:, nh * hd : (nh + nkv) * hd].view(batch, nkv, hd),
+                              qkv_buf[:, (nh + nkv) * hd :].view(batch, nkv, hd))
         tok = self.first.clone()
         pos_dev = torch.full((1, 1), self.context, dtype=torch.int64, device=dev)
         logits = torch.empty(batch, self.VOCAB, device=dev, dtype=torch.bfloat16)
@@ -681,16 +694,21 @@ class E2EQwenDecoder:
         def body(attend):
             x = self.embed[tok]
             cos, sin = self.tables(pos_dev.expand(batch, 1))
+            if fused_rotation:
+                cos_buf.copy_(cos)
+                sin_buf.copy_(sin)
             for lw, d in zip(self.layers, decs):
                 h = self.rms(x, lw["n1"])
-                q, k, v = F.linear(h, lw["w_qkv"], lw["b_qkv"]).split((nh * hd, nkv * hd, nkv * hd), dim=-1)
-                q = q.reshape(batch, nh, 1, hd)
-                k = k.reshape(batch, nkv, 1, hd)
-                v = v.reshape(batch, nkv, hd)
-                # Q/K rotation + FWHT and the V FWHT in one launch
-                ro.qwen_qk_mrope(q, k, cos, sin, self.SECTIONS, apply_hadamard=True, value=v.view(batch, nkv, 1, hd),
-                                 output=(d.query_buffer.view(batch, nh, 1, hd), d.key_buffer.view(batch, nkv, 1, hd),
-                                         d.value_buffer.view(batch, nkv, 1, hd)))
+                if fused_rotation:  # raw projections; the attention call rotates them
+                    torch.addmm(lw["b_qkv"], h, lw["w_qkv"].t(), out=qkv_buf)
+                else:
+                    q, k, v = F.linear(h, lw["w_qkv"], lw["b_qkv"]).split((nh * hd, nkv * hd, nkv * hd), dim=-1)
+                    # Q/K rotation + FWHT and the V FWHT in one launch
+                    ro.qwen_qk_mrope(q.reshape(batch, nh, 1, hd), k.reshape(batch, nkv, 1, hd), cos, sin,
+                                     self.SECTIONS, apply_hadamard=True, value=v.reshape(batch, nkv, 1, hd),
+                                     output=(d.query_buffer.view(batch, nh, 1, hd),
+                                             d.key_buffer.view(batch, nkv, 1, hd),
+                                             d.value_buffer.view(batch, nkv, 1, hd)))
                 attend(d)
                 x = x + F.linear(d.workspace.output.view(batch, hid), lw["wo"])
                 x = self.mlp(x, lw)
@@ -778,6 +796,8 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
     _log(f"e2e eager decode: {eager_ms:.1f} ms for {steps} steps")
     graph_ms, graph_tokens, graph_finite = model.decode(steps, True)
     _log(f"e2e graph decode: {graph_ms:.1f} ms for {steps} steps")
+    sep_ms, sep_tokens, _ = model.decode(steps, True, fused_rotation=False)
+    _log(f"e2e graph decode with a separate rotation launch: {sep_ms:.1f} ms for {steps} steps")
     match = bool(torch.equal(eager_tokens, graph_tokens))
     use_graph = match and graph_ms < eager_ms
     best_ms = graph_ms if use_graph else eager_ms
@@ -786,6 +806,10 @@ def e2e_decode_bench(dev, *, batch: int, context: int, steps: int, n_layers: int
               "mode": "hip_graph_per_step" if use_graph else "eager",
               "eager_tok_s": round(batch * steps / (eager_ms * 1e-3), 1),
               "graph_tok_s": round(batch * steps / (graph_ms * 1e-3), 1), "graph_matches_eager": match,
+              "rotation": "folded into the attention call (FusedRotary): per layer one QKV GEMM into a static "
+                          "buffer, then the partial and combine launches",
+              "graph_tok_s_separate_rotation": round(batch * steps / (sep_ms * 1e-3), 1),
+              "separate_rotation_tokens_match": bool(torch.equal(sep_tokens, graph_tokens)),
               "logits_finite": eager_finite and graph_finite,
               "dtype": "bf16", "data": "synthetic (random-init weights N(0, 0.02), seeded random token ids)",
               "config": {"workload": "cfg4 qwen25omni7b e2e decode", "layers": n_layers, "batch": batch,

@@ -145,7 +145,10 @@ typedef struct r2o_decode_params {
     float* partial_sum;             /* device f32 [n_items, 16]                        */
     float* partial_out;             /* device f32 [n_items, 16, 128], 16-byte aligned  */
     const uint16_t* query;          /* device [batch, hq, 128] (dtype q_dtype)         */
-    uint16_t* out;                  /* device bf16 [batch, hq, 128]                    */
+    int64_t query_batch_stride;     /* elements from one request's query rows to the next (0: hq*128),
+                                       so that the query can be a view into a fused QKV projection;
+                                       a multiple of 8, at least hq*128.  Only with rope_mode 1: other
+                                       calls take dense rows (0 or hq*128), as the reference does. */
     const uint16_t* append_k;       /* device bf16 [batch, hkv, 128] or NULL; 16-byte
                                        aligned, and hkv <= 128 when do_append is set  */
     const uint16_t* append_v;
@@ -167,6 +170,9 @@ typedef struct r2o_decode_params {
     int64_t k_format;               /* R2O_K_INT4 / R2O_K_BF16 / R2O_K_INT2: the history key layout  */
                                     /* of every request (see r2o_request_desc.k_packed)               */
     float sm_scale;                 /* softmax scale (head_dim^-1/2 by default)        */
+    uint16_t* out;                  /* device bf16 [batch, hq, 128]                    */
+    int64_t append_batch_stride;    /* the same for append_k / append_v (0: hkv*128; at least hkv*128;
+                                       only with rope_mode 1)                                          */
     int32_t recent_len[R2O_MAX_BATCH];     /* host-tracked Recent-FP active length     */
     int64_t append_global[R2O_MAX_BATCH];  /* global token index of the appended token */
     int64_t append_logical[R2O_MAX_BATCH]; /* logical position of the appended token   */
@@ -184,6 +190,26 @@ typedef struct r2o_decode_params {
                                        and checks its workspace first (triton_fourq_splitk.py:1607-1692,
                                        qwen_sspa_attention.py:1157-1160).  r2o_decode_noalloc sets it
                                        itself. */
+    /* The decode step's rotation folded into the call (qwen_sspa_attention.py:1239-1247, 230-235):
+     * rope_mode 0: query and append rows are used as given (already rotated).  rope_mode 1 (Qwen mRoPE,
+     * triton_qwen_mrope.py:45-124): query and append_k are the raw projections; the partial kernel
+     * applies x * cos + rotate_half(x) * sin in fp32 (dimension d taking axis 0, 1 or 2 of the tables
+     * by d % 64 against the sections), then with rope_hadamard the orthonormal FWHT-128, rounding each
+     * row once to its dtype, exactly as r2o_qkv_mrope does; append_v takes the FWHT alone with
+     * value_hadamard.  The rotated appended rows go to rotated_k / rotated_v, from which the combine's
+     * fused append writes the ring. */
+    int64_t rope_mode;
+    const void* rope_cos;           /* [3, batch, tokens, 128] tables of the step (token 0 is used)  */
+    const void* rope_sin;
+    int64_t rope_cos_strides[4];    /* element strides of rope_cos: axis, batch, token, dimension     */
+    int64_t rope_sin_strides[4];
+    int64_t rope_table_dtype;       /* 0 = bf16, 1 = fp16, 2 = fp32                                    */
+    int64_t rope_section0;          /* mRoPE sections s0, s1 (the third is 64 - s0 - s1)               */
+    int64_t rope_section1;
+    int64_t rope_hadamard;          /* 1: FWHT-128 of the rotated query and key rows                   */
+    int64_t value_hadamard;         /* 1: FWHT-128 of the appended value row                           */
+    uint16_t* rotated_k;            /* device [batch, hkv, 128] (row_dtype), 16-byte aligned: written  */
+    uint16_t* rotated_v;            /* by the partial pass when rope_mode and do_append are set        */
 } r2o_decode_params;
 
 /* Split-K partial pass.  Replaces _fourq_page_partial_kernel / _full_head_page_partial_kernel

@@ -83,6 +83,8 @@ struct KernelCfg {
 };
 static_assert(2 * KernelCfg<kKInt4>::kSmem <= 160 * 1024 && 2 * KernelCfg<kKBf16>::kSmem <= 160 * 1024,
               "two partial workgroups fit one CU's LDS");
+constexpr int kRotLdsBytes = 18 * 136 * 2;  // the rows of a folded rotation (kRotBytes, below)
+static_assert(2 * (KernelCfg<kKBf16>::kSmem + kRotLdsBytes) <= 160 * 1024, "with the rotation's rows as well");
 
 enum Kind { kFP = 0, kI4 = 1, kI2 = 2, kRecent = 3 };
 
@@ -124,25 +126,221 @@ struct WaveState {
     r2o_f4 acc[8];  // O[4g+i][8*l16 + q] for q = 0..7
 };
 
+// ------------------------------------------------------------------ folded decode-step rotation
+// With r2o_decode_params.rope_mode 1 the query and the appended key arrive as raw projections and the
+// partial kernel applies the decode step's Qwen mRoPE (and FWHT) itself, bit-identically to
+// qk_mrope_kernel (r2o_rope.hip): y = x * cos + rotate_half(x) * sin in fp32, channel c taking cos/sin
+// from table axis 0, 1 or 2 by c % 64 against the sections, then optionally the orthonormal FWHT in
+// the stage order 1, 2, .., 64, then one rounding to the row's dtype; the appended value takes the
+// FWHT alone.  A row is rotated by one 16-lane group, lane c8 holding channels 8 c8 .. 8 c8 + 7 (FWHT
+// strides 1 .. 4 inside the lane, 8 .. 64 across lanes c8 ^ 1 .. c8 ^ 8 of the group; every fp32 sum
+// takes the same operands in the same order as the separate launch).  The 4 waves of a work item
+// share the rows (4 per wave), which meet in LDS; after a barrier each lane reads the channels it holds
+// as an MFMA operand, as it would read rotated rows in memory.
+enum RopeMode { kRopeNone = 0, kRopeMrope = 1 };
+
+// A work item's LDS rows of a folded rotation (row dtype): the KV group's query heads 0 .. 15, then the
+// appended key (row 16) and value (row 17); 272 bytes apart, so that 16 lanes' reads of one channel
+// range from different rows fall on different banks.
+constexpr int kRotStride = 136;
+constexpr int kRotKeyRow = 16;
+constexpr int kRotBytes = 18 * kRotStride * 2;
+static_assert(kRotBytes == kRotLdsBytes, "one size for the rotation's LDS rows");
+
+// Orthonormal FWHT-128 of a row whose dims 8 l16 .. 8 l16 + 7 this lane holds (the V layout of a
+// Recent-FP tile): strides 1 .. 4 inside the lane, 8 .. 64 across lanes l16 ^ 1 .. l16 ^ 8 of a row.
+__device__ __forceinline__ void fwht_row8(float (&y)[8], int l16) {
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if ((i & h) == 0) {
+                const float a = y[i], c = y[i + h];
+                y[i] = a + c;
+                y[i + h] = a - c;
+            }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float v = y[i], o;
+        o = r2o_lane_xor<1>(v);
+        v = (l16 & 1) ? o - v : v + o;
+        o = r2o_lane_xor<2>(v);
+        v = (l16 & 2) ? o - v : v + o;
+        o = r2o_lane_xor<4>(v);
+        v = (l16 & 4) ? o - v : v + o;
+        o = r2o_lane_xor<8>(v);
+        v = (l16 & 8) ? o - v : v + o;
+        y[i] = v * 0.08838834764831845f;
+    }
+}
+
+// Elements from one request's query (appended) rows to the next.  Only calls with a folded rotation
+// take strided rows (views of a fused projection; the launch helpers spell a stride of 0 out as the
+// dense figure); the other calls' rows are dense, as the reference requires, and the kernels
+// compute their addresses without reading a stride, which would sit on the path to the first tile.
+template <int RO>
+__device__ __forceinline__ int64_t q_stride(const r2o_decode_params& p) {
+    return RO != kRopeNone ? p.query_batch_stride : p.hq * 128;
+}
+
+// The query row of head l16 of the KV group (padded heads read head 0; their operand is zeroed).
+template <int RO>
+__device__ __forceinline__ const uint16_t* query_row(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa,
+                                                     int l16) {
+    return p.query + b * q_stride<RO>(p) + (kvh * gqa + (l16 < gqa ? l16 : 0)) * 128;
+}
+
+// The inputs of a lane's part of a rotation, put out ahead of the work item's first tile DMAs: the cos /
+// sin table runs of the lane's 8 channels c = 8 c8 .. 8 c8 + 7 for the three axes, as whole 16-byte
+// pieces (one each for 16-bit tables, two for fp32; the host requires unit channel strides and 16-byte
+// aligned rows), and the raw row (its 8 channels and their rotate-half partners c -/+ 64).  Offsets
+// from the request's table base are 32-bit byte offsets (below 2^31, checked on the host).
+struct RotPrefetch {
+    r2o_u4 tab[2][3][2];  // [cos, sin][axis][piece]
+    r2o_u4 x, xp;
+};
+
+__device__ __forceinline__ void rot_row_loads(const uint16_t* row, int c8, r2o_u4& x, r2o_u4& xp) {
+    x = r2o_ldg(reinterpret_cast<const r2o_u4*>(row + 8 * c8));
+    xp = r2o_ldg(reinterpret_cast<const r2o_u4*>(row + 8 * (c8 ^ 8)));
+}
+
+// The source of rotation row r of a work item: query head r < gqa, the appended key (r == gqa) or value.
+__device__ __forceinline__ const uint16_t* rot_source(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa,
+                                                      int r) {
+    if (r < gqa) return query_row<kRopeMrope>(p, b, kvh, gqa, r);
+    return (r == gqa ? p.append_k : p.append_v) + b * p.append_batch_stride + kvh * 128;
+}
+
+__device__ __forceinline__ void rot_prefetch(const r2o_decode_params& p, int64_t b, const uint16_t* row, int c8,
+                                             RotPrefetch& f) {
+    const int pieces = p.rope_table_dtype == 2 ? 2 : 1;
+    const int64_t esize = p.rope_table_dtype == 2 ? 4 : 2;
+    const char* tab[2] = {reinterpret_cast<const char*>(p.rope_cos) + b * p.rope_cos_strides[1] * esize,
+                          reinterpret_cast<const char*>(p.rope_sin) + b * p.rope_sin_strides[1] * esize};
+    const uint32_t axis_bytes[2] = {(uint32_t)(p.rope_cos_strides[0] * esize), (uint32_t)(p.rope_sin_strides[0] * esize)};
+    const uint32_t o = (uint32_t)(8 * c8 * esize);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                if (q < pieces) f.tab[t][a][q] = r2o_ldg(reinterpret_cast<const r2o_u4*>(tab[t] + (a * axis_bytes[t] + o + 16 * q)));
+    rot_row_loads(row, c8, f.x, f.xp);
+}
+
+// cos / sin of the lane's 8 channels as fp32: channel k takes axis 1 from bit k of m1 and axis 2 from
+// bit k of m2 (bit masks of the lane's channels against the sections, d = c % 64), selected by bit
+// operations (per-channel condition masks would hold a pair of scalar registers each).
+__device__ __forceinline__ void rot_tables(const r2o_decode_params& p, int c8, const RotPrefetch& f, float (&cs)[8],
+                                           float (&sn)[8]) {
+    const int code = (int)p.rope_table_dtype;
+    const int d0 = (8 * c8) & 63, t0 = (int)p.rope_section0 - d0, t1 = t0 + (int)p.rope_section1;
+    const uint32_t m1 = t0 <= 0 ? 0xffu : (t0 >= 8 ? 0u : (0xffu << t0) & 0xffu);
+    const uint32_t m2 = t1 <= 0 ? 0xffu : (t1 >= 8 ? 0u : (0xffu << t1) & 0xffu);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t v[2][3];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                const uint32_t w16 = f.tab[t][a][0][k >> 1];
+                v[t][a] = code == 2 ? f.tab[t][a][k >> 2][k & 3] : ((k & 1) ? w16 >> 16 : w16 & 0xffffu);
+            }
+        const uint32_t f1 = 0u - ((m1 >> k) & 1u), f2 = 0u - ((m2 >> k) & 1u);
+        float out[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t v01 = v[t][0] ^ ((v[t][0] ^ v[t][1]) & f1);
+            const uint32_t bits = v01 ^ ((v01 ^ v[t][2]) & f2);
+            out[t] = code == 2 ? __uint_as_float(bits) : (code == 0 ? r2o_bf16_to_f32(bits) : r2o_f16_to_f32(bits));
+        }
+        cs[k] = out[0];
+        sn[k] = out[1];
+    }
+}
+
+// Channel k of 8 packed 16-bit channels, as fp32.
+__device__ __forceinline__ float row_channel(const r2o_u4& w, int k, int dt) {
+    const uint32_t h = (k & 1) ? w[k >> 1] >> 16 : w[k >> 1] & 0xffffu;
+    return dt == 0 ? r2o_bf16_to_f32(h) : r2o_f16_to_f32(h);
+}
+
+// One row of a folded rotation in a 16-lane group (lane c8: channels 8 c8 .. 8 c8 + 7): mRoPE then, with
+// `had`, the FWHT (rope = false: the FWHT alone, for the appended value), one rounding to the row dtype,
+// as the packed 16-bit channels.
+__device__ __forceinline__ r2o_u4 rot_row(const r2o_decode_params& p, const r2o_u4& x, const r2o_u4& xp,
+                                          const float (&cs)[8], const float (&sn)[8], int c8, bool rope, bool had) {
+    const int dt = (int)p.row_dtype;
+    float y[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float xv = row_channel(x, k, dt), xpv = row_channel(xp, k, dt);
+        const float rk = xv * cs[k] + (c8 < 8 ? -xpv : xpv) * sn[k];  // rotate_half: (-x[c + 64], x[c - 64])
+        y[k] = rope ? rk : xv;
+    }
+    if (had) fwht_row8(y, c8);  // whole 16-lane groups take the same branch
+    r2o_u4 out;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t lo = dt == 0 ? r2o_f32_to_bf16(y[2 * u]) : r2o_f32_to_f16(y[2 * u]);
+        const uint32_t hi = dt == 0 ? r2o_f32_to_bf16(y[2 * u + 1]) : r2o_f32_to_f16(y[2 * u + 1]);
+        out[u] = lo | (hi << 16);
+    }
+    return out;
+}
+
+// Rotation row r of the work item in the 16-lane group lane >> 4 of wave (r / 4) % 4 (rows 16, 17 in
+// a second round): query heads rounded into LDS rows 0 .. gqa - 1; with `kv` (the Recent-FP item of a
+// call with an append) the appended key and value into rows 16, 17 and to rotated_k / rotated_v for
+// the combine's append (that item is their only reader).  The waves meet at a barrier after this;
+// each then reads the rows it needs.
+__device__ __forceinline__ void rot_block_row(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa, int r,
+                                              int c8, const RotPrefetch& f, uint16_t* rot) {
+    float cs[8], sn[8];
+    rot_tables(p, c8, f, cs, sn);
+    const bool is_q = r < gqa, is_v = r == gqa + 1;
+    const r2o_u4 out = rot_row(p, f.x, f.xp, cs, sn, c8, !is_v, is_v ? p.value_hadamard != 0 : p.rope_hadamard != 0);
+    *reinterpret_cast<r2o_u4*>(rot + (is_q ? r : kRotKeyRow + (r - gqa)) * kRotStride + 8 * c8) = out;
+    if (!is_q) *reinterpret_cast<r2o_u4*>((is_v ? p.rotated_v : p.rotated_k) + (b * p.hkv + kvh) * 128 + 8 * c8) = out;
+}
+
+// The lane's rotated query channels 32g .. 32g + 31 of head l16 (zero for the padded heads), after
+// the barrier.
+__device__ __forceinline__ void rot_read_query(const uint16_t* rot, int gqa, int l16, int g, r2o_u4 (&q)[4]) {
+    const r2o_u4* src = reinterpret_cast<const r2o_u4*>(rot + (l16 < gqa ? l16 : 0) * kRotStride + 32 * g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = l16 < gqa ? src[j] : r2o_u4{0, 0, 0, 0};
+}
+
 // Query operand of head l16 of the KV group (padded heads are zero), channels 32g .. 32g+31, in
 // the K operand order of the format: f16 pairs (8j+u, 8j+u+4) for INT4-K, f16 pairs
 // (16(j/2) + 4(j%2) + u, +8) for INT2-K, both scaled by D^-1/2 log2(e), or bf16 pairs in channel
-// order for bf16 keys (BF16-K pools and the Recent-FP ring; fp16 pairs for fp16 rows).
-template <int KF, int RF>
+// order for bf16 keys (BF16-K pools and the Recent-FP ring; fp16 pairs for fp16 rows).  With a folded
+// rotation (RO) `qrot` holds the lane's rotated channels (rot_read_query).
+template <int KF, int RF, int RO>
 __device__ __forceinline__ void load_query(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa, int l16,
-                                           int g, float qscale, uint32_t (&qp)[4][4]) {
+                                           int g, float qscale, uint32_t (&qp)[4][4], const r2o_u4 (&qrot)[4]) {
     const bool head_ok = l16 < gqa;
-    const uint16_t* qrow = p.query + ((b * p.hq) + kvh * gqa + (head_ok ? l16 : 0)) * 128 + 32 * g;
-    const r2o_u4* q4 = reinterpret_cast<const r2o_u4*>(qrow);
-    r2o_u4 raw[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) raw[j] = head_ok ? r2o_ldg(q4 + j) : r2o_u4{0, 0, 0, 0};
     float qf[32];
+    {
+        r2o_u4 raw[4];
+        if constexpr (RO == kRopeMrope) {
 #pragma unroll
-    for (int w = 0; w < 16; ++w) {
-        const uint32_t v = raw[w / 4][w % 4];
-        qf[2 * w] = p.q_dtype == 0 ? r2o_bf16_to_f32(v & 0xffffu) : r2o_f16_to_f32(v & 0xffffu);
-        qf[2 * w + 1] = p.q_dtype == 0 ? r2o_bf16_to_f32(v >> 16) : r2o_f16_to_f32(v >> 16);
+            for (int j = 0; j < 4; ++j) raw[j] = qrot[j];
+        } else {
+            const r2o_u4* q4 = reinterpret_cast<const r2o_u4*>(query_row<RO>(p, b, kvh, gqa, l16) + 32 * g);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) raw[j] = head_ok ? r2o_ldg(q4 + j) : r2o_u4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            const uint32_t v = raw[w / 4][w % 4];
+            qf[2 * w] = p.q_dtype == 0 ? r2o_bf16_to_f32(v & 0xffffu) : r2o_f16_to_f32(v & 0xffffu);
+            qf[2 * w + 1] = p.q_dtype == 0 ? r2o_bf16_to_f32(v >> 16) : r2o_f16_to_f32(v >> 16);
+        }
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -709,9 +907,9 @@ __device__ __forceinline__ void touch_combine_kernarg(const r2o_decode_params& p
                  "s"(p.output_hadamard), "s"(ca.gqa), "s"(ca.n_groups), "s"(range_begin), "s"(range_end));
 }
 
-template <int KIND, int KF, bool TS, int RF>
-__device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
-                            unsigned char* smem, WaveState& st, Stamps& ts) {
+template <int KIND, int KF, bool TS, int RF, int RO>
+__device__ __forceinline__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
+                                            unsigned char* smem, WaveState& st, Stamps& ts) {
     using Cfg = KernelCfg<KF>;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
@@ -720,7 +918,9 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     const int per = (int)((it.ntiles + Cfg::kWaves - 1) / Cfg::kWaves);
     const int t_begin = wave * per;
     const int t_end = min((int)it.ntiles, t_begin + per);
-    if (t_begin >= t_end) return;
+    if constexpr (RO == kRopeNone) {
+        if (t_begin >= t_end) return;
+    }  // with a folded rotation a wave without tiles still rotates its rows and meets the barrier
     unsigned char* ring = smem + wave * Cfg::kWaveLds;
 
     DmaCtx c;
@@ -769,11 +969,24 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
     for (int j = 0; j < kDmaStages; ++j)
         if (j < n) dma_tile<KIND, KF>(c, a_first + 32 * j, ring + j * Cfg::kStage, lane, true);
     stamp(ts, 2);
+    r2o_u4 qrot[4];
+    if constexpr (RO != kRopeNone) {  // the waves share the rotation while their first tiles are in flight
+        uint16_t* rot = reinterpret_cast<uint16_t*>(smem + Cfg::kSmem);
+        const int r = 4 * wave + (lane >> 4);
+        if (r < gqa) {  // whole 16-lane groups
+            RotPrefetch f;
+            rot_prefetch(p, b, query_row<kRopeMrope>(p, b, kvh, gqa, r), l16, f);
+            rot_block_row(p, b, kvh, gqa, r, l16, f, rot);
+        }
+        __syncthreads();
+        if (n <= 0) return;
+        rot_read_query(rot, gqa, l16, g, qrot);
+    }
 
     const VConst vc = make_vconst();
     const float qscale = p.sm_scale * kLog2e;
     SegState<KIND> ss;
-    load_query<KF, RF>(p, b, kvh, gqa, l16, g, qscale, ss.qp);  // BF16-K: row-type pairs, scaled after the MFMA
+    load_query<KF, RF, RO>(p, b, kvh, gqa, l16, g, qscale, ss.qp, qrot);  // BF16-K: row-type pairs, scaled after the MFMA
 #pragma unroll
     for (int e = 0; e < (KIND == kI2 ? 3 : 2); ++e) ss.bias[e] = r2o_f4{0, 0, 0, 0};
     const SegCtx sc = {c.lo, c.hi};
@@ -826,10 +1039,13 @@ __device__ void run_segment(const r2o_decode_params& p, const r2o_work_item& it,
 
 // Recent-FP ring tiles (bf16 K and V, plus the fused-append token).  Every load of a tile is
 // issued before any is used (rows past the valid end read the last valid row, whose
-// probability is 0); a tile with no valid token is skipped.
-template <int KF, int RF>
-__device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
-                           WaveState& st) {
+// probability is 0); a tile with no valid token is skipped.  With a folded rotation (RO) the item's
+// waves rotate the query heads and the appended K and V rows together (rot_block_row, which also
+// stores the appended rows for the combine's fused append), and the tile holding the appended token
+// takes its rows from LDS.
+template <int KF, int RF, int RO>
+__device__ __forceinline__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
+                                           unsigned char* smem, WaveState& st) {
     constexpr int kWaves = KernelCfg<KF>::kWaves;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
@@ -843,15 +1059,33 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
     const int recent_len = min(p.step_positions ? *it.ring_length : p.recent_len[b], (int)it.hi);
     const bool app = p.do_append != 0;
     const int valid_end = recent_len + (app ? 1 : 0);
+    uint16_t* rot = reinterpret_cast<uint16_t*>(smem + KernelCfg<KF>::kSmem);
+    if constexpr (RO != kRopeNone) {  // every wave, before any returns: the rows meet in LDS
+        const int nrows = gqa + (app ? 2 : 0);
+        for (int r0 = 4 * wave; r0 < nrows; r0 += 16) {  // wave-uniform
+            const int r = r0 + (lane >> 4);
+            if (r < nrows) {  // whole 16-lane groups
+                RotPrefetch f;
+                rot_prefetch(p, b, rot_source(p, b, kvh, gqa, r), l16, f);
+                rot_block_row(p, b, kvh, gqa, r, l16, f, rot);
+            }
+        }
+        __syncthreads();
+    }
     if (t_begin >= t_end || valid_end == 0) return;
     const float qscale = p.sm_scale * kLog2e;
     const bool head_ok = l16 < gqa;
     uint32_t qp[4][4];
-    load_query<kKBf16, RF>(p, b, kvh, gqa, l16, g, qscale, qp);
+    r2o_u4 qrot[4];
+    if constexpr (RO != kRopeNone) rot_read_query(rot, gqa, l16, g, qrot);
+    load_query<kKBf16, RF, RO>(p, b, kvh, gqa, l16, g, qscale, qp, qrot);
+    // folded rotation: the tile holding the appended token takes the rotated rows from LDS
+    const int t_new = RO != kRopeNone && app && recent_len >= (int)it.tile0 ? (recent_len - (int)it.tile0) >> 5 : -1;
     const uint16_t* ring_k = reinterpret_cast<const uint16_t*>(it.k_base);
     const uint16_t* ring_v = reinterpret_cast<const uint16_t*>(it.v_base);
-    const uint16_t* new_k = app ? p.append_k + (b * p.hkv + kvh) * 128 : ring_k;
-    const uint16_t* new_v = app ? p.append_v + (b * p.hkv + kvh) * 128 : ring_v;
+    // (with a folded rotation the appended token's rows come from LDS: ring row 0 stands in)
+    const uint16_t* new_k = app && RO == kRopeNone ? p.append_k + (b * p.hkv + kvh) * 128 : ring_k;
+    const uint16_t* new_v = app && RO == kRopeNone ? p.append_v + (b * p.hkv + kvh) * 128 : ring_v;
     for (int t = t_begin; t < t_end; ++t) {
         const int a0 = (int)it.tile0 + 32 * t;
         if (a0 >= valid_end) break;  // wave-uniform
@@ -868,6 +1102,20 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
             const int slot = min(a0 + tile_token(g, k), valid_end - 1);
             const uint16_t* vrow = slot == recent_len ? new_v : ring_v + slot * 128;
             R[k] = r2o_ldg(reinterpret_cast<const r2o_u4*>(vrow + 8 * l16));
+        }
+        if constexpr (RO != kRopeNone) {
+            if (t == t_new) {  // wave-uniform: the appended token's tile takes its rotated rows
+                const r2o_u4* nk = reinterpret_cast<const r2o_u4*>(rot + kRotKeyRow * kRotStride + 32 * g);
+                const r2o_u4 nv = *reinterpret_cast<const r2o_u4*>(rot + (kRotKeyRow + 1) * kRotStride + 8 * l16);
+#pragma unroll
+                for (int mg = 0; mg < 2; ++mg) {
+                    const bool mine = min(a0 + 16 * mg + l16, valid_end - 1) == recent_len;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) kr[mg][j] = mine ? nk[j] : kr[mg][j];
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) R[k] = min(a0 + tile_token(g, k), valid_end - 1) == recent_len ? nv : R[k];
+            }
         }
         r2o_f4 s[2];
 #pragma unroll
@@ -888,11 +1136,11 @@ __device__ void run_recent(const r2o_decode_params& p, const r2o_work_item& it,
     }
 }
 
-template <int KF, int RF>
+template <int KF, int RF, int RO>
 __global__ __launch_bounds__(KernelCfg<KF>::kThreads, KernelCfg<KF>::kWavesPerSimd) void decode_partial_kernel(
         r2o_decode_params p) {
     constexpr int kWaves = KernelCfg<KF>::kWaves;
-    __shared__ __align__(16) unsigned char smem[KernelCfg<KF>::kSmem];
+    __shared__ __align__(16) unsigned char smem[KernelCfg<KF>::kSmem + (RO != kRopeNone ? kRotBytes : 0)];
     Stamps ts{};
     stamp(ts, 0);
     const r2o_work_item it = p.items[blockIdx.x];
@@ -917,13 +1165,13 @@ __global__ __launch_bounds__(KernelCfg<KF>::kThreads, KernelCfg<KF>::kWavesPerSi
     for (int q = 0; q < 8; ++q) st.acc[q] = r2o_f4{0, 0, 0, 0};
 
     switch (it.kind) {
-        case kFP: run_segment<kFP, KF, false, RF>(p, it, smem, st, ts); break;
-        case kI4: run_segment<kI4, KF, false, RF>(p, it, smem, st, ts); break;
+        case kFP: run_segment<kFP, KF, false, RF, RO>(p, it, smem, st, ts); break;
+        case kI4: run_segment<kI4, KF, false, RF, RO>(p, it, smem, st, ts); break;
         case kI2:  // INT2 values: one scale and zero point per token when a group spans all 128 dims
-            if (it.v_group == 128) run_segment<kI2, KF, true, RF>(p, it, smem, st, ts);
-            else run_segment<kI2, KF, false, RF>(p, it, smem, st, ts);
+            if (it.v_group == 128) run_segment<kI2, KF, true, RF, RO>(p, it, smem, st, ts);
+            else run_segment<kI2, KF, false, RF, RO>(p, it, smem, st, ts);
             break;
-        default: run_recent<KF, RF>(p, it, st); break;
+        default: run_recent<KF, RF, RO>(p, it, smem, st); break;
     }
 
     // ---- per-wave epilogue: reduce l (and u) over the 4 lane groups of each head
@@ -998,8 +1246,8 @@ __device__ __forceinline__ void fused_append(const r2o_decode_params& p, int64_t
     // Every load that does not depend on the ring position is issued before it is known: the
     // appended rows (16 bytes a piece) and this step's (global, logical) positions.
     const int pieces = (int)p.hkv * 16;
-    const r2o_u4* src_k = reinterpret_cast<const r2o_u4*>(p.append_k + b * p.hkv * 128);
-    const r2o_u4* src_v = reinterpret_cast<const r2o_u4*>(p.append_v + b * p.hkv * 128);
+    const r2o_u4* src_k = reinterpret_cast<const r2o_u4*>(p.append_k + b * p.hkv * 128);  // dense rows (the
+    const r2o_u4* src_v = reinterpret_cast<const r2o_u4*>(p.append_v + b * p.hkv * 128);  // rotated ones too)
     r2o_u4 rk[kAppendPieces], rv[kAppendPieces];
 #pragma unroll
     for (int k = 0; k < kAppendPieces; ++k) {  // unconditional loads (clamped index), guarded stores
@@ -1212,6 +1460,39 @@ int validate(const r2o_decode_params* p) {
                          reinterpret_cast<uintptr_t>(p->append_v) % 16))
         return R2O_EINVAL;
     if (reinterpret_cast<uintptr_t>(p->partial_out) % 16) return R2O_EINVAL;  // 16-byte vector rows
+    if (reinterpret_cast<uintptr_t>(p->query) % 16) return R2O_EINVAL;        // 16-byte query loads
+    // strided query / appended rows: whole 16-byte pieces per row, rows of one request not overlapping
+    if (p->query_batch_stride && (p->query_batch_stride % 8 || p->query_batch_stride < p->hq * 128)) return R2O_EINVAL;
+    if (p->append_batch_stride && (p->append_batch_stride % 8 || p->append_batch_stride < p->hkv * 128))
+        return R2O_EINVAL;
+    // strided rows only with a folded rotation (the other instances address dense rows)
+    if (p->rope_mode == kRopeNone && ((p->query_batch_stride && p->query_batch_stride != p->hq * 128) ||
+                                      (p->append_batch_stride && p->append_batch_stride != p->hkv * 128)))
+        return R2O_EINVAL;
+#ifdef R2O_TIMELINE
+    if (p->rope_mode != kRopeNone) return R2O_EINVAL;
+#endif
+    if (p->rope_mode != kRopeNone) {  // folded rotation: the tables, sections and rotated-row outputs
+        if (p->rope_mode != kRopeMrope || !p->rope_cos || !p->rope_sin) return R2O_EINVAL;
+        if (p->rope_table_dtype < 0 || p->rope_table_dtype > 2) return R2O_EINVAL;
+        const int64_t esize = p->rope_table_dtype == 2 ? 4 : 2, piece = 16 / esize;
+        for (const int64_t* st : {p->rope_cos_strides, p->rope_sin_strides}) {
+            for (int i = 0; i < 4; ++i)
+                if (st[i] < 0) return R2O_EINVAL;
+            // channel runs read as whole 16-byte pieces: unit channel stride, axis and request rows on
+            // 16 bytes; a request's entries within 2^31 bytes of its base (32-bit offsets in the kernel)
+            if (st[3] != 1 || st[0] % piece || st[1] % piece || st[0] >= (int64_t(1) << 29) ||
+                (2 * st[0] + 128) * esize >= (int64_t(1) << 31))
+                return R2O_EINVAL;
+        }
+        if (reinterpret_cast<uintptr_t>(p->rope_cos) % 16 || reinterpret_cast<uintptr_t>(p->rope_sin) % 16)
+            return R2O_EINVAL;
+        if (p->rope_section0 < 0 || p->rope_section1 < 0 || p->rope_section0 + p->rope_section1 > 64) return R2O_EINVAL;
+        if (p->q_dtype != p->row_dtype) return R2O_EINVAL;  // one dtype for the rotated query and key
+        if (p->do_append && (!p->rotated_k || !p->rotated_v || reinterpret_cast<uintptr_t>(p->rotated_k) % 16 ||
+                             reinterpret_cast<uintptr_t>(p->rotated_v) % 16))
+            return R2O_EINVAL;
+    }
     return R2O_OK;
 }
 
@@ -1249,30 +1530,54 @@ float* scratch_address(int dev) {
     return ptr;
 }
 
-int launch_decode(const r2o_decode_params& p, hipStream_t stream) {
+template <int RO>
+void launch_partial(const r2o_decode_params& p, hipStream_t stream) {
     const dim3 grid((unsigned)p.n_items);
     const dim3 block(KernelCfg<kKInt4>::kThreads), block_bf16(KernelCfg<kKBf16>::kThreads);
     static_assert(KernelCfg<kKInt4>::kThreads == KernelCfg<kKInt2>::kThreads, "one workgroup size for the low-bit K formats");
     const bool f16 = p.row_dtype == kRowF16;
     switch (p.k_format) {
         case kKInt4:
-            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKInt4, kRowF16>), grid, block, 0, stream, p);
-            else hipLaunchKernelGGL((decode_partial_kernel<kKInt4, kRowBf16>), grid, block, 0, stream, p);
+            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKInt4, kRowF16, RO>), grid, block, 0, stream, p);
+            else hipLaunchKernelGGL((decode_partial_kernel<kKInt4, kRowBf16, RO>), grid, block, 0, stream, p);
             break;
         case kKBf16:
-            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowF16>), grid, block_bf16, 0, stream, p);
-            else hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowBf16>), grid, block_bf16, 0, stream, p);
+            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowF16, RO>), grid, block_bf16, 0, stream, p);
+            else hipLaunchKernelGGL((decode_partial_kernel<kKBf16, kRowBf16, RO>), grid, block_bf16, 0, stream, p);
             break;
         default:
-            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKInt2, kRowF16>), grid, block, 0, stream, p);
-            else hipLaunchKernelGGL((decode_partial_kernel<kKInt2, kRowBf16>), grid, block, 0, stream, p);
+            if (f16) hipLaunchKernelGGL((decode_partial_kernel<kKInt2, kRowF16, RO>), grid, block, 0, stream, p);
+            else hipLaunchKernelGGL((decode_partial_kernel<kKInt2, kRowBf16, RO>), grid, block, 0, stream, p);
             break;
     }
+}
+
+// The kernels' copy of the arguments: row strides of 0 (dense) spelled out.
+r2o_decode_params kernel_params(const r2o_decode_params& params) {
+    r2o_decode_params p = params;
+    if (p.query_batch_stride == 0) p.query_batch_stride = p.hq * 128;
+    if (p.append_batch_stride == 0) p.append_batch_stride = p.hkv * 128;
+    return p;
+}
+
+int launch_decode(const r2o_decode_params& params, hipStream_t stream) {
+    const r2o_decode_params p = kernel_params(params);
+#ifndef R2O_TIMELINE  // the phase-stamp build (bench.py --timeline) has no rotating instances
+    if (p.rope_mode == kRopeMrope) launch_partial<kRopeMrope>(p, stream);
+    else
+#endif
+        launch_partial<kRopeNone>(p, stream);
     R2O_CHECK_LAUNCH();
     return R2O_OK;
 }
 
-int launch_combine(const r2o_decode_params& p, hipStream_t stream) {
+int launch_combine(const r2o_decode_params& params, hipStream_t stream) {
+    r2o_decode_params p = kernel_params(params);
+    if (p.rope_mode != kRopeNone) {  // the fused append copies the rows the partial pass rotated
+        p.append_k = p.rotated_k;
+        p.append_v = p.rotated_v;
+        p.append_batch_stride = p.hkv * 128;
+    }
     CombineArgs ca{};
     const int64_t groups = p.batch * p.hkv;
     ca.gqa = (int32_t)(p.hq / p.hkv);

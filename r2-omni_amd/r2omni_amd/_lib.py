@@ -34,7 +34,7 @@ class DecodeParams(ctypes.Structure):
         ("partial_sum", c_vp),
         ("partial_out", c_vp),
         ("query", c_vp),
-        ("out", c_vp),
+        ("query_batch_stride", c_i64),
         ("append_k", c_vp),
         ("append_v", c_vp),
         ("step_positions", c_vp),
@@ -49,12 +49,26 @@ class DecodeParams(ctypes.Structure):
         ("do_append", c_i64),
         ("k_format", c_i64),
         ("sm_scale", ctypes.c_float),
+        ("out", c_vp),
+        ("append_batch_stride", c_i64),
         ("recent_len", ctypes.c_int32 * MAX_BATCH),
         ("append_global", c_i64 * MAX_BATCH),
         ("append_logical", c_i64 * MAX_BATCH),
         ("row_dtype", c_i64),
         ("group_begin_host", ctypes.c_void_p),
         ("partial_capacity", c_i64),
+        ("rope_mode", c_i64),
+        ("rope_cos", c_vp),
+        ("rope_sin", c_vp),
+        ("rope_cos_strides", c_i64 * 4),
+        ("rope_sin_strides", c_i64 * 4),
+        ("rope_table_dtype", c_i64),
+        ("rope_section0", c_i64),
+        ("rope_section1", c_i64),
+        ("rope_hadamard", c_i64),
+        ("value_hadamard", c_i64),
+        ("rotated_k", c_vp),
+        ("rotated_v", c_vp),
     ]
 
 

@@ -53,12 +53,15 @@ class BatchedDecoder:
     attention output of the step (query over history + ring + the new token, whose K/V row is
     appended to each ring by the same launch).  Inputs are copied into static buffers, so the
     caller may reuse its tensors; a caller that writes ``query_buffer`` / ``key_buffer`` /
-    ``value_buffer`` directly can call ``step_in_place``.
+    ``value_buffer`` directly can call ``step_in_place``, and ``bind_inputs`` makes those buffers
+    views the caller owns (for instance slices of a fused QKV projection's output).  With ``rotary``
+    (a ``FusedRotary`` whose tables the caller rewrites in place every step) the inputs are the raw
+    projections and every step's launch applies the mRoPE / FWHT itself.
     """
 
     def __init__(self, caches: Sequence[ThreePrecisionCache], *, num_query_heads: int,
                  output_hadamard: bool = False, use_graph: bool = True,
-                 stats: Sequence[DynamicCacheStats] | None = None):
+                 stats: Sequence[DynamicCacheStats] | None = None, rotary=None):
         self.caches = list(caches)
         if not self.caches:
             raise ValueError("a decode batch needs at least one request")
@@ -73,6 +76,7 @@ class BatchedDecoder:
         self.hq = int(num_query_heads)
         self.output_hadamard = bool(output_hadamard)
         self.use_graph = bool(use_graph)
+        self.rotary = rotary
         self.stats = list(stats) if stats is not None else [DynamicCacheStats() for _ in self.caches]
         if len(self.stats) != len(self.caches):
             raise ValueError("one DynamicCacheStats per request")
@@ -102,13 +106,35 @@ class BatchedDecoder:
         self._params = self.executor._params(self.query_buffer, self.workspace.output,
                                              (self.key_buffer, self.value_buffer, [0] * len(self.caches),
                                               [0] * len(self.caches)),
-                                             step_positions=self.step_positions)
+                                             step_positions=self.step_positions, rotary=self.rotary)
         self.replans += 1
+
+    def bind_inputs(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> None:
+        """Read each step's query [B, Hq, 128] and new K / V rows [B, Hkv, 128] from the caller's tensors
+        (in the ring dtype) instead of the decoder's own buffers: contiguous, or, for a decoder with a
+        folded rotation, with unit strides inside a request and requests a multiple of 8 elements
+        apart (e.g. ``qkv[:, a:b].view(B, H, 128)`` of a fused projection).  They are read when the
+        step's launch runs: a captured graph reads them at every replay."""
+        from .splitk import _row_layout_ok
+
+        b, rows = len(self.caches), self.caches[0].recent_fp_pool.fp_k.dtype
+        for t, heads, what in ((query, self.hq, "query"), (key, self.hkv, "key"), (value, self.hkv, "value")):
+            if tuple(t.shape) != (b, heads, 128) or t.dtype != rows or t.device != self.device \
+                    or not _row_layout_ok(t, heads):
+                raise ValueError(f"bound {what} rows must be [B,{heads},128] of the ring dtype, with unit strides "
+                                 "inside a request and requests a multiple of 8 elements apart")
+            if self.rotary is None and not t.is_contiguous():
+                raise ValueError(f"bound {what} rows must be contiguous without a folded rotation (FusedRotary)")
+        if key.stride() != value.stride():
+            raise ValueError("bound key and value rows must share one layout")
+        self.query_buffer, self.key_buffer, self.value_buffer = query, key, value
+        self._replan()
 
     def _capture(self) -> None:
         # one eager launch first (no append, host-provided lengths: it only rewrites the output) so
         # that nothing is loaded or initialised for the first time while the stream is capturing
-        self.executor._launch(self.executor._params(self.query_buffer, self.workspace.output, None), self.device)
+        self.executor._launch(self.executor._params(self.query_buffer, self.workspace.output, None, rotary=self.rotary),
+                              self.device)
         if self._capture_stream is None:
             self._capture_stream = torch.cuda.Stream(device=self.device)
         self._graph = _capture_launches(self.device, self._capture_stream,
@@ -189,7 +215,8 @@ class DecodeStepGraph:
 
     def _capture(self) -> None:
         for d in self.layers:  # eager warm-up without append (rewrites the outputs only)
-            d.executor._launch(d.executor._params(d.query_buffer, d.workspace.output, None), self.device)
+            d.executor._launch(d.executor._params(d.query_buffer, d.workspace.output, None, rotary=d.rotary),
+                               self.device)
 
         def launches():
             for d in self.layers:

@@ -73,24 +73,67 @@ def _link(sources, path: str, verbose: bool, defines=(), rebuild=None) -> None:
             continue
         obj = os.path.join(build_dir, stem + suffix + ".o")
         cmd = [hipcc, *common_flags(), *[f"-D{d}" for d in defines], "-c", os.path.join(CSRC, src), "-o", obj]
-        _run(cmd, verbose)
+        if src.endswith(".hip"):
+            cmd.append("-Rpass-analysis=kernel-resource-usage")
+        stderr = _run(cmd, verbose)
+        if src.endswith(".hip"):
+            _check_resources(src + suffix, stderr, os.path.join(build_dir, stem + suffix + ".resources.txt"))
         objects.append(obj)
     tmp = path + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", tmp], verbose)
     os.replace(tmp, path)
 
 
-def _run(cmd: list[str], verbose: bool) -> None:
+def _run(cmd: list[str], verbose: bool) -> str:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"HIP build failed: {' '.join(cmd[:3])} ... ({res.returncode})")
-    noise = "is not a recognized feature for this target"
-    rest = [ln for ln in (res.stderr or "").splitlines() if noise not in ln and ln.strip()]
+    noise = ("is not a recognized feature for this target", "-Rpass-analysis=kernel-resource-usage")
+    rest = [ln for ln in (res.stderr or "").splitlines() if not any(n in ln for n in noise) and ln.strip()
+            and not ln.startswith(" ")]
     if verbose and rest:
         sys.stderr.write("\n".join(rest) + "\n")
+    return res.stderr or ""
+
+
+_RESOURCE_KEYS = ("VGPRs", "AGPRs", "TotalSGPRs", "ScratchSize [bytes/lane]", "VGPRs Spill", "SGPRs Spill",
+                  "Occupancy [waves/SIMD]", "LDS Size [bytes/block]")
+
+
+def kernel_resources(stderr: str) -> dict[str, dict[str, int]]:
+    """Per-kernel register, scratch and LDS figures from the compiler's kernel-resource-usage remarks."""
+    out: dict[str, dict[str, int]] = {}
+    name = None
+    for ln in stderr.splitlines():
+        if "remark:" not in ln:
+            continue
+        body = ln.split("remark:", 1)[1].strip()
+        if body.startswith("Function Name:"):
+            name = body.split(":", 1)[1].split("[")[0].strip()
+            out[name] = {}
+            continue
+        for key in _RESOURCE_KEYS:
+            if name is not None and body.startswith(key + ":"):
+                out[name][key] = int(body.split(":", 1)[1].split()[0])
+    return out
+
+
+def _check_resources(what: str, stderr: str, path: str) -> None:
+    """Every kernel keeps its state in registers and LDS: a kernel with scratch (a spill, a private
+    array indexed at run time, or a device function left as a call, whose arguments and saved
+    registers go through the stack) fails the build.  The figures are kept beside the object."""
+    res = kernel_resources(stderr)
+    with open(path, "w") as f:
+        f.write("kernel " + " | ".join(_RESOURCE_KEYS) + "\n")
+        for k, v in sorted(res.items()):
+            f.write(k + " " + " | ".join(str(v.get(key, "?")) for key in _RESOURCE_KEYS) + "\n")
+    bad = [k for k, v in res.items() if v.get("ScratchSize [bytes/lane]", 0) or v.get("VGPRs Spill", 0)
+           or v.get("SGPRs Spill", 0)]
+    if bad:
+        raise RuntimeError(f"{what}: kernels using scratch memory: {', '.join(sorted(bad))}")
 
 
 if __name__ == "__main__":

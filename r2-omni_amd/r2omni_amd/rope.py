@@ -12,12 +12,68 @@ from __future__ import annotations
 
 import ctypes
 from collections.abc import Sequence
+from dataclasses import dataclass
 
 import torch
 
 from . import _lib
 
 _TABLE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+@dataclass(frozen=True)
+class FusedRotary:
+    """The decode step's Qwen mRoPE, folded into the split-K call.
+
+    Given to ``SplitKExecutor.__call__(query, append, rotary=...)`` or ``BatchedDecoder(...,
+    rotary=...)``, the query and the appended key and value are the raw projections, and the partial
+    kernel applies what ``qwen_qk_mrope(q, k, cos, sin, mrope_section, apply_hadamard=...)`` and the
+    manager's value Hadamard (``triton_fwht_128(v)`` when ``value_hadamard``) would (qwen_sspa_attention.py:
+    1239-1247, 230-235; triton_qwen_mrope.py:45-124), bit-identically, without their launch; the rotated
+    appended rows reach the ring through the fused append.  ``cos`` / ``sin``: [3, B, T, 128] tables of
+    the step (token 0 is used), bf16, fp16 or fp32, with unit channel stride and 16-byte aligned
+    (axis, request) rows, such as contiguous tables or a token slice of them.  Under a captured graph the tables' storage is read at every replay: write
+    each step's values into the same tensors."""
+    cos: torch.Tensor
+    sin: torch.Tensor
+    mrope_section: tuple
+    apply_hadamard: bool = False
+    value_hadamard: bool = False
+
+    def fill(self, p: _lib.DecodeParams, batch: int, device: torch.device) -> None:
+        """Write the rotation into the launch arguments (checks as ``qwen_qk_mrope``'s)."""
+        cos, sin = self.cos, self.sin
+        if cos.shape != sin.shape or cos.ndim != 4 or int(cos.shape[0]) != 3 or int(cos.shape[-1]) != 128:
+            raise ValueError("Qwen fused mRoPE requires cos/sin [3,B,S,D]")
+        if int(cos.shape[1]) != batch or int(cos.shape[2]) < 1:
+            raise ValueError("Qwen fused mRoPE rotary positions must match Q/K tokens")
+        if cos.device != device or sin.device != device:
+            raise ValueError("Q/K and rotary tensors must share a device")
+        if cos.dtype != sin.dtype or cos.dtype not in _TABLE_CODES:
+            raise ValueError("Qwen fused mRoPE cos/sin must share a bf16, fp16 or fp32 dtype")
+        sections = tuple(int(v) for v in self.mrope_section)
+        if len(sections) != 3 or sum(sections) != 64:
+            raise ValueError("Qwen mRoPE sections must contain three values summing to 64")
+        if min(sections) < 0:
+            raise ValueError("Qwen mRoPE sections must be non-negative")
+        esize = cos.element_size()
+        piece = 16 // esize
+        for t in (cos, sin):  # the kernel reads 16-byte pieces at 32-bit byte offsets from a request's base
+            st = t.stride()
+            if min(st) < 0 or st[3] != 1 or st[0] % piece or st[1] % piece or t.data_ptr() % 16:
+                raise ValueError("Qwen fused mRoPE tables need unit channel stride and 16-byte aligned "
+                                 "rows (e.g. contiguous [3, B, T, 128] tables)")
+            if (2 * st[0] + 128) * esize >= 1 << 31:
+                raise ValueError("Qwen fused mRoPE tables must span less than 2 GiB per request")
+        p.rope_mode = 1
+        p.rope_cos, p.rope_sin = cos.data_ptr(), sin.data_ptr()
+        for i in range(4):
+            p.rope_cos_strides[i] = int(cos.stride(i))
+            p.rope_sin_strides[i] = int(sin.stride(i))
+        p.rope_table_dtype = _TABLE_CODES[cos.dtype]
+        p.rope_section0, p.rope_section1 = sections[0], sections[1]
+        p.rope_hadamard = int(bool(self.apply_hadamard))
+        p.value_hadamard = int(bool(self.value_hadamard))
 
 
 def _value_operands(value, output, apply_hadamard, what):

@@ -291,6 +291,10 @@ class SplitKExecutor:
     # (triton_fourq_splitk.py:1232-1241, 1543-1546): the source caches are never written.
     batched_recent: list | None = None
     batched_recent_lengths: list | None = None
+    # [B, Hkv, 128] rows of the ring dtype: with a folded rotation (FusedRotary) the partial pass writes
+    # the rotated appended K / V rows here and the combine's fused append copies them into the ring
+    rotated_k: torch.Tensor | None = None
+    rotated_v: torch.Tensor | None = None
     _keep: list = field(default_factory=list)
     _template: tuple | None = field(default=None, repr=False, compare=False)
 
@@ -329,23 +333,37 @@ class SplitKExecutor:
         return p
 
     def _params(self, query: torch.Tensor, out: torch.Tensor, append, *,
-                step_positions: torch.Tensor | None = None) -> _lib.DecodeParams:
+                step_positions: torch.Tensor | None = None, rotary=None) -> _lib.DecodeParams:
         """Launch arguments.  With ``step_positions`` (device int64 [B, 2]) the launch runs in
         device-state mode: ring lengths and append positions are read (and advanced) on the device,
-        so the same arguments stay valid for every later step (graph capture)."""
+        so the same arguments stay valid for every later step (graph capture).  ``query`` and the
+        appended rows are [B, H, 128] with unit strides inside a request (``_row_stride``); ``rotary``
+        (a ``FusedRotary``) folds the decode step's rotation into the launch."""
         p = _lib.DecodeParams.from_buffer_copy(self._static_params())
         if step_positions is not None:
             p.step_positions = step_positions.data_ptr()
         p.query, p.out = query.data_ptr(), out.data_ptr()
+        p.query_batch_stride = _row_stride(query, self.num_query_heads, "query")
+        if p.query_batch_stride and rotary is None:
+            raise ValueError("strided query rows need a folded rotation (FusedRotary); pass a contiguous query")
         p.q_dtype = _lib.dtype_code(query.dtype)
         for r, n in enumerate(self._ring_lengths()):
             p.recent_len[r] = n
         if append is not None:
             ak, av, gidx, lpos = append
             p.append_k, p.append_v, p.do_append = ak.data_ptr(), av.data_ptr(), 1
+            sk = _row_stride(ak, self.num_key_value_heads, "append K")
+            if _row_stride(av, self.num_key_value_heads, "append V") != sk:
+                raise ValueError("append K/V must share one layout")
+            if sk and rotary is None:
+                raise ValueError("strided append K/V rows need a folded rotation (FusedRotary)")
+            p.append_batch_stride = sk
             for r in range(len(self.caches)):
                 p.append_global[r] = int(gidx[r])
                 p.append_logical[r] = int(lpos[r])
+        if rotary is not None:
+            rotary.fill(p, len(self.caches), query.device)
+            p.rotated_k, p.rotated_v = self.rotated_k.data_ptr(), self.rotated_v.data_ptr()
         return p
 
     def _ring_lengths(self) -> list[int]:
@@ -353,13 +371,19 @@ class SplitKExecutor:
             return list(self.batched_recent_lengths)
         return [int(c.recent_fp_pool.active_length) for c in self.caches]
 
-    def __call__(self, query: torch.Tensor, append=None) -> torch.Tensor:
-        p, query, fused = self._prepare_call(query, append, self.workspace.output)
+    def __call__(self, query: torch.Tensor, append=None, *, rotary=None) -> torch.Tensor:
+        """The split-K decode call (partial + combine), with the fused Recent-FP append when ``append`` =
+        (K, V, global index, logical position) is given.  With ``rotary`` (a ``FusedRotary``) the query
+        and the appended rows are the raw projections and the launch applies the decode step's mRoPE
+        (and FWHT) itself, in place of a separate ``qwen_qk_mrope`` launch (an extension of the
+        reference's call, which takes rotated rows)."""
+        p, query, fused = self._prepare_call(query, append, self.workspace.output, rotary)
         self._launch(p, query.device)
         self._finish_call(fused)
         return self.workspace.output
 
-    def call_noalloc(self, query: torch.Tensor, append=None, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    def call_noalloc(self, query: torch.Tensor, append=None, *, out: torch.Tensor | None = None,
+                     rotary=None) -> torch.Tensor:
         """``__call__`` through ``r2o_decode_noalloc``: the partial states live in the library's
         per-GPU device array instead of the workspace, and nothing is allocated (unless ``append``
         rows need a 16-byte-aligned copy).  At most ``_lib.NOALLOC_MAX_ITEMS`` work items; calls that
@@ -370,7 +394,7 @@ class SplitKExecutor:
             raise ValueError("split-K output must be a contiguous bfloat16 tensor")
         if self.n_items > _lib.NOALLOC_MAX_ITEMS:
             raise ValueError(f"workspace-free decode holds at most {_lib.NOALLOC_MAX_ITEMS} work items")
-        p, query, fused = self._prepare_call(query, append, out)
+        p, query, fused = self._prepare_call(query, append, out, rotary)
         p.partial_max = p.partial_sum = p.partial_out = None
         p.partial_capacity = 0
         _noalloc_init(query.device)
@@ -379,13 +403,17 @@ class SplitKExecutor:
         self._finish_call(fused)
         return out
 
-    def _prepare_call(self, query: torch.Tensor, append, out: torch.Tensor):
+    def _prepare_call(self, query: torch.Tensor, append, out: torch.Tensor, rotary=None):
         """Checks of a decode call (before any launch) and its launch arguments."""
         if query.ndim == 4:
             query = query[:, :, 0]
         b = len(self.caches)
+        # contiguous, as the reference requires; with a folded rotation also rows readable in place (a
+        # view into a fused QKV projection: unit strides inside a request, requests a multiple of 8
+        # elements apart)
+        strided = rotary is not None
         if tuple(query.shape) != (b, self.num_query_heads, self.head_dim) or query.device != out.device \
-                or not query.is_contiguous():
+                or not _row_layout_ok(query, self.num_query_heads) or not (strided or query.is_contiguous()):
             raise ValueError("query does not match prepared split-K executor")
         if tuple(out.shape) != (b, self.num_query_heads, self.head_dim):
             raise ValueError("split-K workspace geometry is inconsistent")
@@ -394,15 +422,19 @@ class SplitKExecutor:
             ak, av, gidx, lpos = append
             if ak.ndim == 4:
                 ak, av = ak[:, :, 0], av[:, :, 0]
+            shape = (b, self.num_key_value_heads, self.head_dim)
             n = b * self.num_key_value_heads * self.head_dim
-            if ak.numel() != n or av.numel() != n or ak.device != query.device or av.device != query.device \
-                    or not ak.is_contiguous() or not av.is_contiguous():
+            if ak.numel() == n and av.numel() == n and ak.is_contiguous() and av.is_contiguous():
+                ak, av = ak.view(shape), av.view(shape)  # contiguous rows of the right size, any shape
+            if tuple(ak.shape) != shape or tuple(av.shape) != shape or ak.device != query.device \
+                    or av.device != query.device or not (strided or (ak.is_contiguous() and av.is_contiguous())):
                 raise ValueError("append K/V must be contiguous [B,Hkv,1,D] or [B,Hkv,D]")
             ring_dtype = self.caches[0].recent_fp_pool.fp_k.dtype
             if ak.dtype != ring_dtype or av.dtype != ring_dtype:
                 raise ValueError(f"append K/V must be {ring_dtype} like the Recent-FP ring")
-            if ak.data_ptr() % 16 or av.data_ptr() % 16:  # the kernel moves the rows in 16-byte pieces
-                ak, av = ak.clone(), av.clone()
+            if not _row_layout_ok(ak, self.num_key_value_heads) or not _row_layout_ok(av, self.num_key_value_heads) \
+                    or ak.stride() != av.stride():  # the kernels move the rows in 16-byte pieces
+                ak, av = ak.contiguous().clone(), av.contiguous().clone()
             capacity = self.caches[0].recent_fp_pool.capacity
             if self.batched_recent_lengths is not None:
                 if any(n >= capacity for n in self.batched_recent_lengths):
@@ -417,7 +449,9 @@ class SplitKExecutor:
             gl = _per_request(gidx, b)
             lp = _per_request(lpos, b)
             fused = (ak, av, gl, lp)
-        return self._params(query, out, fused), query, fused
+        if rotary is not None and query.dtype != self.caches[0].recent_fp_pool.fp_k.dtype:
+            raise ValueError("Q/K device and dtype must match")
+        return self._params(query, out, fused, rotary=rotary), query, fused
 
     def _finish_call(self, fused) -> None:
         # A stacked executor advances its private ring lengths; a B=1 executor leaves the cache's
@@ -445,10 +479,31 @@ def _noalloc_init(device: torch.device) -> None:
         _NOALLOC_READY.add(index)
 
 
+def _row_layout_ok(t: torch.Tensor, heads: int) -> bool:
+    """Whether [B, heads, 128] rows can be read in place: unit strides inside a request, whole 16-byte
+    pieces, requests apart by a multiple of 8 elements without overlapping."""
+    if t.ndim != 3 or int(t.shape[1]) != heads or int(t.shape[2]) != 128:
+        return False
+    if t.stride(2) != 1 or (heads > 1 and t.stride(1) != 128) or t.data_ptr() % 16:
+        return False
+    return int(t.shape[0]) == 1 or (t.stride(0) % 8 == 0 and t.stride(0) >= heads * 128)
+
+
+def _row_stride(t: torch.Tensor, heads: int, what: str) -> int:
+    """r2o_decode_params' batch stride of [B, heads, 128] rows (0: dense)."""
+    if not _row_layout_ok(t, heads):
+        raise ValueError(f"{what} rows must be [B,{heads},128] with unit strides inside a request")
+    dense = heads * 128
+    return 0 if int(t.shape[0]) == 1 or t.stride(0) == dense else int(t.stride(0))
+
+
 def _per_request(value, b: int) -> list[int]:
     if isinstance(value, int):
         return [int(value)] * b
-    vals = torch.as_tensor(value).reshape(-1).tolist()
+    if isinstance(value, (list, tuple)) and all(isinstance(v, int) for v in value):
+        vals = list(value)  # plain positions: no tensor round trip (a few microseconds of host time per call)
+    else:
+        vals = torch.as_tensor(value).reshape(-1).tolist()
     if len(vals) == 1:
         return [int(vals[0])] * b
     if len(vals) != b:
@@ -533,6 +588,7 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
     if n > workspace.total_blocks:
         raise ValueError("workspace block capacity is smaller than the active cache")
     reqs, items, group_begin = _upload_plan(dev, host_reqs, host_items, begins)
+    rotated = torch.empty((2, len(caches), hkv, head_dim), device=dev, dtype=rec.fp_k.dtype)
     return SplitKExecutor(
         caches=list(caches), workspace=workspace, reqs=reqs, items=items, group_begin=group_begin,
         n_items=n, num_query_heads=hq, num_key_value_heads=hkv, head_dim=head_dim, superblock=sb, int2_group=group,
@@ -540,6 +596,7 @@ def _build_executor(caches: Sequence[ThreePrecisionCache], workspace: SplitKWork
         host_items=host_items, host_group_begin=begins.contiguous(),
         batched_recent=None if rings is None else list(rings),
         batched_recent_lengths=None if rings is None else [int(r.active_length) for r in rings],
+        rotated_k=rotated[0], rotated_v=rotated[1],
     )
 
 

@@ -89,6 +89,50 @@ def test_host_side_validation_rejects_bad_arguments_without_a_gpu():
     assert lib.r2o_decode(ctypes.byref(params), None) == 1
     params.partial_capacity = 0
     assert lib.r2o_decode_partial(ctypes.byref(params), None) == 1
+
+
+def test_folded_rotation_and_row_strides_are_checked_without_a_gpu():
+    """The rotation fields and the strided query / appended rows are refused before any launch when the
+    kernels could not honour them (placeholder pointers: nothing is dereferenced on the host)."""
+    lib = _lib.load()
+
+    def params(**kw):
+        p = _lib.DecodeParams(reqs=0x1000, items=0x2000, group_begin=0x3000, n_items=40, partial_max=0x4000,
+                              partial_sum=0x5000, partial_out=0x6000, query=0x7000, out=0x8000, batch=2, hq=28,
+                              hkv=4, superblock=32, int2_group=32, page_size=64, k_format=_lib.K_INT4,
+                              partial_capacity=40, append_k=0x9000, append_v=0xA000, do_append=1,
+                              rope_mode=1, rope_cos=0xB000, rope_sin=0xC000, rope_section0=16, rope_section1=24,
+                              rotated_k=0xD000, rotated_v=0xE000,
+                              rope_cos_strides=(ctypes.c_int64 * 4)(256, 128, 128, 1),
+                              rope_sin_strides=(ctypes.c_int64 * 4)(256, 128, 128, 1))
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return p
+
+    bad = {
+        "unknown rotation": dict(rope_mode=2),
+        "no cos table": dict(rope_cos=None),
+        "table dtype": dict(rope_table_dtype=3),
+        "sections past 64": dict(rope_section0=40, rope_section1=30),
+        "query and row dtypes differ": dict(q_dtype=0, row_dtype=1),
+        "no rotated-row output": dict(rotated_k=None),
+        "misaligned rotated rows": dict(rotated_v=0xE008),
+        "query stride not whole pieces": dict(query_batch_stride=28 * 128 + 4),
+        "query stride below a request": dict(query_batch_stride=128),
+        "append stride below a request": dict(append_batch_stride=256),
+        "misaligned query": dict(query=0x7008),
+        "negative table stride": dict(rope_sin_strides=(ctypes.c_int64 * 4)(-256, 128, 128, 1)),
+        "table past 2 GiB": dict(rope_cos_strides=(ctypes.c_int64 * 4)(1 << 30, 128, 128, 1)),
+        "table channels not unit-strided": dict(rope_cos_strides=(ctypes.c_int64 * 4)(512, 256, 128, 2)),
+        "table rows off 16 bytes": dict(rope_sin_strides=(ctypes.c_int64 * 4)(256, 132, 128, 1)),
+        "misaligned table": dict(rope_cos=0xB008),
+        "strided query without the rotation": dict(rope_mode=0, query_batch_stride=36 * 128),
+        "strided append rows without the rotation": dict(rope_mode=0, append_batch_stride=36 * 128),
+    }
+    for what, kw in bad.items():
+        p = params(**kw)
+        for fn in (lib.r2o_decode_partial, lib.r2o_decode_combine, lib.r2o_decode):
+            assert fn(ctypes.byref(p), None) == 1, what
     assert lib.r2o_build_target() == b"gfx950"
     # the planner refuses runs whose groups do not match the group count, without a GPU
     run = _lib.PlanRun(0, 0, _lib.KIND_RECENT, 0, 4, 0, 128, 0)
@@ -155,3 +199,39 @@ def test_phase_stamps_live_only_in_the_measurement_library():
     assert re.search(r"\bT r2o_timeline_read\b", timeline)
     for name in _declared():
         assert re.search(rf"\bT {name}\b", timeline), name
+
+
+def test_built_kernels_keep_their_state_in_registers_and_lds():
+    """The build records the compiler's resource figures of every kernel beside its object and fails
+    on scratch use; here every decode partial instance (3 key formats x 2 row dtypes x rotation folded
+    or not) and the combine are listed, with no scratch, no spills and two workgroups per CU."""
+    from r2omni_amd.build import ROOT_DIR
+
+    path = os.path.join(ROOT_DIR, "_build", "r2o_decode.resources.txt")
+    if not os.path.exists(path):
+        pytest.fail(f"{path} not written: run `python -m r2omni_amd.build` in r2-omni_amd/")
+    rows = [ln.split(" ", 1) for ln in open(path).read().splitlines()[1:]]
+    table = {name: [int(x) for x in vals.split(" | ")] for name, vals in rows}
+    partial = [n for n in table if "decode_partial_kernel" in n]
+    assert len(partial) == 12 and any("decode_combine_kernel" in n for n in table)
+    for name, (vgpr, agpr, sgpr, scratch, vspill, sspill, occupancy, lds) in table.items():
+        assert scratch == 0 and vspill == 0 and sspill == 0, name
+        if name in partial:
+            assert vgpr + agpr <= 256 and occupancy >= 2, name
+
+
+def test_resource_check_rejects_a_kernel_with_scratch(tmp_path):
+    from r2omni_amd.build import _check_resources, kernel_resources
+
+    def remarks(name, scratch):
+        return "\n".join(f"x.hip:1:1: remark: {body} [-Rpass-analysis=kernel-resource-usage]" for body in (
+            f"Function Name: {name}", "VGPRs: 188", "AGPRs: 0", "TotalSGPRs: 86",
+            f"ScratchSize [bytes/lane]: {scratch}", "VGPRs Spill: 0", "SGPRs Spill: 0",
+            "Occupancy [waves/SIMD]: 2", "LDS Size [bytes/block]: 43008"))
+
+    text = remarks("k_clean", 0) + "\n" + remarks("k_stack", 1296)
+    res = kernel_resources(text)
+    assert res["k_clean"]["VGPRs"] == 188 and res["k_stack"]["ScratchSize [bytes/lane]"] == 1296
+    _check_resources("x.hip", remarks("k_clean", 0), str(tmp_path / "ok.txt"))
+    with pytest.raises(RuntimeError, match="k_stack"):
+        _check_resources("x.hip", text, str(tmp_path / "bad.txt"))

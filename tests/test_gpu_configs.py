@@ -185,8 +185,10 @@ def test_config4_e2e_decode_properties():
     flushes every ring inside the batch; after it, the last layer's attention output of every request
     is checked against the oracle (cache rebuilt on the CPU from the same K/V, the step's token
     appended with its flush) and the arenas against the oracle's bit for bit.  Logits stay finite,
-    and the tokens of the HIP-graph run equal those of the eager run."""
+    and the tokens of the HIP-graph run equal those of the eager run and of a run with a separate
+    rotation launch (the decoder folds the mRoPE / FWHT into the attention call)."""
     import bench
+    import r2omni_amd as ro
     from oracle.attention import mixed_reference, output_transform
     from oracle.cache import append_token
 
@@ -203,7 +205,13 @@ def test_config4_e2e_decode_properties():
         if step != 0:
             return
         d = decs[layer]
-        q, k, v = _f32(d.query_buffer), _f32(d.key_buffer), _f32(d.value_buffer)
+        if d.rotary is not None:  # raw projections in the bound inputs: the rows the call rotated
+            rot = d.rotary
+            qr, _ = ro.qwen_qk_mrope(d.query_buffer[:, :, None], d.key_buffer[:, :, None], rot.cos, rot.sin,
+                                     rot.mrope_section, apply_hadamard=rot.apply_hadamard)
+            q, k, v = _f32(qr[:, :, 0]), _f32(d.executor.rotated_k), _f32(d.executor.rotated_v)
+        else:
+            q, k, v = _f32(d.query_buffer), _f32(d.key_buffer), _f32(d.value_buffer)
         out = d.workspace.output.clone()
         for s_i in range(model.batch):
             oc = _oracle(model.request_data(layer, s_i), cfg)
@@ -219,9 +227,11 @@ def test_config4_e2e_decode_properties():
     _, eager_tokens, eager_finite = model.decode(steps, False, inspect)
     print("[cfg4] HIP-graph decode", flush=True)
     _, graph_tokens, graph_finite = model.decode(steps, True)
+    print("[cfg4] HIP-graph decode with a separate rotation launch", flush=True)
+    _, sep_tokens, sep_finite = model.decode(steps, True, fused_rotation=False)
     assert len(checked) == model.batch
-    assert eager_finite and graph_finite
-    assert torch.equal(eager_tokens, graph_tokens)
+    assert eager_finite and graph_finite and sep_finite
+    assert torch.equal(eager_tokens, graph_tokens) and torch.equal(sep_tokens, graph_tokens)
     print(f"[cfg4] tokens of {steps} greedy steps equal in both modes", flush=True)
 
 
