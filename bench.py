@@ -944,6 +944,84 @@ def time_decode_layers(cfg, dev, *, n_layers: int, steps: int, warmup: int, seed
             "graph_calls": replays * n_rot, "n_items": layers[0][2].n_items, "ring_tokens": ring_n}
 
 
+def rotation_bench(cfg, dev, *, n_layers: int, steps: int) -> dict:
+    """The decode step's attention with the Q/K mRoPE + FWHT and the V FWHT folded into the split-K call
+    (``FusedRotary``: two launches) against the same call on rows rotated by a separate ``qwen_qk_mrope``
+    launch (three launches, as the reference's layer: qwen_sspa_attention.py:1239-1247, 230-235), both
+    with the fused append, rotating ``n_layers`` layer caches; and the partial kernel alone with and
+    without the folded rotation.  Every window as ``_time_events``."""
+    import torch
+
+    import r2omni_amd as ro
+    from r2omni_amd import _lib
+    from r2omni_amd.workloads import build_request_cache, make_request
+
+    b = len(cfg.lengths)
+    layers = []
+    for layer in range(n_layers):
+        datas = [make_request(cfg, total, seed=1000 * layer + r, device=dev) for r, total in enumerate(cfg.lengths)]
+        caches = [build_request_cache(cfg, d) for d in datas]
+        exs = [ro.prepare_splitk_executor(c, ro.allocate_splitk_workspace(c, num_query_heads=cfg.hq),
+                                          output_hadamard=True) for c in caches]
+        layers.append((caches, exs[0] if b == 1 else ro.stack_homogeneous_splitk_executors(exs)))
+        del datas
+    torch.cuda.synchronize()
+    gen = torch.Generator(device=dev).manual_seed(98)
+    row_dtype = layers[0][0][0].recent_fp_pool.fp_k.dtype
+    # the step's raw projections, views of one fused QKV row per request, and its mRoPE tables
+    qkv = torch.randn(b, (cfg.hq + 2 * cfg.hkv) * 128, generator=gen, device=dev).to(row_dtype)
+    q = qkv[:, : cfg.hq * 128].view(b, cfg.hq, 128)
+    k = qkv[:, cfg.hq * 128 : (cfg.hq + cfg.hkv) * 128].view(b, cfg.hkv, 128)
+    v = qkv[:, (cfg.hq + cfg.hkv) * 128 :].view(b, cfg.hkv, 128)
+    ang = torch.rand(3, b, 1, 64, generator=gen, device=dev) * 6.0
+    ang = torch.cat([ang, ang], dim=-1)
+    cos, sin = ang.cos().to(row_dtype), ang.sin().to(row_dtype)
+    sections = (16, 24, 24)
+    rot = ro.FusedRotary(cos, sin, sections, True, True)
+    qr, kr, vr = (torch.empty(t.shape, device=dev, dtype=row_dtype) for t in (q, k, v))  # the separate launch's rows
+    ring_n = [min(int(c.recent_fp_pool.active_length), c.recent_fp_pool.capacity - 1) for c in layers[0][0]]
+
+    def with_append(p, caches, kk, vv):
+        p.do_append, p.append_k, p.append_v = 1, kk.data_ptr(), vv.data_ptr()
+        p.append_batch_stride = 0 if kk.is_contiguous() else int(kk.stride(0))
+        for r, c in enumerate(caches):
+            p.recent_len[r] = ring_n[r]
+            p.append_global[r] = p.append_logical[r] = int(c.compact_key.active_length if c.compact_key is not None
+                                                           else c.bf16_key.active_length) + ring_n[r]
+        return p
+
+    fused = [with_append(ex._params(q, ex.workspace.output, None, rotary=rot), caches, k, v) for caches, ex in layers]
+    plain = [with_append(ex._params(qr, ex.workspace.output, None), caches, kr, vr) for caches, ex in layers]
+    part_f = [ex._params(q, ex.workspace.output, None, rotary=rot) for _, ex in layers]
+    part_p = [ex._params(qr, ex.workspace.output, None) for _, ex in layers]
+    refs = {name: [ctypes.byref(p) for p in ps] for name, ps in
+            (("fused", fused), ("plain", plain), ("part_f", part_f), ("part_p", part_p))}
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    n = len(layers)
+    q4, k4, v4 = q[:, :, None], k[:, :, None], v[:, :, None]
+    out4 = (qr[:, :, None], kr[:, :, None], vr[:, :, None])
+
+    def separate(i):  # the rotation launch, then the call on its rows
+        ro.qwen_qk_mrope(q4, k4, cos, sin, sections, apply_hadamard=True, value=v4, output=out4)
+        lib.r2o_decode(refs["plain"][i % n], sp)
+
+    res = {
+        "call_fused_us": _time_events(lambda i: lib.r2o_decode(refs["fused"][i % n], sp), steps, stream) * 1e3,
+        "call_separate_rotation_us": _time_events(separate, steps, stream) * 1e3,
+        "call_on_rotated_rows_us": _time_events(lambda i: lib.r2o_decode(refs["plain"][i % n], sp), steps, stream) * 1e3,
+        "partial_fused_us": _time_events(lambda i: lib.r2o_decode_partial(refs["part_f"][i % n], sp), steps, stream) * 1e3,
+        "partial_us": _time_events(lambda i: lib.r2o_decode_partial(refs["part_p"][i % n], sp), steps, stream) * 1e3,
+    }
+    return {"metric": "decode-step attention with the rotation folded in vs a separate rotation launch",
+            "config": {"workload": cfg.name, "lengths": list(cfg.lengths), "layers": n_layers,
+                       "mrope_sections": list(sections), "hadamard": True, "tables": str(row_dtype)},
+            **{kk: round(vv, 3) for kk, vv in res.items()}, "steps": steps,
+            "note": "call = r2o_decode (partial + combine with the fused append); separate = qwen_qk_mrope "
+                    "(Q/K mRoPE + FWHT and the V FWHT in one launch) then the call on its rows"}
+
+
 def timeline_bench(cfg, dev, *, n_layers: int, warmup: int, trials: int = 3) -> dict:
     """Phase breakdown of the layer call from the measurement build (libr2o_timeline.so, the decode
     library compiled with -DR2O_TIMELINE: every wave keeps real-time counter stamps in registers and
@@ -1119,6 +1197,10 @@ def main() -> int:
     ap.add_argument("--e2e-context", type=int, default=32768)
     ap.add_argument("--e2e-steps", type=int, default=128)
     ap.add_argument("--e2e-layers", type=int, default=28)
+    ap.add_argument("--fused-rotation", action="store_true",
+                    help="only time the layer call of --config with the decode step's rotation folded in "
+                         "(FusedRotary) against a separate rotation launch before the call, and print one "
+                         "JSON line")
     ap.add_argument("--timeline", action="store_true",
                     help="only print the phase breakdown of the layer call of --config (work-item start-up, "
                          "first tile, per-kind tile times, epilogue, combine phases) from libr2o_timeline.so, "
@@ -1179,6 +1261,9 @@ def main() -> int:
         return 0
     if args.timeline:
         print(json.dumps(timeline_bench(cfg, dev, n_layers=args.layers, warmup=args.warmup)), flush=True)
+        return 0
+    if args.fused_rotation:
+        print(json.dumps(rotation_bench(cfg, dev, n_layers=args.layers, steps=args.steps)), flush=True)
         return 0
     if args.sweep:
         factors = [float(f) for f in args.sweep.split(",")]
