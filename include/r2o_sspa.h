@@ -196,8 +196,9 @@ typedef struct r2o_decode_params {
      * applies x * cos + rotate_half(x) * sin in fp32 (dimension d taking axis 0, 1 or 2 of the tables
      * by d % 64 against the sections), then with rope_hadamard the orthonormal FWHT-128, rounding each
      * row once to its dtype, exactly as r2o_qkv_mrope does; append_v takes the FWHT alone with
-     * value_hadamard.  The rotated appended rows go to rotated_k / rotated_v, from which the combine's
-     * fused append writes the ring. */
+     * value_hadamard.  rope_mode 2: the Qwen3 norm + RoPE (below).  The rotated appended rows go to
+     * rotated_k / rotated_v, from which the combine's fused append writes the ring.  The tables' channel
+     * stride must be 1 and their axis and batch strides and base addresses whole 16-byte pieces. */
     int64_t rope_mode;
     const void* rope_cos;           /* [3, batch, tokens, 128] tables of the step (token 0 is used)  */
     const void* rope_sin;
@@ -210,6 +211,15 @@ typedef struct r2o_decode_params {
     int64_t value_hadamard;         /* 1: FWHT-128 of the appended value row                           */
     uint16_t* rotated_k;            /* device [batch, hkv, 128] (row_dtype), 16-byte aligned: written  */
     uint16_t* rotated_v;            /* by the partial pass when rope_mode and do_append are set        */
+    /* rope_mode 2 (the Qwen3 branch, qwen_sspa_attention.py:1228-1235): the query and appended key rows
+     * first take their per-head RMSNorm (transformers' Qwen3RMSNorm: mean of squares in fp32, x *
+     * rsqrt(mean + eps) rounded to the row dtype, times the weight, rounded), then apply_rotary_pos_emb
+     * with every product and the sum rounded to the row dtype, then with rope_hadamard the FWHT-128,
+     * exactly as r2o_qkv_norm_rope does.  The tables are passed as [1, batch, tokens, 128] views (axis
+     * stride 0, rope_section0 = 64, rope_section1 = 0) in the row dtype. */
+    const uint16_t* q_norm_weight;  /* [128], row dtype, 16-byte aligned (rope_mode 2)                */
+    const uint16_t* k_norm_weight;
+    float norm_eps;                 /* RMSNorm epsilon, >= 0 (one for both norms, as r2o_qkv_norm_rope) */
 } r2o_decode_params;
 
 /* Split-K partial pass.  Replaces _fourq_page_partial_kernel / _full_head_page_partial_kernel

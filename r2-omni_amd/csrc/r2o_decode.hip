@@ -137,7 +137,7 @@ struct WaveState {
 // takes the same operands in the same order as the separate launch).  The 4 waves of a work item
 // share the rows (4 per wave), which meet in LDS; after a barrier each lane reads the channels it holds
 // as an MFMA operand, as it would read rotated rows in memory.
-enum RopeMode { kRopeNone = 0, kRopeMrope = 1 };
+enum RopeMode { kRopeNone = 0, kRopeMrope = 1, kRopeQwen3 = 2 };
 
 // A work item's LDS rows of a folded rotation (row dtype): the KV group's query heads 0 .. 15, then the
 // appended key (row 16) and value (row 17); 272 bytes apart, so that 16 lanes' reads of one channel
@@ -212,10 +212,13 @@ __device__ __forceinline__ const uint16_t* rot_source(const r2o_decode_params& p
     return (r == gqa ? p.append_k : p.append_v) + b * p.append_batch_stride + kvh * 128;
 }
 
+// (RM: kRopeMrope reads the three axes' runs, kRopeQwen3 the one table's: 16-bit, one piece.)
+template <int RM>
 __device__ __forceinline__ void rot_prefetch(const r2o_decode_params& p, int64_t b, const uint16_t* row, int c8,
                                              RotPrefetch& f) {
-    const int pieces = p.rope_table_dtype == 2 ? 2 : 1;
-    const int64_t esize = p.rope_table_dtype == 2 ? 4 : 2;
+    constexpr int kAxes = RM == kRopeQwen3 ? 1 : 3;
+    const int pieces = RM == kRopeQwen3 ? 1 : (p.rope_table_dtype == 2 ? 2 : 1);
+    const int64_t esize = RM == kRopeQwen3 ? 2 : (p.rope_table_dtype == 2 ? 4 : 2);
     const char* tab[2] = {reinterpret_cast<const char*>(p.rope_cos) + b * p.rope_cos_strides[1] * esize,
                           reinterpret_cast<const char*>(p.rope_sin) + b * p.rope_sin_strides[1] * esize};
     const uint32_t axis_bytes[2] = {(uint32_t)(p.rope_cos_strides[0] * esize), (uint32_t)(p.rope_sin_strides[0] * esize)};
@@ -223,19 +226,34 @@ __device__ __forceinline__ void rot_prefetch(const r2o_decode_params& p, int64_t
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int a = 0; a < 3; ++a)
+        for (int a = 0; a < kAxes; ++a)
 #pragma unroll
             for (int q = 0; q < 2; ++q)
                 if (q < pieces) f.tab[t][a][q] = r2o_ldg(reinterpret_cast<const r2o_u4*>(tab[t] + (a * axis_bytes[t] + o + 16 * q)));
     rot_row_loads(row, c8, f.x, f.xp);
 }
 
+// Channel k of 8 packed 16-bit channels, as fp32.
+__device__ __forceinline__ float row_channel(const r2o_u4& w, int k, int dt) {
+    const uint32_t h = (k & 1) ? w[k >> 1] >> 16 : w[k >> 1] & 0xffffu;
+    return dt == 0 ? r2o_bf16_to_f32(h) : r2o_f16_to_f32(h);
+}
+
 // cos / sin of the lane's 8 channels as fp32: channel k takes axis 1 from bit k of m1 and axis 2 from
 // bit k of m2 (bit masks of the lane's channels against the sections, d = c % 64), selected by bit
 // operations (per-channel condition masks would hold a pair of scalar registers each).
+template <int RM>
 __device__ __forceinline__ void rot_tables(const r2o_decode_params& p, int c8, const RotPrefetch& f, float (&cs)[8],
                                            float (&sn)[8]) {
     const int code = (int)p.rope_table_dtype;
+    if constexpr (RM == kRopeQwen3) {  // one table in the row dtype
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            cs[k] = row_channel(f.tab[0][0][0], k, code);
+            sn[k] = row_channel(f.tab[1][0][0], k, code);
+        }
+        return;
+    }
     const int d0 = (8 * c8) & 63, t0 = (int)p.rope_section0 - d0, t1 = t0 + (int)p.rope_section1;
     const uint32_t m1 = t0 <= 0 ? 0xffu : (t0 >= 8 ? 0u : (0xffu << t0) & 0xffu);
     const uint32_t m2 = t1 <= 0 ? 0xffu : (t1 >= 8 ? 0u : (0xffu << t1) & 0xffu);
@@ -262,24 +280,62 @@ __device__ __forceinline__ void rot_tables(const r2o_decode_params& p, int c8, c
     }
 }
 
-// Channel k of 8 packed 16-bit channels, as fp32.
-__device__ __forceinline__ float row_channel(const r2o_u4& w, int k, int dt) {
-    const uint32_t h = (k & 1) ? w[k >> 1] >> 16 : w[k >> 1] & 0xffffu;
-    return dt == 0 ? r2o_bf16_to_f32(h) : r2o_f16_to_f32(h);
-}
-
 // One row of a folded rotation in a 16-lane group (lane c8: channels 8 c8 .. 8 c8 + 7): mRoPE then, with
 // `had`, the FWHT (rope = false: the FWHT alone, for the appended value), one rounding to the row dtype,
 // as the packed 16-bit channels.
+// With rope_mode 2 (`qwen3`, the Qwen3 branch) the rotation is that of qk_norm_rope_kernel
+// (r2o_rope.hip): the RMSNorm with `weight` (the row's q_norm or k_norm weights), then
+// apply_rotary_pos_emb with every product and the sum rounded to the row dtype.  The sum of squares
+// follows that kernel's butterfly: pair sums x[t]^2 + x[t + 64]^2 for t = 8 (c8 % 8) + k, combined over
+// t's bits 5, 4, 3 across lanes c8 ^ 4, ^ 2, ^ 1 and bits 2, 1, 0 inside the lane, so the mean and the
+// rounding of every product are those of the separate launch.
+template <int RM>
 __device__ __forceinline__ r2o_u4 rot_row(const r2o_decode_params& p, const r2o_u4& x, const r2o_u4& xp,
-                                          const float (&cs)[8], const float (&sn)[8], int c8, bool rope, bool had) {
+                                          const float (&cs)[8], const float (&sn)[8], int c8, bool rope, bool had,
+                                          const uint16_t* weight) {
     const int dt = (int)p.row_dtype;
     float y[8];
+    if (RM == kRopeQwen3 && rope) {  // whole 16-lane groups take the same branch
+        float xv[8], xpv[8], s[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float xv = row_channel(x, k, dt), xpv = row_channel(xp, k, dt);
-        const float rk = xv * cs[k] + (c8 < 8 ? -xpv : xpv) * sn[k];  // rotate_half: (-x[c + 64], x[c - 64])
-        y[k] = rope ? rk : xv;
+        for (int k = 0; k < 8; ++k) {
+            xv[k] = row_channel(x, k, dt);
+            xpv[k] = row_channel(xp, k, dt);
+            const float lo = c8 < 8 ? xv[k] : xpv[k], hi = c8 < 8 ? xpv[k] : xv[k];  // x[t], x[t + 64]
+            s[k] = __fadd_rn(__fmul_rn(lo, lo), __fmul_rn(hi, hi));
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            s[k] = __fadd_rn(s[k], r2o_lane_xor<4>(s[k]));
+            s[k] = __fadd_rn(s[k], r2o_lane_xor<2>(s[k]));
+            s[k] = __fadd_rn(s[k], r2o_lane_xor<1>(s[k]));
+        }
+#pragma unroll
+        for (int m = 4; m >= 1; m >>= 1)
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if ((k & m) == 0) {
+                    const float a = __fadd_rn(s[k], s[k + m]);
+                    s[k] = a;
+                    s[k + m] = a;
+                }
+        const float inv = __fdiv_rn(1.f, __fsqrt_rn(__fadd_rn(__fdiv_rn(s[0], 128.f), p.norm_eps)));
+        const r2o_u4 wo = r2o_ldg(reinterpret_cast<const r2o_u4*>(weight + 8 * c8));
+        const r2o_u4 wp = r2o_ldg(reinterpret_cast<const r2o_u4*>(weight + 8 * (c8 ^ 8)));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float w = r2o_round_dtype(__fmul_rn(row_channel(wo, k, dt), r2o_round_dtype(__fmul_rn(xv[k], inv), dt)), dt);
+            const float wq = r2o_round_dtype(__fmul_rn(row_channel(wp, k, dt), r2o_round_dtype(__fmul_rn(xpv[k], inv), dt)), dt);
+            y[k] = r2o_round_dtype(__fadd_rn(r2o_round_dtype(__fmul_rn(w, cs[k]), dt),
+                                             r2o_round_dtype(__fmul_rn(c8 < 8 ? -wq : wq, sn[k]), dt)), dt);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float xv = row_channel(x, k, dt), xpv = row_channel(xp, k, dt);
+            const float rk = xv * cs[k] + (c8 < 8 ? -xpv : xpv) * sn[k];  // rotate_half: (-x[c + 64], x[c - 64])
+            y[k] = rope ? rk : xv;
+        }
     }
     if (had) fwht_row8(y, c8);  // whole 16-lane groups take the same branch
     r2o_u4 out;
@@ -297,12 +353,14 @@ __device__ __forceinline__ r2o_u4 rot_row(const r2o_decode_params& p, const r2o_
 // call with an append) the appended key and value into rows 16, 17 and to rotated_k / rotated_v for
 // the combine's append (that item is their only reader).  The waves meet at a barrier after this;
 // each then reads the rows it needs.
+template <int RM>
 __device__ __forceinline__ void rot_block_row(const r2o_decode_params& p, int64_t b, int64_t kvh, int gqa, int r,
                                               int c8, const RotPrefetch& f, uint16_t* rot) {
     float cs[8], sn[8];
-    rot_tables(p, c8, f, cs, sn);
+    rot_tables<RM>(p, c8, f, cs, sn);
     const bool is_q = r < gqa, is_v = r == gqa + 1;
-    const r2o_u4 out = rot_row(p, f.x, f.xp, cs, sn, c8, !is_v, is_v ? p.value_hadamard != 0 : p.rope_hadamard != 0);
+    const r2o_u4 out = rot_row<RM>(p, f.x, f.xp, cs, sn, c8, !is_v, is_v ? p.value_hadamard != 0 : p.rope_hadamard != 0,
+                                   is_q ? p.q_norm_weight : p.k_norm_weight);
     *reinterpret_cast<r2o_u4*>(rot + (is_q ? r : kRotKeyRow + (r - gqa)) * kRotStride + 8 * c8) = out;
     if (!is_q) *reinterpret_cast<r2o_u4*>((is_v ? p.rotated_v : p.rotated_k) + (b * p.hkv + kvh) * 128 + 8 * c8) = out;
 }
@@ -327,7 +385,7 @@ __device__ __forceinline__ void load_query(const r2o_decode_params& p, int64_t b
     float qf[32];
     {
         r2o_u4 raw[4];
-        if constexpr (RO == kRopeMrope) {
+        if constexpr (RO != kRopeNone) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) raw[j] = qrot[j];
         } else {
@@ -975,8 +1033,8 @@ __device__ __forceinline__ void run_segment(const r2o_decode_params& p, const r2
         const int r = 4 * wave + (lane >> 4);
         if (r < gqa) {  // whole 16-lane groups
             RotPrefetch f;
-            rot_prefetch(p, b, query_row<kRopeMrope>(p, b, kvh, gqa, r), l16, f);
-            rot_block_row(p, b, kvh, gqa, r, l16, f, rot);
+            rot_prefetch<RO>(p, b, query_row<RO>(p, b, kvh, gqa, r), l16, f);
+            rot_block_row<RO>(p, b, kvh, gqa, r, l16, f, rot);
         }
         __syncthreads();
         if (n <= 0) return;
@@ -1066,8 +1124,8 @@ __device__ __forceinline__ void run_recent(const r2o_decode_params& p, const r2o
             const int r = r0 + (lane >> 4);
             if (r < nrows) {  // whole 16-lane groups
                 RotPrefetch f;
-                rot_prefetch(p, b, rot_source(p, b, kvh, gqa, r), l16, f);
-                rot_block_row(p, b, kvh, gqa, r, l16, f, rot);
+                rot_prefetch<RO>(p, b, rot_source(p, b, kvh, gqa, r), l16, f);
+                rot_block_row<RO>(p, b, kvh, gqa, r, l16, f, rot);
             }
         }
         __syncthreads();
@@ -1473,7 +1531,14 @@ int validate(const r2o_decode_params* p) {
     if (p->rope_mode != kRopeNone) return R2O_EINVAL;
 #endif
     if (p->rope_mode != kRopeNone) {  // folded rotation: the tables, sections and rotated-row outputs
-        if (p->rope_mode != kRopeMrope || !p->rope_cos || !p->rope_sin) return R2O_EINVAL;
+        if ((p->rope_mode != kRopeMrope && p->rope_mode != kRopeQwen3) || !p->rope_cos || !p->rope_sin)
+            return R2O_EINVAL;
+        if (p->rope_mode == kRopeQwen3) {  // norm weights, epsilon, tables in the row dtype, one axis
+            if (!p->q_norm_weight || !p->k_norm_weight || reinterpret_cast<uintptr_t>(p->q_norm_weight) % 16 ||
+                reinterpret_cast<uintptr_t>(p->k_norm_weight) % 16 || !(p->norm_eps >= 0.f) ||
+                p->rope_table_dtype != p->row_dtype || p->rope_section0 != 64 || p->rope_section1 != 0)
+                return R2O_EINVAL;
+        }
         if (p->rope_table_dtype < 0 || p->rope_table_dtype > 2) return R2O_EINVAL;
         const int64_t esize = p->rope_table_dtype == 2 ? 4 : 2, piece = 16 / esize;
         for (const int64_t* st : {p->rope_cos_strides, p->rope_sin_strides}) {
@@ -1564,6 +1629,7 @@ int launch_decode(const r2o_decode_params& params, hipStream_t stream) {
     const r2o_decode_params p = kernel_params(params);
 #ifndef R2O_TIMELINE  // the phase-stamp build (bench.py --timeline) has no rotating instances
     if (p.rope_mode == kRopeMrope) launch_partial<kRopeMrope>(p, stream);
+    else if (p.rope_mode == kRopeQwen3) launch_partial<kRopeQwen3>(p, stream);
     else
 #endif
         launch_partial<kRopeNone>(p, stream);

@@ -40,7 +40,7 @@ from .policy import (
     project_token_bits_to_pages,
 )
 from .reference import normalized_fwht, triton_mixed_reference
-from .rope import FusedRotary, qwen3_qk_norm_rope, qwen_qk_mrope
+from .rope import FusedQwen3Rotary, FusedRotary, qwen3_qk_norm_rope, qwen_qk_mrope
 from .splitk import (
     SplitKExecutor,
     SplitKWorkspace,

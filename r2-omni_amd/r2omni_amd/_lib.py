@@ -69,6 +69,9 @@ class DecodeParams(ctypes.Structure):
         ("value_hadamard", c_i64),
         ("rotated_k", c_vp),
         ("rotated_v", c_vp),
+        ("q_norm_weight", c_vp),
+        ("k_norm_weight", c_vp),
+        ("norm_eps", ctypes.c_float),
     ]
 
 

@@ -7,6 +7,8 @@
   (qwen_sspa_attention.py:1228-1235: ``q_norm`` / ``k_norm``, ``apply_rotary_pos_emb``, then
   ``triton_fwht_128`` of Q and K when keys are Hadamard-rotated) in one launch, with the rounding of
   every torch op of that sequence.
+* ``FusedRotary`` / ``FusedQwen3Rotary``: either transform folded into the split-K call itself
+  (``executor(q, append=..., rotary=...)``), so that the step's attention is two launches.
 """
 from __future__ import annotations
 
@@ -74,6 +76,61 @@ class FusedRotary:
         p.rope_section0, p.rope_section1 = sections[0], sections[1]
         p.rope_hadamard = int(bool(self.apply_hadamard))
         p.value_hadamard = int(bool(self.value_hadamard))
+
+
+@dataclass(frozen=True)
+class FusedQwen3Rotary:
+    """The Qwen3 branch of the decode step, folded into the split-K call.
+
+    Given as ``rotary=`` like ``FusedRotary``: the query and the appended key are the raw projections,
+    and the partial kernel applies what ``qwen3_qk_norm_rope(q, k, q_norm_weight, k_norm_weight, cos, sin,
+    eps=eps, apply_hadamard=...)`` and the value Hadamard (``value_hadamard``) would
+    (qwen_sspa_attention.py:1228-1235, 230-235), bit-identically, without their launch.  ``cos`` /
+    ``sin``: [B or 1, T, 128] tables of the step in the rows' dtype (token 0 is used), unit channel
+    stride and 16-byte aligned rows; the norm weights [128] in the rows' dtype."""
+    cos: torch.Tensor
+    sin: torch.Tensor
+    q_norm_weight: torch.Tensor
+    k_norm_weight: torch.Tensor
+    eps: float = 1e-6
+    apply_hadamard: bool = False
+    value_hadamard: bool = False
+
+    def fill(self, p: _lib.DecodeParams, batch: int, device: torch.device) -> None:
+        """Write the rotation into the launch arguments (checks as ``qwen3_qk_norm_rope``'s)."""
+        cos, sin = self.cos, self.sin
+        if cos.shape != sin.shape or cos.ndim != 3 or int(cos.shape[-1]) != 128 or int(cos.shape[1]) < 1 \
+                or int(cos.shape[0]) not in (1, batch):
+            raise ValueError("Qwen3 fused norm+RoPE requires cos/sin [B,S,D] matching Q/K tokens")
+        if cos.device != device or sin.device != device:
+            raise ValueError("Q/K and rotary tensors must share a device")
+        code = _lib.dtype_code(cos.dtype) if cos.dtype in (torch.bfloat16, torch.float16) else -1
+        if cos.dtype != sin.dtype or code != p.row_dtype:
+            raise ValueError("Qwen3 fused norm+RoPE cos/sin must share the Q/K dtype and device")
+        for name, w in (("q_norm_weight", self.q_norm_weight), ("k_norm_weight", self.k_norm_weight)):
+            if tuple(w.shape) != (128,) or w.dtype != cos.dtype or w.device != device:
+                raise ValueError(f"{name} must be a [128] tensor of the Q/K dtype on the Q/K device")
+            if not w.is_contiguous() or w.data_ptr() % 16:
+                raise ValueError(f"{name} must be contiguous and 16-byte aligned")
+        if not self.eps >= 0.0:
+            raise ValueError("RMSNorm epsilon must be non-negative")
+        for t in (cos, sin):  # the kernel reads 16-byte pieces at 32-bit byte offsets from a request's base
+            st = t.stride()
+            if st[2] != 1 or min(st) < 0 or st[1] % 8 or (int(t.shape[0]) > 1 and st[0] % 8) or t.data_ptr() % 16:
+                raise ValueError("Qwen3 fused norm+RoPE tables need unit channel stride and 16-byte aligned "
+                                 "rows (e.g. contiguous [B, T, 128] tables)")
+        p.rope_mode = 2
+        p.rope_cos, p.rope_sin = cos.data_ptr(), sin.data_ptr()
+        for t, dst in ((cos, p.rope_cos_strides), (sin, p.rope_sin_strides)):
+            # as a [1, B, T, 128] view: one axis; a table shared by the batch has batch stride 0
+            st = t.stride()
+            dst[0], dst[1], dst[2], dst[3] = 0, (int(st[0]) if int(t.shape[0]) > 1 else 0), int(st[1]), 1
+        p.rope_table_dtype = code
+        p.rope_section0, p.rope_section1 = 64, 0
+        p.rope_hadamard = int(bool(self.apply_hadamard))
+        p.value_hadamard = int(bool(self.value_hadamard))
+        p.q_norm_weight, p.k_norm_weight = self.q_norm_weight.data_ptr(), self.k_norm_weight.data_ptr()
+        p.norm_eps = float(self.eps)
 
 
 def _value_operands(value, output, apply_hadamard, what):

@@ -126,6 +126,14 @@ def test_folded_rotation_and_row_strides_are_checked_without_a_gpu():
         "table channels not unit-strided": dict(rope_cos_strides=(ctypes.c_int64 * 4)(512, 256, 128, 2)),
         "table rows off 16 bytes": dict(rope_sin_strides=(ctypes.c_int64 * 4)(256, 132, 128, 1)),
         "misaligned table": dict(rope_cos=0xB008),
+        "Qwen3 rotation without norm weights": dict(rope_mode=2, rope_section0=64, rope_section1=0),
+        "Qwen3 rotation with misaligned weights": dict(rope_mode=2, rope_section0=64, rope_section1=0,
+                                                       q_norm_weight=0xF008, k_norm_weight=0xF100),
+        "Qwen3 rotation with a negative epsilon": dict(rope_mode=2, rope_section0=64, rope_section1=0,
+                                                       q_norm_weight=0xF000, k_norm_weight=0xF100, norm_eps=-1.0),
+        "Qwen3 rotation with mRoPE sections": dict(rope_mode=2, q_norm_weight=0xF000, k_norm_weight=0xF100),
+        "Qwen3 rotation with fp32 tables": dict(rope_mode=2, rope_section0=64, rope_section1=0, rope_table_dtype=2,
+                                                q_norm_weight=0xF000, k_norm_weight=0xF100),
         "strided query without the rotation": dict(rope_mode=0, query_batch_stride=36 * 128),
         "strided append rows without the rotation": dict(rope_mode=0, append_batch_stride=36 * 128),
     }
@@ -203,8 +211,9 @@ def test_phase_stamps_live_only_in_the_measurement_library():
 
 def test_built_kernels_keep_their_state_in_registers_and_lds():
     """The build records the compiler's resource figures of every kernel beside its object and fails
-    on scratch use; here every decode partial instance (3 key formats x 2 row dtypes x rotation folded
-    or not) and the combine are listed, with no scratch, no spills and two workgroups per CU."""
+    on scratch use; here every decode partial instance (3 key formats x 2 row dtypes x no rotation, the
+    folded mRoPE or the folded Qwen3 norm+RoPE) and the combine are listed, with no scratch, no spills
+    and two workgroups per CU."""
     from r2omni_amd.build import ROOT_DIR
 
     path = os.path.join(ROOT_DIR, "_build", "r2o_decode.resources.txt")
@@ -213,7 +222,7 @@ def test_built_kernels_keep_their_state_in_registers_and_lds():
     rows = [ln.split(" ", 1) for ln in open(path).read().splitlines()[1:]]
     table = {name: [int(x) for x in vals.split(" | ")] for name, vals in rows}
     partial = [n for n in table if "decode_partial_kernel" in n]
-    assert len(partial) == 12 and any("decode_combine_kernel" in n for n in table)
+    assert len(partial) == 18 and any("decode_combine_kernel" in n for n in table)
     for name, (vgpr, agpr, sgpr, scratch, vspill, sspill, occupancy, lds) in table.items():
         assert scratch == 0 and vspill == 0 and sspill == 0, name
         if name in partial:

@@ -183,3 +183,63 @@ def test_batched_decoder_with_fused_rotary_through_a_flush(use_graph):
         assert ra.active_length == rb.active_length
         assert torch.equal(_bits(rb.fp_k), _bits(ra.fp_k)) and torch.equal(_bits(rb.fp_v), _bits(ra.fp_v))
         assert torch.equal(y.compact_key.packed, x.compact_key.packed)
+
+
+QWEN3_CASES = [
+    # totals, rows dtype, hadamard (Q/K), value hadamard, tables per request (else one shared row),
+    # inputs as views of one padded projection row
+    ((2048 + 100,), torch.bfloat16, True, True, False, False),
+    ((1536 + 100, 1024 + 100), torch.bfloat16, True, False, True, True),
+    ((1024 + 100, 2048 + 100), torch.float16, False, True, True, False),
+    ((1024 + 100, 1536 + 100), torch.float16, True, True, False, True),
+]
+
+
+@pytest.mark.parametrize("case", range(len(QWEN3_CASES)))
+def test_fused_qwen3_call_equals_separate_norm_rope(case):
+    """The Qwen3 branch folded into the call (FusedQwen3Rotary) against qwen3_qk_norm_rope and the V
+    FWHT as separate launches before the call (qwen_sspa_attention.py:1228-1235, 230-235): outputs
+    and ring rows bit-identical over 3 steps."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig
+
+    dev = _cuda()
+    totals, rows, had, vhad, per_request, strided = QWEN3_CASES[case]
+    cfg = DecodeConfig("q3", 28, 4, (0,), (0.15, 0.45, 0.4), recent=100,
+                       dtype="float16" if rows == torch.float16 else "bfloat16")
+    b = len(totals)
+    ca, _ = _caches(cfg, totals, 650 + case, dev)
+    cb, _ = _caches(cfg, totals, 650 + case, dev)
+    ex_a, ex_b = _executor(ca, 28, dev), _executor(cb, 28, dev)
+    gen = torch.Generator(device=dev).manual_seed(660 + case)
+    wq = (1.0 + 0.3 * torch.randn(128, generator=gen, device=dev)).to(rows)
+    wk = (1.0 + 0.3 * torch.randn(128, generator=gen, device=dev)).to(rows)
+    pos = [int(c.compact_key.active_length) + c.recent_fp_pool.active_length for c in ca]
+    print(f"[qwen3] case {case}: batch {b}, rows {rows}, hadamard {had}/{vhad}, per-request tables "
+          f"{per_request}, strided {strided}", flush=True)
+    for step in range(3):
+        qkv = torch.randn(b, 36 * 128 + (64 if strided else 0), generator=gen, device=dev).to(rows)
+        q = qkv[:, : 28 * 128].view(b, 28, 128)
+        k = qkv[:, 28 * 128 : 32 * 128].view(b, 4, 128)
+        v = qkv[:, 32 * 128 : 36 * 128].view(b, 4, 128)
+        if not strided:
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        ang = torch.rand(b if per_request else 1, 1, 64, generator=gen, device=dev) * 6.0
+        ang = torch.cat([ang, ang], dim=-1)
+        cos, sin = ang.cos().to(rows), ang.sin().to(rows)
+        qr, kr = ro.qwen3_qk_norm_rope(q[:, :, None], k[:, :, None], wq, wk, cos, sin, eps=1e-6,
+                                       apply_hadamard=had)
+        vr = ro.triton_fwht_128(v.contiguous()) if vhad else v.contiguous()
+        want = ex_a(qr[:, :, 0].contiguous(), append=(kr, vr[:, :, None], pos, pos)).clone()
+        got = ex_b(q, append=(k, v, pos, pos),
+                   rotary=ro.FusedQwen3Rotary(cos, sin, wq, wk, 1e-6, had, vhad)).clone()
+        if b == 1:
+            ca[0].recent_fp_pool.active_length += 1
+            cb[0].recent_fp_pool.active_length += 1
+        pos = [p + 1 for p in pos]
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(got), _bits(want)), f"case {case} step {step}: output"
+    rings_a = ex_a.batched_recent or [c.recent_fp_pool for c in ca]
+    rings_b = ex_b.batched_recent or [c.recent_fp_pool for c in cb]
+    for ra, rb in zip(rings_a, rings_b):
+        assert torch.equal(_bits(rb.fp_k), _bits(ra.fp_k)) and torch.equal(_bits(rb.fp_v), _bits(ra.fp_v))
