@@ -343,8 +343,9 @@ class SplitKExecutor:
         if step_positions is not None:
             p.step_positions = step_positions.data_ptr()
         p.query, p.out = query.data_ptr(), out.data_ptr()
-        p.query_batch_stride = _row_stride(query, self.num_query_heads, "query")
-        if p.query_batch_stride and rotary is None:
+        if rotary is not None:
+            p.query_batch_stride = _row_stride(query, self.num_query_heads, "query")
+        elif not query.is_contiguous():
             raise ValueError("strided query rows need a folded rotation (FusedRotary); pass a contiguous query")
         p.q_dtype = _lib.dtype_code(query.dtype)
         for r, n in enumerate(self._ring_lengths()):
@@ -352,12 +353,13 @@ class SplitKExecutor:
         if append is not None:
             ak, av, gidx, lpos = append
             p.append_k, p.append_v, p.do_append = ak.data_ptr(), av.data_ptr(), 1
-            sk = _row_stride(ak, self.num_key_value_heads, "append K")
-            if _row_stride(av, self.num_key_value_heads, "append V") != sk:
-                raise ValueError("append K/V must share one layout")
-            if sk and rotary is None:
+            if rotary is not None:
+                sk = _row_stride(ak, self.num_key_value_heads, "append K")
+                if _row_stride(av, self.num_key_value_heads, "append V") != sk:
+                    raise ValueError("append K/V must share one layout")
+                p.append_batch_stride = sk
+            elif not (ak.is_contiguous() and av.is_contiguous()):
                 raise ValueError("strided append K/V rows need a folded rotation (FusedRotary)")
-            p.append_batch_stride = sk
             for r in range(len(self.caches)):
                 p.append_global[r] = int(gidx[r])
                 p.append_logical[r] = int(lpos[r])
@@ -410,10 +412,10 @@ class SplitKExecutor:
         b = len(self.caches)
         # contiguous, as the reference requires; with a folded rotation also rows readable in place (a
         # view into a fused QKV projection: unit strides inside a request, requests a multiple of 8
-        # elements apart)
+        # elements apart).  The contiguous case is checked first: it is every call of the manager.
         strided = rotary is not None
         if tuple(query.shape) != (b, self.num_query_heads, self.head_dim) or query.device != out.device \
-                or not _row_layout_ok(query, self.num_query_heads) or not (strided or query.is_contiguous()):
+                or not (query.is_contiguous() or (strided and _row_layout_ok(query, self.num_query_heads))):
             raise ValueError("query does not match prepared split-K executor")
         if tuple(out.shape) != (b, self.num_query_heads, self.head_dim):
             raise ValueError("split-K workspace geometry is inconsistent")
@@ -422,19 +424,24 @@ class SplitKExecutor:
             ak, av, gidx, lpos = append
             if ak.ndim == 4:
                 ak, av = ak[:, :, 0], av[:, :, 0]
-            shape = (b, self.num_key_value_heads, self.head_dim)
             n = b * self.num_key_value_heads * self.head_dim
-            if ak.numel() == n and av.numel() == n and ak.is_contiguous() and av.is_contiguous():
-                ak, av = ak.view(shape), av.view(shape)  # contiguous rows of the right size, any shape
-            if tuple(ak.shape) != shape or tuple(av.shape) != shape or ak.device != query.device \
-                    or av.device != query.device or not (strided or (ak.is_contiguous() and av.is_contiguous())):
+            if ak.device != query.device or av.device != query.device:
                 raise ValueError("append K/V must be contiguous [B,Hkv,1,D] or [B,Hkv,D]")
+            if ak.is_contiguous() and av.is_contiguous():
+                if ak.numel() != n or av.numel() != n:
+                    raise ValueError("append K/V must be contiguous [B,Hkv,1,D] or [B,Hkv,D]")
+                if ak.data_ptr() % 16 or av.data_ptr() % 16:  # the kernels move the rows in 16-byte pieces
+                    ak, av = ak.clone(), av.clone()
+            else:  # views of a projection row: with a folded rotation only
+                shape = (b, self.num_key_value_heads, self.head_dim)
+                if not strided or tuple(ak.shape) != shape or tuple(av.shape) != shape:
+                    raise ValueError("append K/V must be contiguous [B,Hkv,1,D] or [B,Hkv,D]")
+                if not _row_layout_ok(ak, self.num_key_value_heads) or not _row_layout_ok(av, self.num_key_value_heads) \
+                        or ak.stride() != av.stride():
+                    ak, av = ak.contiguous().clone(), av.contiguous().clone()
             ring_dtype = self.caches[0].recent_fp_pool.fp_k.dtype
             if ak.dtype != ring_dtype or av.dtype != ring_dtype:
                 raise ValueError(f"append K/V must be {ring_dtype} like the Recent-FP ring")
-            if not _row_layout_ok(ak, self.num_key_value_heads) or not _row_layout_ok(av, self.num_key_value_heads) \
-                    or ak.stride() != av.stride():  # the kernels move the rows in 16-byte pieces
-                ak, av = ak.contiguous().clone(), av.contiguous().clone()
             capacity = self.caches[0].recent_fp_pool.capacity
             if self.batched_recent_lengths is not None:
                 if any(n >= capacity for n in self.batched_recent_lengths):
