@@ -184,7 +184,10 @@ def test_config4_e2e_decode_properties():
     8 x 32768 tokens, then greedy steps on this path (bench.py's E2EQwenDecoder).  The first step
     flushes every ring inside the batch; after it, the last layer's attention output of every request
     is checked against the oracle (cache rebuilt on the CPU from the same K/V, the step's token
-    appended with its flush) and the arenas against the oracle's bit for bit.  Logits stay finite,
+    appended with its flush) and the arenas against the oracle's bit for bit.  After the last step the
+    same checks run again on that layer, its oracle cache taking every step's appended token (the first
+    one's flush, then the ring appends), so the fused appends of later steps are pinned too (the last
+    layer's raw projections are the ones left in the shared projection buffer).  Logits stay finite,
     and the tokens of the HIP-graph run equal those of the eager run and of a run with a separate
     rotation launch (the decoder folds the mRoPE / FWHT into the attention call)."""
     import bench
@@ -199,29 +202,39 @@ def test_config4_e2e_decode_properties():
     model.prefill()
     layer = model.n_layers - 1
     cfg = model.cache_config()
-    checked = []
+    checked = {}
+    rows = {}  # (layer, step) -> the step's rotated q, k, v rows (float32)
 
-    def inspect(step, decs):
-        if step != 0:
-            return
-        d = decs[layer]
+    def step_rows(d):
         if d.rotary is not None:  # raw projections in the bound inputs: the rows the call rotated
             rot = d.rotary
             qr, _ = ro.qwen_qk_mrope(d.query_buffer[:, :, None], d.key_buffer[:, :, None], rot.cos, rot.sin,
                                      rot.mrope_section, apply_hadamard=rot.apply_hadamard)
-            q, k, v = _f32(qr[:, :, 0]), _f32(d.executor.rotated_k), _f32(d.executor.rotated_v)
-        else:
-            q, k, v = _f32(d.query_buffer), _f32(d.key_buffer), _f32(d.value_buffer)
+            return _f32(qr[:, :, 0]), _f32(d.executor.rotated_k), _f32(d.executor.rotated_v)
+        return _f32(d.query_buffer), _f32(d.key_buffer), _f32(d.value_buffer)
+
+    def check_layer(step, d, lay):
         out = d.workspace.output.clone()
+        q = rows[(lay, step)][0]
+        worst = []
         for s_i in range(model.batch):
-            oc = _oracle(model.request_data(layer, s_i), cfg)
-            assert append_token(oc, k[s_i], v[s_i], global_index=model.context, logical_position=model.context)
-            _check_arenas(d.caches[s_i], oc, f"cfg4 layer {layer} request {s_i}")
-            mx, mn = _errors(out[s_i : s_i + 1], output_transform(mixed_reference(q[s_i : s_i + 1], oc), True),
-                             f"cfg4 layer {layer} request {s_i}")
-            checked.append((mx, mn))
-        print(f"[cfg4] layer {layer} step 0, 8 requests: worst max-abs {max(c[0] for c in checked):.2e}, "
-              f"worst mean-abs {max(c[1] for c in checked):.2e}", flush=True)
+            oc = _oracle(model.request_data(lay, s_i), cfg)
+            for i in range(step + 1):  # the tokens of steps 0 .. step (the first flushes the full ring)
+                _, k, v = rows[(lay, i)]
+                flushed = append_token(oc, k[s_i], v[s_i], global_index=model.context + i,
+                                       logical_position=model.context + i)
+                assert flushed == (i == 0), f"cfg4 layer {lay} step {i}: flush expected only at the first step"
+            _check_arenas(d.caches[s_i], oc, f"cfg4 layer {lay} step {step} request {s_i}")
+            worst.append(_errors(out[s_i : s_i + 1], output_transform(mixed_reference(q[s_i : s_i + 1], oc), True),
+                                 f"cfg4 layer {lay} step {step} request {s_i}"))
+        checked[(lay, step)] = worst
+        print(f"[cfg4] layer {lay} step {step}, 8 requests: worst max-abs {max(c[0] for c in worst):.2e}, "
+              f"worst mean-abs {max(c[1] for c in worst):.2e}", flush=True)
+
+    def inspect(step, decs):
+        rows[(layer, step)] = step_rows(decs[layer])
+        if step in (0, steps - 1):
+            check_layer(step, decs[layer], layer)
 
     print("[cfg4] eager decode", flush=True)
     _, eager_tokens, eager_finite = model.decode(steps, False, inspect)
@@ -229,7 +242,7 @@ def test_config4_e2e_decode_properties():
     _, graph_tokens, graph_finite = model.decode(steps, True)
     print("[cfg4] HIP-graph decode with a separate rotation launch", flush=True)
     _, sep_tokens, sep_finite = model.decode(steps, True, fused_rotation=False)
-    assert len(checked) == model.batch
+    assert sorted(checked) == [(layer, 0), (layer, steps - 1)] and all(len(w) == model.batch for w in checked.values())
     assert eager_finite and graph_finite and sep_finite
     assert torch.equal(eager_tokens, graph_tokens) and torch.equal(sep_tokens, graph_tokens)
     print(f"[cfg4] tokens of {steps} greedy steps equal in both modes", flush=True)
