@@ -1237,8 +1237,11 @@ __global__ __launch_bounds__(KernelCfg<KF>::kThreads, KernelCfg<KF>::kWavesPerSi
     l_h = r2o_sum_lane_pair<16>(l_h);
     l_h = r2o_sum_lane_pair<32>(l_h);
     stamp(ts, 5);
-    __syncthreads();  // every wave is done with its staging area
-    float* mrg = reinterpret_cast<float*>(smem) + wave * kMergeFloats;
+    // each wave's state goes to the start of its own DMA ring, whose tiles it has all read: no wave
+    // waits for the others before writing (one barrier less than a shared merge area)
+    constexpr int kWaveFloats = KernelCfg<KF>::kWaveLds / 4;
+    static_assert(KernelCfg<KF>::kWaveLds >= kMergeFloats * 4, "a wave's state fits its own ring");
+    float* mrg = reinterpret_cast<float*>(smem) + wave * kWaveFloats;
     if (g == 0) {
         mrg[l16] = st.m;
         mrg[16 + l16] = l_h;
@@ -1263,16 +1266,16 @@ __global__ __launch_bounds__(KernelCfg<KF>::kThreads, KernelCfg<KF>::kWavesPerSi
         const int h = e >> 5, d4 = (e & 31) * 4;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, base[w * kMergeFloats + h]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, base[w * kWaveFloats + h]);
         float L = 0.f;
         r2o_f4 A = {0.f, 0.f, 0.f, 0.f};
         if (M != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
-                const float mw = base[w * kMergeFloats + h];
+                const float mw = base[w * kWaveFloats + h];
                 const float sc = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-                L += base[w * kMergeFloats + 16 + h] * sc;
-                A += *reinterpret_cast<const r2o_f4*>(base + w * kMergeFloats + 32 + h * 128 + d4) * sc;
+                L += base[w * kWaveFloats + 16 + h] * sc;
+                A += *reinterpret_cast<const r2o_f4*>(base + w * kWaveFloats + 32 + h * 128 + d4) * sc;
             }
         }
         // plain (write-back) stores: the end-of-kernel writeback leaves the partials in the Infinity
