@@ -361,8 +361,8 @@ class SplitKExecutor:
             elif not (ak.is_contiguous() and av.is_contiguous()):
                 raise ValueError("strided append K/V rows need a folded rotation (FusedRotary)")
             b = len(self.caches)
-            p.append_global[:b] = [int(g) for g in gidx[:b]]
-            p.append_logical[:b] = [int(x) for x in lpos[:b]]
+            p.append_global[:b] = gidx  # lists of b ints (_per_request)
+            p.append_logical[:b] = lpos
         if rotary is not None:
             rotary.fill(p, len(self.caches), query.device)
             p.rotated_k, p.rotated_v = self.rotated_k.data_ptr(), self.rotated_v.data_ptr()
@@ -449,7 +449,7 @@ class SplitKExecutor:
                 raise ValueError(f"append K/V must be {ring_dtype} like the Recent-FP ring")
             capacity = self.caches[0].recent_fp_pool.capacity
             if self.batched_recent_lengths is not None:
-                if any(n >= capacity for n in self.batched_recent_lengths):
+                if max(self.batched_recent_lengths) >= capacity:
                     raise RuntimeError("prepared batched executor cannot fuse an append into a full Recent-FP pool")
             else:
                 for c in self.caches:
@@ -510,6 +510,15 @@ def _row_stride(t: torch.Tensor, heads: int, what: str) -> int:
 
 
 def _per_request(value, b: int) -> list[int]:
+    t = type(value)  # the manager's plain ints and lists of ints first (host time on every call)
+    if t is int:
+        return [value] * b
+    if (t is list or t is tuple) and len(value) == b:
+        for v in value:
+            if type(v) is not int:
+                break
+        else:
+            return list(value)
     if isinstance(value, int):
         return [int(value)] * b
     if isinstance(value, (list, tuple)) and all(isinstance(v, int) for v in value):
