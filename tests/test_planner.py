@@ -252,3 +252,34 @@ def test_planner_rejects_runs_outside_their_arena():
         if what in ("kvh past the request's heads", "negative kvh", "request past the batch", "lo > hi",
                     "empty range", "tile0 > lo", "unaligned tile0", "hi past the tiles"):
             assert _plan_raw([good[0], run], None, n_groups=2)[0] == 1, what  # checked without descriptors too
+
+
+@pytest.mark.parametrize("value,b,want", [
+    (7, 3, [7, 7, 7]), (True, 2, [1, 1]), ([5], 3, [5, 5, 5]), ((4, 5), 2, [4, 5]), ([4, 5, 6], 3, [4, 5, 6]),
+    ([True, 2], 2, [1, 2]), ("tensor", 2, [8, 9]), ("tensor1", 3, [8, 8, 8]),
+])
+def test_per_request_positions_take_every_form_of_the_reference(value, b, want):
+    """The append's (global, logical) positions: an int, one value per request, or a single value
+    broadcast, as ints, lists, tuples or tensors (triton_fourq_splitk.py:1336-1354); the fast path for
+    plain ints and lists of ints gives what the general path gives."""
+    import torch
+
+    from r2omni_amd.splitk import _per_request
+
+    if value == "tensor":
+        value = torch.tensor([8, 9])
+    elif value == "tensor1":
+        value = torch.tensor([8])
+    got = _per_request(value, b)
+    assert got == want and all(type(v) is int for v in got)
+    if isinstance(value, list):  # a fresh list: the caller's is never handed on
+        assert got is not value
+
+
+def test_per_request_positions_reject_a_wrong_count():
+    from r2omni_amd.splitk import _per_request
+
+    with pytest.raises(ValueError, match="one value per request"):
+        _per_request([1, 2, 3], 2)
+    with pytest.raises(ValueError, match="one value per request"):
+        _per_request((1, 2), 3)
