@@ -114,3 +114,48 @@ def test_inline_slot_ranges_equal_device_ranges():
         outs.append(out)
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("rotary", [False, True])
+def test_token_axis_forms_of_the_rows_give_the_same_call(rotary):
+    """The manager's rows arrive as [B, H, 1, 128] or [B, H, 128]; contiguous ones are checked as they
+    are and strided ones (with the folded rotation) are sliced: both forms give the same output and the
+    same ring rows, bit for bit, over three appends on a stacked executor."""
+    import r2omni_amd as ro
+    from r2omni_amd.workloads import DecodeConfig, build_request_cache, make_request
+
+    dev = _cuda()
+    hq, hkv = 28, 4
+    cfg = DecodeConfig("axis", hq, hkv, (0,), (0.15, 0.45, 0.4), recent=100)
+    datas = [make_request(cfg, t, seed=960 + i, device=dev) for i, t in enumerate((1024 + 100, 1536 + 100))]
+
+    def executor():
+        exs = []
+        for d in datas:
+            c = build_request_cache(cfg, d)
+            exs.append(ro.prepare_splitk_executor(c, ro.allocate_splitk_workspace(c, num_query_heads=hq),
+                                                  output_hadamard=True))
+        return ro.stack_homogeneous_splitk_executors(exs)
+
+    ex3, ex4 = executor(), executor()
+    gen = torch.Generator(device=dev).manual_seed(961)
+    pos = [1124, 1636]
+    for step in range(3):
+        q = torch.randn(2, hq, 128, generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn(2, hkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn(2, hkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        rot = None
+        if rotary:
+            ang = torch.rand(3, 2, 1, 64, generator=gen, device=dev) * 6.0
+            ang = torch.cat([ang, ang], dim=-1)
+            rot = ro.FusedRotary(ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16), (16, 24, 24), True, True)
+        print(f"[edge] token-axis forms, rotary={rotary}, step {step}", flush=True)
+        a = ex3(q, append=(k, v, pos, pos), rotary=rot).clone()
+        b = ex4(q[:, :, None], append=(k[:, :, None], v[:, :, None], pos, pos), rotary=rot).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"step {step}"
+        pos = [p + 1 for p in pos]
+    for ra, rb in zip(ex3.batched_recent, ex4.batched_recent):
+        assert torch.equal(ra.fp_k.view(torch.int16), rb.fp_k.view(torch.int16))
+        assert torch.equal(ra.fp_v.view(torch.int16), rb.fp_v.view(torch.int16))
+        assert int(ra.length_device.item()) == int(rb.length_device.item()) == 103
